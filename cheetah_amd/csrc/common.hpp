@@ -1,0 +1,97 @@
+// Shared device/host helpers for the gfx950 decoder-forward kernels.
+//
+// Everything is built with -ffp-contract=off: a*b+c is two roundings unless
+// the code writes fmaf() itself. The reference (Rust) never contracts, and
+// the elementwise steps that must stay bit-identical to it (RoPE, residual
+// adds, bias adds, dequantization, quantization) rely on this.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+namespace chip {
+
+// ---------------------------------------------------------------------------
+// Error plumbing: a thread-local sentence, -1 returns (cheetah_vulkan.c-style).
+// ---------------------------------------------------------------------------
+void set_error(const std::string &message);
+const char *last_error();
+
+#define CHIP_CHECK(expr)                                                                      \
+    do {                                                                                      \
+        hipError_t chip_err_ = (expr);                                                        \
+        if (chip_err_ != hipSuccess) {                                                        \
+            ::chip::set_error(std::string("HIP backend: ") + #expr + " failed: " +             \
+                              hipGetErrorString(chip_err_));                                  \
+            return -1;                                                                        \
+        }                                                                                     \
+    } while (0)
+
+#define CHIP_TRY(expr)                 \
+    do {                               \
+        if ((expr) != 0) return -1;    \
+    } while (0)
+
+inline int fail(const std::string &message) {
+    set_error(message);
+    return -1;
+}
+
+// Weight formats (codes match the reference's format ids: stored BF16 = 1,
+// q8 = 4, q4 = 5; precision.rs registry).
+enum WFmt : int { FMT_BF16 = 1, FMT_Q8 = 4, FMT_Q4 = 5 };
+
+inline size_t q8_row_bytes(size_t cols) { return (cols + 3) / 4 * 4; }
+inline size_t q4_row_bytes(size_t cols) { return ((cols + 2) / 2 + 3) / 4 * 4; }
+inline size_t fmt_row_bytes(int fmt, size_t cols) {
+    return fmt == FMT_BF16 ? cols * 2 : fmt == FMT_Q8 ? q8_row_bytes(cols) : q4_row_bytes(cols);
+}
+inline size_t fmt_buffer_bytes(int fmt, size_t rows, size_t cols) {
+    return fmt == FMT_BF16 ? rows * cols * 2 : rows * 4 + rows * fmt_row_bytes(fmt, cols);
+}
+
+// The library stream used by the op-level entry points.
+hipStream_t lib_stream();
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// Device scalars.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_lo(uint32_t word) { return __uint_as_float(word << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t word) { return __uint_as_float(word & 0xFFFF0000u); }
+__device__ __forceinline__ float bf16_f32(uint16_t bits) { return __uint_as_float((uint32_t)bits << 16); }
+
+// f32 -> BF16 bits, round to nearest even (NaN stays NaN).
+__device__ __forceinline__ uint16_t f32_bf16_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+template <class T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+// Sum over aligned groups of `W` consecutive lanes (W a power of two <= 64).
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int off = W / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+}  // namespace chip

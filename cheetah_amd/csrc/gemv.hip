@@ -1,0 +1,283 @@
+// Decode GEMV y = W x for BF16 / Q8 / Q4 weights in the reference layouts
+// (ops.rs:246 gemv, 544 gemv_q8, 586 gemv_q4). HBM-bound: each weight byte is
+// read once, dequantized in registers (BF16: bits << 16; Q8/Q4: sign-extended
+// code, row scale applied once to the row sum) and FMA'd against x held in LDS.
+//
+// Work split: one wave owns R consecutive rows and strides its 64 lanes along
+// K in "units" of UB bytes (16 = dwordx4 when every row start is 16-byte
+// aligned, else 4 = dword, which Q4's 4-byte row padding needs). Blocks are
+// 4 waves; the grid strides over row groups so a fused RMSNorm prologue runs
+// once per block, not once per row.
+#include "kernels.hpp"
+
+namespace chip {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+
+template <int FMT, int UB>
+struct Unit;
+
+// BF16: 2 elements per dword.
+template <int UB>
+struct Unit<FMT_BF16, UB> {
+    static constexpr int E = UB / 2;
+    static constexpr int D = UB / 4;
+    template <class F>
+    __device__ static void decode(const uint32_t (&raw)[D], F &&f) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            f(2 * d, bf16_lo(raw[d]));
+            f(2 * d + 1, bf16_hi(raw[d]));
+        }
+    }
+    __device__ static float element(const uint8_t *row, int e) {
+        return bf16_f32(*(const uint16_t *)(row + 2 * e));
+    }
+};
+
+// Q8: 4 int8 codes per dword.
+template <int UB>
+struct Unit<FMT_Q8, UB> {
+    static constexpr int E = UB;
+    static constexpr int D = UB / 4;
+    template <class F>
+    __device__ static void decode(const uint32_t (&raw)[D], F &&f) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+#pragma unroll
+            for (int b = 0; b < 4; ++b) f(4 * d + b, (float)(int)(int8_t)(raw[d] >> (8 * b)));
+        }
+    }
+    __device__ static float element(const uint8_t *row, int e) { return (float)(int8_t)row[e]; }
+};
+
+// Q4: 8 int4 codes per dword; nibble n of a dword is column 8*word + n
+// (low nibble = even column, q4.rs:12-24).
+template <int UB>
+struct Unit<FMT_Q4, UB> {
+    static constexpr int E = UB * 2;
+    static constexpr int D = UB / 4;
+    template <class F>
+    __device__ static void decode(const uint32_t (&raw)[D], F &&f) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+#pragma unroll
+            for (int n = 0; n < 8; ++n) f(8 * d + n, (float)(((int)(raw[d] << (28 - 4 * n))) >> 28));
+        }
+    }
+    __device__ static float element(const uint8_t *row, int e) {
+        uint8_t byte = row[e >> 1];
+        int nib = (e & 1) ? (byte >> 4) : (byte & 0xF);
+        return (float)(nib >= 8 ? nib - 16 : nib);
+    }
+};
+
+template <int UB>
+__device__ __forceinline__ void load_raw(const uint8_t *p, uint32_t (&raw)[UB / 4]) {
+    if constexpr (UB == 16) {
+        u32x4 v = __builtin_nontemporal_load((const u32x4 *)p);
+        raw[0] = v[0];
+        raw[1] = v[1];
+        raw[2] = v[2];
+        raw[3] = v[3];
+    } else {
+        raw[0] = __builtin_nontemporal_load((const uint32_t *)p);
+    }
+}
+
+struct Args {
+    const uint8_t *w, *w2;
+    const float *sc, *sc2;
+    size_t stride;
+    int rows, K;
+    const float *x;
+    const uint16_t *gain;
+    float eps;
+    const float *bias;
+    float *y;
+    float *residual;
+    int epi;
+};
+
+template <int FMT, int UB, int R, bool NORM, bool DUAL>
+__global__ __launch_bounds__(kThreads) void gemv_kernel(Args a) {
+    using U = Unit<FMT, UB>;
+    constexpr int E = U::E;
+    constexpr int D = U::D;
+    constexpr int UNROLL = UB == 16 ? 2 : 4;
+    extern __shared__ float xs[];
+    __shared__ float red[kWaves];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int K = a.K;
+
+    // Stage x (optionally RMSNorm'd: x * (inv * gain), ops.rs:646-652) in LDS.
+    if constexpr (NORM) {
+        float ss = 0.f;
+        for (int i = tid; i < K; i += kThreads) {
+            float v = a.x[i];
+            ss = fmaf(v, v, ss);
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        float total = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) total += red[w];
+        const float inv = 1.0f / sqrtf(total / (float)K + a.eps);
+        for (int i = tid; i < K; i += kThreads) xs[i] = a.x[i] * (inv * bf16_f32(a.gain[i]));
+    } else {
+        for (int i = tid; i < K; i += kThreads) xs[i] = a.x[i];
+    }
+    __syncthreads();
+
+    const int n_units = K / E;
+    const int tail0 = n_units * E;
+    const int groups = (a.rows + R - 1) / R;
+    for (int group = blockIdx.x * kWaves + wave; group < groups; group += gridDim.x * kWaves) {
+        const int row0 = group * R;
+        const uint8_t *rp[R];
+        const uint8_t *rp2[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            int row = min(row0 + r, a.rows - 1);
+            rp[r] = a.w + (size_t)row * a.stride;
+            rp2[r] = DUAL ? a.w2 + (size_t)row * a.stride : nullptr;
+        }
+        float acc[R], acc2[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = acc2[r] = 0.f;
+
+        for (int u0 = lane; u0 < n_units; u0 += 64 * UNROLL) {
+            uint32_t raw[UNROLL][R][D];
+            uint32_t raw2[UNROLL][R][DUAL ? D : 1];
+#pragma unroll
+            for (int i = 0; i < UNROLL; ++i) {
+                const int u = u0 + 64 * i;
+                if (u < n_units) {
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        load_raw<UB>(rp[r] + (size_t)u * UB, raw[i][r]);
+                        if constexpr (DUAL) load_raw<UB>(rp2[r] + (size_t)u * UB, raw2[i][r]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < UNROLL; ++i) {
+                const int u = u0 + 64 * i;
+                if (u < n_units) {
+                    const float *xu = xs + u * E;
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        U::decode(raw[i][r], [&](int e, float wv) { acc[r] = fmaf(wv, xu[e], acc[r]); });
+                        if constexpr (DUAL)
+                            U::decode(raw2[i][r], [&](int e, float wv) { acc2[r] = fmaf(wv, xu[e], acc2[r]); });
+                    }
+                }
+            }
+        }
+        // Ragged tail (K not a multiple of the unit width).
+        for (int e = tail0 + lane; e < K; e += 64) {
+            const float xv = xs[e];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                acc[r] = fmaf(U::element(rp[r], e), xv, acc[r]);
+                if constexpr (DUAL) acc2[r] = fmaf(U::element(rp2[r], e), xv, acc2[r]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            acc[r] = wave_sum(acc[r]);
+            if constexpr (DUAL) acc2[r] = wave_sum(acc2[r]);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int row = row0 + r;
+            if (lane == r && row < a.rows) {
+                float v = acc[r];
+                if (a.sc) v = v * a.sc[row];
+                if constexpr (DUAL) {
+                    float u = acc2[r];
+                    if (a.sc2) u = u * a.sc2[row];
+                    // silu_multiply, ops.rs:743-747: g * (u / (1 + exp(-g))).
+                    a.y[row] = v * (u / (1.0f + expf(-v)));
+                } else {
+                    if (a.bias) v = v + a.bias[row];
+                    if (a.epi == EPI_RESIDUAL) a.residual[row] = a.residual[row] + v;
+                    else a.y[row] = v;
+                }
+            }
+        }
+    }
+}
+
+template <int FMT, int UB, int R, bool NORM, bool DUAL>
+int launch_t(const Args &a, hipStream_t s) {
+    const int groups = (a.rows + R - 1) / R;
+    int blocks = (groups + kWaves - 1) / kWaves;
+    if (NORM) blocks = min(blocks, 2048);
+    const size_t lds = (size_t)a.K * sizeof(float);
+    hipLaunchKernelGGL((gemv_kernel<FMT, UB, R, NORM, DUAL>), dim3(blocks), dim3(kThreads), lds, s, a);
+    CHIP_CHECK(hipGetLastError());
+    return 0;
+}
+
+template <int FMT, int UB, bool NORM, bool DUAL>
+int pick_r(const Args &a, hipStream_t s) {
+    if (a.rows >= 16384) return launch_t<FMT, UB, 2, NORM, DUAL>(a, s);
+    return launch_t<FMT, UB, 1, NORM, DUAL>(a, s);
+}
+
+template <int FMT, bool NORM, bool DUAL>
+int pick_ub(const Args &a, bool aligned16, hipStream_t s) {
+    if (aligned16) return pick_r<FMT, 16, NORM, DUAL>(a, s);
+    return pick_r<FMT, 4, NORM, DUAL>(a, s);
+}
+
+template <int FMT>
+int pick_mode(const Args &a, bool aligned16, bool norm, bool dual, hipStream_t s) {
+    if (norm) return dual ? pick_ub<FMT, true, true>(a, aligned16, s) : pick_ub<FMT, true, false>(a, aligned16, s);
+    return dual ? pick_ub<FMT, false, true>(a, aligned16, s) : pick_ub<FMT, false, false>(a, aligned16, s);
+}
+
+}  // namespace
+
+int launch_gemv(const GemvJob &job, hipStream_t s) {
+    const WMat &w = job.w;
+    if (!w.base || !job.x || w.rows == 0 || w.cols == 0) return fail("HIP backend: gemv needs a weight and an input.");
+    if (w.rows > (size_t)INT32_MAX || w.cols > (size_t)INT32_MAX) return fail("HIP backend: gemv shape too large.");
+    const bool dual = job.epi == EPI_SWIGLU;
+    if (dual && (!job.w2.base || job.w2.fmt != w.fmt || job.w2.rows != w.rows || job.w2.cols != w.cols))
+        return fail("HIP backend: SwiGLU gemv needs gate and up matrices of one shape and format.");
+    if (job.epi == EPI_RESIDUAL ? !job.residual : !job.y) return fail("HIP backend: gemv has no output.");
+    if ((size_t)w.cols * sizeof(float) + 64 > device_max_lds())
+        return fail("HIP backend: gemv input width " + std::to_string(w.cols) + " exceeds the LDS staging limit.");
+    Args a{};
+    a.w = w.payload();
+    a.sc = w.scales();
+    a.w2 = dual ? job.w2.payload() : nullptr;
+    a.sc2 = dual ? job.w2.scales() : nullptr;
+    a.stride = w.row_stride();
+    a.rows = (int)w.rows;
+    a.K = (int)w.cols;
+    a.x = job.x;
+    a.gain = job.norm_gain;
+    a.eps = job.eps;
+    a.bias = job.bias;
+    a.y = job.y;
+    a.residual = job.residual;
+    a.epi = job.epi;
+    bool aligned16 = a.stride % 16 == 0 && ((uintptr_t)a.w % 16) == 0 && (!dual || ((uintptr_t)a.w2 % 16) == 0);
+    const bool norm = job.norm_gain != nullptr;
+    switch (w.fmt) {
+        case FMT_BF16: return pick_mode<FMT_BF16>(a, aligned16, norm, dual, s);
+        case FMT_Q8: return pick_mode<FMT_Q8>(a, aligned16, norm, dual, s);
+        case FMT_Q4: return pick_mode<FMT_Q4>(a, aligned16, norm, dual, s);
+    }
+    return fail("HIP backend: unknown weight format.");
+}
+
+}  // namespace chip

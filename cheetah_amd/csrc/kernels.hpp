@@ -1,0 +1,121 @@
+// Host-side launchers of the gfx950 kernels. Every launcher validates the
+// shapes it is given before touching the device and returns 0 / -1.
+#pragma once
+
+#include "common.hpp"
+
+namespace chip {
+
+// Largest LDS allocation one block may make (queried at init).
+size_t device_max_lds();
+
+// ---------------------------------------------------------------------------
+// Weight matrix in device memory, in the reference's layout.
+// ---------------------------------------------------------------------------
+struct WMat {
+    int fmt = FMT_BF16;
+    const uint8_t *base = nullptr;  // start of the buffer (scale head first for q8/q4)
+    size_t rows = 0, cols = 0;
+    const float *scales() const { return fmt == FMT_BF16 ? nullptr : (const float *)base; }
+    const uint8_t *payload() const { return fmt == FMT_BF16 ? base : base + rows * 4; }
+    size_t row_stride() const { return fmt_row_bytes(fmt, cols); }
+    size_t bytes() const { return fmt_buffer_bytes(fmt, rows, cols); }
+};
+
+// Epilogue of a GEMV / GEMM: out = f(acc * row_scale (+ bias)).
+enum Epi : int {
+    EPI_STORE = 0,     // y = v
+    EPI_RESIDUAL = 1,  // residual += v            (y unused)
+    EPI_SWIGLU = 2,    // y = g * (u / (1 + exp(-g)))  (dual matrix: gate, up)
+};
+
+struct GemvJob {
+    WMat w;              // the matrix (gate for EPI_SWIGLU)
+    WMat w2;             // up matrix for EPI_SWIGLU
+    const float *x = nullptr;        // input vector [cols] (hidden when norm_gain is set)
+    const uint16_t *norm_gain = nullptr;  // BF16 RMSNorm gain: x := rmsnorm(x) first
+    float eps = 0.f;
+    const float *bias = nullptr;     // f32 [rows]
+    float *y = nullptr;              // output [rows]
+    float *residual = nullptr;       // EPI_RESIDUAL target [rows]
+    int epi = EPI_STORE;
+};
+int launch_gemv(const GemvJob &job, hipStream_t stream);
+
+struct GemmJob {
+    WMat w, w2;
+    const float *x = nullptr;  // [n][cols] f32
+    size_t n = 0;
+    const float *bias = nullptr;
+    float *y = nullptr;          // [n][rows]
+    float *residual = nullptr;   // [n][rows]
+    int epi = EPI_STORE;
+};
+int launch_gemm(const GemmJob &job, hipStream_t stream);
+
+// ---------------------------------------------------------------------------
+// Quantization (bit-exact to q8.rs / q4.rs quantize) and dequantization.
+// ---------------------------------------------------------------------------
+int launch_quantize(int fmt, const uint16_t *w_bf16, size_t rows, size_t cols, uint8_t *out, hipStream_t s);
+int launch_dequant(const WMat &w, float *out, hipStream_t s);
+
+// ---------------------------------------------------------------------------
+// Small ops.
+// ---------------------------------------------------------------------------
+// hidden[i][:] = bf16 table[tokens[i]][:]
+int launch_embed(const uint16_t *table, size_t hidden, const uint32_t *tokens, size_t rows, float *out,
+                 hipStream_t s);
+// out[i][:] = rmsnorm(x[i][:]) * gain (rows of width n)
+int launch_rmsnorm_rows(const float *x, const uint16_t *gain, float eps, size_t rows, size_t n, float *out,
+                        hipStream_t s);
+
+// Paged KV cache of one layer.
+struct KvLayer {
+    uint16_t *k = nullptr;  // [pages][kv_heads][page_size][head_dim]
+    uint16_t *v = nullptr;
+};
+struct KvGeom {
+    const int32_t *page_table = nullptr;  // device
+    int page_size = 64;
+    int kv_heads = 0;
+    int head_dim = 0;
+};
+
+// RoPE (rotate-half, host cos/sin table) on the q and k parts of packed
+// qkv rows [rows][q_dim + 2*kv_dim], then K and V rows appended to the
+// paged cache as BF16. Positions are pos0 + i, where pos0 is read from
+// *pos_dev when pos_dev is set (decode graph) and is `offset` otherwise.
+int launch_rope_append(float *qkv, size_t rows, int q_heads, const KvGeom &g, const KvLayer &kv,
+                       const float *rope_cos, const float *rope_sin, int rotary_dim, size_t offset,
+                       const int32_t *pos_dev, hipStream_t s);
+
+// GQA attention for `rows` query rows at positions pos0 + i over keys
+// [0, pos0 + i]. q row stride q_stride floats. Splits are fixed by the
+// caller (decode graphs need a fixed grid); partial buffers sized for
+// rows * q_heads * splits * (head_dim + 2) floats.
+struct AttnJob {
+    const float *q = nullptr;
+    size_t q_stride = 0;
+    float *out = nullptr;  // [rows][q_heads*head_dim]
+    const uint16_t *k = nullptr, *v = nullptr;
+    KvGeom g;
+    int q_heads = 0;
+    size_t rows = 0;
+    size_t offset = 0;
+    const int32_t *pos_dev = nullptr;
+    int splits = 1;
+    float *part = nullptr;  // partial buffer
+};
+int launch_attention(const AttnJob &job, hipStream_t s);
+size_t attention_part_floats(size_t rows, int q_heads, int splits, int head_dim);
+
+// Greedy argmax (ties -> last index, total order) of logits[n]; writes the
+// index to *out_token. When `step` is set (the device-side decode loop,
+// step[0] = token, step[1] = position) it also records the index as the
+// token of position step[1] + 1 in hist[] (when that is < hist_cap), stores
+// it in step[0] and advances step[1] by one.
+int launch_argmax(const float *logits, size_t n, uint32_t *out_token, int32_t *step, uint32_t *hist,
+                  size_t hist_cap, void *scratch, hipStream_t s);
+size_t argmax_scratch_bytes();
+
+}  // namespace chip

@@ -1,0 +1,189 @@
+// Small per-row kernels of the decoder forward: embedding gather, RMSNorm
+// rows, fused RoPE + paged BF16 KV append, and greedy argmax.
+#include "kernels.hpp"
+
+namespace chip {
+namespace {
+
+constexpr int kThreads = 256;
+
+// embedding_row_into (ops.rs:1083-1099): BF16 -> f32 widening.
+__global__ __launch_bounds__(kThreads) void embed_kernel(const uint16_t *table, int hidden, const uint32_t *tokens,
+                                                         float *out) {
+    const uint32_t tok = tokens[blockIdx.x];
+    const uint16_t *src = table + (size_t)tok * hidden;
+    float *dst = out + (size_t)blockIdx.x * hidden;
+    for (int i = threadIdx.x; i < hidden; i += kThreads) dst[i] = bf16_f32(src[i]);
+}
+
+// rmsnorm (ops.rs:646-652): x * (inv * gain), inv = 1 / sqrt(mean(x^2) + eps).
+__global__ __launch_bounds__(kThreads) void rmsnorm_rows_kernel(const float *x, const uint16_t *gain, float eps, int n,
+                                                                float *out) {
+    __shared__ float red[kThreads / 64];
+    const float *src = x + (size_t)blockIdx.x * n;
+    float *dst = out + (size_t)blockIdx.x * n;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += kThreads) ss = fmaf(src[i], src[i], ss);
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float total = red[0] + red[1] + red[2] + red[3];
+    const float inv = 1.0f / sqrtf(total / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += kThreads) dst[i] = src[i] * (inv * bf16_f32(gain[i]));
+}
+
+// rope_heads (ops.rs:693-740) with the angle's cos/sin read from a table the
+// host filled with the same libm powf/sinf/cosf the reference calls, so q and
+// k come out bit-identical to the CPU path for identical inputs; then
+// cache_append (ops.rs:1329-1332) into the paged BF16 cache.
+__global__ __launch_bounds__(kThreads) void rope_append_kernel(float *qkv, int q_heads, int kv_heads, int head_dim,
+                                                               int rotary_dim, const float *cos_t,
+                                                               const float *sin_t, const int32_t *page_table,
+                                                               int page_size, uint16_t *kc, uint16_t *vc,
+                                                               long offset, const int32_t *pos_dev) {
+    const int row = blockIdx.x;
+    const long pos = (pos_dev ? (long)*pos_dev : offset) + row;
+    const int q_dim = q_heads * head_dim, kv_dim = kv_heads * head_dim;
+    float *q = qkv + (size_t)row * (q_dim + 2 * kv_dim);
+    float *k = q + q_dim;
+    float *v = k + kv_dim;
+    const int half = rotary_dim / 2;
+    const float *cr = cos_t + (size_t)pos * half;
+    const float *sr = sin_t + (size_t)pos * half;
+    for (int t = threadIdx.x; t < q_heads * half; t += kThreads) {
+        const int h = t / half, i = t % half;
+        float *base = q + h * head_dim;
+        const float a = base[i], b = base[half + i], c = cr[i], s = sr[i];
+        base[i] = a * c - b * s;
+        base[half + i] = b * c + a * s;
+    }
+    const int page = page_table[pos / page_size];
+    const int slot = (int)(pos % page_size);
+    for (int t = threadIdx.x; t < kv_dim; t += kThreads) {
+        const int h = t / head_dim, d = t % head_dim;
+        float kv = k[t];
+        if (d < rotary_dim) {
+            const int i = d < half ? d : d - half;
+            const float c = cr[i], s = sr[i];
+            const float a = k[h * head_dim + i], b = k[h * head_dim + half + i];
+            kv = d < half ? a * c - b * s : b * c + a * s;
+        }
+        const size_t off = (((size_t)page * kv_heads + h) * page_size + slot) * head_dim + d;
+        kc[off] = f32_bf16_rne(kv);
+        vc[off] = f32_bf16_rne(v[t]);
+    }
+}
+
+// Total order of f32::total_cmp as a signed integer key.
+__device__ __forceinline__ int total_key(float f) {
+    int i = __float_as_int(f);
+    return i ^ (int)(((unsigned)(i >> 31)) >> 1);
+}
+
+// max_by(total_cmp) keeps the LAST maximal element (engine.rs:2247-2253):
+// among equal keys the larger index wins.
+__device__ __forceinline__ void better(int &key, uint32_t &idx, int k2, uint32_t i2) {
+    if (k2 > key || (k2 == key && i2 > idx)) {
+        key = k2;
+        idx = i2;
+    }
+}
+
+__device__ __forceinline__ void block_argmax(int &key, uint32_t &idx) {
+    __shared__ int skey[kThreads / 64];
+    __shared__ uint32_t sidx[kThreads / 64];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        int k2 = __shfl_xor(key, off, 64);
+        uint32_t i2 = __shfl_xor(idx, off, 64);
+        better(key, idx, k2, i2);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        skey[threadIdx.x >> 6] = key;
+        sidx[threadIdx.x >> 6] = idx;
+    }
+    __syncthreads();
+    key = skey[0];
+    idx = sidx[0];
+    for (int w = 1; w < kThreads / 64; ++w) better(key, idx, skey[w], sidx[w]);
+}
+
+constexpr int kArgmaxBlocks = 64;
+
+__global__ __launch_bounds__(kThreads) void argmax_partial_kernel(const float *x, int n, int *pkey, uint32_t *pidx) {
+    int key = INT_MIN;
+    uint32_t idx = 0;
+    for (int i = blockIdx.x * kThreads + threadIdx.x; i < n; i += gridDim.x * kThreads)
+        better(key, idx, total_key(x[i]), (uint32_t)i);
+    block_argmax(key, idx);
+    if (threadIdx.x == 0) {
+        pkey[blockIdx.x] = key;
+        pidx[blockIdx.x] = idx;
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void argmax_final_kernel(const int *pkey, const uint32_t *pidx, int parts,
+                                                                uint32_t *out, int32_t *step, uint32_t *hist,
+                                                                long hist_cap) {
+    int key = INT_MIN;
+    uint32_t idx = 0;
+    for (int i = threadIdx.x; i < parts; i += kThreads) better(key, idx, pkey[i], pidx[i]);
+    block_argmax(key, idx);
+    if (threadIdx.x == 0) {
+        if (out) *out = idx;
+        if (step) {
+            const long next = (long)step[1] + 1;
+            if (hist && next < hist_cap) hist[next] = idx;
+            step[0] = (int32_t)idx;
+            step[1] = (int32_t)next;
+        }
+    }
+}
+
+}  // namespace
+
+int launch_embed(const uint16_t *table, size_t hidden, const uint32_t *tokens, size_t rows, float *out,
+                 hipStream_t s) {
+    if (rows == 0) return 0;
+    hipLaunchKernelGGL(embed_kernel, dim3(rows), dim3(kThreads), 0, s, table, (int)hidden, tokens, out);
+    CHIP_CHECK(hipGetLastError());
+    return 0;
+}
+
+int launch_rmsnorm_rows(const float *x, const uint16_t *gain, float eps, size_t rows, size_t n, float *out,
+                        hipStream_t s) {
+    if (rows == 0) return 0;
+    hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(rows), dim3(kThreads), 0, s, x, gain, eps, (int)n, out);
+    CHIP_CHECK(hipGetLastError());
+    return 0;
+}
+
+int launch_rope_append(float *qkv, size_t rows, int q_heads, const KvGeom &g, const KvLayer &kv,
+                       const float *rope_cos, const float *rope_sin, int rotary_dim, size_t offset,
+                       const int32_t *pos_dev, hipStream_t s) {
+    if (rows == 0) return 0;
+    if (rotary_dim <= 0 || rotary_dim > g.head_dim || rotary_dim % 2)
+        return fail("HIP backend: rotary_dim must be even and at most head_dim.");
+    hipLaunchKernelGGL(rope_append_kernel, dim3(rows), dim3(kThreads), 0, s, qkv, q_heads, g.kv_heads, g.head_dim,
+                       rotary_dim, rope_cos, rope_sin, g.page_table, g.page_size, kv.k, kv.v, (long)offset,
+                       pos_dev);
+    CHIP_CHECK(hipGetLastError());
+    return 0;
+}
+
+size_t argmax_scratch_bytes() { return kArgmaxBlocks * (sizeof(int) + sizeof(uint32_t)); }
+
+int launch_argmax(const float *logits, size_t n, uint32_t *out_token, int32_t *step, uint32_t *hist,
+                  size_t hist_cap, void *scratch, hipStream_t s) {
+    if (n == 0 || n > (size_t)INT32_MAX) return fail("HIP backend: argmax over an empty or oversized vector.");
+    int *pkey = (int *)scratch;
+    uint32_t *pidx = (uint32_t *)(pkey + kArgmaxBlocks);
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(kArgmaxBlocks), dim3(kThreads), 0, s, logits, (int)n, pkey, pidx);
+    CHIP_CHECK(hipGetLastError());
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kThreads), 0, s, (const int *)pkey, (const uint32_t *)pidx,
+                       kArgmaxBlocks, out_token, step, hist, (long)hist_cap);
+    CHIP_CHECK(hipGetLastError());
+    return 0;
+}
+
+}  // namespace chip

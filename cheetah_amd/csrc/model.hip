@@ -1,0 +1,893 @@
+// The HIP ModelForward (registry.rs:57-85) for the qwen2 / llama decoder
+// forward (registrations/qwen2.rs:132-597, llama.rs:134-600).
+//
+// Device residency: every weight lives in HBM in the reference's own byte
+// layout (BF16 rows; Q8/Q4 scale head + padded rows). q/k/v are stored as
+// one [q_dim + 2 kv_dim, hidden] matrix (row-wise quantization makes
+// quantize(concat) == concat(quantize)), gate and up stay separate matrices
+// read by one dual GEMV / GEMM whose epilogue applies SwiGLU.
+//
+// KV cache: BF16 pages of 64 positions, [page][kv_head][64][head_dim] per
+// layer for K and for V. A page id indexes every layer's pool; one page
+// table per model maps logical page -> physical page. Pages are refcounted
+// across a model, its clones and snapshots: a snapshot takes references, a
+// restore maps them, and the first write into a shared page copies it.
+//
+// Decode (n == 1) is one captured hipGraph: embedding, 24-32 layers of
+// {QKV GEMV with fused RMSNorm + bias, RoPE + KV append, split-K attention,
+// o GEMV + residual, gate/up GEMV with fused RMSNorm + SwiGLU, down GEMV +
+// residual}, LM head GEMV with fused final norm, argmax. The token and
+// position live in device memory, so the same graph replays every step and
+// the greedy loop can run back to back with no host round trip.
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/cheetah_hip.h"
+#include "kernels.hpp"
+
+namespace chip {
+int ensure_ready();
+}
+
+using namespace chip;
+
+namespace {
+
+constexpr int kPageSize = 64;
+constexpr int kPrefillSplits = 16;
+
+struct DevAlloc {
+    std::vector<void *> ptrs;
+    template <class T>
+    int alloc(T **p, size_t count) {
+        void *q = nullptr;
+        CHIP_CHECK(hipMalloc(&q, count * sizeof(T) > 0 ? count * sizeof(T) : 16));
+        ptrs.push_back(q);
+        *p = (T *)q;
+        return 0;
+    }
+    void release(void *p) {
+        for (auto &q : ptrs)
+            if (q == p) {
+                (void)hipFree(q);
+                q = nullptr;
+            }
+    }
+    ~DevAlloc() {
+        for (void *q : ptrs)
+            if (q) (void)hipFree(q);
+    }
+};
+
+struct Staged {
+    void *dev = nullptr;            // 2-D units: device BF16 copy
+    std::vector<uint16_t> host;     // 1-D units: host BF16 copy
+    std::vector<uint64_t> shape;
+};
+
+struct Layer {
+    WMat qkv, o, gate, up, down;
+    float *qkv_bias = nullptr;  // f32 [q_dim + 2 kv_dim] (zeros when absent)
+    float *o_bias = nullptr;    // f32 [hidden] or null
+    uint16_t *ln1 = nullptr, *ln2 = nullptr;
+    KvLayer kv;
+};
+
+// Weights, rope table and KV pool: shared by a model, its clones and
+// snapshots.
+struct Shared {
+    cheetah_hip_config cfg{};
+    int quant = 0;  // 0, FMT_Q8, FMT_Q4
+    size_t kv_capacity = 0, max_chunk = 0;
+    bool finalized = false;
+    std::unordered_map<std::string, Staged> staged;
+    DevAlloc mem;
+    std::vector<Layer> layers;
+    uint16_t *embed = nullptr;
+    WMat head;
+    uint16_t *final_norm = nullptr;
+    float *rope_cos = nullptr, *rope_sin = nullptr;
+    int num_pages = 0;
+    size_t page_elems = 0;  // BF16 elements of one page of one layer (K or V)
+    std::mutex mu;
+    std::vector<int> refs;
+    std::vector<int> free_list;
+    hipStream_t copy_stream = nullptr;
+
+    int q_dim() const { return (int)(cfg.q_heads * cfg.head_dim); }
+    int kv_dim() const { return (int)(cfg.kv_heads * cfg.head_dim); }
+
+    ~Shared() {
+        if (copy_stream) {
+            (void)hipStreamSynchronize(copy_stream);
+            (void)hipStreamDestroy(copy_stream);
+        }
+        for (auto &kv : staged)
+            if (kv.second.dev) (void)hipFree(kv.second.dev);
+    }
+
+    int page_alloc() {
+        std::lock_guard<std::mutex> lock(mu);
+        if (free_list.empty()) return -1;
+        int p = free_list.back();
+        free_list.pop_back();
+        refs[p] = 1;
+        return p;
+    }
+    void page_ref(int p) {
+        std::lock_guard<std::mutex> lock(mu);
+        ++refs[p];
+    }
+    void page_unref(int p) {
+        std::lock_guard<std::mutex> lock(mu);
+        if (--refs[p] == 0) free_list.push_back(p);
+    }
+    int page_refs(int p) {
+        std::lock_guard<std::mutex> lock(mu);
+        return refs[p];
+    }
+};
+
+}  // namespace
+
+struct cheetah_hip_snapshot {
+    std::shared_ptr<Shared> sh;
+    std::vector<int> pages;
+    size_t positions = 0;
+    ~cheetah_hip_snapshot() {
+        for (int p : pages) sh->page_unref(p);
+    }
+};
+
+struct cheetah_hip_model {
+    std::shared_ptr<Shared> sh;
+    hipStream_t stream = nullptr;
+    DevAlloc mem;
+    std::vector<int> pages;  // logical -> physical
+    std::vector<int32_t> page_host;
+    int32_t *page_dev = nullptr;
+    size_t len = 0;
+    // activations
+    float *hidden = nullptr, *normed = nullptr, *qkv = nullptr, *attn = nullptr, *act = nullptr;
+    float *logits = nullptr, *part = nullptr;
+    uint32_t *tokens_dev = nullptr, *next_dev = nullptr, *hist_dev = nullptr;
+    int32_t *step_dev = nullptr;  // [0] = token, [1] = position
+    void *argmax_scratch = nullptr;
+    int32_t *step_host = nullptr;    // pinned
+    uint32_t *tokens_host = nullptr;  // pinned staging for chunk tokens
+    float *logits_host = nullptr;     // pinned
+    int dec_splits = 1;
+    hipGraphExec_t graph = nullptr;
+
+    ~cheetah_hip_model() {
+        if (stream) (void)hipStreamSynchronize(stream);
+        if (graph) (void)hipGraphExecDestroy(graph);
+        if (stream) (void)hipStreamDestroy(stream);
+        if (step_host) (void)hipHostFree(step_host);
+        if (tokens_host) (void)hipHostFree(tokens_host);
+        if (logits_host) (void)hipHostFree(logits_host);
+        for (int p : pages) sh->page_unref(p);
+    }
+};
+
+namespace {
+
+const cheetah_hip_config &C(const cheetah_hip_model *m) { return m->sh->cfg; }
+
+int upload_bf16_1d(Shared &sh, const std::string &id, size_t expect, uint16_t **out, bool required) {
+    auto it = sh.staged.find(id);
+    if (it == sh.staged.end()) {
+        if (required) return fail("HIP backend: missing unit '" + id + "'.");
+        *out = nullptr;
+        return 0;
+    }
+    if (it->second.host.size() != expect)
+        return fail("HIP backend: unit '" + id + "' has " + std::to_string(it->second.host.size()) +
+                    " elements, expected " + std::to_string(expect) + ".");
+    CHIP_TRY(sh.mem.alloc(out, expect));
+    CHIP_CHECK(hipMemcpy(*out, it->second.host.data(), expect * 2, hipMemcpyHostToDevice));
+    return 0;
+}
+
+// Bias units widened to f32 on the host (bias adds are v + bf16_f32(b),
+// ops.rs:1156-1166); absent units become zeros (unit-optional adds).
+int append_bias(Shared &sh, const std::string &id, size_t n, std::vector<float> &out) {
+    auto it = sh.staged.find(id);
+    if (it == sh.staged.end()) {
+        out.insert(out.end(), n, 0.0f);
+        return 0;
+    }
+    if (it->second.host.size() != n) return fail("HIP backend: bias unit '" + id + "' has the wrong length.");
+    for (uint16_t b : it->second.host) {
+        uint32_t u = (uint32_t)b << 16;
+        float f;
+        std::memcpy(&f, &u, 4);
+        out.push_back(f);
+    }
+    return 0;
+}
+
+int take_2d(Shared &sh, const std::string &id, size_t rows, size_t cols, void **dev) {
+    auto it = sh.staged.find(id);
+    if (it == sh.staged.end() || !it->second.dev) return fail("HIP backend: missing unit '" + id + "'.");
+    const auto &s = it->second.shape;
+    if (s.size() != 2 || s[0] != rows || s[1] != cols)
+        return fail("Linear unit '" + id + "' does not match its " + std::to_string(rows) + "x" +
+                    std::to_string(cols) + " shape.");
+    *dev = it->second.dev;
+    it->second.dev = nullptr;
+    return 0;
+}
+
+// BF16 device matrix -> the model's linear format (quantized when selected).
+int make_linear(Shared &sh, void *bf16, size_t rows, size_t cols, WMat *out) {
+    if (!sh.quant) {
+        sh.mem.ptrs.push_back(bf16);
+        *out = WMat{FMT_BF16, (const uint8_t *)bf16, rows, cols};
+        return 0;
+    }
+    uint8_t *q = nullptr;
+    CHIP_TRY(sh.mem.alloc(&q, fmt_buffer_bytes(sh.quant, rows, cols)));
+    CHIP_TRY(launch_quantize(sh.quant, (const uint16_t *)bf16, rows, cols, q, sh.copy_stream));
+    CHIP_CHECK(hipStreamSynchronize(sh.copy_stream));
+    CHIP_CHECK(hipFree(bf16));
+    *out = WMat{sh.quant, q, rows, cols};
+    return 0;
+}
+
+int finalize(cheetah_hip_model *m) {
+    Shared &sh = *m->sh;
+    const auto &c = sh.cfg;
+    const size_t H = c.hidden_size, qd = sh.q_dim(), kvd = sh.kv_dim(), I = c.intermediate_size, V = c.vocab_size;
+    CHIP_CHECK(hipStreamCreateWithFlags(&sh.copy_stream, hipStreamNonBlocking));
+    // Embedding and head (BF16, never quantized: ops.rs:1533-1537).
+    void *emb = nullptr;
+    CHIP_TRY(take_2d(sh, "model.embed_tokens.weight", V, H, &emb));
+    sh.mem.ptrs.push_back(emb);
+    sh.embed = (uint16_t *)emb;
+    if (c.tie_word_embeddings) {
+        sh.head = WMat{FMT_BF16, (const uint8_t *)emb, V, H};
+    } else {
+        void *head = nullptr;
+        if (take_2d(sh, "lm_head.weight", V, H, &head))
+            return fail("Native backend: neither tied embeddings nor a separate 'lm_head.weight' tensor are present.");
+        sh.mem.ptrs.push_back(head);
+        sh.head = WMat{FMT_BF16, (const uint8_t *)head, V, H};
+    }
+    CHIP_TRY(upload_bf16_1d(sh, "model.norm.weight", H, &sh.final_norm, true));
+    sh.layers.resize(c.num_layers);
+    for (uint32_t l = 0; l < c.num_layers; ++l) {
+        Layer &L = sh.layers[l];
+        const std::string p = "model.layers." + std::to_string(l) + ".";
+        CHIP_TRY(upload_bf16_1d(sh, p + "input_layernorm.weight", H, &L.ln1, true));
+        CHIP_TRY(upload_bf16_1d(sh, p + "post_attention_layernorm.weight", H, &L.ln2, true));
+        void *q = nullptr, *k = nullptr, *v = nullptr;
+        CHIP_TRY(take_2d(sh, p + "self_attn.q_proj.weight", qd, H, &q));
+        CHIP_TRY(take_2d(sh, p + "self_attn.k_proj.weight", kvd, H, &k));
+        CHIP_TRY(take_2d(sh, p + "self_attn.v_proj.weight", kvd, H, &v));
+        uint16_t *qkv = nullptr;
+        CHIP_CHECK(hipMalloc(&qkv, (qd + 2 * kvd) * H * 2));
+        CHIP_CHECK(hipMemcpyAsync(qkv, q, qd * H * 2, hipMemcpyDeviceToDevice, sh.copy_stream));
+        CHIP_CHECK(hipMemcpyAsync(qkv + qd * H, k, kvd * H * 2, hipMemcpyDeviceToDevice, sh.copy_stream));
+        CHIP_CHECK(hipMemcpyAsync(qkv + (qd + kvd) * H, v, kvd * H * 2, hipMemcpyDeviceToDevice, sh.copy_stream));
+        CHIP_CHECK(hipStreamSynchronize(sh.copy_stream));
+        CHIP_CHECK(hipFree(q));
+        CHIP_CHECK(hipFree(k));
+        CHIP_CHECK(hipFree(v));
+        CHIP_TRY(make_linear(sh, qkv, qd + 2 * kvd, H, &L.qkv));
+        std::vector<float> bias;
+        CHIP_TRY(append_bias(sh, p + "self_attn.q_proj.bias", qd, bias));
+        CHIP_TRY(append_bias(sh, p + "self_attn.k_proj.bias", kvd, bias));
+        CHIP_TRY(append_bias(sh, p + "self_attn.v_proj.bias", kvd, bias));
+        CHIP_TRY(sh.mem.alloc(&L.qkv_bias, bias.size()));
+        CHIP_CHECK(hipMemcpy(L.qkv_bias, bias.data(), bias.size() * 4, hipMemcpyHostToDevice));
+        if (sh.staged.count(p + "self_attn.o_proj.bias")) {
+            std::vector<float> ob;
+            CHIP_TRY(append_bias(sh, p + "self_attn.o_proj.bias", H, ob));
+            CHIP_TRY(sh.mem.alloc(&L.o_bias, H));
+            CHIP_CHECK(hipMemcpy(L.o_bias, ob.data(), H * 4, hipMemcpyHostToDevice));
+        }
+        void *o = nullptr, *g = nullptr, *u = nullptr, *d = nullptr;
+        CHIP_TRY(take_2d(sh, p + "self_attn.o_proj.weight", H, qd, &o));
+        CHIP_TRY(take_2d(sh, p + "mlp.gate_proj.weight", I, H, &g));
+        CHIP_TRY(take_2d(sh, p + "mlp.up_proj.weight", I, H, &u));
+        CHIP_TRY(take_2d(sh, p + "mlp.down_proj.weight", H, I, &d));
+        CHIP_TRY(make_linear(sh, o, H, qd, &L.o));
+        CHIP_TRY(make_linear(sh, g, I, H, &L.gate));
+        CHIP_TRY(make_linear(sh, u, I, H, &L.up));
+        CHIP_TRY(make_linear(sh, d, H, I, &L.down));
+    }
+    for (auto &kv : sh.staged)
+        if (kv.second.dev) {
+            (void)hipFree(kv.second.dev);
+            kv.second.dev = nullptr;
+        }
+    sh.staged.clear();
+
+    // RoPE table: angle = pos * theta^(-2i/rotary_dim), with libm powf/sinf/
+    // cosf exactly as rope_in_place computes it (ops.rs:702-707).
+    const size_t half = c.rotary_dim / 2;
+    std::vector<float> cs(sh.kv_capacity * half), sn(sh.kv_capacity * half);
+    std::vector<float> freq(half);
+    for (size_t i = 0; i < half; ++i) freq[i] = powf(c.rope_theta, -2.0f * (float)i / (float)c.rotary_dim);
+    for (size_t pos = 0; pos < sh.kv_capacity; ++pos)
+        for (size_t i = 0; i < half; ++i) {
+            const float angle = (float)pos * freq[i];
+            sn[pos * half + i] = sinf(angle);
+            cs[pos * half + i] = cosf(angle);
+        }
+    CHIP_TRY(sh.mem.alloc(&sh.rope_cos, cs.size()));
+    CHIP_TRY(sh.mem.alloc(&sh.rope_sin, sn.size()));
+    CHIP_CHECK(hipMemcpy(sh.rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+    CHIP_CHECK(hipMemcpy(sh.rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+
+    // KV pool.
+    sh.num_pages = (int)((sh.kv_capacity + kPageSize - 1) / kPageSize);
+    sh.page_elems = (size_t)c.kv_heads * kPageSize * c.head_dim;
+    for (auto &L : sh.layers) {
+        CHIP_TRY(sh.mem.alloc(&L.kv.k, sh.page_elems * sh.num_pages));
+        CHIP_TRY(sh.mem.alloc(&L.kv.v, sh.page_elems * sh.num_pages));
+    }
+    sh.refs.assign(sh.num_pages, 0);
+    sh.free_list.clear();
+    for (int p = sh.num_pages - 1; p >= 0; --p) sh.free_list.push_back(p);
+    sh.finalized = true;
+    return 0;
+}
+
+// Per-instance buffers (a fresh model and every clone).
+int init_instance(cheetah_hip_model *m) {
+    Shared &sh = *m->sh;
+    const auto &c = sh.cfg;
+    const size_t H = c.hidden_size, qd = sh.q_dim(), kvd = sh.kv_dim(), R = sh.max_chunk;
+    CHIP_CHECK(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
+    m->dec_splits = (int)std::max<uint32_t>(8, std::min<uint32_t>(64, 256 / c.kv_heads));
+    CHIP_TRY(m->mem.alloc(&m->hidden, R * H));
+    CHIP_TRY(m->mem.alloc(&m->normed, R * H));
+    CHIP_TRY(m->mem.alloc(&m->qkv, R * (qd + 2 * kvd)));
+    CHIP_TRY(m->mem.alloc(&m->attn, R * qd));
+    CHIP_TRY(m->mem.alloc(&m->act, R * c.intermediate_size));
+    CHIP_TRY(m->mem.alloc(&m->logits, c.vocab_size));
+    const size_t part_rows = std::max(R * (size_t)kPrefillSplits, (size_t)m->dec_splits);
+    CHIP_TRY(m->mem.alloc(&m->part, part_rows * c.q_heads * (c.head_dim + 2)));
+    CHIP_TRY(m->mem.alloc(&m->tokens_dev, sh.kv_capacity));
+    CHIP_TRY(m->mem.alloc(&m->next_dev, 1));
+    CHIP_TRY(m->mem.alloc(&m->hist_dev, sh.kv_capacity + 1));
+    CHIP_TRY(m->mem.alloc(&m->step_dev, 2));
+    uint8_t *scratch = nullptr;
+    CHIP_TRY(m->mem.alloc(&scratch, argmax_scratch_bytes()));
+    m->argmax_scratch = scratch;
+    CHIP_TRY(m->mem.alloc(&m->page_dev, (size_t)sh.num_pages));
+    CHIP_CHECK(hipHostMalloc((void **)&m->step_host, 2 * sizeof(int32_t), hipHostMallocDefault));
+    CHIP_CHECK(hipHostMalloc((void **)&m->tokens_host, sh.kv_capacity * sizeof(uint32_t), hipHostMallocDefault));
+    CHIP_CHECK(hipHostMalloc((void **)&m->logits_host, (size_t)c.vocab_size * sizeof(float), hipHostMallocDefault));
+    m->page_host.assign(sh.num_pages, 0);
+    return 0;
+}
+
+// Makes positions [m->len, m->len + n) writable: maps new pages and copies a
+// shared page before its first write. Uploads the page table if it changed.
+int reserve_positions(cheetah_hip_model *m, size_t n) {
+    Shared &sh = *m->sh;
+    const size_t end = m->len + n;
+    if (end > sh.kv_capacity)
+        return fail("HIP backend: KV cache capacity of " + std::to_string(sh.kv_capacity) +
+                    " positions exceeded (needs " + std::to_string(end) + ").");
+    bool changed = false;
+    const size_t first = m->len / kPageSize, last = (end - 1) / kPageSize;
+    for (size_t lp = first; lp <= last; ++lp) {
+        if (lp < m->pages.size()) {
+            const int p = m->pages[lp];
+            if (sh.page_refs(p) > 1) {  // copy on write
+                const int np = sh.page_alloc();
+                if (np < 0) return fail("HIP backend: KV page pool exhausted.");
+                for (auto &L : sh.layers) {
+                    CHIP_CHECK(hipMemcpyAsync(L.kv.k + (size_t)np * sh.page_elems, L.kv.k + (size_t)p * sh.page_elems,
+                                              sh.page_elems * 2, hipMemcpyDeviceToDevice, m->stream));
+                    CHIP_CHECK(hipMemcpyAsync(L.kv.v + (size_t)np * sh.page_elems, L.kv.v + (size_t)p * sh.page_elems,
+                                              sh.page_elems * 2, hipMemcpyDeviceToDevice, m->stream));
+                }
+                sh.page_unref(p);
+                m->pages[lp] = np;
+                changed = true;
+            }
+        } else {
+            const int np = sh.page_alloc();
+            if (np < 0) return fail("HIP backend: KV page pool exhausted.");
+            m->pages.push_back(np);
+            changed = true;
+        }
+    }
+    if (changed) {
+        for (size_t i = 0; i < m->pages.size(); ++i) m->page_host[i] = m->pages[i];
+        CHIP_CHECK(hipMemcpyAsync(m->page_dev, m->page_host.data(), m->pages.size() * sizeof(int32_t),
+                                  hipMemcpyHostToDevice, m->stream));
+        CHIP_CHECK(hipStreamSynchronize(m->stream));  // page_host is pageable
+    }
+    return 0;
+}
+
+KvGeom geom(const cheetah_hip_model *m) {
+    return KvGeom{m->page_dev, kPageSize, (int)C(m).kv_heads, (int)C(m).head_dim};
+}
+
+// One decode step's kernels; token and position are read from step_dev.
+int enqueue_decode(cheetah_hip_model *m) {
+    Shared &sh = *m->sh;
+    const auto &c = sh.cfg;
+    hipStream_t s = m->stream;
+    const int32_t *pos = m->step_dev + 1;
+    CHIP_TRY(launch_embed(sh.embed, c.hidden_size, (const uint32_t *)m->step_dev, 1, m->hidden, s));
+    for (uint32_t l = 0; l < c.num_layers; ++l) {
+        Layer &L = sh.layers[l];
+        GemvJob qkv;
+        qkv.w = L.qkv;
+        qkv.x = m->hidden;
+        qkv.norm_gain = L.ln1;
+        qkv.eps = c.rms_eps;
+        qkv.bias = L.qkv_bias;
+        qkv.y = m->qkv;
+        CHIP_TRY(launch_gemv(qkv, s));
+        CHIP_TRY(launch_rope_append(m->qkv, 1, (int)c.q_heads, geom(m), L.kv, sh.rope_cos, sh.rope_sin,
+                                    (int)c.rotary_dim, 0, pos, s));
+        AttnJob aj;
+        aj.q = m->qkv;
+        aj.q_stride = sh.q_dim() + 2 * sh.kv_dim();
+        aj.out = m->attn;
+        aj.k = L.kv.k;
+        aj.v = L.kv.v;
+        aj.g = geom(m);
+        aj.q_heads = (int)c.q_heads;
+        aj.rows = 1;
+        aj.pos_dev = pos;
+        aj.splits = m->dec_splits;
+        aj.part = m->part;
+        CHIP_TRY(launch_attention(aj, s));
+        GemvJob o;
+        o.w = L.o;
+        o.x = m->attn;
+        o.bias = L.o_bias;
+        o.residual = m->hidden;
+        o.epi = EPI_RESIDUAL;
+        CHIP_TRY(launch_gemv(o, s));
+        GemvJob gu;
+        gu.w = L.gate;
+        gu.w2 = L.up;
+        gu.x = m->hidden;
+        gu.norm_gain = L.ln2;
+        gu.eps = c.rms_eps;
+        gu.y = m->act;
+        gu.epi = EPI_SWIGLU;
+        CHIP_TRY(launch_gemv(gu, s));
+        GemvJob dn;
+        dn.w = L.down;
+        dn.x = m->act;
+        dn.residual = m->hidden;
+        dn.epi = EPI_RESIDUAL;
+        CHIP_TRY(launch_gemv(dn, s));
+    }
+    GemvJob head;
+    head.w = sh.head;
+    head.x = m->hidden;
+    head.norm_gain = sh.final_norm;
+    head.eps = c.rms_eps;
+    head.y = m->logits;
+    CHIP_TRY(launch_gemv(head, s));
+    CHIP_TRY(launch_argmax(m->logits, c.vocab_size, m->next_dev, m->step_dev, m->hist_dev, sh.kv_capacity + 1,
+                           m->argmax_scratch, s));
+    return 0;
+}
+
+bool graphs_enabled() {
+    const char *e = getenv("CHEETAH_HIP_GRAPH");
+    return !(e && (e[0] == '0' || e[0] == 'f' || e[0] == 'F' || e[0] == 'n' || e[0] == 'N'));
+}
+
+int launch_decode(cheetah_hip_model *m) {
+    if (!graphs_enabled()) return enqueue_decode(m);
+    if (!m->graph) {
+        hipGraph_t g = nullptr;
+        CHIP_CHECK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+        const int rc = enqueue_decode(m);
+        hipError_t e = hipStreamEndCapture(m->stream, &g);
+        if (rc != 0) {
+            if (g) (void)hipGraphDestroy(g);
+            return -1;
+        }
+        if (e != hipSuccess) return fail(std::string("HIP backend: decode graph capture failed: ") + hipGetErrorString(e));
+        e = hipGraphInstantiate(&m->graph, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        if (e != hipSuccess) {
+            m->graph = nullptr;
+            return fail(std::string("HIP backend: decode graph instantiation failed: ") + hipGetErrorString(e));
+        }
+    }
+    CHIP_CHECK(hipGraphLaunch(m->graph, m->stream));
+    return 0;
+}
+
+int write_step(cheetah_hip_model *m, uint32_t token, size_t pos) {
+    CHIP_CHECK(hipStreamSynchronize(m->stream));  // step_host may still be in flight
+    m->step_host[0] = (int32_t)token;
+    m->step_host[1] = (int32_t)pos;
+    CHIP_CHECK(hipMemcpyAsync(m->step_dev, m->step_host, 2 * sizeof(int32_t), hipMemcpyHostToDevice, m->stream));
+    return 0;
+}
+
+// One prefill chunk of `rows` tokens at absolute position `pos`.
+// tokens_dev holds the chunk's ids (already on the device).
+int enqueue_chunk(cheetah_hip_model *m, const uint32_t *tokens_dev, size_t rows, size_t pos, bool last_chunk) {
+    Shared &sh = *m->sh;
+    const auto &c = sh.cfg;
+    hipStream_t s = m->stream;
+    const size_t H = c.hidden_size;
+    CHIP_TRY(launch_embed(sh.embed, H, tokens_dev, rows, m->hidden, s));
+    // A fixed split count makes each row's split boundaries a function of its
+    // own context length only, so a position's attention output does not
+    // depend on how the prompt was cut into chunks (KV continuation stays
+    // bit-exact, decoder.rs:1710-1728).
+    const size_t splits = kPrefillSplits;
+    for (uint32_t l = 0; l < c.num_layers; ++l) {
+        Layer &L = sh.layers[l];
+        CHIP_TRY(launch_rmsnorm_rows(m->hidden, L.ln1, c.rms_eps, rows, H, m->normed, s));
+        GemmJob qkv;
+        qkv.w = L.qkv;
+        qkv.x = m->normed;
+        qkv.n = rows;
+        qkv.bias = L.qkv_bias;
+        qkv.y = m->qkv;
+        CHIP_TRY(launch_gemm(qkv, s));
+        CHIP_TRY(launch_rope_append(m->qkv, rows, (int)c.q_heads, geom(m), L.kv, sh.rope_cos, sh.rope_sin,
+                                    (int)c.rotary_dim, pos, nullptr, s));
+        AttnJob aj;
+        aj.q = m->qkv;
+        aj.q_stride = sh.q_dim() + 2 * sh.kv_dim();
+        aj.out = m->attn;
+        aj.k = L.kv.k;
+        aj.v = L.kv.v;
+        aj.g = geom(m);
+        aj.q_heads = (int)c.q_heads;
+        aj.rows = rows;
+        aj.offset = pos;
+        aj.splits = (int)splits;
+        aj.part = m->part;
+        CHIP_TRY(launch_attention(aj, s));
+        GemmJob o;
+        o.w = L.o;
+        o.x = m->attn;
+        o.n = rows;
+        o.bias = L.o_bias;
+        o.residual = m->hidden;
+        o.epi = EPI_RESIDUAL;
+        CHIP_TRY(launch_gemm(o, s));
+        CHIP_TRY(launch_rmsnorm_rows(m->hidden, L.ln2, c.rms_eps, rows, H, m->normed, s));
+        GemmJob gu;
+        gu.w = L.gate;
+        gu.w2 = L.up;
+        gu.x = m->normed;
+        gu.n = rows;
+        gu.y = m->act;
+        gu.epi = EPI_SWIGLU;
+        CHIP_TRY(launch_gemm(gu, s));
+        GemmJob dn;
+        dn.w = L.down;
+        dn.x = m->act;
+        dn.n = rows;
+        dn.residual = m->hidden;
+        dn.epi = EPI_RESIDUAL;
+        CHIP_TRY(launch_gemm(dn, s));
+    }
+    if (last_chunk) {
+        // Final norm of the last row only, fused into the LM head GEMV
+        // (qwen2.rs:227-232 then lm_head, ops.rs:1513-1563).
+        GemvJob head;
+        head.w = sh.head;
+        head.x = m->hidden + (rows - 1) * H;
+        head.norm_gain = sh.final_norm;
+        head.eps = c.rms_eps;
+        head.y = m->logits;
+        CHIP_TRY(launch_gemv(head, s));
+    }
+    return 0;
+}
+
+int check_model(const cheetah_hip_model *m) {
+    if (!m) return fail("HIP backend: no model.");
+    if (!m->sh->finalized) return fail("HIP backend: model not finalized; call cheetah_hip_model_finalize.");
+    return ensure_ready();
+}
+
+// validate_tokens (ops.rs:1065-1078) + the device-backend offset contract
+// (transformer.rs:799-810).
+int validate(const cheetah_hip_model *m, const uint32_t *tokens, size_t n, size_t offset) {
+    if (n == 0) return fail("HIP backend: empty token input.");
+    if (!tokens) return fail("HIP backend: null token pointer.");
+    for (size_t i = 0; i < n; ++i)
+        if (tokens[i] >= C(m).vocab_size)
+            return fail("HIP backend: token id " + std::to_string(tokens[i]) + " exceeds the vocabulary size " +
+                        std::to_string(C(m).vocab_size) + ".");
+    if (offset != m->len) return fail("HIP backend: KV cache position does not match the input offset.");
+    if (offset + n > m->sh->kv_capacity)
+        return fail("HIP backend: input exceeds the KV cache capacity of " + std::to_string(m->sh->kv_capacity) +
+                    " positions.");
+    return 0;
+}
+
+int validate_decode(const cheetah_hip_model *m, uint32_t token, size_t offset, size_t steps) {
+    CHIP_TRY(validate(m, &token, 1, offset));
+    if (offset + steps > m->sh->kv_capacity)
+        return fail("HIP backend: decode exceeds the KV cache capacity of " + std::to_string(m->sh->kv_capacity) +
+                    " positions.");
+    return 0;
+}
+
+// Runs the forward; leaves the final logits in m->logits (and, for decode,
+// the argmax in m->next_dev).
+int run_forward(cheetah_hip_model *m, const uint32_t *tokens, size_t n, size_t offset, size_t chunk_rows) {
+    CHIP_TRY(check_model(m));
+    CHIP_TRY(validate(m, tokens, n, offset));
+    if (chunk_rows == 0) chunk_rows = 256;
+    chunk_rows = std::min(chunk_rows, m->sh->max_chunk);
+    CHIP_TRY(reserve_positions(m, n));
+    if (n == 1) {
+        CHIP_TRY(write_step(m, tokens[0], offset));
+        CHIP_TRY(launch_decode(m));
+    } else {
+        CHIP_CHECK(hipStreamSynchronize(m->stream));  // tokens_host reuse
+        std::memcpy(m->tokens_host, tokens, n * sizeof(uint32_t));
+        CHIP_CHECK(hipMemcpyAsync(m->tokens_dev, m->tokens_host, n * sizeof(uint32_t), hipMemcpyHostToDevice,
+                                  m->stream));
+        for (size_t start = 0; start < n; start += chunk_rows) {
+            const size_t rows = std::min(chunk_rows, n - start);
+            CHIP_TRY(enqueue_chunk(m, m->tokens_dev + start, rows, offset + start, start + rows == n));
+        }
+        CHIP_TRY(launch_argmax(m->logits, C(m).vocab_size, m->next_dev, nullptr, nullptr, 0, m->argmax_scratch,
+                               m->stream));
+    }
+    m->len = offset + n;
+    return 0;
+}
+
+int read_logits(cheetah_hip_model *m, float *logits_out) {
+    const size_t V = C(m).vocab_size;
+    CHIP_CHECK(hipMemcpyAsync(m->logits_host, m->logits, V * sizeof(float), hipMemcpyDeviceToHost, m->stream));
+    CHIP_CHECK(hipStreamSynchronize(m->stream));
+    std::memcpy(logits_out, m->logits_host, V * sizeof(float));
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+cheetah_hip_model *cheetah_hip_model_create(const cheetah_hip_config *cfg, uint32_t quant_format, size_t kv_capacity,
+                                            size_t max_chunk_rows) {
+    if (ensure_ready()) return nullptr;
+    if (!cfg) {
+        fail("HIP backend: null config.");
+        return nullptr;
+    }
+    cheetah_hip_config c = *cfg;
+    if (c.rotary_dim == 0) c.rotary_dim = c.head_dim;
+    if (c.num_layers == 0 || c.hidden_size == 0 || c.q_heads == 0 || c.kv_heads == 0 || c.head_dim == 0 ||
+        c.intermediate_size == 0 || c.vocab_size == 0 || c.q_heads % c.kv_heads != 0) {
+        fail("HIP backend: invalid decoder configuration.");
+        return nullptr;
+    }
+    if (c.family > 1) {
+        fail("HIP backend: only the qwen2 (0) and llama (1) families are served.");
+        return nullptr;
+    }
+    if (c.sliding_window != 0) {
+        fail("HIP backend: sliding-window attention is not served (qwen2 and llama resolve it to 0).");
+        return nullptr;
+    }
+    if ((c.head_dim != 64 && c.head_dim != 128) || c.q_heads / c.kv_heads > 8 || c.rotary_dim % 2 ||
+        c.rotary_dim > c.head_dim) {
+        fail("HIP backend: head_dim must be 64 or 128 with at most 8 query heads per KV head.");
+        return nullptr;
+    }
+    if (c.hidden_size > 16384 || c.q_heads * c.head_dim > 16384 || c.intermediate_size > 32768) {
+        fail("HIP backend: hidden / intermediate width above the served maximum.");
+        return nullptr;
+    }
+    if (quant_format != 0 && quant_format != FMT_Q8 && quant_format != FMT_Q4) {
+        fail("HIP backend: quant_format must be 0 (stored), 4 (q8) or 5 (q4).");
+        return nullptr;
+    }
+    auto *m = new cheetah_hip_model();
+    m->sh = std::make_shared<Shared>();
+    m->sh->cfg = c;
+    m->sh->quant = (int)quant_format;
+    m->sh->kv_capacity = kv_capacity ? kv_capacity : 65536;
+    m->sh->max_chunk = max_chunk_rows ? max_chunk_rows : 1024;
+    return m;
+}
+
+int cheetah_hip_model_set_unit(cheetah_hip_model *m, const char *unit_id, const void *bytes, size_t nbytes,
+                               uint32_t dtype, const uint64_t *shape, size_t ndim) {
+    CHIP_TRY(ensure_ready());
+    if (!m || !unit_id || !bytes || (ndim && !shape)) return fail("HIP backend: set_unit with a null argument.");
+    if (m->sh->finalized) return fail("HIP backend: units cannot change after finalize.");
+    if (dtype != 1) return fail(std::string("HIP backend: unit '") + unit_id + "' is not BF16 (the served stored precision).");
+    if (ndim < 1 || ndim > 2) return fail(std::string("HIP backend: unit '") + unit_id + "' must be 1-D or 2-D.");
+    uint64_t count = 1;
+    for (size_t i = 0; i < ndim; ++i) count *= shape[i];
+    if (count * 2 != nbytes)
+        return fail(std::string("HIP backend: unit '") + unit_id + "' byte length does not match its shape.");
+    Staged st;
+    st.shape.assign(shape, shape + ndim);
+    if (ndim == 2) {
+        CHIP_CHECK(hipMalloc(&st.dev, nbytes));
+        CHIP_CHECK(hipMemcpy(st.dev, bytes, nbytes, hipMemcpyHostToDevice));
+    } else {
+        st.host.resize(count);
+        std::memcpy(st.host.data(), bytes, nbytes);
+    }
+    auto it = m->sh->staged.find(unit_id);
+    if (it != m->sh->staged.end() && it->second.dev) (void)hipFree(it->second.dev);
+    m->sh->staged[unit_id] = std::move(st);
+    return 0;
+}
+
+int cheetah_hip_model_finalize(cheetah_hip_model *m) {
+    CHIP_TRY(ensure_ready());
+    if (!m) return fail("HIP backend: no model.");
+    if (m->sh->finalized) return 0;
+    CHIP_TRY(finalize(m));
+    return init_instance(m);
+}
+
+int cheetah_hip_forward(cheetah_hip_model *m, const uint32_t *tokens, size_t n, size_t offset, size_t chunk_rows,
+                        float *logits_out) {
+    if (!logits_out) return fail("HIP backend: null logits buffer.");
+    if (run_forward(m, tokens, n, offset, chunk_rows)) return -1;
+    return read_logits(m, logits_out);
+}
+
+int cheetah_hip_forward_greedy(cheetah_hip_model *m, const uint32_t *tokens, size_t n, size_t offset,
+                               size_t chunk_rows, uint32_t *next_token, float *logits_out) {
+    if (!next_token) return fail("HIP backend: null next_token pointer.");
+    if (run_forward(m, tokens, n, offset, chunk_rows)) return -1;
+    CHIP_CHECK(hipMemcpyAsync(m->step_host, m->next_dev, sizeof(uint32_t), hipMemcpyDeviceToHost, m->stream));
+    CHIP_CHECK(hipStreamSynchronize(m->stream));
+    *next_token = (uint32_t)m->step_host[0];
+    if (logits_out) CHIP_TRY(read_logits(m, logits_out));
+    return 0;
+}
+
+int cheetah_hip_decode_greedy(cheetah_hip_model *m, uint32_t token, size_t offset, size_t steps,
+                              uint32_t *tokens_out) {
+    CHIP_TRY(check_model(m));
+    if (steps == 0) return 0;
+    if (!tokens_out) return fail("HIP backend: null tokens_out.");
+    CHIP_TRY(validate_decode(m, token, offset, steps));
+    CHIP_TRY(reserve_positions(m, steps));
+    CHIP_TRY(write_step(m, token, offset));
+    for (size_t i = 0; i < steps; ++i) CHIP_TRY(launch_decode(m));
+    CHIP_CHECK(hipMemcpyAsync(tokens_out, m->hist_dev + offset + 1, steps * sizeof(uint32_t), hipMemcpyDeviceToHost,
+                              m->stream));
+    CHIP_CHECK(hipStreamSynchronize(m->stream));
+    m->len = offset + steps;
+    return 0;
+}
+
+int cheetah_hip_time_decode(cheetah_hip_model *m, uint32_t token, size_t offset, size_t steps, float *ms_per_step,
+                            float *gemv_ms, uint32_t *tokens_out) {
+    CHIP_TRY(check_model(m));
+    if (steps == 0 || !ms_per_step) return fail("HIP backend: time_decode needs steps and an output.");
+    CHIP_TRY(validate_decode(m, token, offset, steps));
+    CHIP_TRY(reserve_positions(m, steps));
+    CHIP_TRY(write_step(m, token, offset));
+    hipEvent_t e0, e1;
+    CHIP_CHECK(hipEventCreate(&e0));
+    CHIP_CHECK(hipEventCreate(&e1));
+    CHIP_CHECK(hipEventRecord(e0, m->stream));
+    for (size_t i = 0; i < steps; ++i) CHIP_TRY(launch_decode(m));
+    CHIP_CHECK(hipEventRecord(e1, m->stream));
+    CHIP_CHECK(hipEventSynchronize(e1));
+    float total = 0.f;
+    CHIP_CHECK(hipEventElapsedTime(&total, e0, e1));
+    *ms_per_step = total / (float)steps;
+    if (tokens_out)
+        CHIP_CHECK(hipMemcpy(tokens_out, m->hist_dev + offset + 1, steps * sizeof(uint32_t), hipMemcpyDeviceToHost));
+    m->len = offset + steps;
+    if (gemv_ms) {
+        // The dominant GEMV of the step (gate/up, SwiGLU epilogue, fused norm)
+        // timed alone on the same stream, cycling through the layers so each
+        // launch streams weights that are not cache resident.
+        Shared &sh = *m->sh;
+        const uint32_t L = sh.cfg.num_layers;
+        const size_t iters = std::max<size_t>(steps, L);
+        CHIP_CHECK(hipEventRecord(e0, m->stream));
+        for (size_t i = 0; i < iters; ++i) {
+            Layer &Ly = sh.layers[i % L];
+            GemvJob gu;
+            gu.w = Ly.gate;
+            gu.w2 = Ly.up;
+            gu.x = m->hidden;
+            gu.norm_gain = Ly.ln2;
+            gu.eps = sh.cfg.rms_eps;
+            gu.y = m->act;
+            gu.epi = EPI_SWIGLU;
+            CHIP_TRY(launch_gemv(gu, m->stream));
+        }
+        CHIP_CHECK(hipEventRecord(e1, m->stream));
+        CHIP_CHECK(hipEventSynchronize(e1));
+        CHIP_CHECK(hipEventElapsedTime(&total, e0, e1));
+        *gemv_ms = total / (float)iters;
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return 0;
+}
+
+void cheetah_hip_clear_cache(cheetah_hip_model *m) {
+    if (!m) return;
+    if (m->stream) (void)hipStreamSynchronize(m->stream);
+    for (int p : m->pages) m->sh->page_unref(p);
+    m->pages.clear();
+    m->len = 0;
+}
+
+cheetah_hip_model *cheetah_hip_clone(const cheetah_hip_model *src) {
+    if (check_model(src)) return nullptr;
+    auto *m = new cheetah_hip_model();
+    m->sh = src->sh;
+    if (init_instance(m)) {
+        delete m;
+        return nullptr;
+    }
+    return m;
+}
+
+size_t cheetah_hip_kv_len(const cheetah_hip_model *m) { return m ? m->len : 0; }
+
+int cheetah_hip_kv_snapshot(const cheetah_hip_model *m, cheetah_hip_snapshot **out, size_t *positions) {
+    CHIP_TRY(check_model(m));
+    if (!out) return fail("HIP backend: null snapshot pointer.");
+    CHIP_CHECK(hipStreamSynchronize(m->stream));
+    auto *s = new cheetah_hip_snapshot();
+    s->sh = m->sh;
+    s->positions = m->len;
+    const size_t used = (m->len + kPageSize - 1) / kPageSize;
+    for (size_t i = 0; i < used; ++i) {
+        m->sh->page_ref(m->pages[i]);
+        s->pages.push_back(m->pages[i]);
+    }
+    *out = s;
+    if (positions) *positions = s->positions;
+    return 0;
+}
+
+int cheetah_hip_restore_kv_prefix(cheetah_hip_model *m, const cheetah_hip_snapshot *s, size_t positions) {
+    CHIP_TRY(check_model(m));
+    if (!s) return fail("HIP backend: null snapshot.");
+    if (s->sh != m->sh) return fail("HIP backend: snapshot belongs to another model's weights.");
+    cheetah_hip_clear_cache(m);
+    const size_t keep = std::min(positions, s->positions);
+    const size_t used = (keep + kPageSize - 1) / kPageSize;
+    for (size_t i = 0; i < used; ++i) {
+        m->sh->page_ref(s->pages[i]);
+        m->pages.push_back(s->pages[i]);
+        m->page_host[i] = s->pages[i];
+    }
+    if (used) {
+        CHIP_CHECK(hipMemcpyAsync(m->page_dev, m->page_host.data(), used * sizeof(int32_t), hipMemcpyHostToDevice,
+                                  m->stream));
+        CHIP_CHECK(hipStreamSynchronize(m->stream));
+    }
+    m->len = keep;
+    return 0;
+}
+
+void cheetah_hip_snapshot_free(cheetah_hip_snapshot *s) { delete s; }
+
+void cheetah_hip_model_free(cheetah_hip_model *m) { delete m; }
+
+}  // extern "C"

@@ -1,0 +1,194 @@
+"""Forward-level parity of the HIP ModelForward against the CPU oracle.
+
+Bars (north star): logits within 1e-2 relative of the reference path
+(f32 accumulation; the device keeps K/V in BF16 where the reference keeps
+f32), greedy token sequences identical for the first 32 decode steps.
+Device invariants from the reference's decoder tests (decoder.rs:1710-1818):
+KV continuation and snapshot -> restore -> continue are bit-exact.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from cheetah_amd import configs, synth
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+@pytest.fixture(scope="module")
+def hip():
+    from cheetah_amd import hip as h
+    h.init(0)
+    return h
+
+
+def rel_err(got, ref):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return float(np.max(np.abs(got - ref)) / max(np.max(np.abs(ref)), 1e-30))
+
+
+def bits(a):
+    return np.asarray(a, np.float32).view(np.uint32)
+
+
+_WEIGHTS = {}
+
+
+def weights(shape):
+    if shape.name not in _WEIGHTS:
+        _WEIGHTS.clear()
+        _WEIGHTS[shape.name] = synth.make_weights(shape)
+    return _WEIGHTS[shape.name]
+
+
+TINY = [configs.TINY_QWEN2, configs.TINY_LLAMA]
+
+
+@pytest.mark.parametrize("quant", [None, "q8", "q4"])
+@pytest.mark.parametrize("shape", TINY, ids=lambda s: s.name)
+def test_tiny_forward_matches_oracle(hip, oracle, shape, quant):
+    w = weights(shape)
+    g = hip.HipForward(shape, w, quant=quant, kv_capacity=512, max_chunk_rows=64)
+    r_bf = oracle.RefModel(shape, w, quant=quant, kv_bf16=True)
+    r_ref = oracle.RefModel(shape, w, quant=quant)
+    toks = synth.make_tokens(shape.vocab_size, 60, seed=2)
+    lg = g.forward(toks[:45], 0, chunk_rows=16)
+    lb = r_bf.forward(toks[:45], 0, chunk_rows=16)
+    lr = r_ref.forward(toks[:45], 0, chunk_rows=16)
+    assert rel_err(lg, lb) < 1e-3
+    assert rel_err(lg, lr) < 1e-2
+    for i in range(45, 60):
+        lg = g.forward(toks[i:i + 1], i)
+        lb = r_bf.forward(toks[i:i + 1], i)
+        lr = r_ref.forward(toks[i:i + 1], i)
+        assert rel_err(lg, lb) < 1e-3, i
+        assert rel_err(lg, lr) < 1e-2, i
+    assert g.kv_len() == 60
+
+
+@pytest.mark.parametrize("shape", TINY, ids=lambda s: s.name)
+def test_tiny_greedy_32_steps_token_exact(hip, oracle, shape):
+    w = weights(shape)
+    g = hip.HipForward(shape, w, kv_capacity=512, max_chunk_rows=64)
+    r = oracle.RefModel(shape, w)
+    prompt = synth.make_tokens(shape.vocab_size, 40, seed=3)
+    ref_tokens = []
+    logits = r.forward(prompt, 0, chunk_rows=16)
+    for step in range(32):
+        t = int(len(logits) - 1 - np.argmax(logits[::-1]))
+        ref_tokens.append(t)
+        logits = r.forward([t], 40 + step)
+    first, = [g.forward_greedy(prompt, 0, chunk_rows=16)]
+    assert first == ref_tokens[0]
+    rest = g.decode_greedy(first, 40, 31)
+    assert [first] + rest.tolist() == ref_tokens
+
+
+def test_kv_continuation_bit_exact_on_device(hip):
+    # decoder.rs:1710-1728: prefill in one call == prefill in two calls.
+    shape = configs.TINY_QWEN2
+    g = hip.HipForward(shape, weights(shape), kv_capacity=512, max_chunk_rows=64)
+    toks = synth.make_tokens(shape.vocab_size, 90, seed=4)
+    full = g.forward(toks[:70], 0, chunk_rows=32)
+    dec_full = [g.forward(toks[i:i + 1], i) for i in range(70, 90)]
+    g.clear_cache()
+    g.forward(toks[:23], 0, chunk_rows=32)
+    cont = g.forward(toks[23:70], 23, chunk_rows=16)
+    assert np.array_equal(bits(full), bits(cont))
+    for i in range(70, 90):
+        assert np.array_equal(bits(g.forward(toks[i:i + 1], i)), bits(dec_full[i - 70])), i
+
+
+def test_snapshot_restore_clone_bit_exact_on_device(hip):
+    # decoder.rs:1761-1818: a clone starts empty; snapshot -> restore ->
+    # continue equals the uninterrupted run, including a restore that ends
+    # mid-page (copy on write of the shared page).
+    shape = configs.TINY_LLAMA
+    g = hip.HipForward(shape, weights(shape), kv_capacity=1024, max_chunk_rows=64)
+    toks = synth.make_tokens(shape.vocab_size, 150, seed=5)
+    g.forward(toks[:130], 0, chunk_rows=64)
+    snap = g.kv_snapshot()
+    assert snap.positions == 130
+    ref_next = [g.forward(toks[i:i + 1], i) for i in range(130, 150)]
+    c = g.clone()
+    assert c.kv_len() == 0
+    for keep in (130, 100, 64):
+        c.clear_cache()
+        assert c.restore_kv_prefix(snap, keep)
+        assert c.kv_len() == keep
+        if keep < 130:
+            c.forward(toks[keep:130], keep, chunk_rows=64)
+        got = [c.forward(toks[i:i + 1], i) for i in range(130, 150)]
+        for a, b in zip(got, ref_next):
+            if keep == 130:
+                assert np.array_equal(bits(a), bits(b))
+            else:
+                assert rel_err(a, b) < 1e-4  # re-prefilled tail: same math, prefill kernels
+    # the original keeps its own cache untouched by the clone's writes
+    g.clear_cache()
+    g.forward(toks[:130], 0, chunk_rows=64)
+    again = g.forward(toks[130:131], 130)
+    assert np.array_equal(bits(again), bits(ref_next[0]))
+
+
+def test_restore_then_continue_matches_full_prefill_bit_exact(hip):
+    # The engine's prefix reuse (engine.rs:1880-1890): restoring n cached
+    # positions then prefilling the suffix gives the same logits as the
+    # uninterrupted prefill, bit for bit (prefill split boundaries depend only
+    # on each row's position).
+    shape = configs.TINY_QWEN2
+    g = hip.HipForward(shape, weights(shape), kv_capacity=1024, max_chunk_rows=64)
+    toks = synth.make_tokens(shape.vocab_size, 200, seed=6)
+    full = g.forward(toks, 0, chunk_rows=64)
+    snap = g.kv_snapshot()
+    c = g.clone()
+    c.restore_kv_prefix(snap, 150)
+    cont = c.forward(toks[150:], 150, chunk_rows=64)
+    assert np.array_equal(bits(full), bits(cont))
+
+
+def test_forward_errors_are_reported_before_device_work(hip):
+    shape = configs.TINY_QWEN2
+    g = hip.HipForward(shape, weights(shape), kv_capacity=128, max_chunk_rows=64)
+    with pytest.raises(hip.HipError, match="empty token input"):
+        g.forward(np.array([], np.uint32), 0)
+    with pytest.raises(hip.HipError, match="exceeds the vocabulary size 1000"):
+        g.forward(np.array([5, 1000], np.uint32), 0)
+    with pytest.raises(hip.HipError, match="does not match the input offset"):
+        g.forward(np.array([5], np.uint32), 3)
+    with pytest.raises(hip.HipError, match="capacity"):
+        g.forward(np.zeros(129, np.uint32), 0)
+    assert g.kv_len() == 0
+    g.forward(np.array([5, 6], np.uint32), 0)
+    assert g.kv_len() == 2
+
+
+def test_missing_unit_is_rejected(hip):
+    shape = configs.TINY_QWEN2
+    w = dict(weights(shape))
+    del w["model.layers.1.mlp.down_proj.weight"]
+    with pytest.raises(hip.HipError, match="missing unit 'model.layers.1.mlp.down_proj.weight'"):
+        hip.HipForward(shape, w)
+
+
+def test_qwen2_0_5b_greedy_matches_golden(hip):
+    """Config 1 (Qwen2-0.5B shape, BF16): 512-token prompt prefilled in
+    chunks of 128, then greedy decode; the first 32 tokens must equal the CPU
+    oracle's (committed golden, generated by tests/golden/make_golden.py)."""
+    with open(os.path.join(GOLDEN, "qwen2_0_5b_greedy.json")) as f:
+        gold = json.load(f)
+    shape = configs.QWEN2_0_5B
+    g = hip.HipForward(shape, weights(shape), kv_capacity=1024, max_chunk_rows=128)
+    prompt = synth.make_tokens(shape.vocab_size, gold["prompt_len"], seed=gold["prompt_seed"])
+    first, logits = g.forward_greedy(prompt, 0, chunk_rows=gold["chunk_rows"], want_logits=True)
+    head = np.array(gold["prefill_logits_head"], np.float32)
+    assert rel_err(logits[: head.size], head) < 1e-2
+    n = len(gold["tokens"])
+    rest = g.decode_greedy(first, gold["prompt_len"], n - 1)
+    got = [first] + rest.tolist()
+    assert got[:32] == gold["tokens"][:32], (got, gold["tokens"])

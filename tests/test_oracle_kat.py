@@ -1,0 +1,270 @@
+"""Pins the CPU oracle against the reference's own known-answer tests and
+against what the mathematics fixes (closed forms, invariants, brute force).
+
+Each test names the reference test it restates (file:line). The oracle is
+only trusted as the GPU checker because these pass.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from cheetah_amd.synth import bf16_to_f32, f32_to_bf16
+
+
+def trunc_bf16(values):
+    """`(value.to_bits() >> 16) as u16` — the truncating conversion the
+    reference's tests use to build BF16 fixtures."""
+    return (np.asarray(values, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def test_gemv_kat_f32_and_bf16(oracle):
+    # ops.rs:1701-1721 gemv_multiplies_rows_in_parallel.
+    w = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
+    x = np.array([1, 0, -1], np.float32)
+    assert oracle.gemv(w, x, dtype="f32").tolist() == [-2.0, -2.0]
+    assert oracle.gemv(trunc_bf16(w), x).tolist() == [-2.0, -2.0]
+
+
+@pytest.mark.parametrize("cols", [8, 100, 896])
+def test_gemm_matches_per_row_gemv_bit_exact(oracle, cols):
+    # ops.rs:1727-1795 (rows = 2*128+3, n = 7); cols 8 is the reference case,
+    # 100 and 896 also run the 16-lane FMA body and its tail.
+    rows, n = 128 * 2 + 3, 7
+    idx = np.arange(rows * cols)
+    weight = trunc_bf16(((idx * 37 % 23).astype(np.float32) - 11.0) / 8.0).reshape(rows, cols)
+    xi = np.arange(n * cols)
+    x = (((xi * 11 % 17).astype(np.float32) - 8.0) / 4.0).reshape(n, cols)
+    y_gemm = oracle.gemm_bf16(weight, x)
+    for t in range(n):
+        y_gemv = oracle.gemv(weight, x[t])
+        assert np.array_equal(y_gemm[t].view(np.uint32), y_gemv.view(np.uint32)), t
+
+
+def _reference_q_buffer(weights, fmt):
+    """The packer written inline in ops.rs:1801-1832 / 1838-1870."""
+    rows, cols = len(weights), len(weights[0])
+    limit = 127.0 if fmt == "q8" else 7.0
+    stride = (cols + 3) // 4 * 4 if fmt == "q8" else ((cols + 2) // 2 + 3) // 4 * 4
+    buf = np.zeros(rows * 4 + rows * stride, np.uint8)
+    for r, row in enumerate(weights):
+        row = np.asarray(row, np.float32)
+        max_abs = np.float32(0.0)
+        for v in row:
+            max_abs = max(max_abs, abs(v))
+        scale = np.float32(max_abs / np.float32(limit)) if max_abs > 0 else np.float32(1.0)
+        buf[r * 4:r * 4 + 4] = np.frombuffer(np.float32(scale).tobytes(), np.uint8)
+        for c, v in enumerate(row):
+            q = np.float32(v) / scale
+            code = int(math.copysign(math.floor(abs(float(q)) + 0.5), float(q)))  # round half away
+            code = max(-int(limit), min(int(limit), code))
+            if fmt == "q8":
+                buf[rows * 4 + r * stride + c] = code & 0xFF
+            else:
+                buf[rows * 4 + r * stride + c // 2] |= (code & 0x0F) << ((c % 2) * 4)
+    return buf
+
+
+def test_gemv_q8_kat(oracle):
+    # ops.rs:1801-1832 gemv_q8_matches_rowwise_scale_code_reference.
+    weights = [[1.0, -2.0, 0.0, 3.5, -0.25, 2.0], [0.0] * 6, [-7.0, 7.0, -1.0, 1.0, -0.5, 0.5]]
+    x = np.array([0.5 - i * 0.1 for i in range(6)], np.float32)
+    buf = _reference_q_buffer(weights, "q8")
+    assert np.array_equal(buf, oracle.quantize(np.array(weights, np.float32), "q8"))
+    y = oracle.gemv_quant(buf, 3, 6, x, "q8")
+    deq = oracle.dequant(buf, 3, 6, "q8")
+    for r in range(3):
+        expect = np.float32(0.0)
+        for c in range(6):
+            expect = np.float32(expect + np.float32(deq[r, c]) * x[c])
+        assert abs(y[r] - expect) < 1e-5
+    assert np.frombuffer(buf[4:8].tobytes(), np.float32)[0] == 1.0  # zero row keeps scale 1.0
+
+
+def test_gemv_q4_kat(oracle):
+    # ops.rs:1838-1870 gemv_q4_matches_rowwise_scale_code_reference (cols 9:
+    # both nibble parities and the padded tail).
+    weights = [[1.0, -2.0, 0.0, 3.5, -0.25, 2.0, -1.5, 0.75, 4.0], [0.0] * 9,
+               [-7.0, 7.0, -1.0, 1.0, -0.5, 0.5, -3.0, 3.0, 0.0]]
+    x = np.array([0.5 - i * 0.1 for i in range(9)], np.float32)
+    buf = _reference_q_buffer(weights, "q4")
+    assert np.array_equal(buf, oracle.quantize(np.array(weights, np.float32), "q4"))
+    y = oracle.gemv_quant(buf, 3, 9, x, "q4")
+    deq = oracle.dequant(buf, 3, 9, "q4")
+    for r in range(3):
+        expect = sum(float(deq[r, c]) * float(x[c]) for c in range(9))
+        assert abs(y[r] - expect) < 1e-5
+
+
+@pytest.mark.parametrize("fmt", ["q8", "q4"])
+def test_quantize_then_gemv_agree(oracle, fmt):
+    # ops.rs:1876-1932 gemv_q{4,8}_consumes_the_registered_quantize_output.
+    rows, cols = 5, 9
+    values = (((np.arange(rows * cols) % 23).astype(np.float32) - 11.0) * np.float32(0.3)).reshape(rows, cols)
+    buf = oracle.quantize(values, fmt)
+    x = np.sin(np.arange(cols, dtype=np.float32) * np.float32(0.7) - np.float32(2.0)).astype(np.float32)
+    y = oracle.gemv_quant(buf, rows, cols, x, fmt)
+    deq = oracle.dequant(buf, rows, cols, fmt)
+    for r in range(rows):
+        want = sum(float(deq[r, c]) * float(x[c]) for c in range(cols))
+        assert abs(y[r] - want) < 1e-4
+    # dequant_value agrees with the vectorised numpy dequant, bit for bit.
+    fn = oracle.lib().ref_q8_dequant_value if fmt == "q8" else oracle.lib().ref_q4_dequant_value
+    pbuf = buf.ctypes.data_as(oracle._U8P)
+    for r in range(rows):
+        for c in range(cols):
+            assert np.float32(fn(pbuf, rows, cols, r, c)) == deq[r, c]
+
+
+@pytest.mark.parametrize("fmt", ["q8", "q4"])
+def test_buffer_layout_matches_ffi_contract(oracle, fmt):
+    # q8.rs:210-226 / q4.rs:240-256, plus the row stride quirk (K=4096 -> 2052).
+    for rows, cols in [(3, 5), (8, 64), (128, 151936 // 128)]:
+        values = ((np.arange(rows * cols) % 17).astype(np.float32) - 8.0).reshape(rows, cols)
+        buf = oracle.quantize(values, fmt)
+        stride = (cols + 3) // 4 * 4 if fmt == "q8" else oracle.q4_row_stride(cols)
+        assert buf.size == rows * 4 + rows * stride
+    assert oracle.q4_row_stride(4096) == 2052
+    assert oracle.q4_row_stride(14336) == 7172
+    assert oracle.q8_buffer_bytes(4096, 4096) == 4096 * 4 + 4096 * 4096
+
+
+@pytest.mark.parametrize("fmt,cols,limit", [("q8", 7, 127.0), ("q4", 9, 7.0)])
+def test_quantize_round_trip_within_half_code(oracle, fmt, cols, limit):
+    # q8.rs:228-256 / q4.rs:258-288.
+    rows = 2
+    values = np.full(rows * cols, 0.25, np.float32)
+    values[cols] = -40.0
+    buf = oracle.quantize(values.reshape(rows, cols), fmt)
+    scales = buf[:8].view(np.float32)
+    assert abs(scales[0] - 0.25 / limit) < 1e-9
+    assert abs(scales[1] - 40.0 / limit) < 1e-9
+    deq = oracle.dequant(buf, rows, cols, fmt).reshape(-1)
+    for i, v in enumerate(values):
+        assert abs(deq[i] - v) <= scales[i // cols] / 2 + 1e-6
+
+
+def test_q4_nibble_parity(oracle):
+    # q4.rs:290-310 nibble_packing_matches_column_parity.
+    values = ((np.arange(8, dtype=np.float32) + 1.0) * 0.5).reshape(1, 8)
+    buf = oracle.quantize(values, "q4")
+    scale = buf[:4].view(np.float32)[0]
+    deq = oracle.dequant(buf, 1, 8, "q4")[0]
+    for c in range(8):
+        code = max(-7, min(7, int(round(float(values[0, c] / scale)))))
+        assert abs(deq[c] - code * scale) < 1e-6
+    # low nibble = even column, high nibble = odd column
+    b0 = buf[4]
+    assert (b0 & 0xF) == (int(round(float(values[0, 0] / scale))) & 0xF)
+
+
+def test_quantize_rounds_half_away_from_zero(oracle):
+    # Rust f32::round: 2.5 -> 3, -2.5 -> -3 (q8.rs:118). max|w| = 127 gives scale 1.
+    values = np.array([[127.0, 2.5, -2.5, 0.5, -0.5, 1.49999988]], np.float32)
+    buf = oracle.quantize(values, "q8")
+    codes = buf[4:4 + 6].view(np.int8).tolist()
+    assert codes == [127, 3, -3, 1, -1, 1]
+
+
+def test_rmsnorm_kat(oracle):
+    # ops.rs:1935-1944.
+    y = oracle.rmsnorm([3.0, 4.0], np.array([0x3F80, 0x3F80], np.uint16), 1e-6)
+    inv = 1.0 / math.sqrt(12.5 + 1e-6)
+    assert abs(y[0] - 3.0 * inv) < 1e-5 and abs(y[1] - 4.0 * inv) < 1e-5
+
+
+def test_rope_kat(oracle):
+    # ops.rs:1947-1958: hd 2, position 1 rotates by exactly 1 radian.
+    v = oracle.rope_heads([3.0, 4.0], 1, 2, 2, 1, 1e6)
+    assert abs(v[0] ** 2 + v[1] ** 2 - 25.0) < 1e-4
+    assert abs(v[0] - (3 * math.cos(1) - 4 * math.sin(1))) < 1e-5
+    assert abs(v[1] - (4 * math.cos(1) + 3 * math.sin(1))) < 1e-5
+
+
+def test_rope_heads_partial_span(oracle):
+    # ops.rs:1963-1978.
+    v = oracle.rope_heads([1.0, 0.0, 9.0, 8.0, 0.0, 1.0, 7.0, 6.0], 2, 4, 2, 1, 10_000.0)
+    s, c = math.sin(1.0), math.cos(1.0)
+    assert abs(v[0] - c) < 1e-5 and abs(v[1] - s) < 1e-5
+    assert abs(v[4] + s) < 1e-5 and abs(v[5] - c) < 1e-5
+    assert v[2:4].tolist() == [9.0, 8.0] and v[6:8].tolist() == [7.0, 6.0]
+
+
+def test_rope_matches_rotate_half_reference(oracle):
+    # ops.rs:2004-2035 (theta 1e6, hd 64, positions 1..8), plus an fp64
+    # closed form for the rotation.
+    hd, theta = 64, 1e6
+    inp = (np.array([(i * 37 % 11) for i in range(hd)], np.float32) / np.float32(7.0)) - np.float32(0.6)
+    for pos in range(1, 9):
+        out = oracle.rope_heads(inp, 1, hd, hd, pos, theta)
+        i = np.arange(hd // 2)
+        ang = pos * (theta ** (-2.0 * i / hd))
+        a, b = inp[: hd // 2].astype(np.float64), inp[hd // 2:].astype(np.float64)
+        exp = np.concatenate([a * np.cos(ang) - b * np.sin(ang), b * np.cos(ang) + a * np.sin(ang)])
+        assert np.max(np.abs(out - exp)) < 1e-4
+
+
+def test_silu_and_softmax(oracle):
+    # ops.rs:1981-1999.
+    g = oracle.silu_multiply([1.0, -2.0], [2.0, 3.0])
+    silu = lambda v: v / (1 + math.exp(-v))
+    assert abs(g[0] - silu(1.0) * 2) < 1e-6 and abs(g[1] - silu(-2.0) * 3) < 1e-6
+    s = oracle.softmax([1.0, 2.0, 3.0])
+    assert abs(s.sum() - 1) < 1e-6 and s[2] > s[1] > s[0]
+    t = oracle.softmax([1001.0, 1002.0, 1003.0])
+    assert abs(s[0] - t[0]) < 1e-5
+
+
+def test_fused_bf16_dot_matches_dequant_dot(oracle):
+    # ops.rs:2040-2091 at 8 and 896 lanes: fused dot vs dequant + dot_f32.
+    for cols, fn in [(8, lambda i: float(i % 251)), (896, lambda i: (i % 251) * 0.5 - 60.0)]:
+        row = trunc_bf16(np.array([fn(i) for i in range(cols)], np.float32)).reshape(1, cols)
+        if cols == 8:
+            x = np.array([(i % 17) / 8.0 - 1.0 for i in range(cols)], np.float32)
+        else:
+            x = np.array([(i % 31) * 0.25 - 4.0 for i in range(cols)], np.float32)
+        fused = oracle.gemv(row, x)[0]
+        naive = oracle.gemv(bf16_to_f32(row).reshape(1, cols), x, dtype="f32")[0]
+        assert abs(fused - naive) / max(abs(naive), 1.0) < 1e-5
+
+
+def test_attention_two_token_gqa_kat(oracle):
+    # native.rs:2017-2033: 2 q heads share 1 kv head, head_dim 2.
+    keys = np.array([[1.0, 0.0], [0.0, 1.0]], np.float32)
+    values = np.array([[2.0, 3.0], [5.0, 7.0]], np.float32)
+    q = np.array([1.0, 0.0, 0.0, 1.0], np.float32)
+    out0 = oracle.attention(keys[:1], values[:1], q, 2, 1, 2, position=0)
+    assert out0.tolist() == [2.0, 3.0, 2.0, 3.0]
+    out1 = oracle.attention(keys, values, q, 2, 1, 2, position=1)
+    w = 1.0 / (1.0 + math.exp(-1.0 / math.sqrt(2.0)))
+    exp = [2 * w + 5 * (1 - w), 3 * w + 7 * (1 - w), 2 * (1 - w) + 5 * w, 3 * (1 - w) + 7 * w]
+    assert np.max(np.abs(out1 - np.array(exp))) < 1e-5
+
+
+def test_attention_matches_fp64_brute_force(oracle):
+    rng = np.random.default_rng(5)
+    qh, kvh, hd, L = 8, 2, 16, 37
+    k = rng.standard_normal((L, kvh, hd)).astype(np.float32)
+    v = rng.standard_normal((L, kvh, hd)).astype(np.float32)
+    q = rng.standard_normal(qh * hd).astype(np.float32)
+    out = oracle.attention(k, v, q, qh, kvh, hd, position=L - 1)
+    exp = np.zeros(qh * hd)
+    for h in range(qh):
+        g = h // (qh // kvh)
+        s = k[:, g, :].astype(np.float64) @ q[h * hd:(h + 1) * hd] / math.sqrt(hd)
+        p = np.exp(s - s.max())
+        p /= p.sum()
+        exp[h * hd:(h + 1) * hd] = p @ v[:, g, :]
+    assert np.max(np.abs(out - exp)) < 1e-5
+    # a sliding window of 5 sees only the last five keys
+    out_w = oracle.attention(k, v, q, qh, kvh, hd, position=L - 1, sliding_window=5)
+    out_tail = oracle.attention(k[-5:], v[-5:], q, qh, kvh, hd, position=4)
+    assert np.array_equal(out_w, out_tail)
+
+
+def test_bf16_rounding_helper():
+    vals = np.array([1.0, 1.00390625, 1.01171875, -3.5, 0.0], np.float32)
+    bits = f32_to_bf16(vals)
+    # 1 + 2^-8 is a tie between 1.0 and 1+2^-7: rounds to even (1.0)
+    assert bits.tolist()[:2] == [0x3F80, 0x3F80]
+    assert bf16_to_f32(bits)[3] == -3.5
