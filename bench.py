@@ -128,7 +128,7 @@ def main() -> int:
     step_bytes = weight_bytes + kv_bytes
 
     golden_ok = None
-    gpath = os.path.join(ROOT, "tests", "golden", "qwen2_0_5b_greedy.json")
+    gpath = os.path.join(ROOT, "tests", "golden", "qwen2_0_5b_bf16kv_greedy.json")
     if os.path.exists(gpath):
         with open(gpath) as f:
             gold = json.load(f)["tokens"]

@@ -27,7 +27,7 @@ constexpr int TP = 64;  // positions per tile (page_size is a multiple of it)
 struct AttnArgs {
     const float *q;
     long q_stride;
-    const uint16_t *k, *v;
+    const void *k, *v;
     const int32_t *page_table;
     int page_size, kv_heads, q_heads;
     long offset;
@@ -35,7 +35,19 @@ struct AttnArgs {
     float *part;
 };
 
-template <int HD, int G>
+// Eight consecutive K or V elements of one row as f32.
+__device__ __forceinline__ void load8(const uint16_t *p, float (&f)[8]) {
+    const u32x4 w = *(const u32x4 *)p;
+    f[0] = bf16_lo(w[0]); f[1] = bf16_hi(w[0]); f[2] = bf16_lo(w[1]); f[3] = bf16_hi(w[1]);
+    f[4] = bf16_lo(w[2]); f[5] = bf16_hi(w[2]); f[6] = bf16_lo(w[3]); f[7] = bf16_hi(w[3]);
+}
+__device__ __forceinline__ void load8(const float *p, float (&f)[8]) {
+    const f32x4 a = *(const f32x4 *)p, b = *(const f32x4 *)(p + 4);
+    f[0] = a[0]; f[1] = a[1]; f[2] = a[2]; f[3] = a[3];
+    f[4] = b[0]; f[5] = b[1]; f[6] = b[2]; f[7] = b[3];
+}
+
+template <int HD, int G, class KT>
 __global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
     constexpr int T = HD / 8;          // threads per position row (8 dims each)
     constexpr int P = kThreads / T;    // positions per pass
@@ -93,8 +105,8 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
         const int page = a.page_table[t0 / a.page_size];
         const long slot0 = t0 % a.page_size;
         const size_t tile_off = (((size_t)page * a.kv_heads + g) * a.page_size + slot0) * HD;
-        const uint16_t *kt = a.k + tile_off;
-        const uint16_t *vt = a.v + tile_off;
+        const KT *kt = (const KT *)a.k + tile_off;
+        const KT *vt = (const KT *)a.v + tile_off;
         // Phase A: scores of every head of the group for the tile's rows.
 #pragma unroll
         for (int p = 0; p < TP / P; ++p) {
@@ -104,9 +116,8 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
 #pragma unroll
             for (int j = 0; j < G; ++j) dot[j] = 0.f;
             if (valid) {
-                u32x4 kw = *(const u32x4 *)(kt + (size_t)pi * HD + d8 * 8);
-                float kf[8] = {bf16_lo(kw[0]), bf16_hi(kw[0]), bf16_lo(kw[1]), bf16_hi(kw[1]),
-                               bf16_lo(kw[2]), bf16_hi(kw[2]), bf16_lo(kw[3]), bf16_hi(kw[3])};
+                float kf[8];
+                load8(kt + (size_t)pi * HD + d8 * 8, kf);
 #pragma unroll
                 for (int j = 0; j < G; ++j)
 #pragma unroll
@@ -148,9 +159,8 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
         for (int p = 0; p < TP / P; ++p) {
             const int pi = p * P + pg;
             if (t0 + pi < end) {
-                u32x4 vw = *(const u32x4 *)(vt + (size_t)pi * HD + d8 * 8);
-                float vf[8] = {bf16_lo(vw[0]), bf16_hi(vw[0]), bf16_lo(vw[1]), bf16_hi(vw[1]),
-                               bf16_lo(vw[2]), bf16_hi(vw[2]), bf16_lo(vw[3]), bf16_hi(vw[3])};
+                float vf[8];
+                load8(vt + (size_t)pi * HD + d8 * 8, vf);
 #pragma unroll
                 for (int j = 0; j < G; ++j) {
                     const float pj = s_p[j][pi];
@@ -212,7 +222,9 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(const float *part, int
 
 template <int HD, int G>
 int launch_hg(const AttnJob &j, const AttnArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL((attn_split_kernel<HD, G>), dim3(j.splits, j.g.kv_heads, j.rows), dim3(kThreads), 0, s, a);
+    const dim3 grid(j.splits, j.g.kv_heads, j.rows);
+    if (j.g.kv_f32) hipLaunchKernelGGL((attn_split_kernel<HD, G, float>), grid, dim3(kThreads), 0, s, a);
+    else hipLaunchKernelGGL((attn_split_kernel<HD, G, uint16_t>), grid, dim3(kThreads), 0, s, a);
     CHIP_CHECK(hipGetLastError());
     hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3(j.q_heads, j.rows), dim3(HD), 0, s, a.part, j.splits,
                        j.q_heads, j.out);

@@ -69,16 +69,18 @@ int launch_embed(const uint16_t *table, size_t hidden, const uint32_t *tokens, s
 int launch_rmsnorm_rows(const float *x, const uint16_t *gain, float eps, size_t rows, size_t n, float *out,
                         hipStream_t s);
 
-// Paged KV cache of one layer.
+// Paged KV cache of one layer: [pages][kv_heads][page_size][head_dim]
+// elements, BF16 (default) or f32 (the reference's own cache precision).
 struct KvLayer {
-    uint16_t *k = nullptr;  // [pages][kv_heads][page_size][head_dim]
-    uint16_t *v = nullptr;
+    void *k = nullptr;
+    void *v = nullptr;
 };
 struct KvGeom {
     const int32_t *page_table = nullptr;  // device
     int page_size = 64;
     int kv_heads = 0;
     int head_dim = 0;
+    int kv_f32 = 0;  // 0 = BF16 elements, 1 = f32 elements
 };
 
 // RoPE (rotate-half, host cos/sin table) on the q and k parts of packed
@@ -97,7 +99,7 @@ struct AttnJob {
     const float *q = nullptr;
     size_t q_stride = 0;
     float *out = nullptr;  // [rows][q_heads*head_dim]
-    const uint16_t *k = nullptr, *v = nullptr;
+    const void *k = nullptr, *v = nullptr;
     KvGeom g;
     int q_heads = 0;
     size_t rows = 0;

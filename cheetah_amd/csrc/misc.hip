@@ -36,11 +36,15 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_rows_kernel(const float *x, 
 // host filled with the same libm powf/sinf/cosf the reference calls, so q and
 // k come out bit-identical to the CPU path for identical inputs; then
 // cache_append (ops.rs:1329-1332) into the paged BF16 cache.
+__device__ __forceinline__ void store_kv(uint16_t *p, float v) { *p = f32_bf16_rne(v); }
+__device__ __forceinline__ void store_kv(float *p, float v) { *p = v; }
+
+template <class KT>
 __global__ __launch_bounds__(kThreads) void rope_append_kernel(float *qkv, int q_heads, int kv_heads, int head_dim,
                                                                int rotary_dim, const float *cos_t,
                                                                const float *sin_t, const int32_t *page_table,
-                                                               int page_size, uint16_t *kc, uint16_t *vc,
-                                                               long offset, const int32_t *pos_dev) {
+                                                               int page_size, KT *kc, KT *vc, long offset,
+                                                               const int32_t *pos_dev) {
     const int row = blockIdx.x;
     const long pos = (pos_dev ? (long)*pos_dev : offset) + row;
     const int q_dim = q_heads * head_dim, kv_dim = kv_heads * head_dim;
@@ -69,8 +73,8 @@ __global__ __launch_bounds__(kThreads) void rope_append_kernel(float *qkv, int q
             kv = d < half ? a * c - b * s : b * c + a * s;
         }
         const size_t off = (((size_t)page * kv_heads + h) * page_size + slot) * head_dim + d;
-        kc[off] = f32_bf16_rne(kv);
-        vc[off] = f32_bf16_rne(v[t]);
+        store_kv(kc + off, kv);
+        store_kv(vc + off, v[t]);
     }
 }
 
@@ -164,9 +168,14 @@ int launch_rope_append(float *qkv, size_t rows, int q_heads, const KvGeom &g, co
     if (rows == 0) return 0;
     if (rotary_dim <= 0 || rotary_dim > g.head_dim || rotary_dim % 2)
         return fail("HIP backend: rotary_dim must be even and at most head_dim.");
-    hipLaunchKernelGGL(rope_append_kernel, dim3(rows), dim3(kThreads), 0, s, qkv, q_heads, g.kv_heads, g.head_dim,
-                       rotary_dim, rope_cos, rope_sin, g.page_table, g.page_size, kv.k, kv.v, (long)offset,
-                       pos_dev);
+    if (g.kv_f32)
+        hipLaunchKernelGGL(rope_append_kernel<float>, dim3(rows), dim3(kThreads), 0, s, qkv, q_heads, g.kv_heads,
+                           g.head_dim, rotary_dim, rope_cos, rope_sin, g.page_table, g.page_size, (float *)kv.k,
+                           (float *)kv.v, (long)offset, pos_dev);
+    else
+        hipLaunchKernelGGL(rope_append_kernel<uint16_t>, dim3(rows), dim3(kThreads), 0, s, qkv, q_heads,
+                           g.kv_heads, g.head_dim, rotary_dim, rope_cos, rope_sin, g.page_table, g.page_size,
+                           (uint16_t *)kv.k, (uint16_t *)kv.v, (long)offset, pos_dev);
     CHIP_CHECK(hipGetLastError());
     return 0;
 }

@@ -83,6 +83,7 @@ struct Layer {
 struct Shared {
     cheetah_hip_config cfg{};
     int quant = 0;  // 0, FMT_Q8, FMT_Q4
+    int kv_f32 = 0;  // KV element type: 0 = BF16, 1 = f32
     size_t kv_capacity = 0, max_chunk = 0;
     bool finalized = false;
     std::unordered_map<std::string, Staged> staged;
@@ -93,7 +94,8 @@ struct Shared {
     uint16_t *final_norm = nullptr;
     float *rope_cos = nullptr, *rope_sin = nullptr;
     int num_pages = 0;
-    size_t page_elems = 0;  // BF16 elements of one page of one layer (K or V)
+    size_t page_elems = 0;  // elements of one page of one layer (K or V)
+    size_t page_bytes() const { return page_elems * (kv_f32 ? 4 : 2); }
     std::mutex mu;
     std::vector<int> refs;
     std::vector<int> free_list;
@@ -330,8 +332,11 @@ int finalize(cheetah_hip_model *m) {
     sh.num_pages = (int)((sh.kv_capacity + kPageSize - 1) / kPageSize);
     sh.page_elems = (size_t)c.kv_heads * kPageSize * c.head_dim;
     for (auto &L : sh.layers) {
-        CHIP_TRY(sh.mem.alloc(&L.kv.k, sh.page_elems * sh.num_pages));
-        CHIP_TRY(sh.mem.alloc(&L.kv.v, sh.page_elems * sh.num_pages));
+        uint8_t *k = nullptr, *v = nullptr;
+        CHIP_TRY(sh.mem.alloc(&k, sh.page_bytes() * sh.num_pages));
+        CHIP_TRY(sh.mem.alloc(&v, sh.page_bytes() * sh.num_pages));
+        L.kv.k = k;
+        L.kv.v = v;
     }
     sh.refs.assign(sh.num_pages, 0);
     sh.free_list.clear();
@@ -387,10 +392,12 @@ int reserve_positions(cheetah_hip_model *m, size_t n) {
                 const int np = sh.page_alloc();
                 if (np < 0) return fail("HIP backend: KV page pool exhausted.");
                 for (auto &L : sh.layers) {
-                    CHIP_CHECK(hipMemcpyAsync(L.kv.k + (size_t)np * sh.page_elems, L.kv.k + (size_t)p * sh.page_elems,
-                                              sh.page_elems * 2, hipMemcpyDeviceToDevice, m->stream));
-                    CHIP_CHECK(hipMemcpyAsync(L.kv.v + (size_t)np * sh.page_elems, L.kv.v + (size_t)p * sh.page_elems,
-                                              sh.page_elems * 2, hipMemcpyDeviceToDevice, m->stream));
+                    const size_t pb = sh.page_bytes();
+                    uint8_t *k = (uint8_t *)L.kv.k, *v = (uint8_t *)L.kv.v;
+                    CHIP_CHECK(hipMemcpyAsync(k + (size_t)np * pb, k + (size_t)p * pb, pb, hipMemcpyDeviceToDevice,
+                                              m->stream));
+                    CHIP_CHECK(hipMemcpyAsync(v + (size_t)np * pb, v + (size_t)p * pb, pb, hipMemcpyDeviceToDevice,
+                                              m->stream));
                 }
                 sh.page_unref(p);
                 m->pages[lp] = np;
@@ -413,7 +420,7 @@ int reserve_positions(cheetah_hip_model *m, size_t n) {
 }
 
 KvGeom geom(const cheetah_hip_model *m) {
-    return KvGeom{m->page_dev, kPageSize, (int)C(m).kv_heads, (int)C(m).head_dim};
+    return KvGeom{m->page_dev, kPageSize, (int)C(m).kv_heads, (int)C(m).head_dim, m->sh->kv_f32};
 }
 
 // One decode step's kernels; token and position are read from step_dev.
@@ -665,8 +672,8 @@ int read_logits(cheetah_hip_model *m, float *logits_out) {
 
 extern "C" {
 
-cheetah_hip_model *cheetah_hip_model_create(const cheetah_hip_config *cfg, uint32_t quant_format, size_t kv_capacity,
-                                            size_t max_chunk_rows) {
+cheetah_hip_model *cheetah_hip_model_create(const cheetah_hip_config *cfg, uint32_t quant_format, uint32_t kv_format,
+                                            size_t kv_capacity, size_t max_chunk_rows) {
     if (ensure_ready()) return nullptr;
     if (!cfg) {
         fail("HIP backend: null config.");
@@ -700,10 +707,15 @@ cheetah_hip_model *cheetah_hip_model_create(const cheetah_hip_config *cfg, uint3
         fail("HIP backend: quant_format must be 0 (stored), 4 (q8) or 5 (q4).");
         return nullptr;
     }
+    if (kv_format > 1) {
+        fail("HIP backend: kv_format must be 0 (BF16) or 1 (f32).");
+        return nullptr;
+    }
     auto *m = new cheetah_hip_model();
     m->sh = std::make_shared<Shared>();
     m->sh->cfg = c;
     m->sh->quant = (int)quant_format;
+    m->sh->kv_f32 = (int)kv_format;
     m->sh->kv_capacity = kv_capacity ? kv_capacity : 65536;
     m->sh->max_chunk = max_chunk_rows ? max_chunk_rows : 1024;
     return m;

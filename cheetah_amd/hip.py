@@ -20,6 +20,7 @@ LIB_PATH = os.path.join(HERE, "libcheetah_hip.so")
 
 FMT_BF16, FMT_Q8, FMT_Q4 = 1, 4, 5
 QUANT = {None: 0, "bf16": 0, "q8": FMT_Q8, "q4": FMT_Q4}
+KV_FORMATS = {"bf16": 0, "f32": 1}
 
 _c = ctypes
 _SZ = _c.c_size_t
@@ -68,7 +69,7 @@ SIGNATURES = {
     "cheetah_hip_dequant_q8": (_c.c_int, [_VP, _SZ, _SZ, _VP]),
     "cheetah_hip_dequant_q4": (_c.c_int, [_VP, _SZ, _SZ, _VP]),
     "cheetah_hip_attention": (_c.c_int, [_VP, _c.POINTER(KvView), _c.c_uint32, _SZ, _SZ, _VP]),
-    "cheetah_hip_model_create": (_VP, [_c.POINTER(Config), _c.c_uint32, _SZ, _SZ]),
+    "cheetah_hip_model_create": (_VP, [_c.POINTER(Config), _c.c_uint32, _c.c_uint32, _SZ, _SZ]),
     "cheetah_hip_model_set_unit": (_c.c_int, [_VP, _c.c_char_p, _VP, _SZ, _c.c_uint32,
                                               _c.POINTER(_c.c_uint64), _SZ]),
     "cheetah_hip_model_finalize": (_c.c_int, [_VP]),
@@ -285,15 +286,17 @@ class HipForward:
     clone, with the ModelForward semantics (registry.rs:57-85)."""
 
     def __init__(self, shape, weights: dict | None = None, quant=None, kv_capacity: int = 0,
-                 max_chunk_rows: int = 0, _handle=None):
+                 max_chunk_rows: int = 0, kv: str = "bf16", _handle=None):
         init()
         self.shape = shape
         L = lib()
         if _handle is not None:
             self._h = _handle
             return
+        if kv not in KV_FORMATS:
+            raise ValueError(f"kv must be one of {sorted(KV_FORMATS)}")
         cfg = make_config(shape)
-        h = L.cheetah_hip_model_create(_c.byref(cfg), QUANT[quant], kv_capacity, max_chunk_rows)
+        h = L.cheetah_hip_model_create(_c.byref(cfg), QUANT[quant], KV_FORMATS[kv], kv_capacity, max_chunk_rows)
         if not h:
             raise HipError(_err())
         self._h = h

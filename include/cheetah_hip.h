@@ -128,11 +128,13 @@ typedef struct cheetah_hip_snapshot cheetah_hip_snapshot;
 /* Creates a model shell. quant_format: 0 = stored precision (BF16), 4 = q8,
  * 5 = q4 (CHEETAH_QUANT_Q8 / CHEETAH_QUANT_Q4, precision.rs:333-356; linear
  * projections only — embedding, head, norms and biases keep BF16,
- * ops.rs:1533-1537). kv_capacity: positions the paged KV pool holds across
- * this model, its clones and its snapshots (0 = 65536). max_chunk_rows:
- * largest prefill chunk (0 = 1024). */
+ * ops.rs:1533-1537). kv_format: element type of the paged KV cache, 0 = BF16
+ * (half the KV bytes), 1 = f32 (the reference's own cache precision,
+ * ops.rs:995-999). kv_capacity: positions the KV pool holds across this
+ * model, its clones and its snapshots (0 = 65536). max_chunk_rows: largest
+ * prefill chunk (0 = 1024). */
 cheetah_hip_model *cheetah_hip_model_create(const cheetah_hip_config *cfg, uint32_t quant_format,
-                                            size_t kv_capacity, size_t max_chunk_rows);
+                                            uint32_t kv_format, size_t kv_capacity, size_t max_chunk_rows);
 /* Uploads one weight unit (host bytes, as MmapWeightStore::slice serves
  * them, store.rs:189-203). dtype: 1 = BF16 (the only stored precision
  * served). Unit ids are the safetensors names ("model.layers.3.mlp.up_proj.weight"). */

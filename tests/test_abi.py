@@ -48,7 +48,7 @@ def test_calls_before_init_fail_with_a_sentence(lib):
     assert lib.cheetah_hip_gemv_bf16(None, 1, 1, None, None) == -1
     assert b"not initialized" in lib.cheetah_hip_last_error()
     assert lib.cheetah_hip_synchronize() == -1
-    assert lib.cheetah_hip_model_create(None, 0, 0, 0) is None
+    assert lib.cheetah_hip_model_create(None, 0, 0, 0, 0) is None
     assert b"not initialized" in lib.cheetah_hip_last_error()
 
 
