@@ -214,6 +214,7 @@ int cheetah_hip_attention(const float *q, const cheetah_hip_kv_view *kv, uint32_
     const size_t tiles = (ctx + 63) / 64;
     size_t splits = (2048 + rows * kv->kv_heads - 1) / (rows * kv->kv_heads);
     if (splits > tiles) splits = tiles;
+    if (splits > (size_t)attention_max_splits()) splits = attention_max_splits();
     if (splits < 1) splits = 1;
     j.splits = (int)splits;
     const size_t need = attention_part_floats(rows, (int)q_heads, (int)splits, (int)kv->head_dim);

@@ -1,21 +1,25 @@
-// GQA causal attention over the paged BF16 KV cache (the math of
+// GQA causal attention over the paged KV cache (the math of
 // OpsToolbox::attention / attention_head, ops.rs:1357-1467: scores k·q scaled
 // by 1/sqrt(head_dim), softmax, weighted value mix), as split-K flash
 // decoding:
 //
-//   grid (splits, kv_heads, rows); block = 256 threads.
+//   attn_kernel: grid (splits, kv_heads, rows); block = 256 threads.
 //   Each block owns one KV head, one query row and one contiguous slice of
 //   that row's visible positions [0, pos]; it streams the slice in tiles of
-//   64 positions (one page-aligned 64 x head_dim BF16 tile of K, then of V),
+//   64 positions (one page-aligned 64 x head_dim tile of K, then of V),
 //   scores all G = q_heads / kv_heads query heads of the group against each K
 //   row it loads (K and V are read once per group, not once per head), keeps
 //   an online softmax (running max / sum) per head and accumulates p * V.
-//   The partial (unnormalised sum, max, denominator) per split is merged by a
-//   second kernel in fixed split order, so results are deterministic.
+//   With one split it writes the normalised output; otherwise it writes a
+//   partial (unnormalised sum, max, denominator) and
+//   attn_combine_kernel merges the splits of each (row, q head) in split
+//   order, so results are deterministic.
 //
-// Decode is rows == 1; chunked prefill passes the chunk's rows, each with its
-// own causal length. The position base comes from a device word in the
-// decode graph (pos_dev) or from the host.
+// Split boundaries depend only on a row's own context length and the split
+// count. Decode is rows == 1; chunked prefill passes the chunk's rows, each
+// with its own causal length. The position base comes from a device word in
+// the decode graph (pos_dev) or from the host. K/V elements are BF16
+// (default) or f32.
 #include "kernels.hpp"
 
 namespace chip {
@@ -23,6 +27,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int TP = 64;  // positions per tile (page_size is a multiple of it)
+constexpr int kMaxSplits = 64;
 
 struct AttnArgs {
     const float *q;
@@ -33,6 +38,7 @@ struct AttnArgs {
     long offset;
     const int32_t *pos_dev;
     float *part;
+    float *out;
 };
 
 // Eight consecutive K or V elements of one row as f32.
@@ -47,13 +53,15 @@ __device__ __forceinline__ void load8(const float *p, float (&f)[8]) {
     f[4] = b[0]; f[5] = b[1]; f[6] = b[2]; f[7] = b[3];
 }
 
-template <int HD, int G, class KT>
-__global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
+template <int HD, int G, class KT, bool DIRECT>
+__global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
     constexpr int T = HD / 8;          // threads per position row (8 dims each)
     constexpr int P = kThreads / T;    // positions per pass
+    constexpr int JW = (G + 3) / 4;    // heads per wave in the softmax step
     __shared__ float s_p[G][TP];
     __shared__ float s_alpha[G];
     __shared__ float s_red[kThreads / 64][G][HD];
+    __shared__ float s_l[G];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -67,14 +75,11 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
     chunk = (chunk + TP - 1) / TP * TP;
     const long start = (long)split * chunk;
     const long end = min(start + chunk, ctx);
-    float *part = a.part + (((size_t)row * a.q_heads + (size_t)g * G) * S + split) * (HD + 2);
     const size_t part_head = (size_t)S * (HD + 2);
+    float *part = a.part + ((size_t)row * a.q_heads + (size_t)g * G) * part_head + (size_t)split * (HD + 2);
 
     if (start >= ctx) {  // empty split: contributes nothing to the merge
-        for (int t = tid; t < G * (HD + 2); t += kThreads) {
-            const int j = t / (HD + 2), e = t % (HD + 2);
-            part[j * part_head + e] = e == HD ? -INFINITY : 0.f;
-        }
+        if (tid < G) part[tid * part_head + HD] = -INFINITY;
         return;
     }
 
@@ -83,7 +88,7 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
 #pragma unroll
     for (int j = 0; j < G; ++j) {
         const float *qp = a.q + (size_t)row * a.q_stride + (size_t)(g * G + j) * HD + d8 * 8;
-        f32x4 q0 = *(const f32x4 *)qp, q1 = *(const f32x4 *)(qp + 4);
+        const f32x4 q0 = *(const f32x4 *)qp, q1 = *(const f32x4 *)(qp + 4);
         qr[j][0] = q0[0]; qr[j][1] = q0[1]; qr[j][2] = q0[2]; qr[j][3] = q0[3];
         qr[j][4] = q1[0]; qr[j][5] = q1[1]; qr[j][6] = q1[2]; qr[j][7] = q1[3];
     }
@@ -92,8 +97,6 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
     for (int j = 0; j < G; ++j)
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[j][e] = 0.f;
-    // Running max / denominator of the heads this wave owns (j = wave + 4i).
-    constexpr int JW = (G + 3) / 4;
     float m_run[JW], l_run[JW];
 #pragma unroll
     for (int i = 0; i < JW; ++i) {
@@ -107,7 +110,14 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
         const size_t tile_off = (((size_t)page * a.kv_heads + g) * a.page_size + slot0) * HD;
         const KT *kt = (const KT *)a.k + tile_off;
         const KT *vt = (const KT *)a.v + tile_off;
-        // Phase A: scores of every head of the group for the tile's rows.
+        // V rows are independent of the scores: start their loads now.
+        float vf[TP / P][8];
+#pragma unroll
+        for (int p = 0; p < TP / P; ++p) {
+            const int pi = p * P + pg;
+            if (t0 + pi < end) load8(vt + (size_t)pi * HD + d8 * 8, vf[p]);
+        }
+        // Scores of every head of the group for the tile's rows.
 #pragma unroll
         for (int p = 0; p < TP / P; ++p) {
             const int pi = p * P + pg;
@@ -125,19 +135,18 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
             }
 #pragma unroll
             for (int j = 0; j < G; ++j) {
-                float sum = group_sum<T>(dot[j]);
+                const float sum = group_sum<T>(dot[j]);
                 if (d8 == 0) s_p[j][pi] = valid ? sum * scale : -INFINITY;
             }
         }
         __syncthreads();
-        // Phase B: online softmax per head, one wave per head, one lane per position.
+        // Online softmax per head: one wave per head, one lane per position.
 #pragma unroll
         for (int i = 0; i < JW; ++i) {
             const int j = wave + 4 * i;
             if (j < G) {
                 const float sc = s_p[j][lane];
-                const float m_tile = wave_max(sc);
-                const float m_new = fmaxf(m_run[i], m_tile);
+                const float m_new = fmaxf(m_run[i], wave_max(sc));
                 const float pv = sc == -INFINITY ? 0.f : expf(sc - m_new);
                 s_p[j][lane] = pv;
                 const float l_tile = wave_sum(pv);
@@ -148,7 +157,7 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
             }
         }
         __syncthreads();
-        // Phase C: acc = acc * alpha + sum_p p * V[p].
+        // acc = acc * alpha + sum_p p * V[p].
 #pragma unroll
         for (int j = 0; j < G; ++j) {
             const float al = s_alpha[j];
@@ -159,13 +168,11 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
         for (int p = 0; p < TP / P; ++p) {
             const int pi = p * P + pg;
             if (t0 + pi < end) {
-                float vf[8];
-                load8(vt + (size_t)pi * HD + d8 * 8, vf);
 #pragma unroll
                 for (int j = 0; j < G; ++j) {
                     const float pj = s_p[j][pi];
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) acc[j][e] = fmaf(pj, vf[e], acc[j][e]);
+                    for (int e = 0; e < 8; ++e) acc[j][e] = fmaf(pj, vf[p][e], acc[j][e]);
                 }
             }
         }
@@ -192,44 +199,80 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(AttnArgs a) {
     for (int i = 0; i < JW; ++i) {
         const int j = wave + 4 * i;
         if (j < G && lane == 0) {
-            part[j * part_head + HD] = m_run[i];
-            part[j * part_head + HD + 1] = l_run[i];
+            if constexpr (DIRECT) {
+                s_l[j] = l_run[i];
+            } else {
+                part[j * part_head + HD] = m_run[i];
+                part[j * part_head + HD + 1] = l_run[i];
+            }
         }
     }
     __syncthreads();
     for (int t = tid; t < G * HD; t += kThreads) {
         const int j = t / HD, d = t % HD;
-        part[j * part_head + d] = s_red[0][j][d] + s_red[1][j][d] + s_red[2][j][d] + s_red[3][j][d];
+        const float o = s_red[0][j][d] + s_red[1][j][d] + s_red[2][j][d] + s_red[3][j][d];
+        if constexpr (DIRECT) a.out[((size_t)row * a.q_heads + g * G + j) * HD + d] = o / s_l[j];
+        else part[j * part_head + d] = o;
     }
 }
 
-// Merge the splits of one (row, q head) in split order.
+// Merge the splits of one (row, q head) in split order: one wave turns the
+// split maxima into weights w_s = exp(m_s - M) and 1 / sum_s w_s l_s, then
+// all threads sum w_s * o_s[d] over the non-empty splits.
 template <int HD>
-__global__ __launch_bounds__(HD) void attn_combine_kernel(const float *part, int S, int q_heads, float *out) {
-    const int h = blockIdx.x, row = blockIdx.y, d = threadIdx.x;
-    const float *p = part + ((size_t)row * q_heads + h) * S * (HD + 2);
-    float M = -INFINITY;
-    for (int s = 0; s < S; ++s) M = fmaxf(M, p[s * (HD + 2) + HD]);
-    float L = 0.f, o = 0.f;
-    for (int s = 0; s < S; ++s) {
-        const float m = p[s * (HD + 2) + HD];
+__global__ __launch_bounds__(kThreads) void attn_combine_kernel(const float *part, int S, int q_heads, float *out) {
+    constexpr int GR = kThreads / HD;  // split groups
+    __shared__ float s_w[kMaxSplits];
+    __shared__ float s_inv;
+    __shared__ float s_o[GR][HD];
+    const int h = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+    const float *p = part + ((size_t)row * q_heads + h) * (size_t)S * (HD + 2);
+    if (tid < 64) {
+        const float m = tid < S ? p[(size_t)tid * (HD + 2) + HD] : -INFINITY;
+        const float M = wave_max(m);
         const float w = m == -INFINITY ? 0.f : expf(m - M);
-        L = fmaf(w, p[s * (HD + 2) + HD + 1], L);
-        o = fmaf(w, p[s * (HD + 2) + d], o);
+        const float l = w != 0.f ? p[(size_t)tid * (HD + 2) + HD + 1] : 0.f;
+        const float L = wave_sum(w * l);
+        if (tid < S) s_w[tid] = w;
+        if (tid == 0) s_inv = 1.0f / L;
     }
-    out[((size_t)row * q_heads + h) * HD + d] = o / L;
+    __syncthreads();
+    const int d = tid % HD, grp = tid / HD;
+    float o = 0.f;
+    for (int s = grp; s < S; s += GR) {
+        const float w = s_w[s];
+        if (w != 0.f) o = fmaf(w, p[(size_t)s * (HD + 2) + d], o);
+    }
+    s_o[grp][d] = o;
+    __syncthreads();
+    if (tid < HD) {
+        float sum = s_o[0][tid];
+#pragma unroll
+        for (int k = 1; k < GR; ++k) sum += s_o[k][tid];
+        out[((size_t)row * q_heads + h) * HD + tid] = sum * s_inv;
+    }
+}
+
+template <int HD, int G, class KT>
+int launch_hgk(const AttnJob &j, const AttnArgs &a, hipStream_t s) {
+    const dim3 grid(j.splits, j.g.kv_heads, j.rows);
+    if (j.splits == 1) {
+        hipLaunchKernelGGL((attn_kernel<HD, G, KT, true>), grid, dim3(kThreads), 0, s, a);
+        CHIP_CHECK(hipGetLastError());
+        return 0;
+    }
+    hipLaunchKernelGGL((attn_kernel<HD, G, KT, false>), grid, dim3(kThreads), 0, s, a);
+    CHIP_CHECK(hipGetLastError());
+    hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3(j.q_heads, j.rows), dim3(kThreads), 0, s, a.part, j.splits,
+                       j.q_heads, a.out);
+    CHIP_CHECK(hipGetLastError());
+    return 0;
 }
 
 template <int HD, int G>
 int launch_hg(const AttnJob &j, const AttnArgs &a, hipStream_t s) {
-    const dim3 grid(j.splits, j.g.kv_heads, j.rows);
-    if (j.g.kv_f32) hipLaunchKernelGGL((attn_split_kernel<HD, G, float>), grid, dim3(kThreads), 0, s, a);
-    else hipLaunchKernelGGL((attn_split_kernel<HD, G, uint16_t>), grid, dim3(kThreads), 0, s, a);
-    CHIP_CHECK(hipGetLastError());
-    hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3(j.q_heads, j.rows), dim3(HD), 0, s, a.part, j.splits,
-                       j.q_heads, j.out);
-    CHIP_CHECK(hipGetLastError());
-    return 0;
+    if (j.g.kv_f32) return launch_hgk<HD, G, float>(j, a, s);
+    return launch_hgk<HD, G, uint16_t>(j, a, s);
 }
 
 template <int HD>
@@ -253,15 +296,17 @@ size_t attention_part_floats(size_t rows, int q_heads, int splits, int head_dim)
     return rows * (size_t)q_heads * (size_t)splits * (size_t)(head_dim + 2);
 }
 
+int attention_max_splits() { return kMaxSplits; }
+
 int launch_attention(const AttnJob &j, hipStream_t s) {
     if (j.rows == 0) return 0;
-    if (!j.q || !j.out || !j.k || !j.v || !j.g.page_table || !j.part)
+    if (!j.q || !j.out || !j.k || !j.v || !j.g.page_table || (j.splits > 1 && !j.part))
         return fail("HIP backend: attention is missing a buffer.");
     if (j.g.kv_heads <= 0 || j.q_heads <= 0 || j.q_heads % j.g.kv_heads)
         return fail("HIP backend: q_heads must be a multiple of kv_heads.");
     if (j.g.page_size <= 0 || j.g.page_size % TP)
         return fail("HIP backend: the KV page size must be a multiple of 64 positions.");
-    if (j.splits <= 0 || j.splits > 65535 || j.rows > 65535)
+    if (j.splits <= 0 || j.splits > kMaxSplits || j.rows > 65535 || j.q_heads > 65535)
         return fail("HIP backend: attention grid out of range.");
     AttnArgs a{};
     a.q = j.q;
@@ -275,6 +320,7 @@ int launch_attention(const AttnJob &j, hipStream_t s) {
     a.offset = (long)j.offset;
     a.pos_dev = j.pos_dev;
     a.part = j.part;
+    a.out = j.out;
     const int G = j.q_heads / j.g.kv_heads;
     if (j.g.head_dim == 64) return launch_h<64>(j, a, G, s);
     if (j.g.head_dim == 128) return launch_h<128>(j, a, G, s);

@@ -3,11 +3,14 @@
 // read once, dequantized in registers (BF16: bits << 16; Q8/Q4: sign-extended
 // code, row scale applied once to the row sum) and FMA'd against x held in LDS.
 //
-// Work split: one wave owns R consecutive rows and strides its 64 lanes along
-// K in "units" of UB bytes (16 = dwordx4 when every row start is 16-byte
-// aligned, else 4 = dword, which Q4's 4-byte row padding needs). Blocks are
-// 4 waves; the grid strides over row groups so a fused RMSNorm prologue runs
-// once per block, not once per row.
+// Work split: a group of KS waves owns R consecutive rows; its 64*KS lanes
+// stride along K in "units" of UB bytes (16 = dwordx4 when every row start
+// is 16-byte aligned, else 4 = dword, which Q4's 4-byte row padding needs)
+// and the KS partial sums meet in LDS in a fixed order. Blocks are 4 waves
+// and stride over row groups, so a fused RMSNorm prologue runs once per
+// block. The first weight loads are issued before the prologue and the
+// stream is double-buffered in registers, so weight traffic starts at once
+// and overlaps the x staging.
 #include "kernels.hpp"
 
 namespace chip {
@@ -77,7 +80,7 @@ struct Unit<FMT_Q4, UB> {
 template <int UB>
 __device__ __forceinline__ void load_raw(const uint8_t *p, uint32_t (&raw)[UB / 4]) {
     if constexpr (UB == 16) {
-        u32x4 v = __builtin_nontemporal_load((const u32x4 *)p);
+        const u32x4 v = __builtin_nontemporal_load((const u32x4 *)p);
         raw[0] = v[0];
         raw[1] = v[1];
         raw[2] = v[2];
@@ -101,24 +104,61 @@ struct Args {
     int epi;
 };
 
-template <int FMT, int UB, int R, bool NORM, bool DUAL>
+template <int FMT, int UB, int R, int KS, bool NORM, bool DUAL>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(Args a) {
     using U = Unit<FMT, UB>;
     constexpr int E = U::E;
     constexpr int D = U::D;
     constexpr int UNROLL = UB == 16 ? 2 : 4;
+    constexpr int GPB = kWaves / KS;        // row groups per block
+    constexpr int STEP = 64 * KS * UNROLL;  // units per batch of one group
+    constexpr int NM = DUAL ? 2 : 1;        // matrices read
     extern __shared__ float xs[];
     __shared__ float red[kWaves];
+    __shared__ float kred[kWaves][NM * R];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
+    const int sub = wave % KS, gib = wave / KS;
+    const int klane = sub * 64 + lane;
     const int K = a.K;
+    const int n_units = K / E;
+    const int groups = (a.rows + R - 1) / R;
 
-    // Stage x (optionally RMSNorm'd: x * (inv * gain), ops.rs:646-652) in LDS.
+    const uint8_t *rp[NM][R];
+    auto set_rows = [&](int group) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int row = min(group * R + r, a.rows - 1);
+            rp[0][r] = a.w + (size_t)row * a.stride;
+            if constexpr (DUAL) rp[1][r] = a.w2 + (size_t)row * a.stride;
+        }
+    };
+    uint32_t cur[UNROLL][NM][R][D];
+    auto load_batch = [&](uint32_t (&buf)[UNROLL][NM][R][D], int u0) {
+#pragma unroll
+        for (int i = 0; i < UNROLL; ++i) {
+            const int u = u0 + 64 * KS * i;
+            if (u < n_units) {
+#pragma unroll
+                for (int m = 0; m < NM; ++m)
+#pragma unroll
+                    for (int r = 0; r < R; ++r) load_raw<UB>(rp[m][r] + (size_t)u * UB, buf[i][m][r]);
+            }
+        }
+    };
+
+    // Start this block's first weight loads, then stage x while they fly.
+    int base = blockIdx.x * GPB;
+    if (base + gib < groups) {
+        set_rows(base + gib);
+        load_batch(cur, klane);
+    }
     if constexpr (NORM) {
+        // RMSNorm (ops.rs:646-652): x * (inv * gain), inv = 1/sqrt(mean(x^2)+eps).
         float ss = 0.f;
         for (int i = tid; i < K; i += kThreads) {
-            float v = a.x[i];
+            const float v = a.x[i];
             ss = fmaf(v, v, ss);
         }
         ss = wave_sum(ss);
@@ -134,107 +174,135 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(Args a) {
     }
     __syncthreads();
 
-    const int n_units = K / E;
-    const int tail0 = n_units * E;
-    const int groups = (a.rows + R - 1) / R;
-    for (int group = blockIdx.x * kWaves + wave; group < groups; group += gridDim.x * kWaves) {
-        const int row0 = group * R;
-        const uint8_t *rp[R];
-        const uint8_t *rp2[R];
+    for (; base < groups; base += gridDim.x * GPB) {
+        const int group = base + gib;
+        const bool valid = group < groups;
+        float acc[NM][R];
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            int row = min(row0 + r, a.rows - 1);
-            rp[r] = a.w + (size_t)row * a.stride;
-            rp2[r] = DUAL ? a.w2 + (size_t)row * a.stride : nullptr;
-        }
-        float acc[R], acc2[R];
+        for (int m = 0; m < NM; ++m)
 #pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] = acc2[r] = 0.f;
-
-        for (int u0 = lane; u0 < n_units; u0 += 64 * UNROLL) {
-            uint32_t raw[UNROLL][R][D];
-            uint32_t raw2[UNROLL][R][DUAL ? D : 1];
+            for (int r = 0; r < R; ++r) acc[m][r] = 0.f;
+        if (valid) {
+            for (int u0 = klane; u0 < n_units; u0 += STEP) {
+                uint32_t nxt[UNROLL][NM][R][D];
+                const bool more = u0 + STEP < n_units;
+                if (more) load_batch(nxt, u0 + STEP);
 #pragma unroll
-            for (int i = 0; i < UNROLL; ++i) {
-                const int u = u0 + 64 * i;
-                if (u < n_units) {
+                for (int i = 0; i < UNROLL; ++i) {
+                    const int u = u0 + 64 * KS * i;
+                    if (u < n_units) {
+                        const float *xu = xs + u * E;
 #pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        load_raw<UB>(rp[r] + (size_t)u * UB, raw[i][r]);
-                        if constexpr (DUAL) load_raw<UB>(rp2[r] + (size_t)u * UB, raw2[i][r]);
+                        for (int m = 0; m < NM; ++m)
+#pragma unroll
+                            for (int r = 0; r < R; ++r)
+                                U::decode(cur[i][m][r], [&](int e, float wv) { acc[m][r] = fmaf(wv, xu[e], acc[m][r]); });
                     }
                 }
-            }
+                if (more) {
 #pragma unroll
-            for (int i = 0; i < UNROLL; ++i) {
-                const int u = u0 + 64 * i;
-                if (u < n_units) {
-                    const float *xu = xs + u * E;
+                    for (int i = 0; i < UNROLL; ++i)
 #pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        U::decode(raw[i][r], [&](int e, float wv) { acc[r] = fmaf(wv, xu[e], acc[r]); });
-                        if constexpr (DUAL)
-                            U::decode(raw2[i][r], [&](int e, float wv) { acc2[r] = fmaf(wv, xu[e], acc2[r]); });
-                    }
+                        for (int m = 0; m < NM; ++m)
+#pragma unroll
+                            for (int r = 0; r < R; ++r)
+#pragma unroll
+                                for (int d = 0; d < D; ++d) cur[i][m][r][d] = nxt[i][m][r][d];
                 }
             }
+            // Ragged tail (K not a multiple of the unit width).
+            for (int e = n_units * E + klane; e < K; e += 64 * KS) {
+                const float xv = xs[e];
+#pragma unroll
+                for (int m = 0; m < NM; ++m)
+#pragma unroll
+                    for (int r = 0; r < R; ++r) acc[m][r] = fmaf(U::element(rp[m][r], e), xv, acc[m][r]);
+            }
         }
-        // Ragged tail (K not a multiple of the unit width).
-        for (int e = tail0 + lane; e < K; e += 64) {
-            const float xv = xs[e];
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[m][r] = wave_sum(acc[m][r]);
+        // Prefetch the next group's first batch before the epilogue.
+        const int nbase = base + gridDim.x * GPB;
+        if (nbase + gib < groups) {
+            set_rows(nbase + gib);
+            load_batch(cur, klane);
+        }
+        if constexpr (KS > 1) {
+            if (lane == 0) {
+#pragma unroll
+                for (int m = 0; m < NM; ++m)
+#pragma unroll
+                    for (int r = 0; r < R; ++r) kred[wave][m * R + r] = acc[m][r];
+            }
+            __syncthreads();
+            if (sub == 0) {
+#pragma unroll
+                for (int m = 0; m < NM; ++m)
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        float s = kred[wave][m * R + r];
+#pragma unroll
+                        for (int k = 1; k < KS; ++k) s += kred[wave + k][m * R + r];
+                        acc[m][r] = s;
+                    }
+            }
+            __syncthreads();
+        }
+        if (sub == 0 && valid) {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                acc[r] = fmaf(U::element(rp[r], e), xv, acc[r]);
-                if constexpr (DUAL) acc2[r] = fmaf(U::element(rp2[r], e), xv, acc2[r]);
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            acc[r] = wave_sum(acc[r]);
-            if constexpr (DUAL) acc2[r] = wave_sum(acc2[r]);
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int row = row0 + r;
-            if (lane == r && row < a.rows) {
-                float v = acc[r];
-                if (a.sc) v = v * a.sc[row];
-                if constexpr (DUAL) {
-                    float u = acc2[r];
-                    if (a.sc2) u = u * a.sc2[row];
-                    // silu_multiply, ops.rs:743-747: g * (u / (1 + exp(-g))).
-                    a.y[row] = v * (u / (1.0f + expf(-v)));
-                } else {
-                    if (a.bias) v = v + a.bias[row];
-                    if (a.epi == EPI_RESIDUAL) a.residual[row] = a.residual[row] + v;
-                    else a.y[row] = v;
+                const int row = group * R + r;
+                if (lane == r && row < a.rows) {
+                    float v = acc[0][r];
+                    if (a.sc) v = v * a.sc[row];
+                    if constexpr (DUAL) {
+                        float u = acc[1][r];
+                        if (a.sc2) u = u * a.sc2[row];
+                        // silu_multiply, ops.rs:743-747: g * (u / (1 + exp(-g))).
+                        a.y[row] = v * (u / (1.0f + expf(-v)));
+                    } else {
+                        if (a.bias) v = v + a.bias[row];
+                        if (a.epi == EPI_RESIDUAL) a.residual[row] = a.residual[row] + v;
+                        else a.y[row] = v;
+                    }
                 }
             }
         }
     }
 }
 
-template <int FMT, int UB, int R, bool NORM, bool DUAL>
+template <int FMT, int UB, int R, int KS, bool NORM, bool DUAL>
 int launch_t(const Args &a, hipStream_t s) {
+    constexpr int GPB = kWaves / KS;
     const int groups = (a.rows + R - 1) / R;
-    int blocks = (groups + kWaves - 1) / kWaves;
+    int blocks = (groups + GPB - 1) / GPB;
     if (NORM) blocks = min(blocks, 2048);
     const size_t lds = (size_t)a.K * sizeof(float);
-    hipLaunchKernelGGL((gemv_kernel<FMT, UB, R, NORM, DUAL>), dim3(blocks), dim3(kThreads), lds, s, a);
+    hipLaunchKernelGGL((gemv_kernel<FMT, UB, R, KS, NORM, DUAL>), dim3(blocks), dim3(kThreads), lds, s, a);
     CHIP_CHECK(hipGetLastError());
     return 0;
 }
 
+// Rows per group and waves per group: enough waves to keep every CU busy
+// (~8 per CU) while each lane still streams at least two units.
 template <int FMT, int UB, bool NORM, bool DUAL>
-int pick_r(const Args &a, hipStream_t s) {
-    if (a.rows >= 16384) return launch_t<FMT, UB, 2, NORM, DUAL>(a, s);
-    return launch_t<FMT, UB, 1, NORM, DUAL>(a, s);
+int pick_shape(const Args &a, hipStream_t s) {
+    constexpr int E = Unit<FMT, UB>::E;
+    const int n_units = a.K / E;
+    if (a.rows >= 16384) return launch_t<FMT, UB, 2, 1, NORM, DUAL>(a, s);
+    int ks = 1;
+    while (ks < 4 && a.rows * ks < 2048 && n_units >= 64 * ks * 2 * 2) ks *= 2;
+    if (ks == 4) return launch_t<FMT, UB, 1, 4, NORM, DUAL>(a, s);
+    if (ks == 2) return launch_t<FMT, UB, 1, 2, NORM, DUAL>(a, s);
+    return launch_t<FMT, UB, 1, 1, NORM, DUAL>(a, s);
 }
 
 template <int FMT, bool NORM, bool DUAL>
 int pick_ub(const Args &a, bool aligned16, hipStream_t s) {
-    if (aligned16) return pick_r<FMT, 16, NORM, DUAL>(a, s);
-    return pick_r<FMT, 4, NORM, DUAL>(a, s);
+    if (aligned16) return pick_shape<FMT, 16, NORM, DUAL>(a, s);
+    return pick_shape<FMT, 4, NORM, DUAL>(a, s);
 }
 
 template <int FMT>
@@ -253,7 +321,7 @@ int launch_gemv(const GemvJob &job, hipStream_t s) {
     if (dual && (!job.w2.base || job.w2.fmt != w.fmt || job.w2.rows != w.rows || job.w2.cols != w.cols))
         return fail("HIP backend: SwiGLU gemv needs gate and up matrices of one shape and format.");
     if (job.epi == EPI_RESIDUAL ? !job.residual : !job.y) return fail("HIP backend: gemv has no output.");
-    if ((size_t)w.cols * sizeof(float) + 64 > device_max_lds())
+    if ((size_t)w.cols * sizeof(float) + 256 > device_max_lds())
         return fail("HIP backend: gemv input width " + std::to_string(w.cols) + " exceeds the LDS staging limit.");
     Args a{};
     a.w = w.payload();
@@ -270,7 +338,8 @@ int launch_gemv(const GemvJob &job, hipStream_t s) {
     a.y = job.y;
     a.residual = job.residual;
     a.epi = job.epi;
-    bool aligned16 = a.stride % 16 == 0 && ((uintptr_t)a.w % 16) == 0 && (!dual || ((uintptr_t)a.w2 % 16) == 0);
+    const bool aligned16 =
+        a.stride % 16 == 0 && ((uintptr_t)a.w % 16) == 0 && (!dual || ((uintptr_t)a.w2 % 16) == 0);
     const bool norm = job.norm_gain != nullptr;
     switch (w.fmt) {
         case FMT_BF16: return pick_mode<FMT_BF16>(a, aligned16, norm, dual, s);

@@ -92,9 +92,9 @@ int launch_rope_append(float *qkv, size_t rows, int q_heads, const KvGeom &g, co
                        const int32_t *pos_dev, hipStream_t s);
 
 // GQA attention for `rows` query rows at positions pos0 + i over keys
-// [0, pos0 + i]. q row stride q_stride floats. Splits are fixed by the
-// caller (decode graphs need a fixed grid); partial buffers sized for
-// rows * q_heads * splits * (head_dim + 2) floats.
+// [0, pos0 + i]. q row stride q_stride floats. The split count (at most
+// attention_max_splits()) is the caller's: decode graphs need a fixed grid.
+// Partial buffers hold rows * q_heads * splits * (head_dim + 2) floats.
 struct AttnJob {
     const float *q = nullptr;
     size_t q_stride = 0;
@@ -106,10 +106,11 @@ struct AttnJob {
     size_t offset = 0;
     const int32_t *pos_dev = nullptr;
     int splits = 1;
-    float *part = nullptr;  // partial buffer
+    float *part = nullptr;  // partial buffer (splits > 1)
 };
 int launch_attention(const AttnJob &job, hipStream_t s);
 size_t attention_part_floats(size_t rows, int q_heads, int splits, int head_dim);
+int attention_max_splits();
 
 // Greedy argmax (ties -> last index, total order) of logits[n]; writes the
 // index to *out_token. When `step` is set (the device-side decode loop,

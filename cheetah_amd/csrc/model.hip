@@ -163,12 +163,14 @@ struct cheetah_hip_model {
     int32_t *step_host = nullptr;    // pinned
     uint32_t *tokens_host = nullptr;  // pinned staging for chunk tokens
     float *logits_host = nullptr;     // pinned
-    int dec_splits = 1;
-    hipGraphExec_t graph = nullptr;
+    // Decode graphs, one per attention split count (the grid of a captured
+    // launch is fixed; the split count follows the context length).
+    hipGraphExec_t graphs[65] = {};
 
     ~cheetah_hip_model() {
         if (stream) (void)hipStreamSynchronize(stream);
-        if (graph) (void)hipGraphExecDestroy(graph);
+        for (hipGraphExec_t g : graphs)
+            if (g) (void)hipGraphExecDestroy(g);
         if (stream) (void)hipStreamDestroy(stream);
         if (step_host) (void)hipHostFree(step_host);
         if (tokens_host) (void)hipHostFree(tokens_host);
@@ -351,14 +353,13 @@ int init_instance(cheetah_hip_model *m) {
     const auto &c = sh.cfg;
     const size_t H = c.hidden_size, qd = sh.q_dim(), kvd = sh.kv_dim(), R = sh.max_chunk;
     CHIP_CHECK(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
-    m->dec_splits = (int)std::max<uint32_t>(8, std::min<uint32_t>(64, 256 / c.kv_heads));
     CHIP_TRY(m->mem.alloc(&m->hidden, R * H));
     CHIP_TRY(m->mem.alloc(&m->normed, R * H));
     CHIP_TRY(m->mem.alloc(&m->qkv, R * (qd + 2 * kvd)));
     CHIP_TRY(m->mem.alloc(&m->attn, R * qd));
     CHIP_TRY(m->mem.alloc(&m->act, R * c.intermediate_size));
     CHIP_TRY(m->mem.alloc(&m->logits, c.vocab_size));
-    const size_t part_rows = std::max(R * (size_t)kPrefillSplits, (size_t)m->dec_splits);
+    const size_t part_rows = std::max(R * (size_t)kPrefillSplits, (size_t)attention_max_splits());
     CHIP_TRY(m->mem.alloc(&m->part, part_rows * c.q_heads * (c.head_dim + 2)));
     CHIP_TRY(m->mem.alloc(&m->tokens_dev, sh.kv_capacity));
     CHIP_TRY(m->mem.alloc(&m->next_dev, 1));
@@ -423,8 +424,14 @@ KvGeom geom(const cheetah_hip_model *m) {
     return KvGeom{m->page_dev, kPageSize, (int)C(m).kv_heads, (int)C(m).head_dim, m->sh->kv_f32};
 }
 
+// Attention splits of a decode step over `ctx` keys: ~128 positions each.
+int decode_splits(size_t ctx) {
+    const size_t s = (ctx + 127) / 128;
+    return (int)std::max<size_t>(1, std::min<size_t>(s, (size_t)attention_max_splits()));
+}
+
 // One decode step's kernels; token and position are read from step_dev.
-int enqueue_decode(cheetah_hip_model *m) {
+int enqueue_decode(cheetah_hip_model *m, int splits) {
     Shared &sh = *m->sh;
     const auto &c = sh.cfg;
     hipStream_t s = m->stream;
@@ -452,7 +459,7 @@ int enqueue_decode(cheetah_hip_model *m) {
         aj.q_heads = (int)c.q_heads;
         aj.rows = 1;
         aj.pos_dev = pos;
-        aj.splits = m->dec_splits;
+        aj.splits = splits;
         aj.part = m->part;
         CHIP_TRY(launch_attention(aj, s));
         GemvJob o;
@@ -495,26 +502,30 @@ bool graphs_enabled() {
     return !(e && (e[0] == '0' || e[0] == 'f' || e[0] == 'F' || e[0] == 'n' || e[0] == 'N'));
 }
 
-int launch_decode(cheetah_hip_model *m) {
-    if (!graphs_enabled()) return enqueue_decode(m);
-    if (!m->graph) {
+// One decode step at absolute position `pos` (the device step word must
+// already hold it): the captured graph for the step's split count.
+int launch_decode(cheetah_hip_model *m, size_t pos) {
+    const int splits = decode_splits(pos + 1);
+    if (!graphs_enabled()) return enqueue_decode(m, splits);
+    hipGraphExec_t &exec = m->graphs[splits];
+    if (!exec) {
         hipGraph_t g = nullptr;
         CHIP_CHECK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
-        const int rc = enqueue_decode(m);
+        const int rc = enqueue_decode(m, splits);
         hipError_t e = hipStreamEndCapture(m->stream, &g);
         if (rc != 0) {
             if (g) (void)hipGraphDestroy(g);
             return -1;
         }
         if (e != hipSuccess) return fail(std::string("HIP backend: decode graph capture failed: ") + hipGetErrorString(e));
-        e = hipGraphInstantiate(&m->graph, g, nullptr, nullptr, 0);
+        e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
         (void)hipGraphDestroy(g);
         if (e != hipSuccess) {
-            m->graph = nullptr;
+            exec = nullptr;
             return fail(std::string("HIP backend: decode graph instantiation failed: ") + hipGetErrorString(e));
         }
     }
-    CHIP_CHECK(hipGraphLaunch(m->graph, m->stream));
+    CHIP_CHECK(hipGraphLaunch(exec, m->stream));
     return 0;
 }
 
@@ -643,7 +654,7 @@ int run_forward(cheetah_hip_model *m, const uint32_t *tokens, size_t n, size_t o
     CHIP_TRY(reserve_positions(m, n));
     if (n == 1) {
         CHIP_TRY(write_step(m, tokens[0], offset));
-        CHIP_TRY(launch_decode(m));
+        CHIP_TRY(launch_decode(m, offset));
     } else {
         CHIP_CHECK(hipStreamSynchronize(m->stream));  // tokens_host reuse
         std::memcpy(m->tokens_host, tokens, n * sizeof(uint32_t));
@@ -781,7 +792,7 @@ int cheetah_hip_decode_greedy(cheetah_hip_model *m, uint32_t token, size_t offse
     CHIP_TRY(validate_decode(m, token, offset, steps));
     CHIP_TRY(reserve_positions(m, steps));
     CHIP_TRY(write_step(m, token, offset));
-    for (size_t i = 0; i < steps; ++i) CHIP_TRY(launch_decode(m));
+    for (size_t i = 0; i < steps; ++i) CHIP_TRY(launch_decode(m, offset + i));
     CHIP_CHECK(hipMemcpyAsync(tokens_out, m->hist_dev + offset + 1, steps * sizeof(uint32_t), hipMemcpyDeviceToHost,
                               m->stream));
     CHIP_CHECK(hipStreamSynchronize(m->stream));
@@ -800,7 +811,7 @@ int cheetah_hip_time_decode(cheetah_hip_model *m, uint32_t token, size_t offset,
     CHIP_CHECK(hipEventCreate(&e0));
     CHIP_CHECK(hipEventCreate(&e1));
     CHIP_CHECK(hipEventRecord(e0, m->stream));
-    for (size_t i = 0; i < steps; ++i) CHIP_TRY(launch_decode(m));
+    for (size_t i = 0; i < steps; ++i) CHIP_TRY(launch_decode(m, offset + i));
     CHIP_CHECK(hipEventRecord(e1, m->stream));
     CHIP_CHECK(hipEventSynchronize(e1));
     float total = 0.f;
