@@ -83,13 +83,25 @@ struct KvGeom {
     int kv_f32 = 0;  // 0 = BF16 elements, 1 = f32 elements
 };
 
-// RoPE (rotate-half, host cos/sin table) on the q and k parts of packed
-// qkv rows [rows][q_dim + 2*kv_dim], then K and V rows appended to the
-// paged cache as BF16. Positions are pos0 + i, where pos0 is read from
-// *pos_dev when pos_dev is set (decode graph) and is `offset` otherwise.
-int launch_rope_append(float *qkv, size_t rows, int q_heads, const KvGeom &g, const KvLayer &kv,
+// The q/k rows of a layer's packed QKV matrix are stored pair-permuted: in
+// every head, output rows i and i + rotary_dim/2 (the two halves a RoPE
+// rotation mixes) sit next to each other at 2i and 2i + 1; dims at or past
+// rotary_dim keep their place; v rows are unpermuted. qkv_perm_row maps a
+// stored row to the reference row it holds.
+int qkv_perm_row(int stored_row, int q_heads, int kv_heads, int head_dim, int rotary_dim);
+
+// RoPE (rotate-half, host cos/sin table) on the q and k parts of packed,
+// pair-permuted qkv rows [rows][q_dim + 2*kv_dim]: rotated q goes to
+// qrot[rows][q_dim] in reference order, K and V rows are appended to the
+// paged cache. Positions are pos0 + i, where pos0 is read from *pos_dev when
+// pos_dev is set (decode graph) and is `offset` otherwise.
+int launch_rope_append(const float *qkv, float *qrot, size_t rows, int q_heads, const KvGeom &g, const KvLayer &kv,
                        const float *rope_cos, const float *rope_sin, int rotary_dim, size_t offset,
                        const int32_t *pos_dev, hipStream_t s);
+
+// dst[r][:] = src[map[r]][:] for rows of row_bytes bytes (load-time layout).
+int launch_gather_rows(const uint8_t *src, uint8_t *dst, const int32_t *map, size_t rows, size_t row_bytes,
+                       hipStream_t s);
 
 // GQA attention for `rows` query rows at positions pos0 + i over keys
 // [0, pos0 + i]. q row stride q_stride floats. The split count (at most

@@ -39,43 +39,52 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_rows_kernel(const float *x, 
 __device__ __forceinline__ void store_kv(uint16_t *p, float v) { *p = f32_bf16_rne(v); }
 __device__ __forceinline__ void store_kv(float *p, float v) { *p = v; }
 
+// Element d of one rotated head whose pair-permuted projection is `src`
+// (pair i at src[2i], src[2i+1]): x1' = x1*cos - x2*sin, x2' = x2*cos + x1*sin.
+__device__ __forceinline__ float rope_elem(const float *src, int d, int half, int rotary_dim, const float *cr,
+                                           const float *sr) {
+    if (d >= rotary_dim) return src[d];
+    const int i = d < half ? d : d - half;
+    const float a = src[2 * i], b = src[2 * i + 1], c = cr[i], s = sr[i];
+    return d < half ? a * c - b * s : b * c + a * s;
+}
+
 template <class KT>
-__global__ __launch_bounds__(kThreads) void rope_append_kernel(float *qkv, int q_heads, int kv_heads, int head_dim,
-                                                               int rotary_dim, const float *cos_t,
-                                                               const float *sin_t, const int32_t *page_table,
-                                                               int page_size, KT *kc, KT *vc, long offset,
-                                                               const int32_t *pos_dev) {
+__global__ __launch_bounds__(kThreads) void rope_append_kernel(const float *qkv, float *qrot, int q_heads,
+                                                               int kv_heads, int head_dim, int rotary_dim,
+                                                               const float *cos_t, const float *sin_t,
+                                                               const int32_t *page_table, int page_size, KT *kc,
+                                                               KT *vc, long offset, const int32_t *pos_dev) {
     const int row = blockIdx.x;
     const long pos = (pos_dev ? (long)*pos_dev : offset) + row;
     const int q_dim = q_heads * head_dim, kv_dim = kv_heads * head_dim;
-    float *q = qkv + (size_t)row * (q_dim + 2 * kv_dim);
-    float *k = q + q_dim;
-    float *v = k + kv_dim;
+    const float *q = qkv + (size_t)row * (q_dim + 2 * kv_dim);
+    const float *k = q + q_dim;
+    const float *v = k + kv_dim;
+    float *qo = qrot + (size_t)row * q_dim;
     const int half = rotary_dim / 2;
     const float *cr = cos_t + (size_t)pos * half;
     const float *sr = sin_t + (size_t)pos * half;
-    for (int t = threadIdx.x; t < q_heads * half; t += kThreads) {
-        const int h = t / half, i = t % half;
-        float *base = q + h * head_dim;
-        const float a = base[i], b = base[half + i], c = cr[i], s = sr[i];
-        base[i] = a * c - b * s;
-        base[half + i] = b * c + a * s;
+    for (int t = threadIdx.x; t < q_dim; t += kThreads) {
+        const int h = t / head_dim, d = t % head_dim;
+        qo[t] = rope_elem(q + h * head_dim, d, half, rotary_dim, cr, sr);
     }
     const int page = page_table[pos / page_size];
     const int slot = (int)(pos % page_size);
     for (int t = threadIdx.x; t < kv_dim; t += kThreads) {
         const int h = t / head_dim, d = t % head_dim;
-        float kv = k[t];
-        if (d < rotary_dim) {
-            const int i = d < half ? d : d - half;
-            const float c = cr[i], s = sr[i];
-            const float a = k[h * head_dim + i], b = k[h * head_dim + half + i];
-            kv = d < half ? a * c - b * s : b * c + a * s;
-        }
+        const float kv = rope_elem(k + h * head_dim, d, half, rotary_dim, cr, sr);
         const size_t off = (((size_t)page * kv_heads + h) * page_size + slot) * head_dim + d;
         store_kv(kc + off, kv);
         store_kv(vc + off, v[t]);
     }
+}
+
+__global__ __launch_bounds__(kThreads) void gather_rows_kernel(const uint8_t *src, uint8_t *dst, const int32_t *map,
+                                                               size_t row_bytes) {
+    const uint8_t *s = src + (size_t)map[blockIdx.x] * row_bytes;
+    uint8_t *d = dst + (size_t)blockIdx.x * row_bytes;
+    for (size_t i = threadIdx.x; i < row_bytes; i += kThreads) d[i] = s[i];
 }
 
 // Total order of f32::total_cmp as a signed integer key.
@@ -162,20 +171,37 @@ int launch_rmsnorm_rows(const float *x, const uint16_t *gain, float eps, size_t 
     return 0;
 }
 
-int launch_rope_append(float *qkv, size_t rows, int q_heads, const KvGeom &g, const KvLayer &kv,
+int qkv_perm_row(int stored, int q_heads, int kv_heads, int head_dim, int rotary_dim) {
+    const int q_dim = q_heads * head_dim, k_end = q_dim + kv_heads * head_dim;
+    if (stored >= k_end) return stored;  // v rows
+    const int head_base = stored - stored % head_dim, d = stored % head_dim;
+    if (d >= rotary_dim) return stored;
+    const int half = rotary_dim / 2;
+    return head_base + (d % 2 == 0 ? d / 2 : half + d / 2);
+}
+
+int launch_rope_append(const float *qkv, float *qrot, size_t rows, int q_heads, const KvGeom &g, const KvLayer &kv,
                        const float *rope_cos, const float *rope_sin, int rotary_dim, size_t offset,
                        const int32_t *pos_dev, hipStream_t s) {
     if (rows == 0) return 0;
     if (rotary_dim <= 0 || rotary_dim > g.head_dim || rotary_dim % 2)
         return fail("HIP backend: rotary_dim must be even and at most head_dim.");
     if (g.kv_f32)
-        hipLaunchKernelGGL(rope_append_kernel<float>, dim3(rows), dim3(kThreads), 0, s, qkv, q_heads, g.kv_heads,
-                           g.head_dim, rotary_dim, rope_cos, rope_sin, g.page_table, g.page_size, (float *)kv.k,
-                           (float *)kv.v, (long)offset, pos_dev);
+        hipLaunchKernelGGL(rope_append_kernel<float>, dim3(rows), dim3(kThreads), 0, s, qkv, qrot, q_heads,
+                           g.kv_heads, g.head_dim, rotary_dim, rope_cos, rope_sin, g.page_table, g.page_size,
+                           (float *)kv.k, (float *)kv.v, (long)offset, pos_dev);
     else
-        hipLaunchKernelGGL(rope_append_kernel<uint16_t>, dim3(rows), dim3(kThreads), 0, s, qkv, q_heads,
+        hipLaunchKernelGGL(rope_append_kernel<uint16_t>, dim3(rows), dim3(kThreads), 0, s, qkv, qrot, q_heads,
                            g.kv_heads, g.head_dim, rotary_dim, rope_cos, rope_sin, g.page_table, g.page_size,
                            (uint16_t *)kv.k, (uint16_t *)kv.v, (long)offset, pos_dev);
+    CHIP_CHECK(hipGetLastError());
+    return 0;
+}
+
+int launch_gather_rows(const uint8_t *src, uint8_t *dst, const int32_t *map, size_t rows, size_t row_bytes,
+                       hipStream_t s) {
+    if (rows == 0) return 0;
+    hipLaunchKernelGGL(gather_rows_kernel, dim3(rows), dim3(kThreads), 0, s, src, dst, map, row_bytes);
     CHIP_CHECK(hipGetLastError());
     return 0;
 }

@@ -28,6 +28,7 @@
 #include <vector>
 
 #include "../../include/cheetah_hip.h"
+#include "decode_fused.hpp"
 #include "kernels.hpp"
 
 namespace chip {
@@ -155,7 +156,7 @@ struct cheetah_hip_model {
     int32_t *page_dev = nullptr;
     size_t len = 0;
     // activations
-    float *hidden = nullptr, *normed = nullptr, *qkv = nullptr, *attn = nullptr, *act = nullptr;
+    float *hidden = nullptr, *normed = nullptr, *qkv = nullptr, *qrot = nullptr, *attn = nullptr, *act = nullptr;
     float *logits = nullptr, *part = nullptr;
     uint32_t *tokens_dev = nullptr, *next_dev = nullptr, *hist_dev = nullptr;
     int32_t *step_dev = nullptr;  // [0] = token, [1] = position
@@ -166,6 +167,14 @@ struct cheetah_hip_model {
     // Decode graphs, one per attention split count (the grid of a captured
     // launch is fixed; the split count follows the context length).
     hipGraphExec_t graphs[65] = {};
+    // Persistent decode kernel state (decode_fused.hip).
+    bool fused_ok = false;
+    FusedLayer *fused_layers = nullptr;  // device [L]
+    unsigned *sync_words = nullptr;      // arrive[NB] | go | epoch_base | abort | attn_count[kv]
+    int fused_blocks = 0;
+    int *am_key = nullptr;
+    uint32_t *am_idx = nullptr;
+    int32_t *abort_host = nullptr;  // pinned
 
     ~cheetah_hip_model() {
         if (stream) (void)hipStreamSynchronize(stream);
@@ -175,6 +184,7 @@ struct cheetah_hip_model {
         if (step_host) (void)hipHostFree(step_host);
         if (tokens_host) (void)hipHostFree(tokens_host);
         if (logits_host) (void)hipHostFree(logits_host);
+        if (abort_host) (void)hipHostFree(abort_host);
         for (int p : pages) sh->page_unref(p);
     }
 };
@@ -265,6 +275,11 @@ int finalize(cheetah_hip_model *m) {
     }
     CHIP_TRY(upload_bf16_1d(sh, "model.norm.weight", H, &sh.final_norm, true));
     sh.layers.resize(c.num_layers);
+    std::vector<int32_t> perm(qd + 2 * kvd);
+    for (size_t r = 0; r < perm.size(); ++r)
+        perm[r] = qkv_perm_row((int)r, (int)c.q_heads, (int)c.kv_heads, (int)c.head_dim, (int)c.rotary_dim);
+    int32_t *perm_dev = nullptr;
+    CHIP_TRY(sh.mem.alloc(&perm_dev, perm.size()));
     for (uint32_t l = 0; l < c.num_layers; ++l) {
         Layer &L = sh.layers[l];
         const std::string p = "model.layers." + std::to_string(l) + ".";
@@ -279,15 +294,24 @@ int finalize(cheetah_hip_model *m) {
         CHIP_CHECK(hipMemcpyAsync(qkv, q, qd * H * 2, hipMemcpyDeviceToDevice, sh.copy_stream));
         CHIP_CHECK(hipMemcpyAsync(qkv + qd * H, k, kvd * H * 2, hipMemcpyDeviceToDevice, sh.copy_stream));
         CHIP_CHECK(hipMemcpyAsync(qkv + (qd + kvd) * H, v, kvd * H * 2, hipMemcpyDeviceToDevice, sh.copy_stream));
+        // Pair-permute the q/k rows so each RoPE pair is two adjacent rows
+        // (qkv_perm_row); quantization below is per row, so it commutes.
+        uint16_t *qkv_p = nullptr;
+        CHIP_CHECK(hipMalloc(&qkv_p, (qd + 2 * kvd) * H * 2));
+        CHIP_CHECK(hipMemcpyAsync(perm_dev, perm.data(), perm.size() * 4, hipMemcpyHostToDevice, sh.copy_stream));
+        CHIP_TRY(launch_gather_rows((const uint8_t *)qkv, (uint8_t *)qkv_p, perm_dev, qd + 2 * kvd, H * 2,
+                                    sh.copy_stream));
         CHIP_CHECK(hipStreamSynchronize(sh.copy_stream));
         CHIP_CHECK(hipFree(q));
         CHIP_CHECK(hipFree(k));
         CHIP_CHECK(hipFree(v));
-        CHIP_TRY(make_linear(sh, qkv, qd + 2 * kvd, H, &L.qkv));
-        std::vector<float> bias;
-        CHIP_TRY(append_bias(sh, p + "self_attn.q_proj.bias", qd, bias));
-        CHIP_TRY(append_bias(sh, p + "self_attn.k_proj.bias", kvd, bias));
-        CHIP_TRY(append_bias(sh, p + "self_attn.v_proj.bias", kvd, bias));
+        CHIP_CHECK(hipFree(qkv));
+        CHIP_TRY(make_linear(sh, qkv_p, qd + 2 * kvd, H, &L.qkv));
+        std::vector<float> bias_ref, bias;
+        CHIP_TRY(append_bias(sh, p + "self_attn.q_proj.bias", qd, bias_ref));
+        CHIP_TRY(append_bias(sh, p + "self_attn.k_proj.bias", kvd, bias_ref));
+        CHIP_TRY(append_bias(sh, p + "self_attn.v_proj.bias", kvd, bias_ref));
+        for (int32_t r : perm) bias.push_back(bias_ref[r]);
         CHIP_TRY(sh.mem.alloc(&L.qkv_bias, bias.size()));
         CHIP_CHECK(hipMemcpy(L.qkv_bias, bias.data(), bias.size() * 4, hipMemcpyHostToDevice));
         if (sh.staged.count(p + "self_attn.o_proj.bias")) {
@@ -347,6 +371,108 @@ int finalize(cheetah_hip_model *m) {
     return 0;
 }
 
+// Persistent decode state of one instance: the per-layer pointer table and
+// the barrier words. Sets fused_ok when the model's shape and layout have a
+// persistent kernel; otherwise decode keeps the graph path.
+int init_fused(cheetah_hip_model *m) {
+    Shared &sh = *m->sh;
+    const auto &c = sh.cfg;
+    const int G = (int)(c.q_heads / c.kv_heads);
+    const Layer &L0 = sh.layers[0];
+    auto aligned = [](const WMat &w) { return w.row_stride() % 16 == 0 && ((uintptr_t)w.payload() % 16) == 0; };
+    bool al = true;
+    for (const Layer &L : sh.layers) al = al && aligned(L.qkv) && aligned(L.o) && aligned(L.gate) && aligned(L.up) && aligned(L.down);
+    const size_t lds = (size_t)std::max(std::max(c.hidden_size, c.q_heads * c.head_dim), c.intermediate_size) * 4;
+    m->fused_blocks = fused_decode_blocks();
+    m->fused_ok = m->fused_blocks > 0 && fused_decode_supported(L0.qkv.fmt, (int)c.head_dim, G, al) &&
+                  c.hidden_size % 8 == 0 && lds + 32768 <= device_max_lds();
+    if (!m->fused_ok) return 0;
+    std::vector<FusedLayer> fl(c.num_layers);
+    for (uint32_t l = 0; l < c.num_layers; ++l) {
+        const Layer &L = sh.layers[l];
+        fl[l] = FusedLayer{L.qkv.payload(), L.o.payload(), L.gate.payload(), L.up.payload(), L.down.payload(),
+                           L.qkv.scales(), L.o.scales(), L.gate.scales(), L.up.scales(), L.down.scales(),
+                           L.qkv_bias, L.o_bias, L.ln1, L.ln2, L.kv.k, L.kv.v};
+    }
+    CHIP_TRY(m->mem.alloc(&m->fused_layers, fl.size()));
+    CHIP_CHECK(hipMemcpy(m->fused_layers, fl.data(), fl.size() * sizeof(FusedLayer), hipMemcpyHostToDevice));
+    const size_t words = (size_t)m->fused_blocks + 3 + c.kv_heads;
+    CHIP_TRY(m->mem.alloc(&m->sync_words, words));
+    CHIP_CHECK(hipMemset(m->sync_words, 0, words * sizeof(unsigned)));
+    CHIP_TRY(m->mem.alloc(&m->am_key, (size_t)m->fused_blocks * 4));
+    CHIP_TRY(m->mem.alloc(&m->am_idx, (size_t)m->fused_blocks * 4));
+    CHIP_CHECK(hipHostMalloc((void **)&m->abort_host, sizeof(int32_t), hipHostMallocDefault));
+    return 0;
+}
+
+bool fused_enabled(const cheetah_hip_model *m) {
+    if (!m->fused_ok) return false;
+    // Opt-in: the per-step graph path is the faster decode today.
+    const char *e = getenv("CHEETAH_HIP_FUSED");
+    return e && (e[0] == '1' || e[0] == 't' || e[0] == 'T' || e[0] == 'y' || e[0] == 'Y');
+}
+
+// Runs `steps` decode steps in one persistent launch from the token and
+// position in step_dev; leaves the last step's logits in m->logits, its
+// argmax in next_dev and every sampled id in hist_dev. Waits for the launch.
+int run_fused(cheetah_hip_model *m, size_t steps) {
+    Shared &sh = *m->sh;
+    const auto &c = sh.cfg;
+    FusedArgs a{};
+    a.layers = m->fused_layers;
+    a.L = (int)c.num_layers;
+    a.H = (int)c.hidden_size;
+    a.q_heads = (int)c.q_heads;
+    a.kv_heads = (int)c.kv_heads;
+    a.rotary = (int)c.rotary_dim;
+    a.I = (int)c.intermediate_size;
+    a.V = (int)c.vocab_size;
+    a.eps = c.rms_eps;
+    const Layer &L0 = sh.layers[0];
+    a.qkv_stride = L0.qkv.row_stride();
+    a.o_stride = L0.o.row_stride();
+    a.gu_stride = L0.gate.row_stride();
+    a.down_stride = L0.down.row_stride();
+    a.embed = sh.embed;
+    a.head = (const uint16_t *)sh.head.base;
+    a.final_norm = sh.final_norm;
+    a.rope_cos = sh.rope_cos;
+    a.rope_sin = sh.rope_sin;
+    a.page_table = m->page_dev;
+    a.page_size = kPageSize;
+    a.step = m->step_dev;
+    a.hist = m->hist_dev;
+    a.hist_cap = (long)sh.kv_capacity + 1;
+    a.hidden = m->hidden;
+    a.qrot = m->qrot;
+    a.part = m->part;
+    a.attn = m->attn;
+    a.act = m->act;
+    a.logits = m->logits;
+    a.am_key = m->am_key;
+    a.am_idx = m->am_idx;
+    a.arrive = m->sync_words;
+    a.go = m->sync_words + m->fused_blocks;
+    a.epoch_base = a.go + 1;
+    a.abort_flag = (int *)(a.go + 2);
+    a.attn_count = a.go + 3;
+    a.steps = (int)steps;
+    a.max_splits = 64;
+    CHIP_TRY(launch_decode_fused(a, L0.qkv.fmt, (int)c.head_dim, (int)(c.q_heads / c.kv_heads), sh.kv_f32 != 0,
+                                 m->stream));
+    CHIP_CHECK(hipMemcpyAsync(m->next_dev, m->step_dev, sizeof(uint32_t), hipMemcpyDeviceToDevice, m->stream));
+    CHIP_CHECK(hipMemcpyAsync(m->abort_host, a.abort_flag, sizeof(int32_t), hipMemcpyDeviceToHost, m->stream));
+    CHIP_CHECK(hipStreamSynchronize(m->stream));
+    if (*m->abort_host) {
+        // A barrier spin timed out: the step is incomplete. Reset the
+        // barrier words so the next launch starts clean.
+        const size_t words = (size_t)m->fused_blocks + 3 + c.kv_heads;
+        CHIP_CHECK(hipMemset(m->sync_words, 0, words * sizeof(unsigned)));
+        return fail("HIP backend: persistent decode barrier timed out; the step was abandoned.");
+    }
+    return 0;
+}
+
 // Per-instance buffers (a fresh model and every clone).
 int init_instance(cheetah_hip_model *m) {
     Shared &sh = *m->sh;
@@ -357,6 +483,7 @@ int init_instance(cheetah_hip_model *m) {
     CHIP_TRY(m->mem.alloc(&m->normed, R * H));
     CHIP_TRY(m->mem.alloc(&m->qkv, R * (qd + 2 * kvd)));
     CHIP_TRY(m->mem.alloc(&m->attn, R * qd));
+    CHIP_TRY(m->mem.alloc(&m->qrot, R * qd));
     CHIP_TRY(m->mem.alloc(&m->act, R * c.intermediate_size));
     CHIP_TRY(m->mem.alloc(&m->logits, c.vocab_size));
     const size_t part_rows = std::max(R * (size_t)kPrefillSplits, (size_t)attention_max_splits());
@@ -373,7 +500,7 @@ int init_instance(cheetah_hip_model *m) {
     CHIP_CHECK(hipHostMalloc((void **)&m->tokens_host, sh.kv_capacity * sizeof(uint32_t), hipHostMallocDefault));
     CHIP_CHECK(hipHostMalloc((void **)&m->logits_host, (size_t)c.vocab_size * sizeof(float), hipHostMallocDefault));
     m->page_host.assign(sh.num_pages, 0);
-    return 0;
+    return init_fused(m);
 }
 
 // Makes positions [m->len, m->len + n) writable: maps new pages and copies a
@@ -447,11 +574,11 @@ int enqueue_decode(cheetah_hip_model *m, int splits) {
         qkv.bias = L.qkv_bias;
         qkv.y = m->qkv;
         CHIP_TRY(launch_gemv(qkv, s));
-        CHIP_TRY(launch_rope_append(m->qkv, 1, (int)c.q_heads, geom(m), L.kv, sh.rope_cos, sh.rope_sin,
+        CHIP_TRY(launch_rope_append(m->qkv, m->qrot, 1, (int)c.q_heads, geom(m), L.kv, sh.rope_cos, sh.rope_sin,
                                     (int)c.rotary_dim, 0, pos, s));
         AttnJob aj;
-        aj.q = m->qkv;
-        aj.q_stride = sh.q_dim() + 2 * sh.kv_dim();
+        aj.q = m->qrot;
+        aj.q_stride = sh.q_dim();
         aj.out = m->attn;
         aj.k = L.kv.k;
         aj.v = L.kv.v;
@@ -560,11 +687,11 @@ int enqueue_chunk(cheetah_hip_model *m, const uint32_t *tokens_dev, size_t rows,
         qkv.bias = L.qkv_bias;
         qkv.y = m->qkv;
         CHIP_TRY(launch_gemm(qkv, s));
-        CHIP_TRY(launch_rope_append(m->qkv, rows, (int)c.q_heads, geom(m), L.kv, sh.rope_cos, sh.rope_sin,
+        CHIP_TRY(launch_rope_append(m->qkv, m->qrot, rows, (int)c.q_heads, geom(m), L.kv, sh.rope_cos, sh.rope_sin,
                                     (int)c.rotary_dim, pos, nullptr, s));
         AttnJob aj;
-        aj.q = m->qkv;
-        aj.q_stride = sh.q_dim() + 2 * sh.kv_dim();
+        aj.q = m->qrot;
+        aj.q_stride = sh.q_dim();
         aj.out = m->attn;
         aj.k = L.kv.k;
         aj.v = L.kv.v;
@@ -654,7 +781,8 @@ int run_forward(cheetah_hip_model *m, const uint32_t *tokens, size_t n, size_t o
     CHIP_TRY(reserve_positions(m, n));
     if (n == 1) {
         CHIP_TRY(write_step(m, tokens[0], offset));
-        CHIP_TRY(launch_decode(m, offset));
+        if (fused_enabled(m)) CHIP_TRY(run_fused(m, 1));
+        else CHIP_TRY(launch_decode(m, offset));
     } else {
         CHIP_CHECK(hipStreamSynchronize(m->stream));  // tokens_host reuse
         std::memcpy(m->tokens_host, tokens, n * sizeof(uint32_t));
@@ -792,7 +920,9 @@ int cheetah_hip_decode_greedy(cheetah_hip_model *m, uint32_t token, size_t offse
     CHIP_TRY(validate_decode(m, token, offset, steps));
     CHIP_TRY(reserve_positions(m, steps));
     CHIP_TRY(write_step(m, token, offset));
-    for (size_t i = 0; i < steps; ++i) CHIP_TRY(launch_decode(m, offset + i));
+    if (fused_enabled(m)) CHIP_TRY(run_fused(m, steps));
+    else
+        for (size_t i = 0; i < steps; ++i) CHIP_TRY(launch_decode(m, offset + i));
     CHIP_CHECK(hipMemcpyAsync(tokens_out, m->hist_dev + offset + 1, steps * sizeof(uint32_t), hipMemcpyDeviceToHost,
                               m->stream));
     CHIP_CHECK(hipStreamSynchronize(m->stream));
@@ -811,7 +941,11 @@ int cheetah_hip_time_decode(cheetah_hip_model *m, uint32_t token, size_t offset,
     CHIP_CHECK(hipEventCreate(&e0));
     CHIP_CHECK(hipEventCreate(&e1));
     CHIP_CHECK(hipEventRecord(e0, m->stream));
-    for (size_t i = 0; i < steps; ++i) CHIP_TRY(launch_decode(m, offset + i));
+    if (fused_enabled(m)) {
+        CHIP_TRY(run_fused(m, steps));  // waits for the launch
+    } else {
+        for (size_t i = 0; i < steps; ++i) CHIP_TRY(launch_decode(m, offset + i));
+    }
     CHIP_CHECK(hipEventRecord(e1, m->stream));
     CHIP_CHECK(hipEventSynchronize(e1));
     float total = 0.f;
