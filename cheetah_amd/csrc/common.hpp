@@ -73,25 +73,48 @@ __device__ __forceinline__ uint16_t f32_bf16_rne(float f) {
     return (uint16_t)(u >> 16);
 }
 
-template <class T>
-__device__ __forceinline__ T wave_sum(T v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+// Cross-lane reductions with DPP row permutations (register-to-register,
+// no LDS round trip) inside each row of 16 lanes, then the four row results
+// read into a scalar. Steps, each exact once the previous one made its
+// sub-groups uniform: quad_perm [1,0,3,2] (lane ^ 1), quad_perm [2,3,0,1]
+// (lane ^ 2), row_half_mirror (lane 7 - i of 8: the other quad), row_mirror
+// (lane 15 - i of 16: the other half row). The result is the same in every
+// lane, with a fixed summation order.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+constexpr int kDppXor1 = 0xB1;
+constexpr int kDppXor2 = 0x4E;
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+
+__device__ __forceinline__ float lane_read(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Sum over aligned groups of `W` consecutive lanes (W a power of two <= 16).
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(W >= 1 && W <= 16 && (W & (W - 1)) == 0, "group of 1..16 lanes");
+    if constexpr (W >= 2) v += dpp_mov<kDppXor1>(v);
+    if constexpr (W >= 4) v += dpp_mov<kDppXor2>(v);
+    if constexpr (W >= 8) v += dpp_mov<kDppHalfMirror>(v);
+    if constexpr (W >= 16) v += dpp_mov<kDppMirror>(v);
     return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+    v = group_sum<16>(v);
+    return (lane_read(v, 0) + lane_read(v, 16)) + (lane_read(v, 32) + lane_read(v, 48));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
-}
-
-// Sum over aligned groups of `W` consecutive lanes (W a power of two <= 64).
-template <int W>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int off = W / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
+    v = fmaxf(v, dpp_mov<kDppXor1>(v));
+    v = fmaxf(v, dpp_mov<kDppXor2>(v));
+    v = fmaxf(v, dpp_mov<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp_mov<kDppMirror>(v));
+    return fmaxf(fmaxf(lane_read(v, 0), lane_read(v, 16)), fmaxf(lane_read(v, 32), lane_read(v, 48)));
 }
 
 }  // namespace chip

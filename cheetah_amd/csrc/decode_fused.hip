@@ -1,29 +1,46 @@
-// Persistent decode kernel: one cooperative launch runs whole decode steps
-// (embedding, every layer, LM head, greedy argmax) with device-wide barriers
-// between the dependent phases instead of kernel boundaries:
+// Persistent dataflow decode kernel: one cooperative launch (one 256-thread
+// block per CU) runs whole decode steps -- embedding, every layer, LM head,
+// greedy argmax -- with no device-wide barrier.
 //
-//   per layer  A  QKV GEMV (fused RMSNorm, bias) + RoPE + KV page append
-//              B  GQA attention over the paged cache, split over positions;
-//                 the last split to arrive for a KV head merges it
-//              C  o_proj GEMV + residual
-//              D  gate/up GEMV (fused RMSNorm) + SwiGLU
-//              E  down GEMV + residual
-//   per step   LM head GEMV (fused final RMSNorm) + per-wave argmax partials;
-//              every block then reduces the partials itself (ties to the
-//              last index, engine.rs:2247-2253) and starts the next step.
+// Per layer five phases, per step one more:
+//   A  QKV rows (fused RMSNorm, bias, RoPE); K/V rows appended to the pages
+//   B  GQA attention: one item = (KV head, run of positions), two-pass softmax
+//   C  attention partials merged in split order, o_proj + residual
+//   D  gate/up (fused RMSNorm) + SwiGLU
+//   E  down + residual
+//   H  LM head (fused final RMSNorm) + per-block argmax partials; blocks that
+//      need the next token reduce all partials themselves (ties to the last
+//      index, engine.rs:2247-2253)
+//
+// Phases are chained through the data. Every value one block hands to
+// another is a 64-bit word {f32 bits, tag}, where the tag names the phase
+// instance that produced it (launch base + step * (5L + 1) + 5 * layer +
+// phase). A consumer copies the words it needs into LDS with direct
+// global->LDS loads (16 bytes per lane, device-coherent sc1, many in flight,
+// no registers), checks the tags there, and re-loads only the 128-word
+// chunks that are still stale; aligned 8-byte stores are single-copy atomic,
+// so value and tag arrive together. A phase therefore starts as soon as its
+// own inputs exist. Producers write with device-scope relaxed atomic stores
+// (sc1), coherent across the XCDs' separate L2 caches, and so are the K/V
+// pages, which attention reads the same way into LDS. Weights are read-only
+// and use plain non-temporal loads.
+//
+// Each wave owns fixed rows of every projection and issues the loads of a
+// phase's weight rows into registers before it polls that phase's inputs,
+// so HBM streaming overlaps the wait for the producers.
+//
+// Buffer reuse needs no barrier: a block polls a phase's inputs only in a
+// phase where it also produces outputs, and every buffer is rewritten only by
+// a phase that transitively depends on all of those outputs. Only blocks
+// that own LM-head rows (and so wait for the final hidden state) write
+// argmax partials; those alternate between two buffers by step parity.
+//
+// Every poll is bounded: on timeout a block raises the abort word, which all
+// polls watch, and every wave returns; the host then resets the tagged words.
 //
 // Math per phase is that of the multi-kernel path (gemv.hip, attention.hip,
-// misc.hip), which follows the reference path in ops.rs / qwen2.rs.
-//
-// Cross-block data (hidden, q, K/V rows, attention partials and output, act,
-// argmax partials) is written and read with device-scope relaxed atomics,
-// i.e. sc1 loads and stores that stay coherent across the XCDs' separate L2
-// caches, so no barrier needs an L2 writeback or invalidate. A barrier is:
-// every thread waits for its own stores (s_waitcnt), block 0 gathers one
-// arrival word per block, then publishes a release word. Every spin is
-// bounded: on timeout the kernel raises an abort word that all spins watch,
-// and every wave exits. Weights and older KV pages are only read, so they
-// use ordinary (non-temporal) loads.
+// misc.hip), i.e. the reference path of ops.rs / qwen2.rs; only f32
+// summation orders differ.
 #include "decode_fused.hpp"
 #include "wunit.hpp"
 
@@ -32,41 +49,182 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-constexpr int TP = 64;
-constexpr long kSpinLimit = 1L << 22;
+constexpr int TP = 64;            // positions per KV page
+constexpr int kChunk = 128;       // tagged words per wave-wide 16-byte-per-lane load
+constexpr int kLdsBudget = 140 * 1024;  // dynamic LDS the layout may use
+constexpr long kSpinLimit = 1L << 20;
 
-__device__ __forceinline__ float ld1(const float *p) {
-    return __uint_as_float(__hip_atomic_load((const unsigned *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+// threadIdx.x through an opaque copy: address arithmetic stays next to its
+// use inside the step loop instead of being hoisted out of it and held in
+// registers for the whole kernel.
+__device__ __forceinline__ int tid_here() {
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
 }
-__device__ __forceinline__ void st1(float *p, float v) {
-    __hip_atomic_store((unsigned *)p, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Global wave index, recomputed where used (same reason).
+__device__ __forceinline__ int gw_here() { return (int)blockIdx.x * kWaves + (tid_here() >> 6); }
+
+__device__ __forceinline__ void stt(uint64_t *p, uint32_t bits, unsigned tag) {
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ unsigned ldu(const unsigned *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void stu(unsigned *p, unsigned v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+__device__ __forceinline__ void stf(uint64_t *p, float v, unsigned tag) { stt(p, __float_as_uint(v), tag); }
+__device__ __forceinline__ unsigned tag_of(uint64_t w) { return (unsigned)(w >> 32); }
+__device__ __forceinline__ float val_of(uint64_t w) { return __uint_as_float((uint32_t)w); }
+
 __device__ __forceinline__ void st_kv(uint16_t *p, float v) {
     __hip_atomic_store(p, f32_bf16_rne(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void st_kv(float *p, float v) { st1(p, v); }
-
-// Eight consecutive K/V elements, device-coherent loads.
-__device__ __forceinline__ void ld8(const uint16_t *p, float (&f)[8]) {
-    const unsigned long long a = __hip_atomic_load((const unsigned long long *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const unsigned long long b = __hip_atomic_load((const unsigned long long *)(p + 4), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint32_t w0 = (uint32_t)a, w1 = (uint32_t)(a >> 32), w2 = (uint32_t)b, w3 = (uint32_t)(b >> 32);
-    f[0] = bf16_lo(w0); f[1] = bf16_hi(w0); f[2] = bf16_lo(w1); f[3] = bf16_hi(w1);
-    f[4] = bf16_lo(w2); f[5] = bf16_hi(w2); f[6] = bf16_lo(w3); f[7] = bf16_hi(w3);
+__device__ __forceinline__ void st_kv(float *p, float v) {
+    __hip_atomic_store((unsigned *)p, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void ld8(const float *p, float (&f)[8]) {
-#pragma unroll
-    for (int i = 0; i < 8; i += 2) {
-        const unsigned long long a = __hip_atomic_load((const unsigned long long *)(p + i), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        f[i] = __uint_as_float((uint32_t)a);
-        f[i + 1] = __uint_as_float((uint32_t)(a >> 32));
+// The value a K/V element has once stored in the cache.
+template <class KT>
+__device__ __forceinline__ float kv_round(float v) {
+    if constexpr (sizeof(KT) == 2) return bf16_f32(f32_bf16_rne(v));
+    else return v;
+}
+
+__device__ __forceinline__ bool aborted(const int *f) {
+    return __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+}
+__device__ __forceinline__ void raise_abort(int *f) {
+    __hip_atomic_store(f, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// 16 bytes per lane from global memory straight into LDS at lds + 16 * lane
+// (lds must be the same in every lane of the wave), device-coherent (sc1).
+__device__ __forceinline__ void dma16(const void *g, void *lds) {
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)lds, 16, 0, 16);
+}
+__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Copies tagged words src[0, n) into LDS dst[0, n) and waits until each
+// carries `tag`. Wave w loads chunks w, w + 4, ... (128 words each); after
+// each round only chunks with a stale word are loaded again. Block-wide:
+// starts with a barrier (dst may still be read by the previous phase) and
+// ends with one; false in every thread on timeout or abort.
+__device__ __noinline__ bool gather_lds(uint64_t *dst, const uint64_t *src, int n, unsigned tag, int *abort_flag) {
+    const int tid = tid_here(), lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int chunks = (n + kChunk - 1) / kChunk;
+    __syncthreads();
+    uint64_t pend = 0;  // bit i: chunk wave + 4 i is stale
+    for (int c = wave, i = 0; c < chunks; c += kWaves, ++i) pend |= 1ull << i;
+    long spins = 0;
+    bool ok = true;
+    while (pend) {
+        for (int c = wave, i = 0; c < chunks; c += kWaves, ++i)
+            if ((pend >> i) & 1) {
+                const int w = c * kChunk + lane * 2;
+                if (w < n) dma16(src + w, dst + c * kChunk);
+            }
+        wait_dma();
+        uint64_t still = 0;
+        for (int c = wave, i = 0; c < chunks; c += kWaves, ++i)
+            if ((pend >> i) & 1) {
+                const int w = c * kChunk + lane * 2;
+                bool stale = w < n && tag_of(dst[w]) != tag;
+                stale |= w + 1 < n && tag_of(dst[w + 1]) != tag;
+                if (__any(stale)) still |= 1ull << i;
+            }
+        pend = still;
+        if (pend) {
+            if (++spins > kSpinLimit || ((spins & 15) == 0 && aborted(abort_flag))) {
+                raise_abort(abort_flag);
+                ok = false;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
     }
+    return __syncthreads_and(ok);
+}
+
+// xs[i] = value of tb[i] (i < n); with a gain, RMSNorm'd in place as the
+// GEMV prologue does: x * (inv * g), inv = 1 / sqrt(mean(x^2) + eps)
+// (ops.rs:646-652). Block-wide; ends with a barrier.
+__device__ void stage_lds(float *xs, const uint64_t *tb, int n, const uint16_t *gain, float eps, float *red) {
+    const int tid = tid_here(), lane = tid & 63, wave = tid >> 6;
+    float ss = 0.f;
+    for (int i = tid; i < n; i += kThreads) {
+        const float v = val_of(tb[i]);
+        xs[i] = v;
+        ss = fmaf(v, v, ss);
+    }
+    if (gain) {
+        ss = wave_sum(ss);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        float total = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) total += red[w];
+        const float inv = 1.0f / sqrtf(total / (float)n + eps);
+        for (int i = tid; i < n; i += kThreads) xs[i] = xs[i] * (inv * bf16_f32(gain[i]));
+    }
+    __syncthreads();
+}
+
+// The embedding row, RMSNorm'd (layer 0's QKV input).
+__device__ void stage_embed(float *xs, const uint16_t *row, int n, const uint16_t *gain, float eps, float *red) {
+    const int tid = tid_here(), lane = tid & 63, wave = tid >> 6;
+    float ss = 0.f;
+    for (int i = tid; i < n; i += kThreads) {
+        const float v = bf16_f32(row[i]);
+        xs[i] = v;
+        ss = fmaf(v, v, ss);
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    float total = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) total += red[w];
+    const float inv = 1.0f / sqrtf(total / (float)n + eps);
+    for (int i = tid; i < n; i += kThreads) xs[i] = xs[i] * (inv * bf16_f32(gain[i]));
+    __syncthreads();
+}
+
+// One weight row as 16-byte units, unit u in lane u % 64, slot u / 64.
+template <int N>
+__device__ __forceinline__ void load_row(u32x4 (&w)[N], const uint8_t *row, int n_units) {
+    const int lane = tid_here() & 63;
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        const int u = lane + 64 * k;
+        if (u < n_units) w[k] = __builtin_nontemporal_load((const u32x4 *)(row + (size_t)u * 16));
+    }
+}
+
+// Wave-wide dot products of R loaded rows (the first nr valid, nr uniform
+// across the wave) with xs; a unit's x values are read once for all rows.
+// Per row the summation order is fixed (unit, then element). Results land
+// in every lane.
+template <int FMT, int R, int N>
+__device__ __forceinline__ void dot_rows(const u32x4 (&w)[R][N], const float *xs, int n_units, int nr,
+                                         float (&out)[R]) {
+    using U = Unit<FMT, 16>;
+    const int lane = tid_here() & 63;
+    float acc[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) acc[i] = 0.f;
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        const int u = lane + 64 * k;
+        if (u < n_units) {
+            float xv[U::E];
+#pragma unroll
+            for (int e = 0; e < U::E; ++e) xv[e] = xs[u * U::E + e];
+#pragma unroll
+            for (int i = 0; i < R; ++i)
+                if (i < nr) {
+                    const uint32_t raw[4] = {w[i][k][0], w[i][k][1], w[i][k][2], w[i][k][3]};
+                    U::decode(raw, [&](int e, float v) { acc[i] = fmaf(v, xv[e], acc[i]); });
+                }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < R; ++i) out[i] = i < nr ? wave_sum(acc[i]) : 0.f;
 }
 
 __device__ __forceinline__ int total_key(float f) {
@@ -82,346 +240,425 @@ __device__ __forceinline__ void better(int &key, uint32_t &idx, int k2, uint32_t
 
 struct Shm {
     float red[kWaves];
-    int flag;
     int ikey[kWaves];
     uint32_t iidx[kWaves];
 };
 
-// Device-wide barrier (see the file comment). Returns false when the kernel
-// must stop (a spin timed out here or elsewhere).
-__device__ bool grid_sync(const FusedArgs &a, unsigned epoch, Shm &sm) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    const int tid = threadIdx.x;
-    if (blockIdx.x == 0) {
-        int ok = 1;
-        for (int b = tid + 1; b < (int)gridDim.x; b += kThreads) {
-            long spins = 0;
-            while (ldu(a.arrive + b) < epoch) {
-                if (++spins > kSpinLimit || ldu((const unsigned *)a.abort_flag)) {
-                    stu((unsigned *)a.abort_flag, 1u);
-                    ok = 0;
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(1);
-            }
-            if (!ok) break;
-        }
-        if (!ok) sm.flag = 0;
-        __syncthreads();
-        if (tid == 0) {
-            if (sm.flag) stu(a.go, epoch);
-            else stu(a.go, 0xFFFFFFFFu);
-        }
-    } else if (tid == 0) {
-        stu(a.arrive + blockIdx.x, epoch);
-        long spins = 0;
-        unsigned g;
-        while ((g = ldu(a.go)) < epoch) {
-            if (++spins > kSpinLimit || ldu((const unsigned *)a.abort_flag)) {
-                stu((unsigned *)a.abort_flag, 1u);
-                sm.flag = 0;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
-        if (g == 0xFFFFFFFFu) sm.flag = 0;
-    }
-    __syncthreads();
-    return sm.flag != 0;
-}
-
-// x (device-coherent source, or BF16 table row) -> LDS, optionally RMSNorm'd
-// exactly as the GEMV prologue does: x * (inv * gain).
-template <bool FROM_BF16>
-__device__ void stage(float *xs, const void *src, int n, const uint16_t *gain, float eps, Shm &sm) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    float ss = 0.f;
-    for (int i = tid; i < n; i += kThreads) {
-        const float v = FROM_BF16 ? bf16_f32(((const uint16_t *)src)[i]) : ld1((const float *)src + i);
-        xs[i] = v;
-        ss = fmaf(v, v, ss);
-    }
-    if (gain) {
-        ss = wave_sum(ss);
-        if (lane == 0) sm.red[wave] = ss;
-        __syncthreads();
-        float total = 0.f;
+// Reduces (key, idx) over the block; the result lands in every thread.
+__device__ void block_best(int &key, uint32_t &idx, Shm &sm) {
+    const int tid = tid_here(), lane = tid & 63, wave = tid >> 6;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) total += sm.red[w];
-        const float inv = 1.0f / sqrtf(total / (float)n + eps);
-        for (int i = tid; i < n; i += kThreads) xs[i] = xs[i] * (inv * bf16_f32(gain[i]));
+    for (int off = 32; off > 0; off >>= 1) {
+        const int k2 = __shfl_xor(key, off, 64);
+        const uint32_t i2 = __shfl_xor(idx, off, 64);
+        better(key, idx, k2, i2);
     }
+    if (lane == 0) {
+        sm.ikey[wave] = key;
+        sm.iidx[wave] = idx;
+    }
+    __syncthreads();
+    key = sm.ikey[0];
+    idx = sm.iidx[0];
+    for (int w = 1; w < kWaves; ++w) better(key, idx, sm.ikey[w], sm.iidx[w]);
     __syncthreads();
 }
 
-// NM row dot products against xs (wave-wide; the sums land in every lane).
-template <int FMT, int UB, int NM>
-__device__ void wave_dots(const uint8_t *const (&rp)[NM], const float *xs, int K, float (&out)[NM]) {
-    using U = Unit<FMT, UB>;
-    constexpr int E = U::E, D = U::D;
-    constexpr int UNROLL = UB == 16 ? 4 : 8;
-    const int lane = threadIdx.x & 63;
-    const int n_units = K / E;
-    float acc[NM];
-#pragma unroll
-    for (int m = 0; m < NM; ++m) acc[m] = 0.f;
-    for (int u0 = lane; u0 < n_units; u0 += 64 * UNROLL) {
-        uint32_t raw[UNROLL][NM][D];
-#pragma unroll
-        for (int i = 0; i < UNROLL; ++i) {
-            const int u = u0 + 64 * i;
-            if (u < n_units)
-#pragma unroll
-                for (int m = 0; m < NM; ++m) load_raw<UB>(rp[m] + (size_t)u * UB, raw[i][m]);
-        }
-#pragma unroll
-        for (int i = 0; i < UNROLL; ++i) {
-            const int u = u0 + 64 * i;
-            if (u < n_units) {
-                const float *xu = xs + u * E;
-#pragma unroll
-                for (int m = 0; m < NM; ++m)
-                    U::decode(raw[i][m], [&](int e, float wv) { acc[m] = fmaf(wv, xu[e], acc[m]); });
-            }
-        }
-    }
-    for (int e = n_units * E + lane; e < K; e += 64) {
-        const float xv = xs[e];
-#pragma unroll
-        for (int m = 0; m < NM; ++m) acc[m] = fmaf(U::element(rp[m], e), xv, acc[m]);
-    }
-#pragma unroll
-    for (int m = 0; m < NM; ++m) out[m] = wave_sum(acc[m]);
-}
-
-template <int HD, int G>
-struct AttnShm {
-    float p[G][TP];
-    float alpha[G];
-    float red[kWaves][G][HD];
-    float l[G];
-    float w[G][64];
-    float inv[G];
-    int last;
+// Attention work-item geometry: T threads per position (8 elements each),
+// P positions per pass, CH positions per item (one 64-position page: many
+// small items keep each block's share of the attention short).
+template <int HD, class KT>
+struct AttnGeo {
+    static constexpr int T = HD / 8;
+    static constexpr int P = kThreads / T;
+    static constexpr int ROW = HD * (int)sizeof(KT);  // bytes of one K or V row
+    static constexpr int CH = TP;
 };
 
-// One attention item: KV head g, positions [start, end) of ctx, all G heads.
-// With one split the output is written normalised; otherwise a partial and
-// the last block to arrive for this KV head merges the S partials.
+template <int HD, int G, int CH>
+struct AttnShm {
+    static constexpr int GP = (G + 3) / 4 * 4;
+    float p[CH][GP];  // scores, then weights, of position x head
+    float red[kWaves][G][HD];
+    float m[G], l[G];
+};
+
+__host__ __device__ constexpr int round_up(int x, int m) { return (x + m - 1) / m * m; }
+
+// Dynamic LDS layout (byte offsets): tagged-word staging, the f32 vector,
+// merge weights. The staging area also holds one attention item's q/K/V:
+// the group's q and new K/V words first, then its K rows and V rows.
+struct LdsLayout {
+    int qkw;    // words reserved for a group's q + new K/V
+    int tbw;    // staging words
+    int xs, total;
+};
+__host__ __device__ inline LdsLayout lds_layout(int H, int I, int nq, int hd, int G, int kv_bytes, int blocks,
+                                                int max_splits) {
+    LdsLayout o{};
+    o.qkw = round_up((G + 2) * hd, kChunk);
+    int tbw = o.qkw + 2 * TP * hd * kv_bytes / 8;
+    tbw = tbw > H ? tbw : H;
+    tbw = tbw > I ? tbw : I;
+    tbw = tbw > 2 * blocks ? tbw : 2 * blocks;
+    const int parts = max_splits * G * (hd + 2);
+    tbw = tbw > parts ? tbw : parts;
+    o.tbw = round_up(tbw + 2, kChunk);
+    int xf = H > I ? H : I;
+    xf = xf > nq * hd ? xf : nq * hd;
+    o.xs = o.tbw * 8;
+    o.total = o.xs + xf * 4;
+    return o;
+}
+
+// Loads the cached K and V rows of positions [start, lim) of KV head g into
+// LDS (row p - start of each), 64-position pages at a time.
+template <int HD, class KT>
+__device__ void load_kv_lds(uint8_t *k_lds, uint8_t *v_lds, const FusedArgs &a, const FusedLayer &ly, int g,
+                            long start, long lim) {
+    using Geo = AttnGeo<HD, KT>;
+    const int tid = tid_here(), lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    constexpr int NT = Geo::CH / TP;
+    int pages[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) pages[t] = start + t * TP < lim ? a.page_table[(start + t * TP) / TP] : 0;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const long t0 = start + t * TP;
+        if (t0 >= lim) break;
+        const int page = pages[t];
+        const int bytes = (int)(min((long)TP, lim - t0)) * Geo::ROW;
+        const size_t off = (((size_t)page * a.kv_heads + g) * TP) * Geo::ROW;
+        const uint8_t *ks = (const uint8_t *)ly.kc + off, *vs = (const uint8_t *)ly.vc + off;
+        uint8_t *kd = k_lds + (t0 - start) * Geo::ROW, *vd = v_lds + (t0 - start) * Geo::ROW;
+        for (int c = wave * 1024; c < bytes; c += kWaves * 1024) {
+            const int byte = c + lane * 16;
+            if (byte < bytes) {
+                dma16(ks + byte, kd + c);
+                dma16(vs + byte, vd + c);
+            }
+        }
+    }
+}
+
+template <class KT>
+__device__ __forceinline__ void ld8(const KT *p, float (&f)[8]) {
+    if constexpr (sizeof(KT) == 2) {
+        const u32x4 v = *(const u32x4 *)p;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f[2 * i] = bf16_lo(v[i]);
+            f[2 * i + 1] = bf16_hi(v[i]);
+        }
+    } else {
+        const f32x4 a = *(const f32x4 *)p, b = *(const f32x4 *)(p + 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f[i] = a[i];
+            f[4 + i] = b[i];
+        }
+    }
+}
+
+// Attention item (KV head g, positions [split * CH, ...)) for all G heads of
+// the group; writes (unnormalised output, max, sum) partials per q head.
+// With `late`, the cached rows are loaded only after the q gather (whose
+// tags prove every earlier position of this layer is written); otherwise
+// they were loaded into LDS beforehand.
 template <int HD, int G, class KT>
-__device__ void attn_item(const FusedArgs &a, const FusedLayer &ly, int g, int split, int S, long ctx,
-                          AttnShm<HD, G> &sh) {
-    constexpr int T = HD / 8, P = kThreads / T, JW = (G + 3) / 4;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+__device__ bool attn_item(const FusedArgs &a, const FusedLayer &ly, uint64_t *tb, int g, int split, int S, long pos,
+                          unsigned tA, unsigned tB, bool late, int qkw,
+                          AttnShm<HD, G, AttnGeo<HD, KT>::CH> &sh, uint64_t *tr) {
+    using Geo = AttnGeo<HD, KT>;
+    constexpr int T = Geo::T, P = Geo::P, CH = Geo::CH;
+    const int tid = tid_here(), lane = tid & 63, wave = tid >> 6;
     const int d8 = tid % T, pg = tid / T;
-    long chunk = (ctx + S - 1) / S;
-    chunk = (chunk + TP - 1) / TP * TP;
-    const long start = (long)split * chunk;
-    const long end = min(start + chunk, ctx);
-    const size_t part_head = (size_t)S * (HD + 2);
-    float *part = a.part + (size_t)g * G * part_head + (size_t)split * (HD + 2);
+    auto mark = [&](int ev) {
+        if (tr && tid == 0) tr[ev] = wall_clock64();
+    };
+    const long ctx = pos + 1;
+    const long start = (long)split * CH;
+    const long end = min(start + CH, ctx);
+    const int nv = (int)(end - start);
+    uint8_t *k_lds = (uint8_t *)(tb + qkw), *v_lds = k_lds + CH * Geo::ROW;
+    if (!gather_lds(tb, a.qkvn + (size_t)g * (G + 2) * HD, (G + 2) * HD, tA, a.abort_flag)) return false;
+    if (late) {
+        load_kv_lds<HD, KT>(k_lds, v_lds, a, ly, g, start, min(end, pos));
+        wait_dma();
+        __syncthreads();
+    }
+    if (end == ctx) {
+        // The new position's K and V rows, as stored in the cache.
+        for (int i = tid; i < 2 * HD; i += kThreads) {
+            const float v = val_of(tb[G * HD + i]);
+            KT *row = (KT *)((i < HD ? k_lds : v_lds) + (size_t)(nv - 1) * Geo::ROW);
+            if constexpr (sizeof(KT) == 2) row[i % HD] = f32_bf16_rne(v);
+            else row[i % HD] = v;
+        }
+        __syncthreads();
+    }
+    mark(0);
+    float qr[G][8];
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qr[j][e] = val_of(tb[j * HD + d8 * 8 + e]);
     const float scale = 1.0f / sqrtf((float)HD);
-    float m_run[JW], l_run[JW];
+    const int passes = (nv + P - 1) / P;
+#pragma unroll 2
+    for (int ps = 0; ps < passes; ++ps) {
+        const int pi = ps * P + pg;
+        const bool valid = pi < nv;
+        float dot[G];
 #pragma unroll
-    for (int i = 0; i < JW; ++i) {
-        m_run[i] = -INFINITY;
-        l_run[i] = 0.f;
-    }
-    float acc[G][8];
+        for (int j = 0; j < G; ++j) dot[j] = 0.f;
+        if (valid) {
+            float kf[8];
+            ld8<KT>((const KT *)(k_lds + (size_t)pi * Geo::ROW) + d8 * 8, kf);
 #pragma unroll
-    for (int j = 0; j < G; ++j)
+            for (int j = 0; j < G; ++j)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[j][e] = 0.f;
-    if (start < ctx) {
-        float qr[G][8];
-#pragma unroll
-        for (int j = 0; j < G; ++j)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) qr[j][e] = ld1(a.qrot + (size_t)(g * G + j) * HD + d8 * 8 + e);
-        for (long t0 = start; t0 < end; t0 += TP) {
-            const int page = a.page_table[t0 / a.page_size];
-            const size_t tile_off = (((size_t)page * a.kv_heads + g) * a.page_size + t0 % a.page_size) * HD;
-            const KT *kt = (const KT *)ly.kc + tile_off;
-            const KT *vt = (const KT *)ly.vc + tile_off;
-            float vf[TP / P][8];
-#pragma unroll
-            for (int p = 0; p < TP / P; ++p)
-                if (t0 + p * P + pg < end) ld8(vt + (size_t)(p * P + pg) * HD + d8 * 8, vf[p]);
-#pragma unroll
-            for (int p = 0; p < TP / P; ++p) {
-                const int pi = p * P + pg;
-                const bool valid = t0 + pi < end;
-                float dot[G];
-#pragma unroll
-                for (int j = 0; j < G; ++j) dot[j] = 0.f;
-                if (valid) {
-                    float kf[8];
-                    ld8(kt + (size_t)pi * HD + d8 * 8, kf);
-#pragma unroll
-                    for (int j = 0; j < G; ++j)
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) dot[j] = fmaf(kf[e], qr[j][e], dot[j]);
-                }
-#pragma unroll
-                for (int j = 0; j < G; ++j) {
-                    const float sum = group_sum<T>(dot[j]);
-                    if (d8 == 0) sh.p[j][pi] = valid ? sum * scale : -INFINITY;
-                }
-            }
-            __syncthreads();
-#pragma unroll
-            for (int i = 0; i < JW; ++i) {
-                const int j = wave + 4 * i;
-                if (j < G) {
-                    const float sc = sh.p[j][lane];
-                    const float m_new = fmaxf(m_run[i], wave_max(sc));
-                    const float pv = sc == -INFINITY ? 0.f : expf(sc - m_new);
-                    sh.p[j][lane] = pv;
-                    const float l_tile = wave_sum(pv);
-                    const float alpha = m_run[i] == -INFINITY ? 0.f : expf(m_run[i] - m_new);
-                    l_run[i] = l_run[i] * alpha + l_tile;
-                    m_run[i] = m_new;
-                    if (lane == 0) sh.alpha[j] = alpha;
-                }
-            }
-            __syncthreads();
-#pragma unroll
-            for (int j = 0; j < G; ++j) {
-                const float al = sh.alpha[j];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[j][e] *= al;
-            }
-#pragma unroll
-            for (int p = 0; p < TP / P; ++p) {
-                const int pi = p * P + pg;
-                if (t0 + pi < end) {
-#pragma unroll
-                    for (int j = 0; j < G; ++j) {
-                        const float pj = sh.p[j][pi];
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) acc[j][e] = fmaf(pj, vf[p][e], acc[j][e]);
-                    }
-                }
-            }
-            __syncthreads();
+                for (int e = 0; e < 8; ++e) dot[j] = fmaf(kf[e], qr[j][e], dot[j]);
         }
-    }
 #pragma unroll
-    for (int j = 0; j < G; ++j)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            float v = acc[j][e];
-#pragma unroll
-            for (int off = T; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
-            acc[j][e] = v;
-        }
-    if (lane < T) {
-#pragma unroll
-        for (int j = 0; j < G; ++j)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) sh.red[wave][j][d8 * 8 + e] = acc[j][e];
-    }
-#pragma unroll
-    for (int i = 0; i < JW; ++i) {
-        const int j = wave + 4 * i;
-        if (j < G && lane == 0) {
-            sh.l[j] = l_run[i];
-            if (S > 1) {
-                st1(part + j * part_head + HD, m_run[i]);
-                st1(part + j * part_head + HD + 1, l_run[i]);
-            }
+        for (int j = 0; j < G; ++j) {
+            const float s = group_sum<T>(dot[j]);
+            if (d8 == 0 && valid) sh.p[pi][j] = s * scale;
         }
     }
     __syncthreads();
+    mark(1);
+    for (int j = wave; j < G; j += kWaves) {
+        float mx = -INFINITY;
+        for (int c = lane; c < nv; c += 64) mx = fmaxf(mx, sh.p[c][j]);
+        mx = wave_max(mx);
+        float sum = 0.f;
+        for (int c = lane; c < nv; c += 64) {
+            const float pv = expf(sh.p[c][j] - mx);
+            sh.p[c][j] = pv;
+            sum += pv;
+        }
+        sum = wave_sum(sum);
+        if (lane == 0) {
+            sh.m[j] = mx;
+            sh.l[j] = sum;
+        }
+    }
+    __syncthreads();
+    mark(2);
+    // Weighted V: lane owns DPL head dimensions, wave w positions w, w + 4,
+    // ...; the four waves' sums are added in wave order.
+    constexpr int DPL = HD / 64;
+    float acc[G][DPL];
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) acc[j][e] = 0.f;
+#pragma unroll 4
+    for (int pi = wave; pi < nv; pi += kWaves) {
+        const KT *vrow = (const KT *)(v_lds + (size_t)pi * Geo::ROW) + lane * DPL;
+        float vf[DPL];
+        if constexpr (sizeof(KT) == 2) {
+            if constexpr (DPL == 1) {
+                vf[0] = bf16_f32(*vrow);
+            } else {
+                const uint32_t w2 = *(const uint32_t *)vrow;
+                vf[0] = bf16_lo(w2);
+                vf[1] = bf16_hi(w2);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < DPL; ++e) vf[e] = vrow[e];
+        }
+        float pj[AttnShm<HD, G, CH>::GP];
+#pragma unroll
+        for (int j4 = 0; j4 < AttnShm<HD, G, CH>::GP; j4 += 4) {
+            const f32x4 q4 = *(const f32x4 *)&sh.p[pi][j4];
+            pj[j4] = q4[0];
+            pj[j4 + 1] = q4[1];
+            pj[j4 + 2] = q4[2];
+            pj[j4 + 3] = q4[3];
+        }
+#pragma unroll
+        for (int j = 0; j < G; ++j)
+#pragma unroll
+            for (int e = 0; e < DPL; ++e) acc[j][e] = fmaf(pj[j], vf[e], acc[j][e]);
+    }
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) sh.red[wave][j][lane * DPL + e] = acc[j][e];
+    __syncthreads();
+    mark(3);
+    // Partials of group g, split-major: [split][head of group][HD + 2].
+    uint64_t *gpart = a.part + (size_t)g * a.max_splits * G * (HD + 2);
+    uint64_t *part = gpart + (size_t)split * G * (HD + 2);
     for (int t = tid; t < G * HD; t += kThreads) {
         const int j = t / HD, d = t % HD;
         const float o = sh.red[0][j][d] + sh.red[1][j][d] + sh.red[2][j][d] + sh.red[3][j][d];
-        if (S == 1) st1(a.attn + (size_t)(g * G + j) * HD + d, o / sh.l[j]);
-        else st1(part + j * part_head + d, o);
+        stf(part + (size_t)j * (HD + 2) + d, o, tB);
     }
-    if (S == 1) return;
-    // Count this split in; the last one merges (split order, deterministic).
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned old = __hip_atomic_fetch_add(a.attn_count + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        sh.last = old == (unsigned)(S - 1);
-        if (sh.last) stu(a.attn_count + g, 0u);
+    if (tid < G) {
+        stf(part + (size_t)tid * (HD + 2) + HD, sh.m[tid], tB);
+        stf(part + (size_t)tid * (HD + 2) + HD + 1, sh.l[tid], tB);
     }
-    __syncthreads();
-    if (!sh.last) return;
-    const float *pg0 = a.part + (size_t)g * G * part_head;
-#pragma unroll
-    for (int i = 0; i < JW; ++i) {
-        const int j = wave + 4 * i;
-        if (j < G) {
-            const float *pj = pg0 + (size_t)j * part_head;
-            const float m = lane < S ? ld1(pj + (size_t)lane * (HD + 2) + HD) : -INFINITY;
-            const float M = wave_max(m);
-            const float w = m == -INFINITY ? 0.f : expf(m - M);
-            const float l = w != 0.f ? ld1(pj + (size_t)lane * (HD + 2) + HD + 1) : 0.f;
-            const float L = wave_sum(w * l);
-            if (lane < S) sh.w[j][lane] = w;
-            if (lane == 0) sh.inv[j] = 1.0f / L;
+    if (split != 0) return true;
+    // The split-0 item merges the group's S partials in split order
+    // (weights exp(m_s - M), sum L = sum_s w_s l_s) and publishes the
+    // group's attention output.
+    if (!gather_lds(tb, gpart, S * G * (HD + 2), tB, a.abort_flag)) return false;
+    if (tid < G) {
+        float M = -INFINITY;
+        for (int s = 0; s < S; ++s) M = fmaxf(M, val_of(tb[((size_t)s * G + tid) * (HD + 2) + HD]));
+        float L = 0.f;
+        for (int s = 0; s < S; ++s) {
+            const uint64_t *ps = tb + ((size_t)s * G + tid) * (HD + 2);
+            const float w = expf(val_of(ps[HD]) - M);
+            sh.p[s][tid] = w;
+            L = fmaf(w, val_of(ps[HD + 1]), L);
         }
+        sh.l[tid] = 1.0f / L;
     }
     __syncthreads();
     for (int t = tid; t < G * HD; t += kThreads) {
         const int j = t / HD, d = t % HD;
-        const float *pj = pg0 + (size_t)j * part_head;
         float o = 0.f;
-        for (int s = 0; s < S; ++s) {
-            const float w = sh.w[j][s];
-            if (w != 0.f) o = fmaf(w, ld1(pj + (size_t)s * (HD + 2) + d), o);
-        }
-        st1(a.attn + (size_t)(g * G + j) * HD + d, o * sh.inv[j]);
+        for (int s = 0; s < S; ++s) o = fmaf(sh.p[s][j], val_of(tb[((size_t)s * G + j) * (HD + 2) + d]), o);
+        stf(a.attn + (size_t)(g * G + j) * HD + d, o * sh.l[j], tB);
     }
+    return true;
 }
 
-template <int FMT, int UB, int HD, int G, class KT>
-__global__ __launch_bounds__(kThreads) void decode_fused_kernel(FusedArgs a) {
-    extern __shared__ float xs[];
+// UH/UQ/UI: 16-byte units per lane of a row with H / q_heads*HD / I
+// columns; RGU: gate/up rows per wave; UHB: units per lane of a BF16 head row.
+template <int FMT, int HD, int G, class KT, int UH, int UQ, int UI, int RGU, int UHB>
+__global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs a) {
+    using Geo = AttnGeo<HD, KT>;
+    using U = Unit<FMT, 16>;
+    constexpr int HB = 4;  // head rows per batch
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ Shm sm;
-    __shared__ AttnShm<HD, G> ash;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int NB = gridDim.x, W = NB * kWaves;
-    const int gw = blockIdx.x * kWaves + wave;
-    const int H = a.H, qd = a.q_heads * HD, kvd = a.kv_heads * HD;
+    __shared__ AttnShm<HD, G, Geo::CH> ash;
+    const int tid = tid_here(), lane = tid & 63, wave = tid >> 6;
+    const int NB = gridDim.x, W = NB * kWaves, b = blockIdx.x;
+    const int gw0 = b * kWaves + wave;
+    const int H = a.H, I = a.I, V = a.V;
+    const int qd = a.q_heads * HD, kvd = a.kv_heads * HD;
+    const int nH = H / U::E, nQ = qd / U::E, nI = I / U::E, nHB = H / 8;
+    const int npairs = (qd + 2 * kvd) / 2;
     const int half = a.rotary / 2;
-    if (tid == 0) sm.flag = 1;
-    __syncthreads();
-    unsigned epoch = ldu(a.epoch_base);
+    const LdsLayout lay = lds_layout(H, I, a.q_heads, HD, G, (int)sizeof(KT), NB, a.max_splits);
+    uint64_t *tb = (uint64_t *)lds;
+    float *xs = (float *)(lds + lay.xs);
+
+    const bool hasA = b * kWaves < npairs, myA = gw0 < npairs;
+    const bool hasH = b * kWaves < H, myH = gw0 < H;
+    const bool hasD = b * kWaves < I;
+    const int head_rows = gw0 < V ? (V - 1 - gw0) / W + 1 : 0;
+    const bool hasHead = b * kWaves < V;
+    // Blocks that own head rows write argmax partials. Blocks without would
+    // have nothing pacing them and could overwrite a step's partials before
+    // they are read, so they write none.
+    const int head_blocks = min(NB, (V + kWaves - 1) / kWaves);
+    const size_t head_stride = (size_t)H * 2;
+
     int token = __hip_atomic_load(a.step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     long pos = __hip_atomic_load(a.step + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    float h_own = 0.f;
 
-    for (int step = 0; step < a.steps; ++step, ++pos) {
+    u32x4 wA[2][UH], wC[1][UQ], wD[2 * RGU][UH], wE[1][UI];
+
+    const int PH = fused_phases_per_step(a.L);
+    // A block is paced when it waited on the previous step's last layer (or
+    // this is the launch's first step): only then are the cached K/V rows of
+    // every earlier position written when it starts a step. Blocks with no
+    // role in the previous step may run ahead and must not prefetch them.
+    const bool always_paced = hasA || hasH || hasD || hasHead;
+    bool item_prev = false;
+    for (int s = 0; s < a.steps; ++s, ++pos) {
+        // Optional per-phase timestamps of one step (thread 0 of each block).
+        const bool traced = a.trace && s == a.trace_step;
+        auto mark = [&](int ev) {
+            if (traced && tid == 0) a.trace[(size_t)b * (16 * a.L + 3) + ev] = wall_clock64();
+        };
+        const unsigned tb0 = a.tag0 + (unsigned)(s * PH);
         const long ctx = pos + 1;
-        const int S = (int)max(1L, min((ctx + TP - 1) / TP, (long)a.max_splits));
+        const int S = (int)((ctx + Geo::CH - 1) / Geo::CH);
+        const int it = NB - 1 - b;
+        const bool hasB = it < a.kv_heads * S;
+        const int ig = hasB ? it / S : 0, isplit = hasB ? it % S : 0;
+        const bool paced = s == 0 || always_paced || item_prev;
+        item_prev = hasB;
         const float *cr = a.rope_cos + (size_t)pos * half;
         const float *sr = a.rope_sin + (size_t)pos * half;
-        const int page = a.page_table[pos / a.page_size];
-        const int slot = (int)(pos % a.page_size);
+        const int page = a.page_table[pos / TP];
+        const int slot = (int)(pos % TP);
         const uint16_t *emb = a.embed + (size_t)token * H;
+
         for (int l = 0; l < a.L; ++l) {
-            const FusedLayer &ly = a.layers[l];
-            // ---- A: QKV (pair-permuted rows) + RoPE + KV append.
-            if (l == 0) stage<true>(xs, emb, H, ly.ln1, a.eps, sm);
-            else stage<false>(xs, a.hidden, H, ly.ln1, a.eps, sm);
-            const int pairs = (qd + 2 * kvd) / 2;
-            for (int j = gw; j < pairs; j += W) {
-                const int r0 = 2 * j;
-                const uint8_t *rp[2] = {ly.qkv + (size_t)r0 * a.qkv_stride, ly.qkv + (size_t)(r0 + 1) * a.qkv_stride};
+            // By value: a reference would be re-read from memory after every
+            // store (the stores might alias the table).
+            const FusedLayer ly = a.layers[l];
+            const int gw = gw_here();
+            const unsigned tA = tb0 + 5 * l, tB = tA + 1, tC = tA + 2, tD = tA + 3, tE = tA + 4;
+            const long kv_start = (long)isplit * Geo::CH, kv_lim = min(kv_start + Geo::CH, pos);
+            // Weight rows of the o, gate/up and down phases go out right after
+            // the QKV phase (attention blocks: gate/up before attention, the
+            // rest after it), so they stream while attention runs.
+            auto load_wD = [&]() {
+#pragma unroll
+                for (int k = 0; k < RGU; ++k) {
+                    const int r = gw + W * k;
+                    if (r < I) {
+                        load_row(wD[2 * k], ly.gate + (size_t)r * a.gu_stride, nH);
+                        load_row(wD[2 * k + 1], ly.up + (size_t)r * a.gu_stride, nH);
+                    }
+                }
+            };
+            auto load_wCE = [&]() {
+                if (myH) {
+                    load_row(wC[0], ly.o + (size_t)gw * a.o_stride, nQ);
+                    load_row(wE[0], ly.down + (size_t)gw * a.down_stride, nI);
+                }
+            };
+            mark(16 * l);
+
+            // ---- A: QKV pairs + RoPE + K/V append. Attention blocks without
+            // QKV rows start loading their cached K/V rows now.
+            const bool kv_early = hasB && !hasA && (l > 0 || paced);
+            if (kv_early) {
+                uint8_t *k_lds = (uint8_t *)(tb + lay.qkw);
+                load_kv_lds<HD, KT>(k_lds, k_lds + Geo::CH * Geo::ROW, a, ly, ig, kv_start, kv_lim);
+            }
+            if (hasB) load_wD();
+            if (myA) {
+                load_row(wA[0], ly.qkv + (size_t)(2 * gw) * a.qkv_stride, nH);
+                load_row(wA[1], ly.qkv + (size_t)(2 * gw + 1) * a.qkv_stride, nH);
+            }
+            if (hasA) {
+                if (l == 0) {
+                    stage_embed(xs, emb, H, ly.ln1, a.eps, sm.red);
+                } else {
+                    if (!gather_lds(tb, a.hid1, H, tA - 1, a.abort_flag)) return;
+                    stage_lds(xs, tb, H, ly.ln1, a.eps, sm.red);
+                }
+            }
+            mark(16 * l + 1);
+            if (myA) {
+                const int r0 = 2 * gw;
                 float y[2];
-                wave_dots<FMT, UB, 2>(rp, xs, H, y);
+                dot_rows<FMT>(wA, xs, nH, 2, y);
+                float v0 = y[0], v1 = y[1];
                 if (lane == 0) {
-                    float v0 = y[0], v1 = y[1];
                     if (ly.qkv_sc) {
                         v0 = v0 * ly.qkv_sc[r0];
                         v1 = v1 * ly.qkv_sc[r0 + 1];
                     }
-                    v0 = v0 + ly.qkv_bias[r0];
-                    v1 = v1 + ly.qkv_bias[r0 + 1];
+                    if (ly.qkv_bias) {
+                        v0 = v0 + ly.qkv_bias[r0];
+                        v1 = v1 + ly.qkv_bias[r0 + 1];
+                    }
                     if (r0 < qd + kvd) {
                         const bool is_q = r0 < qd;
                         const int base = is_q ? r0 : r0 - qd;
@@ -429,159 +666,246 @@ __global__ __launch_bounds__(kThreads) void decode_fused_kernel(FusedArgs a) {
                         int o0 = d0, o1 = d0 + 1;
                         if (d0 < a.rotary) {
                             const int i = d0 / 2;
-                            const float c = cr[i], s = sr[i];
-                            const float x1 = v0 * c - v1 * s, x2 = v1 * c + v0 * s;
+                            const float c = cr[i], sn = sr[i];
+                            const float x1 = v0 * c - v1 * sn, x2 = v1 * c + v0 * sn;
                             v0 = x1;
                             v1 = x2;
                             o0 = i;
                             o1 = half + i;
                         }
                         if (is_q) {
-                            st1(a.qrot + h * HD + o0, v0);
-                            st1(a.qrot + h * HD + o1, v1);
+                            uint64_t *q = a.qkvn + (size_t)(h / G) * (G + 2) * HD + (h % G) * HD;
+                            stf(q + o0, v0, tA);
+                            stf(q + o1, v1, tA);
                         } else {
-                            KT *kc = (KT *)ly.kc + (((size_t)page * a.kv_heads + h) * a.page_size + slot) * HD;
+                            KT *kc = (KT *)ly.kc + (((size_t)page * a.kv_heads + h) * TP + slot) * HD;
                             st_kv(kc + o0, v0);
                             st_kv(kc + o1, v1);
+                            uint64_t *kn = a.qkvn + (size_t)h * (G + 2) * HD + G * HD;
+                            stf(kn + o0, kv_round<KT>(v0), tA);
+                            stf(kn + o1, kv_round<KT>(v1), tA);
                         }
                     } else {
                         const int base = r0 - qd - kvd;
                         const int h = base / HD, d0 = base % HD;
-                        KT *vc = (KT *)ly.vc + (((size_t)page * a.kv_heads + h) * a.page_size + slot) * HD;
+                        KT *vc = (KT *)ly.vc + (((size_t)page * a.kv_heads + h) * TP + slot) * HD;
                         st_kv(vc + d0, v0);
                         st_kv(vc + d0 + 1, v1);
+                        uint64_t *vn = a.qkvn + (size_t)h * (G + 2) * HD + (G + 1) * HD;
+                        stf(vn + d0, kv_round<KT>(v0), tA);
+                        stf(vn + d0 + 1, kv_round<KT>(v1), tA);
                     }
                 }
             }
-            if (!grid_sync(a, ++epoch, sm)) return;
-            // ---- B: attention.
-            const int items = a.kv_heads * S;
-            for (int it = blockIdx.x; it < items; it += NB) attn_item<HD, G, KT>(a, ly, it / S, it % S, S, ctx, ash);
-            if (!grid_sync(a, ++epoch, sm)) return;
-            // ---- C: o_proj + residual.
-            stage<false>(xs, a.attn, qd, nullptr, 0.f, sm);
-            for (int r = gw; r < H; r += W) {
-                const uint8_t *rp[1] = {ly.o + (size_t)r * a.o_stride};
-                float y[1];
-                wave_dots<FMT, UB, 1>(rp, xs, qd, y);
-                if (lane == 0) {
-                    float v = y[0];
-                    if (ly.o_sc) v = v * ly.o_sc[r];
-                    if (ly.o_bias) v = v + ly.o_bias[r];
-                    const float old = l == 0 ? bf16_f32(emb[r]) : ld1(a.hidden + r);
-                    st1(a.hidden + r, old + v);
-                }
+            mark(16 * l + 2);
+            if (!hasB) {
+                load_wCE();
+                load_wD();
             }
-            if (!grid_sync(a, ++epoch, sm)) return;
+
+            // ---- B: attention item.
+            if (hasB) {
+                if (hasA) {
+                    uint8_t *k_lds = (uint8_t *)(tb + lay.qkw);
+                    load_kv_lds<HD, KT>(k_lds, k_lds + Geo::CH * Geo::ROW, a, ly, ig, kv_start, kv_lim);
+                }
+                uint64_t *tr = traced ? a.trace + (size_t)b * (16 * a.L + 3) + 16 * l + 3 : nullptr;
+                if (!attn_item<HD, G, KT>(a, ly, tb, ig, isplit, S, pos, tA, tB, !hasA && !kv_early, lay.qkw, ash, tr))
+                    return;
+                load_wCE();
+            }
+            mark(16 * l + 7);
+
+            // ---- C: merge + o_proj + residual.
+            if (hasH) {
+                if (!gather_lds(tb, a.attn, qd, tB, a.abort_flag)) return;
+                stage_lds(xs, tb, qd, nullptr, 0.f, sm.red);
+            }
+            mark(16 * l + 8);
+            if (myH) {
+                float y[1];
+                dot_rows<FMT>(wC, xs, nQ, 1, y);
+                float v = y[0];
+                if (ly.o_sc) v = v * ly.o_sc[gw];
+                if (ly.o_bias) v = v + ly.o_bias[gw];
+                const float old = l == 0 ? bf16_f32(emb[gw]) : h_own;
+                h_own = old + v;
+                if (lane == 0) stf(a.hid0 + gw, h_own, tC);
+            }
+            mark(16 * l + 9);
+
             // ---- D: gate/up + SwiGLU.
-            stage<false>(xs, a.hidden, H, ly.ln2, a.eps, sm);
-            for (int r = gw; r < a.I; r += W) {
-                const uint8_t *rp[2] = {ly.gate + (size_t)r * a.gu_stride, ly.up + (size_t)r * a.gu_stride};
-                float y[2];
-                wave_dots<FMT, UB, 2>(rp, xs, H, y);
-                if (lane == 0) {
-                    float g = y[0], u = y[1];
-                    if (ly.gate_sc) {
-                        g = g * ly.gate_sc[r];
-                        u = u * ly.up_sc[r];
+            if (hasD) {
+                if (!gather_lds(tb, a.hid0, H, tC, a.abort_flag)) return;
+                stage_lds(xs, tb, H, ly.ln2, a.eps, sm.red);
+            }
+            mark(16 * l + 10);
+            {
+                int nr = 0;
+#pragma unroll
+                for (int k = 0; k < RGU; ++k) nr += gw + W * k < I ? 2 : 0;
+                float y[2 * RGU];
+                dot_rows<FMT>(wD, xs, nH, nr, y);
+#pragma unroll
+                for (int k = 0; k < RGU; ++k) {
+                    const int r = gw + W * k;
+                    if (r < I) {
+                        float gv = y[2 * k], uv = y[2 * k + 1];
+                        if (ly.gate_sc) {
+                            gv = gv * ly.gate_sc[r];
+                            uv = uv * ly.up_sc[r];
+                        }
+                        if (lane == 0) stf(a.act + r, gv * (uv / (1.0f + expf(-gv))), tD);
                     }
-                    st1(a.act + r, g * (u / (1.0f + expf(-g))));
                 }
             }
-            if (!grid_sync(a, ++epoch, sm)) return;
+            mark(16 * l + 11);
+
             // ---- E: down + residual.
-            stage<false>(xs, a.act, a.I, nullptr, 0.f, sm);
-            for (int r = gw; r < H; r += W) {
-                const uint8_t *rp[1] = {ly.down + (size_t)r * a.down_stride};
-                float y[1];
-                wave_dots<FMT, UB, 1>(rp, xs, a.I, y);
-                if (lane == 0) {
-                    float v = y[0];
-                    if (ly.down_sc) v = v * ly.down_sc[r];
-                    st1(a.hidden + r, ld1(a.hidden + r) + v);
-                }
+            if (hasH) {
+                if (!gather_lds(tb, a.act, I, tD, a.abort_flag)) return;
+                stage_lds(xs, tb, I, nullptr, 0.f, sm.red);
             }
-            if (!grid_sync(a, ++epoch, sm)) return;
+            mark(16 * l + 12);
+            if (myH) {
+                float y[1];
+                dot_rows<FMT>(wE, xs, nI, 1, y);
+                float v = y[0];
+                if (ly.down_sc) v = v * ly.down_sc[gw];
+                h_own = h_own + v;
+                if (lane == 0) stf(a.hid1 + gw, h_own, tE);
+            }
+            mark(16 * l + 13);
         }
+
         // ---- LM head (BF16, final norm fused) + argmax partials.
-        stage<false>(xs, a.hidden, H, a.final_norm, a.eps, sm);
+        const unsigned tH = tb0 + 5 * a.L;
         int key = INT_MIN;
         uint32_t idx = 0;
-        const size_t head_stride = (size_t)H * 2;
-        for (int r = gw; r < a.V; r += W) {
-            const uint8_t *rp[1] = {(const uint8_t *)a.head + (size_t)r * head_stride};
-            float y[1];
-            wave_dots<FMT_BF16, 16, 1>(rp, xs, H, y);
-            if (lane == 0) {
-                a.logits[r] = y[0];
-                better(key, idx, total_key(y[0]), (uint32_t)r);
+        if (hasHead) {
+            const int gw = gw_here();
+            u32x4 hb[2][HB][UHB];
+            const int nbat = (head_rows + HB - 1) / HB;
+            auto issue = [&](u32x4 (&buf)[HB][UHB], int bi) {
+#pragma unroll
+                for (int k = 0; k < HB; ++k) {
+                    const int i = bi * HB + k;
+                    if (i < head_rows) load_row(buf[k], (const uint8_t *)a.head + (size_t)(gw + W * i) * head_stride, nHB);
+                }
+            };
+            auto consume = [&](const u32x4 (&buf)[HB][UHB], int bi) {
+                const int nr = min(HB, head_rows - bi * HB);
+                float y[HB];
+                dot_rows<FMT_BF16>(buf, xs, nHB, nr, y);
+#pragma unroll
+                for (int k = 0; k < HB; ++k)
+                    if (k < nr) {
+                        const uint32_t r = (uint32_t)(gw + W * (bi * HB + k));
+                        if (lane == 0) a.logits[r] = y[k];
+                        better(key, idx, total_key(y[k]), r);
+                    }
+            };
+            issue(hb[0], 0);
+            if (!gather_lds(tb, a.hid1, H, tH - 1, a.abort_flag)) return;
+            stage_lds(xs, tb, H, a.final_norm, a.eps, sm.red);
+            mark(16 * a.L);
+            for (int bi = 0; bi < nbat; bi += 2) {
+                if (bi + 1 < nbat) issue(hb[1], bi + 1);
+                consume(hb[0], bi);
+                if (bi + 2 < nbat) issue(hb[0], bi + 2);
+                if (bi + 1 < nbat) consume(hb[1], bi + 1);
             }
         }
-        if (lane == 0) {
-            stu((unsigned *)a.am_key + gw, (unsigned)key);
-            stu(a.am_idx + gw, idx);
+        block_best(key, idx, sm);
+        mark(16 * a.L + 1);
+        uint64_t *am = a.am + (size_t)(s & 1) * NB * 2;
+        if (hasHead && tid == 0) {
+            stt(am + 2 * b, (uint32_t)key, tH);
+            stt(am + 2 * b + 1, idx, tH);
         }
-        if (!grid_sync(a, ++epoch, sm)) return;
-        // Every block reduces the W partials itself.
-        key = INT_MIN;
-        idx = 0;
-        for (int w = tid; w < W; w += kThreads) better(key, idx, (int)ldu((const unsigned *)a.am_key + w), ldu(a.am_idx + w));
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            const int k2 = __shfl_xor(key, off, 64);
-            const uint32_t i2 = __shfl_xor(idx, off, 64);
-            better(key, idx, k2, i2);
+        // Blocks that use the token (embedding row, residual) reduce the
+        // partials of every head block.
+        if (hasA || hasH) {
+            if (!gather_lds(tb, am, 2 * head_blocks, tH, a.abort_flag)) return;
+            key = INT_MIN;
+            idx = 0;
+            for (int i = tid; i < head_blocks; i += kThreads)
+                better(key, idx, (int)(uint32_t)tb[2 * i], (uint32_t)tb[2 * i + 1]);
+            block_best(key, idx, sm);
+            token = (int)idx;
+            if (b == 0 && tid == 0) {
+                if (pos + 1 < a.hist_cap)
+                    __hip_atomic_store(a.hist + pos + 1, idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store((uint32_t *)a.step, idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(a.step + 1, (int32_t)(pos + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
         }
-        if (lane == 0) {
-            sm.ikey[wave] = key;
-            sm.iidx[wave] = idx;
-        }
-        __syncthreads();
-        key = sm.ikey[0];
-        idx = sm.iidx[0];
-        for (int w = 1; w < kWaves; ++w) better(key, idx, sm.ikey[w], sm.iidx[w]);
-        token = (int)idx;
-        if (blockIdx.x == 0 && tid == 0) {
-            if (pos + 1 < a.hist_cap) stu(a.hist + pos + 1, idx);
-            stu((unsigned *)a.step, idx);
-            stu((unsigned *)a.step + 1, (unsigned)(pos + 1));
-        }
-        __syncthreads();
+        mark(16 * a.L + 2);
     }
-    if (blockIdx.x == 0 && tid == 0) stu(a.epoch_base, epoch);
 }
 
-template <int FMT, int UB, int HD, int G>
-int launch_kt(const FusedArgs &a, int nb, size_t lds, bool kv_f32, hipStream_t s) {
-    void *args[] = {(void *)&a};
-    if (kv_f32) {
-        auto k = decode_fused_kernel<FMT, UB, HD, G, float>;
-        CHIP_CHECK(hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        CHIP_CHECK(hipLaunchCooperativeKernel((const void *)k, dim3(nb), dim3(kThreads), args, (unsigned)lds, s));
-    } else {
-        auto k = decode_fused_kernel<FMT, UB, HD, G, uint16_t>;
-        CHIP_CHECK(hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        CHIP_CHECK(hipLaunchCooperativeKernel((const void *)k, dim3(nb), dim3(kThreads), args, (unsigned)lds, s));
+struct Variant {
+    int fmt, hd, g, uh, uq, ui, rgu, uhb;
+};
+
+// Shapes with a built kernel: Qwen2-0.5B (hidden 896, 14/2 heads of 64,
+// intermediate 4864) and the two small test shapes.
+constexpr Variant kVariants[] = {
+    {FMT_BF16, 64, 7, 2, 2, 10, 5, 2},
+    {FMT_BF16, 64, 2, 1, 1, 1, 1, 1},
+    {FMT_BF16, 128, 4, 1, 2, 2, 1, 1},
+};
+
+int units_per_lane(int cols, int elems_per_unit) { return (cols / elems_per_unit + 63) / 64; }
+
+const Variant *find_variant(int fmt, int H, int q_heads, int kv_heads, int hd, int I, int blocks) {
+    if (kv_heads <= 0 || q_heads % kv_heads) return nullptr;
+    const int g = q_heads / kv_heads, E = fmt == FMT_Q8 ? 16 : 8, W = blocks * kWaves;
+    const int qd = q_heads * hd, kvd = kv_heads * hd;
+    if (H % 8 || qd % E || H % E || I % E) return nullptr;
+    if ((qd + 2 * kvd) / 2 > W || H > W) return nullptr;
+    for (const Variant &v : kVariants) {
+        if (v.fmt != fmt || v.hd != hd || v.g != g) continue;
+        if (units_per_lane(H, E) > v.uh || units_per_lane(qd, E) > v.uq || units_per_lane(I, E) > v.ui) continue;
+        if ((I + W - 1) / W > v.rgu || units_per_lane(H, 8) > v.uhb) continue;
+        return &v;
     }
+    return nullptr;
+}
+
+template <int FMT, int HD, int G, class KT, int UH, int UQ, int UI, int RGU, int UHB>
+int launch_one(const FusedArgs &a, int nb, hipStream_t s) {
+    auto k = decode_flow_kernel<FMT, HD, G, KT, UH, UQ, UI, RGU, UHB>;
+    const size_t lds = (size_t)lds_layout(a.H, a.I, a.q_heads, HD, G, (int)sizeof(KT), nb, a.max_splits).total;
+    hipFuncAttributes attr{};
+    CHIP_CHECK(hipFuncGetAttributes(&attr, (const void *)k));
+    if (attr.sharedSizeBytes + lds > device_max_lds())
+        return fail("HIP backend: persistent decode needs more LDS than a block has.");
+    void *args[] = {(void *)&a};
+    CHIP_CHECK(hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    CHIP_CHECK(hipLaunchCooperativeKernel((const void *)k, dim3(nb), dim3(kThreads), args, (unsigned)lds, s));
     return 0;
 }
 
-template <int FMT, int UB>
-int launch_fmt(const FusedArgs &a, int nb, size_t lds, int hd, int g, bool kv_f32, hipStream_t s) {
-    if (hd == 64 && g == 2) return launch_kt<FMT, UB, 64, 2>(a, nb, lds, kv_f32, s);
-    if (hd == 64 && g == 7) return launch_kt<FMT, UB, 64, 7>(a, nb, lds, kv_f32, s);
-    if (hd == 128 && g == 4) return launch_kt<FMT, UB, 128, 4>(a, nb, lds, kv_f32, s);
-    if (hd == 128 && g == 7) return launch_kt<FMT, UB, 128, 7>(a, nb, lds, kv_f32, s);
-    return fail("HIP backend: no persistent decode kernel for this head shape.");
+template <class KT>
+int launch_kt(const Variant &v, const FusedArgs &a, int nb, hipStream_t s) {
+    if (v.hd == 64 && v.g == 7) return launch_one<FMT_BF16, 64, 7, KT, 2, 2, 10, 5, 2>(a, nb, s);
+    if (v.hd == 64 && v.g == 2) return launch_one<FMT_BF16, 64, 2, KT, 1, 1, 1, 1, 1>(a, nb, s);
+    if (v.hd == 128 && v.g == 4) return launch_one<FMT_BF16, 128, 4, KT, 1, 2, 2, 1, 1>(a, nb, s);
+    return fail("HIP backend: no persistent decode kernel for this shape.");
 }
 
 }  // namespace
 
-bool fused_decode_supported(int fmt, int head_dim, int group, bool aligned16) {
-    if (!((head_dim == 64 && (group == 2 || group == 7)) || (head_dim == 128 && (group == 4 || group == 7))))
-        return false;
-    if (fmt == FMT_Q4) return true;  // dword units
-    return aligned16;
+int fused_positions_per_item(int head_dim, bool kv_f32) {
+    (void)head_dim;
+    (void)kv_f32;
+    return TP;
+}
+
+bool fused_decode_supported(int fmt, int H, int q_heads, int kv_heads, int head_dim, int I, bool aligned16,
+                            int blocks) {
+    return aligned16 && blocks > 0 && find_variant(fmt, H, q_heads, kv_heads, head_dim, I, blocks) != nullptr;
 }
 
 int fused_decode_blocks() {
@@ -591,15 +915,28 @@ int fused_decode_blocks() {
     return cus;
 }
 
+int fused_max_splits(int H, int q_heads, int kv_heads, int head_dim, int I, bool kv_f32, int blocks,
+                     size_t capacity) {
+    // Splits whose partials fit the LDS budget next to everything else.
+    const int kvb = kv_f32 ? 4 : 2;
+    const LdsLayout base = lds_layout(H, I, q_heads, head_dim, q_heads / kv_heads, kvb, blocks, 1);
+    const int G = q_heads / kv_heads;
+    const int spare_words = (kLdsBudget - (base.total - base.tbw * 8)) / 8 - kChunk - 2;
+    const int fit = std::min(spare_words / (G * (head_dim + 2)), TP);  // merge weights fill one LDS row per split
+    const size_t per_item = (size_t)fused_positions_per_item(head_dim, kv_f32);
+    const size_t need = (capacity + per_item - 1) / per_item;
+    int ms = blocks / kv_heads;
+    ms = std::min(ms, fit);
+    ms = (int)std::min((size_t)ms, need);
+    return std::max(ms, 1);
+}
+
 int launch_decode_fused(const FusedArgs &a, int fmt, int head_dim, int group, bool kv_f32, hipStream_t s) {
     const int nb = fused_decode_blocks();
     if (nb <= 0) return fail("HIP backend: cannot size the persistent decode grid.");
-    const size_t lds = (size_t)std::max(std::max(a.H, a.q_heads * head_dim), a.I) * sizeof(float);
-    if (lds + 32768 > device_max_lds()) return fail("HIP backend: persistent decode needs more LDS than a block has.");
-    if (fmt == FMT_BF16) return launch_fmt<FMT_BF16, 16>(a, nb, lds, head_dim, group, kv_f32, s);
-    if (fmt == FMT_Q8) return launch_fmt<FMT_Q8, 16>(a, nb, lds, head_dim, group, kv_f32, s);
-    if (fmt == FMT_Q4) return launch_fmt<FMT_Q4, 4>(a, nb, lds, head_dim, group, kv_f32, s);
-    return fail("HIP backend: unknown weight format.");
+    const Variant *v = find_variant(fmt, a.H, a.q_heads, a.kv_heads, head_dim, a.I, nb);
+    if (!v || v->g != group) return fail("HIP backend: no persistent decode kernel for this shape.");
+    return kv_f32 ? launch_kt<float>(*v, a, nb, s) : launch_kt<uint16_t>(*v, a, nb, s);
 }
 
 }  // namespace chip

@@ -1,4 +1,4 @@
-// Persistent decode kernel interface (decode_fused.hip).
+// Persistent dataflow decode kernel interface (decode_fused.hip).
 #pragma once
 
 #include "kernels.hpp"
@@ -16,6 +16,11 @@ struct FusedLayer {
     void *kc, *vc;
 };
 
+// Cross-block values travel as 64-bit words: low half the f32 bits, high
+// half the tag of the phase instance that wrote them (never 0, so zeroed
+// memory never matches). Every tagged array is followed by at least 2 more
+// words of the same allocation, so a 16-byte read at its last word stays in
+// bounds.
 struct FusedArgs {
     const FusedLayer *layers;  // device array [L]
     int L, H, q_heads, kv_heads, rotary, I, V;
@@ -23,25 +28,41 @@ struct FusedArgs {
     size_t qkv_stride, o_stride, gu_stride, down_stride;  // payload row strides (bytes)
     const uint16_t *embed, *head, *final_norm;
     const float *rope_cos, *rope_sin;
-    const int32_t *page_table;
-    int page_size;
-    int32_t *step;  // [0] = token, [1] = position; advanced by the kernel
+    const int32_t *page_table;  // 64-position pages
+    int32_t *step;              // [0] = token, [1] = position; advanced by the kernel
     uint32_t *hist;
     long hist_cap;
-    float *hidden, *qrot, *part, *attn, *act, *logits;
-    int *am_key;
-    uint32_t *am_idx;       // [blocks * 4] argmax partials
-    unsigned *arrive;       // [blocks] barrier arrival epochs
-    unsigned *go;           // barrier release epoch
-    unsigned *epoch_base;   // last epoch of the previous launch
-    unsigned *attn_count;   // [kv_heads] split arrival counters, zero at rest
-    int *abort_flag;        // raised when a barrier spin times out
+    float *logits;              // [V], the last step's
+    uint64_t *hid0, *hid1;      // [H] residual stream after o_proj / after down
+    uint64_t *qkvn;             // [kv_heads][(G + 2) * hd]: a group's rotated q heads, then its new K and V rows
+    uint64_t *part;             // [kv_heads][max_splits][G][hd + 2] attention partials (output, max, sum)
+    uint64_t *attn;             // [q_heads * hd] merged attention output
+    uint64_t *act;              // [I] SwiGLU output
+    uint64_t *am;               // [2][blocks][2] argmax partials (key, index) by step parity
+    int *abort_flag;            // raised when a poll times out
+    unsigned tag0;              // tag of step 0, phase 0 of this launch
     int steps;
-    int max_splits;         // at most 64
+    int max_splits;
+    uint64_t *trace;            // null, or [blocks][16L + 3] phase-end timestamps
+    int trace_step;             // the step traced
 };
 
-bool fused_decode_supported(int fmt, int head_dim, int group, bool aligned16);
+// Phases per decode step: 5 per layer (qkv, attention, o, gate/up, down) + head.
+__host__ __device__ constexpr int fused_phases_per_step(int layers) { return 5 * layers + 1; }
+
+// Positions one attention work item covers (one block; K and V in LDS).
+int fused_positions_per_item(int head_dim, bool kv_f32);
+
+// Whether a kernel is built for this model shape on `blocks` blocks.
+bool fused_decode_supported(int fmt, int H, int q_heads, int kv_heads, int head_dim, int I, bool aligned16,
+                            int blocks);
 int fused_decode_blocks();
+
+// Largest attention split count the kernel's LDS holds for this shape
+// (capped by the grid and by `capacity` positions).
+int fused_max_splits(int H, int q_heads, int kv_heads, int head_dim, int I, bool kv_f32, int blocks,
+                     size_t capacity);
+
 int launch_decode_fused(const FusedArgs &a, int fmt, int head_dim, int group, bool kv_f32, hipStream_t s);
 
 }  // namespace chip

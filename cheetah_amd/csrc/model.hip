@@ -20,6 +20,7 @@
 // position live in device memory, so the same graph replays every step and
 // the greedy loop can run back to back with no host round trip.
 #include <cmath>
+#include <cstdio>
 #include <cstring>
 #include <memory>
 #include <mutex>
@@ -170,10 +171,12 @@ struct cheetah_hip_model {
     // Persistent decode kernel state (decode_fused.hip).
     bool fused_ok = false;
     FusedLayer *fused_layers = nullptr;  // device [L]
-    unsigned *sync_words = nullptr;      // arrive[NB] | go | epoch_base | abort | attn_count[kv]
     int fused_blocks = 0;
-    int *am_key = nullptr;
-    uint32_t *am_idx = nullptr;
+    int fused_max_splits = 0;
+    uint64_t *tagged = nullptr;  // hid0 | hid1 | qkvn | part | attn | act | am, tagged words
+    size_t tagged_words = 0;
+    int32_t *abort_dev = nullptr;
+    unsigned next_tag = 1;          // tag of the next launch's first phase
     int32_t *abort_host = nullptr;  // pinned
 
     ~cheetah_hip_model() {
@@ -371,22 +374,37 @@ int finalize(cheetah_hip_model *m) {
     return 0;
 }
 
+// Sizes (words) of the tagged arrays in one allocation: hid0, hid1, qkvn,
+// part, attn, act, am; each rounded to an even count plus 2 words, so every array
+// starts 16-byte aligned and a 16-byte read at its last word stays inside.
+std::vector<size_t> fused_tagged_sizes(const cheetah_hip_model *m) {
+    const auto &c = m->sh->cfg;
+    const size_t hd = c.head_dim, G = c.q_heads / c.kv_heads;
+    const size_t raw[] = {c.hidden_size, c.hidden_size, c.kv_heads * (G + 2) * hd,
+                          (size_t)m->fused_max_splits * c.q_heads * (hd + 2), c.q_heads * hd, c.intermediate_size,
+                          4 * (size_t)m->fused_blocks};
+    std::vector<size_t> out;
+    for (size_t n : raw) out.push_back((n + 1) / 2 * 2 + 2);
+    return out;
+}
+
 // Persistent decode state of one instance: the per-layer pointer table and
-// the barrier words. Sets fused_ok when the model's shape and layout have a
-// persistent kernel; otherwise decode keeps the graph path.
+// the tagged hand-off words. Sets fused_ok when the model's shape and layout
+// have a persistent kernel; otherwise decode keeps the graph path.
 int init_fused(cheetah_hip_model *m) {
     Shared &sh = *m->sh;
     const auto &c = sh.cfg;
-    const int G = (int)(c.q_heads / c.kv_heads);
     const Layer &L0 = sh.layers[0];
     auto aligned = [](const WMat &w) { return w.row_stride() % 16 == 0 && ((uintptr_t)w.payload() % 16) == 0; };
-    bool al = true;
+    bool al = (uintptr_t)sh.head.base % 16 == 0;
     for (const Layer &L : sh.layers) al = al && aligned(L.qkv) && aligned(L.o) && aligned(L.gate) && aligned(L.up) && aligned(L.down);
-    const size_t lds = (size_t)std::max(std::max(c.hidden_size, c.q_heads * c.head_dim), c.intermediate_size) * 4;
     m->fused_blocks = fused_decode_blocks();
-    m->fused_ok = m->fused_blocks > 0 && fused_decode_supported(L0.qkv.fmt, (int)c.head_dim, G, al) &&
-                  c.hidden_size % 8 == 0 && lds + 32768 <= device_max_lds();
+    m->fused_ok = fused_decode_supported(L0.qkv.fmt, (int)c.hidden_size, (int)c.q_heads, (int)c.kv_heads,
+                                         (int)c.head_dim, (int)c.intermediate_size, al, m->fused_blocks);
     if (!m->fused_ok) return 0;
+    m->fused_max_splits = fused_max_splits((int)c.hidden_size, (int)c.q_heads, (int)c.kv_heads, (int)c.head_dim,
+                                           (int)c.intermediate_size, sh.kv_f32 != 0, m->fused_blocks,
+                                           sh.kv_capacity);
     std::vector<FusedLayer> fl(c.num_layers);
     for (uint32_t l = 0; l < c.num_layers; ++l) {
         const Layer &L = sh.layers[l];
@@ -396,20 +414,33 @@ int init_fused(cheetah_hip_model *m) {
     }
     CHIP_TRY(m->mem.alloc(&m->fused_layers, fl.size()));
     CHIP_CHECK(hipMemcpy(m->fused_layers, fl.data(), fl.size() * sizeof(FusedLayer), hipMemcpyHostToDevice));
-    const size_t words = (size_t)m->fused_blocks + 3 + c.kv_heads;
-    CHIP_TRY(m->mem.alloc(&m->sync_words, words));
-    CHIP_CHECK(hipMemset(m->sync_words, 0, words * sizeof(unsigned)));
-    CHIP_TRY(m->mem.alloc(&m->am_key, (size_t)m->fused_blocks * 4));
-    CHIP_TRY(m->mem.alloc(&m->am_idx, (size_t)m->fused_blocks * 4));
+    m->tagged_words = 0;
+    for (size_t n : fused_tagged_sizes(m)) m->tagged_words += n;
+    CHIP_TRY(m->mem.alloc(&m->tagged, m->tagged_words));
+    CHIP_CHECK(hipMemset(m->tagged, 0, m->tagged_words * sizeof(uint64_t)));
+    CHIP_TRY(m->mem.alloc(&m->abort_dev, 1));
+    CHIP_CHECK(hipMemset(m->abort_dev, 0, sizeof(int32_t)));
+    m->next_tag = 1;
     CHIP_CHECK(hipHostMalloc((void **)&m->abort_host, sizeof(int32_t), hipHostMallocDefault));
     return 0;
 }
 
 bool fused_enabled(const cheetah_hip_model *m) {
     if (!m->fused_ok) return false;
-    // Opt-in: the per-step graph path is the faster decode today.
+    // CHEETAH_HIP_FUSED=0 selects the per-step graph path instead.
     const char *e = getenv("CHEETAH_HIP_FUSED");
-    return e && (e[0] == '1' || e[0] == 't' || e[0] == 'T' || e[0] == 'y' || e[0] == 'Y');
+    return !(e && (e[0] == '0' || e[0] == 'f' || e[0] == 'F' || e[0] == 'n' || e[0] == 'N'));
+}
+
+// Whether one persistent launch can run decode steps at positions
+// [offset, offset + steps): the attention items of the longest context must
+// fit the grid.
+bool fused_fits(const cheetah_hip_model *m, size_t offset, size_t steps) {
+    if (!fused_enabled(m)) return false;
+    const Shared &sh = *m->sh;
+    const size_t per_item = (size_t)fused_positions_per_item((int)sh.cfg.head_dim, sh.kv_f32 != 0);
+    const size_t ctx = offset + steps;
+    return (ctx + per_item - 1) / per_item <= (size_t)m->fused_max_splits;
 }
 
 // Runs `steps` decode steps in one persistent launch from the token and
@@ -418,6 +449,12 @@ bool fused_enabled(const cheetah_hip_model *m) {
 int run_fused(cheetah_hip_model *m, size_t steps) {
     Shared &sh = *m->sh;
     const auto &c = sh.cfg;
+    const unsigned per_step = (unsigned)fused_phases_per_step((int)c.num_layers);
+    if ((uint64_t)m->next_tag + (uint64_t)steps * per_step >= 0xFFFFFF00ull) {
+        // Tags are about to wrap: start over from zeroed words.
+        CHIP_CHECK(hipMemsetAsync(m->tagged, 0, m->tagged_words * sizeof(uint64_t), m->stream));
+        m->next_tag = 1;
+    }
     FusedArgs a{};
     a.layers = m->fused_layers;
     a.L = (int)c.num_layers;
@@ -439,36 +476,56 @@ int run_fused(cheetah_hip_model *m, size_t steps) {
     a.rope_cos = sh.rope_cos;
     a.rope_sin = sh.rope_sin;
     a.page_table = m->page_dev;
-    a.page_size = kPageSize;
     a.step = m->step_dev;
     a.hist = m->hist_dev;
     a.hist_cap = (long)sh.kv_capacity + 1;
-    a.hidden = m->hidden;
-    a.qrot = m->qrot;
-    a.part = m->part;
-    a.attn = m->attn;
-    a.act = m->act;
     a.logits = m->logits;
-    a.am_key = m->am_key;
-    a.am_idx = m->am_idx;
-    a.arrive = m->sync_words;
-    a.go = m->sync_words + m->fused_blocks;
-    a.epoch_base = a.go + 1;
-    a.abort_flag = (int *)(a.go + 2);
-    a.attn_count = a.go + 3;
+    uint64_t *t = m->tagged;
+    uint64_t **dst[] = {&a.hid0, &a.hid1, &a.qkvn, &a.part, &a.attn, &a.act, &a.am};
+    const std::vector<size_t> sizes = fused_tagged_sizes(m);
+    for (size_t i = 0; i < sizes.size(); ++i) {
+        *dst[i] = t;
+        t += sizes[i];
+    }
+    a.abort_flag = m->abort_dev;
+    a.tag0 = m->next_tag;
     a.steps = (int)steps;
-    a.max_splits = 64;
+    a.max_splits = m->fused_max_splits;
+    // CHEETAH_HIP_FUSED_TRACE=<file>: per-phase timestamps of the launch's
+    // last step, one line per block (wall clock ticks).
+    const char *trace_path = getenv("CHEETAH_HIP_FUSED_TRACE");
+    const size_t trace_events = 16 * (size_t)c.num_layers + 3;
+    if (trace_path && *trace_path) {
+        CHIP_CHECK(hipMalloc((void **)&a.trace, (size_t)m->fused_blocks * trace_events * sizeof(uint64_t)));
+        CHIP_CHECK(hipMemsetAsync(a.trace, 0, (size_t)m->fused_blocks * trace_events * sizeof(uint64_t), m->stream));
+        a.trace_step = (int)steps - 1;
+    }
     CHIP_TRY(launch_decode_fused(a, L0.qkv.fmt, (int)c.head_dim, (int)(c.q_heads / c.kv_heads), sh.kv_f32 != 0,
                                  m->stream));
+    if (a.trace) {
+        std::vector<uint64_t> tr((size_t)m->fused_blocks * trace_events);
+        CHIP_CHECK(hipMemcpyAsync(tr.data(), a.trace, tr.size() * sizeof(uint64_t), hipMemcpyDeviceToHost, m->stream));
+        CHIP_CHECK(hipStreamSynchronize(m->stream));
+        CHIP_CHECK(hipFree(a.trace));
+        if (FILE *f = fopen(trace_path, "w")) {
+            for (int blk = 0; blk < m->fused_blocks; ++blk) {
+                for (size_t e = 0; e < trace_events; ++e) fprintf(f, e ? " %llu" : "%llu", (unsigned long long)tr[blk * trace_events + e]);
+                fprintf(f, "\n");
+            }
+            fclose(f);
+        }
+    }
+    m->next_tag += (unsigned)steps * per_step;
     CHIP_CHECK(hipMemcpyAsync(m->next_dev, m->step_dev, sizeof(uint32_t), hipMemcpyDeviceToDevice, m->stream));
-    CHIP_CHECK(hipMemcpyAsync(m->abort_host, a.abort_flag, sizeof(int32_t), hipMemcpyDeviceToHost, m->stream));
+    CHIP_CHECK(hipMemcpyAsync(m->abort_host, m->abort_dev, sizeof(int32_t), hipMemcpyDeviceToHost, m->stream));
     CHIP_CHECK(hipStreamSynchronize(m->stream));
     if (*m->abort_host) {
-        // A barrier spin timed out: the step is incomplete. Reset the
-        // barrier words so the next launch starts clean.
-        const size_t words = (size_t)m->fused_blocks + 3 + c.kv_heads;
-        CHIP_CHECK(hipMemset(m->sync_words, 0, words * sizeof(unsigned)));
-        return fail("HIP backend: persistent decode barrier timed out; the step was abandoned.");
+        // A poll timed out: the steps are incomplete. Reset the hand-off
+        // words so the next launch starts clean.
+        CHIP_CHECK(hipMemset(m->tagged, 0, m->tagged_words * sizeof(uint64_t)));
+        CHIP_CHECK(hipMemset(m->abort_dev, 0, sizeof(int32_t)));
+        m->next_tag = 1;
+        return fail("HIP backend: persistent decode timed out waiting for its inputs; the steps were abandoned.");
     }
     return 0;
 }
@@ -781,7 +838,7 @@ int run_forward(cheetah_hip_model *m, const uint32_t *tokens, size_t n, size_t o
     CHIP_TRY(reserve_positions(m, n));
     if (n == 1) {
         CHIP_TRY(write_step(m, tokens[0], offset));
-        if (fused_enabled(m)) CHIP_TRY(run_fused(m, 1));
+        if (fused_fits(m, offset, 1)) CHIP_TRY(run_fused(m, 1));
         else CHIP_TRY(launch_decode(m, offset));
     } else {
         CHIP_CHECK(hipStreamSynchronize(m->stream));  // tokens_host reuse
@@ -920,7 +977,7 @@ int cheetah_hip_decode_greedy(cheetah_hip_model *m, uint32_t token, size_t offse
     CHIP_TRY(validate_decode(m, token, offset, steps));
     CHIP_TRY(reserve_positions(m, steps));
     CHIP_TRY(write_step(m, token, offset));
-    if (fused_enabled(m)) CHIP_TRY(run_fused(m, steps));
+    if (fused_fits(m, offset, steps)) CHIP_TRY(run_fused(m, steps));
     else
         for (size_t i = 0; i < steps; ++i) CHIP_TRY(launch_decode(m, offset + i));
     CHIP_CHECK(hipMemcpyAsync(tokens_out, m->hist_dev + offset + 1, steps * sizeof(uint32_t), hipMemcpyDeviceToHost,
@@ -941,7 +998,7 @@ int cheetah_hip_time_decode(cheetah_hip_model *m, uint32_t token, size_t offset,
     CHIP_CHECK(hipEventCreate(&e0));
     CHIP_CHECK(hipEventCreate(&e1));
     CHIP_CHECK(hipEventRecord(e0, m->stream));
-    if (fused_enabled(m)) {
+    if (fused_fits(m, offset, steps)) {
         CHIP_TRY(run_fused(m, steps));  // waits for the launch
     } else {
         for (size_t i = 0; i < steps; ++i) CHIP_TRY(launch_decode(m, offset + i));
