@@ -1,4 +1,4 @@
-// Persistent dataflow decode kernel: one cooperative launch (one 256-thread
+// Persistent dataflow decode kernel: one cooperative launch (one 512-thread
 // block per CU) runs whole decode steps -- embedding, every layer, LM head,
 // greedy argmax -- with no device-wide barrier.
 //
@@ -47,11 +47,11 @@
 namespace chip {
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
 constexpr int TP = 64;            // positions per KV page
 constexpr int kChunk = 128;       // tagged words per wave-wide 16-byte-per-lane load
-constexpr int kLdsBudget = 140 * 1024;  // dynamic LDS the layout may use
+constexpr int kLdsBudget = 128 * 1024;  // dynamic LDS the layout may use
 constexpr long kSpinLimit = 1L << 20;
 
 // threadIdx.x through an opaque copy: address arithmetic stays next to its
@@ -92,6 +92,32 @@ __device__ __forceinline__ void raise_abort(int *f) {
     __hip_atomic_store(f, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// One layer's pointer table by value, read through the constant address
+// space: scalar loads into scalar registers, not re-read after every store
+// (a reference into global memory would be, as the stores might alias it).
+__device__ __forceinline__ FusedLayer load_layer(const FusedLayer *table, int l) {
+    typedef const __attribute__((address_space(4))) FusedLayer CLayer;
+    CLayer *p = (CLayer *)table + l;
+    FusedLayer o;
+    o.qkv = p->qkv;
+    o.o = p->o;
+    o.gate = p->gate;
+    o.up = p->up;
+    o.down = p->down;
+    o.qkv_sc = p->qkv_sc;
+    o.o_sc = p->o_sc;
+    o.gate_sc = p->gate_sc;
+    o.up_sc = p->up_sc;
+    o.down_sc = p->down_sc;
+    o.qkv_bias = p->qkv_bias;
+    o.o_bias = p->o_bias;
+    o.ln1 = p->ln1;
+    o.ln2 = p->ln2;
+    o.kc = p->kc;
+    o.vc = p->vc;
+    return o;
+}
+
 // 16 bytes per lane from global memory straight into LDS at lds + 16 * lane
 // (lds must be the same in every lane of the wave), device-coherent (sc1).
 __device__ __forceinline__ void dma16(const void *g, void *lds) {
@@ -104,7 +130,7 @@ __device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" :
 // each round only chunks with a stale word are loaded again. Block-wide:
 // starts with a barrier (dst may still be read by the previous phase) and
 // ends with one; false in every thread on timeout or abort.
-__device__ __noinline__ bool gather_lds(uint64_t *dst, const uint64_t *src, int n, unsigned tag, int *abort_flag) {
+__device__ __forceinline__ bool gather_lds(uint64_t *dst, const uint64_t *src, int n, unsigned tag, int *abort_flag) {
     const int tid = tid_here(), lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int chunks = (n + kChunk - 1) / kChunk;
@@ -399,11 +425,20 @@ __device__ bool attn_item(const FusedArgs &a, const FusedLayer &ly, uint64_t *tb
         __syncthreads();
     }
     mark(0);
-    float qr[G][8];
+    // q as f32 in LDS (reusing the staging words it came in).
+    float *qs = (float *)tb;
+    __syncthreads();
+    {
+        float qv[(G * HD + kThreads - 1) / kThreads];
 #pragma unroll
-    for (int j = 0; j < G; ++j)
+        for (int k = 0; k * kThreads < G * HD; ++k)
+            if (tid + k * kThreads < G * HD) qv[k] = val_of(tb[tid + k * kThreads]);
+        __syncthreads();
 #pragma unroll
-        for (int e = 0; e < 8; ++e) qr[j][e] = val_of(tb[j * HD + d8 * 8 + e]);
+        for (int k = 0; k * kThreads < G * HD; ++k)
+            if (tid + k * kThreads < G * HD) qs[tid + k * kThreads] = qv[k];
+        __syncthreads();
+    }
     const float scale = 1.0f / sqrtf((float)HD);
     const int passes = (nv + P - 1) / P;
 #pragma unroll 2
@@ -419,7 +454,7 @@ __device__ bool attn_item(const FusedArgs &a, const FusedLayer &ly, uint64_t *tb
 #pragma unroll
             for (int j = 0; j < G; ++j)
 #pragma unroll
-                for (int e = 0; e < 8; ++e) dot[j] = fmaf(kf[e], qr[j][e], dot[j]);
+                for (int e = 0; e < 8; ++e) dot[j] = fmaf(kf[e], qs[j * HD + d8 * 8 + e], dot[j]);
         }
 #pragma unroll
         for (int j = 0; j < G; ++j) {
@@ -496,7 +531,9 @@ __device__ bool attn_item(const FusedArgs &a, const FusedLayer &ly, uint64_t *tb
     uint64_t *part = gpart + (size_t)split * G * (HD + 2);
     for (int t = tid; t < G * HD; t += kThreads) {
         const int j = t / HD, d = t % HD;
-        const float o = sh.red[0][j][d] + sh.red[1][j][d] + sh.red[2][j][d] + sh.red[3][j][d];
+        float o = sh.red[0][j][d];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) o += sh.red[w][j][d];
         stf(part + (size_t)j * (HD + 2) + d, o, tB);
     }
     if (tid < G) {
@@ -597,15 +634,14 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs a) {
         const uint16_t *emb = a.embed + (size_t)token * H;
 
         for (int l = 0; l < a.L; ++l) {
-            // By value: a reference would be re-read from memory after every
-            // store (the stores might alias the table).
-            const FusedLayer ly = a.layers[l];
+            const FusedLayer ly = load_layer(a.layers, l);
             const int gw = gw_here();
             const unsigned tA = tb0 + 5 * l, tB = tA + 1, tC = tA + 2, tD = tA + 3, tE = tA + 4;
             const long kv_start = (long)isplit * Geo::CH, kv_lim = min(kv_start + Geo::CH, pos);
-            // Weight rows of the o, gate/up and down phases go out right after
-            // the QKV phase (attention blocks: gate/up before attention, the
-            // rest after it), so they stream while attention runs.
+            // Weight rows of the o and gate/up phases go out right after the
+            // QKV phase (attention blocks: gate/up before attention, o after
+            // it), so they stream while attention runs; down rows go out
+            // before the down phase's input wait.
             auto load_wD = [&]() {
 #pragma unroll
                 for (int k = 0; k < RGU; ++k) {
@@ -616,11 +652,8 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs a) {
                     }
                 }
             };
-            auto load_wCE = [&]() {
-                if (myH) {
-                    load_row(wC[0], ly.o + (size_t)gw * a.o_stride, nQ);
-                    load_row(wE[0], ly.down + (size_t)gw * a.down_stride, nI);
-                }
+            auto load_wC = [&]() {
+                if (myH) load_row(wC[0], ly.o + (size_t)gw * a.o_stride, nQ);
             };
             mark(16 * l);
 
@@ -699,7 +732,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs a) {
             }
             mark(16 * l + 2);
             if (!hasB) {
-                load_wCE();
+                load_wC();
                 load_wD();
             }
 
@@ -712,7 +745,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs a) {
                 uint64_t *tr = traced ? a.trace + (size_t)b * (16 * a.L + 3) + 16 * l + 3 : nullptr;
                 if (!attn_item<HD, G, KT>(a, ly, tb, ig, isplit, S, pos, tA, tB, !hasA && !kv_early, lay.qkw, ash, tr))
                     return;
-                load_wCE();
+                load_wC();
             }
             mark(16 * l + 7);
 
@@ -762,6 +795,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs a) {
             mark(16 * l + 11);
 
             // ---- E: down + residual.
+            if (myH) load_row(wE[0], ly.down + (size_t)gw * a.down_stride, nI);
             if (hasH) {
                 if (!gather_lds(tb, a.act, I, tD, a.abort_flag)) return;
                 stage_lds(xs, tb, I, nullptr, 0.f, sm.red);
@@ -851,7 +885,7 @@ struct Variant {
 // Shapes with a built kernel: Qwen2-0.5B (hidden 896, 14/2 heads of 64,
 // intermediate 4864) and the two small test shapes.
 constexpr Variant kVariants[] = {
-    {FMT_BF16, 64, 7, 2, 2, 10, 5, 2},
+    {FMT_BF16, 64, 7, 2, 2, 10, 3, 2},
     {FMT_BF16, 64, 2, 1, 1, 1, 1, 1},
     {FMT_BF16, 128, 4, 1, 2, 2, 1, 1},
 };
@@ -889,7 +923,7 @@ int launch_one(const FusedArgs &a, int nb, hipStream_t s) {
 
 template <class KT>
 int launch_kt(const Variant &v, const FusedArgs &a, int nb, hipStream_t s) {
-    if (v.hd == 64 && v.g == 7) return launch_one<FMT_BF16, 64, 7, KT, 2, 2, 10, 5, 2>(a, nb, s);
+    if (v.hd == 64 && v.g == 7) return launch_one<FMT_BF16, 64, 7, KT, 2, 2, 10, 3, 2>(a, nb, s);
     if (v.hd == 64 && v.g == 2) return launch_one<FMT_BF16, 64, 2, KT, 1, 1, 1, 1, 1>(a, nb, s);
     if (v.hd == 128 && v.g == 4) return launch_one<FMT_BF16, 128, 4, KT, 1, 2, 2, 1, 1>(a, nb, s);
     return fail("HIP backend: no persistent decode kernel for this shape.");
