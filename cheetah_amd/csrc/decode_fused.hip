@@ -264,11 +264,27 @@ __device__ __forceinline__ void better(int &key, uint32_t &idx, int k2, uint32_t
     }
 }
 
+constexpr int kStage = 64;  // outputs one block publishes per phase, at most
+
 struct Shm {
     float red[kWaves];
     int ikey[kWaves];
     uint32_t iidx[kWaves];
+    // A phase's outputs of the block's waves, stored by one wave afterwards
+    // so that consecutive words leave in one coalesced run.
+    float outv[kStage];
+    int outi[kStage];   // destination word (QKV: index into the q/K/V words)
+    int outc[kStage];   // QKV: cache element (bit 30: V cache), or -1
 };
+
+// Stores vals[0, n) as the tagged words dst[0, n): one run by the first
+// threads. Block-wide; starts with a barrier (the values are staged by other
+// waves).
+__device__ __forceinline__ void publish(uint64_t *dst, const float *vals, int n, unsigned tag) {
+    __syncthreads();
+    const int tid = tid_here();
+    if (tid < n) stf(dst + tid, vals[tid], tag);
+}
 
 // Reduces (key, idx) over the block; the result lands in every thread.
 __device__ void block_best(int &key, uint32_t &idx, Shm &sm) {
@@ -591,7 +607,9 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs a) {
 
     const bool hasA = b * kWaves < npairs, myA = gw0 < npairs;
     const bool hasH = b * kWaves < H, myH = gw0 < H;
-    const bool hasD = b * kWaves < I;
+    // Gate/up rows: block b owns RB consecutive rows, wave w rows w, w + 8, ...
+    const int RB = (I + NB - 1) / NB;
+    const bool hasD = b * RB < I;
     const int head_rows = gw0 < V ? (V - 1 - gw0) / W + 1 : 0;
     const bool hasHead = b * kWaves < V;
     // Blocks that own head rows write argmax partials. Blocks without would
@@ -645,8 +663,8 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs a) {
             auto load_wD = [&]() {
 #pragma unroll
                 for (int k = 0; k < RGU; ++k) {
-                    const int r = gw + W * k;
-                    if (r < I) {
+                    const int j = (gw - b * kWaves) + kWaves * k, r = b * RB + j;
+                    if (j < RB && r < I) {
                         load_row(wD[2 * k], ly.gate + (size_t)r * a.gu_stride, nH);
                         load_row(wD[2 * k + 1], ly.up + (size_t)r * a.gu_stride, nH);
                     }
@@ -692,6 +710,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs a) {
                         v0 = v0 + ly.qkv_bias[r0];
                         v1 = v1 + ly.qkv_bias[r0 + 1];
                     }
+                    int i0, i1, c0 = -1, c1 = -1;  // q/K/V word, cache element
                     if (r0 < qd + kvd) {
                         const bool is_q = r0 < qd;
                         const int base = is_q ? r0 : r0 - qd;
@@ -707,27 +726,48 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs a) {
                             o1 = half + i;
                         }
                         if (is_q) {
-                            uint64_t *q = a.qkvn + (size_t)(h / G) * (G + 2) * HD + (h % G) * HD;
-                            stf(q + o0, v0, tA);
-                            stf(q + o1, v1, tA);
+                            const int q0 = (h / G) * (G + 2) * HD + (h % G) * HD;
+                            i0 = q0 + o0;
+                            i1 = q0 + o1;
                         } else {
-                            KT *kc = (KT *)ly.kc + (((size_t)page * a.kv_heads + h) * TP + slot) * HD;
-                            st_kv(kc + o0, v0);
-                            st_kv(kc + o1, v1);
-                            uint64_t *kn = a.qkvn + (size_t)h * (G + 2) * HD + G * HD;
-                            stf(kn + o0, kv_round<KT>(v0), tA);
-                            stf(kn + o1, kv_round<KT>(v1), tA);
+                            const int k0 = h * (G + 2) * HD + G * HD;
+                            i0 = k0 + o0;
+                            i1 = k0 + o1;
+                            const int e0 = ((page * a.kv_heads + h) * TP + slot) * HD;
+                            c0 = e0 + o0;
+                            c1 = e0 + o1;
                         }
                     } else {
                         const int base = r0 - qd - kvd;
                         const int h = base / HD, d0 = base % HD;
-                        KT *vc = (KT *)ly.vc + (((size_t)page * a.kv_heads + h) * TP + slot) * HD;
-                        st_kv(vc + d0, v0);
-                        st_kv(vc + d0 + 1, v1);
-                        uint64_t *vn = a.qkvn + (size_t)h * (G + 2) * HD + (G + 1) * HD;
-                        stf(vn + d0, kv_round<KT>(v0), tA);
-                        stf(vn + d0 + 1, kv_round<KT>(v1), tA);
+                        const int v0i = h * (G + 2) * HD + (G + 1) * HD;
+                        i0 = v0i + d0;
+                        i1 = v0i + d0 + 1;
+                        const int e0 = ((page * a.kv_heads + h) * TP + slot) * HD;
+                        c0 = (e0 + d0) | (1 << 30);
+                        c1 = (e0 + d0 + 1) | (1 << 30);
                     }
+                    sm.outv[2 * wave] = v0;
+                    sm.outv[2 * wave + 1] = v1;
+                    sm.outi[2 * wave] = i0;
+                    sm.outi[2 * wave + 1] = i1;
+                    sm.outc[2 * wave] = c0;
+                    sm.outc[2 * wave + 1] = c1;
+                }
+            }
+            if (hasA) {
+                // The block's pairs leave as one run: q/K/V words (K/V as
+                // the cache holds them) and the K/V cache elements.
+                __syncthreads();
+                const int n = 2 * min(kWaves, npairs - b * kWaves);
+                if (tid < n) {
+                    const float v = sm.outv[tid];
+                    const int c = sm.outc[tid];
+                    if (c >= 0) {
+                        KT *cache = (KT *)((c >> 30) ? ly.vc : ly.kc);
+                        st_kv(cache + (c & ((1 << 30) - 1)), v);
+                    }
+                    stf(a.qkvn + sm.outi[tid], c >= 0 ? kv_round<KT>(v) : v, tA);
                 }
             }
             mark(16 * l + 2);
@@ -763,8 +803,9 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs a) {
                 if (ly.o_bias) v = v + ly.o_bias[gw];
                 const float old = l == 0 ? bf16_f32(emb[gw]) : h_own;
                 h_own = old + v;
-                if (lane == 0) stf(a.hid0 + gw, h_own, tC);
+                if (lane == 0) sm.outv[wave] = h_own;
             }
+            if (hasH) publish(a.hid0 + b * kWaves, sm.outv, min(kWaves, H - b * kWaves), tC);
             mark(16 * l + 9);
 
             // ---- D: gate/up + SwiGLU.
@@ -776,22 +817,26 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs a) {
             {
                 int nr = 0;
 #pragma unroll
-                for (int k = 0; k < RGU; ++k) nr += gw + W * k < I ? 2 : 0;
+                for (int k = 0; k < RGU; ++k) {
+                    const int j = wave + kWaves * k;
+                    nr += j < RB && b * RB + j < I ? 2 : 0;
+                }
                 float y[2 * RGU];
                 dot_rows<FMT>(wD, xs, nH, nr, y);
 #pragma unroll
                 for (int k = 0; k < RGU; ++k) {
-                    const int r = gw + W * k;
-                    if (r < I) {
+                    const int j = wave + kWaves * k, r = b * RB + j;
+                    if (j < RB && r < I) {
                         float gv = y[2 * k], uv = y[2 * k + 1];
                         if (ly.gate_sc) {
                             gv = gv * ly.gate_sc[r];
                             uv = uv * ly.up_sc[r];
                         }
-                        if (lane == 0) stf(a.act + r, gv * (uv / (1.0f + expf(-gv))), tD);
+                        if (lane == 0) sm.outv[j] = gv * (uv / (1.0f + expf(-gv)));
                     }
                 }
             }
+            if (hasD) publish(a.act + b * RB, sm.outv, min(RB, I - b * RB), tD);
             mark(16 * l + 11);
 
             // ---- E: down + residual.
@@ -807,8 +852,9 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs a) {
                 float v = y[0];
                 if (ly.down_sc) v = v * ly.down_sc[gw];
                 h_own = h_own + v;
-                if (lane == 0) stf(a.hid1 + gw, h_own, tE);
+                if (lane == 0) sm.outv[wave] = h_own;
             }
+            if (hasH) publish(a.hid1 + b * kWaves, sm.outv, min(kWaves, H - b * kWaves), tE);
             mark(16 * l + 13);
         }
 
@@ -901,7 +947,8 @@ const Variant *find_variant(int fmt, int H, int q_heads, int kv_heads, int hd, i
     for (const Variant &v : kVariants) {
         if (v.fmt != fmt || v.hd != hd || v.g != g) continue;
         if (units_per_lane(H, E) > v.uh || units_per_lane(qd, E) > v.uq || units_per_lane(I, E) > v.ui) continue;
-        if ((I + W - 1) / W > v.rgu || units_per_lane(H, 8) > v.uhb) continue;
+        const int rb = (I + blocks - 1) / blocks;
+        if (rb > kStage || (rb + kWaves - 1) / kWaves > v.rgu || units_per_lane(H, 8) > v.uhb) continue;
         return &v;
     }
     return nullptr;

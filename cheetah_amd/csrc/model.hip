@@ -399,8 +399,12 @@ int init_fused(cheetah_hip_model *m) {
     bool al = (uintptr_t)sh.head.base % 16 == 0;
     for (const Layer &L : sh.layers) al = al && aligned(L.qkv) && aligned(L.o) && aligned(L.gate) && aligned(L.up) && aligned(L.down);
     m->fused_blocks = fused_decode_blocks();
-    m->fused_ok = fused_decode_supported(L0.qkv.fmt, (int)c.hidden_size, (int)c.q_heads, (int)c.kv_heads,
-                                         (int)c.head_dim, (int)c.intermediate_size, al, m->fused_blocks);
+    // The kernel addresses one layer's K (or V) pool with 30-bit element
+    // indices.
+    const bool small_pool = (size_t)sh.num_pages * c.kv_heads * kPageSize * c.head_dim < (size_t(1) << 30);
+    m->fused_ok = small_pool && fused_decode_supported(L0.qkv.fmt, (int)c.hidden_size, (int)c.q_heads,
+                                                       (int)c.kv_heads, (int)c.head_dim, (int)c.intermediate_size,
+                                                       al, m->fused_blocks);
     if (!m->fused_ok) return 0;
     m->fused_max_splits = fused_max_splits((int)c.hidden_size, (int)c.q_heads, (int)c.kv_heads, (int)c.head_dim,
                                            (int)c.intermediate_size, sh.kv_f32 != 0, m->fused_blocks,
