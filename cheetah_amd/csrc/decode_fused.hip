@@ -583,13 +583,51 @@ __device__ bool attn_item(const FusedArgs &a, const FusedLayer &ly, uint64_t *tb
     return true;
 }
 
+// LM head rows gw, gw + W, ... of one wave against the final-normed hidden
+// state xs: logits, and the wave's best (key, index). Out of line, so that
+// its double-buffered rows are register-allocated apart from the layer loop.
+template <int UHB>
+__device__ __noinline__ void head_dots(const uint16_t *head, float *logits, const float *xs, int H, int V, int gw,
+                                       int W, int head_rows, int &key, uint32_t &idx) {
+    constexpr int HB = 4;  // rows per batch, two batches in flight
+    const int lane = tid_here() & 63, nHB = H / 8;
+    const size_t stride = (size_t)H * 2;
+    u32x4 hb[2][HB][UHB];
+    const int nbat = (head_rows + HB - 1) / HB;
+    auto issue = [&](u32x4 (&buf)[HB][UHB], int bi) {
+#pragma unroll
+        for (int k = 0; k < HB; ++k) {
+            const int i = bi * HB + k;
+            if (i < head_rows) load_row(buf[k], (const uint8_t *)head + (size_t)(gw + W * i) * stride, nHB);
+        }
+    };
+    auto consume = [&](const u32x4 (&buf)[HB][UHB], int bi) {
+        const int nr = min(HB, head_rows - bi * HB);
+        float y[HB];
+        dot_rows<FMT_BF16>(buf, xs, nHB, nr, y);
+#pragma unroll
+        for (int k = 0; k < HB; ++k)
+            if (k < nr) {
+                const uint32_t r = (uint32_t)(gw + W * (bi * HB + k));
+                if (lane == 0) logits[r] = y[k];
+                better(key, idx, total_key(y[k]), r);
+            }
+    };
+    issue(hb[0], 0);
+    for (int bi = 0; bi < nbat; bi += 2) {
+        if (bi + 1 < nbat) issue(hb[1], bi + 1);
+        consume(hb[0], bi);
+        if (bi + 2 < nbat) issue(hb[0], bi + 2);
+        if (bi + 1 < nbat) consume(hb[1], bi + 1);
+    }
+}
+
 // UH/UQ/UI: 16-byte units per lane of a row with H / q_heads*HD / I
 // columns; RGU: gate/up rows per wave; UHB: units per lane of a BF16 head row.
 template <int FMT, int HD, int G, class KT, int UH, int UQ, int UI, int RGU, int UHB>
 __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs a) {
     using Geo = AttnGeo<HD, KT>;
     using U = Unit<FMT, 16>;
-    constexpr int HB = 4;  // head rows per batch
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ Shm sm;
     __shared__ AttnShm<HD, G, Geo::CH> ash;
@@ -598,7 +636,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs a) {
     const int gw0 = b * kWaves + wave;
     const int H = a.H, I = a.I, V = a.V;
     const int qd = a.q_heads * HD, kvd = a.kv_heads * HD;
-    const int nH = H / U::E, nQ = qd / U::E, nI = I / U::E, nHB = H / 8;
+    const int nH = H / U::E, nQ = qd / U::E, nI = I / U::E;
     const int npairs = (qd + 2 * kvd) / 2;
     const int half = a.rotary / 2;
     const LdsLayout lay = lds_layout(H, I, a.q_heads, HD, G, (int)sizeof(KT), NB, a.max_splits);
@@ -616,13 +654,24 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs a) {
     // have nothing pacing them and could overwrite a step's partials before
     // they are read, so they write none.
     const int head_blocks = min(NB, (V + kWaves - 1) / kWaves);
-    const size_t head_stride = (size_t)H * 2;
 
     int token = __hip_atomic_load(a.step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     long pos = __hip_atomic_load(a.step + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     float h_own = 0.f;
 
     u32x4 wA[2][UH], wC[1][UQ], wD[2 * RGU][UH], wE[1][UI];
+
+    // QKV rows of layer l: issued one phase early (before the previous
+    // layer's down-phase wait, or before the argmax wait for layer 0).
+    auto load_wA = [&](int l) {
+        if (myA) {
+            const FusedLayer ly = load_layer(a.layers, l);
+            const int gw = gw_here();
+            load_row(wA[0], ly.qkv + (size_t)(2 * gw) * a.qkv_stride, nH);
+            load_row(wA[1], ly.qkv + (size_t)(2 * gw + 1) * a.qkv_stride, nH);
+        }
+    };
+    load_wA(0);
 
     const int PH = fused_phases_per_step(a.L);
     // A block is paced when it waited on the previous step's last layer (or
@@ -683,10 +732,6 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs a) {
                 load_kv_lds<HD, KT>(k_lds, k_lds + Geo::CH * Geo::ROW, a, ly, ig, kv_start, kv_lim);
             }
             if (hasB) load_wD();
-            if (myA) {
-                load_row(wA[0], ly.qkv + (size_t)(2 * gw) * a.qkv_stride, nH);
-                load_row(wA[1], ly.qkv + (size_t)(2 * gw + 1) * a.qkv_stride, nH);
-            }
             if (hasA) {
                 if (l == 0) {
                     stage_embed(xs, emb, H, ly.ln1, a.eps, sm.red);
@@ -841,6 +886,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs a) {
 
             // ---- E: down + residual.
             if (myH) load_row(wE[0], ly.down + (size_t)gw * a.down_stride, nI);
+            if (l + 1 < a.L) load_wA(l + 1);
             if (hasH) {
                 if (!gather_lds(tb, a.act, I, tD, a.abort_flag)) return;
                 stage_lds(xs, tb, I, nullptr, 0.f, sm.red);
@@ -863,38 +909,10 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs a) {
         int key = INT_MIN;
         uint32_t idx = 0;
         if (hasHead) {
-            const int gw = gw_here();
-            u32x4 hb[2][HB][UHB];
-            const int nbat = (head_rows + HB - 1) / HB;
-            auto issue = [&](u32x4 (&buf)[HB][UHB], int bi) {
-#pragma unroll
-                for (int k = 0; k < HB; ++k) {
-                    const int i = bi * HB + k;
-                    if (i < head_rows) load_row(buf[k], (const uint8_t *)a.head + (size_t)(gw + W * i) * head_stride, nHB);
-                }
-            };
-            auto consume = [&](const u32x4 (&buf)[HB][UHB], int bi) {
-                const int nr = min(HB, head_rows - bi * HB);
-                float y[HB];
-                dot_rows<FMT_BF16>(buf, xs, nHB, nr, y);
-#pragma unroll
-                for (int k = 0; k < HB; ++k)
-                    if (k < nr) {
-                        const uint32_t r = (uint32_t)(gw + W * (bi * HB + k));
-                        if (lane == 0) a.logits[r] = y[k];
-                        better(key, idx, total_key(y[k]), r);
-                    }
-            };
-            issue(hb[0], 0);
             if (!gather_lds(tb, a.hid1, H, tH - 1, a.abort_flag)) return;
             stage_lds(xs, tb, H, a.final_norm, a.eps, sm.red);
             mark(16 * a.L);
-            for (int bi = 0; bi < nbat; bi += 2) {
-                if (bi + 1 < nbat) issue(hb[1], bi + 1);
-                consume(hb[0], bi);
-                if (bi + 2 < nbat) issue(hb[0], bi + 2);
-                if (bi + 1 < nbat) consume(hb[1], bi + 1);
-            }
+            head_dots<UHB>(a.head, a.logits, xs, H, V, gw_here(), W, head_rows, key, idx);
         }
         block_best(key, idx, sm);
         mark(16 * a.L + 1);
@@ -903,6 +921,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs a) {
             stt(am + 2 * b, (uint32_t)key, tH);
             stt(am + 2 * b + 1, idx, tH);
         }
+        if (s + 1 < a.steps) load_wA(0);
         // Blocks that use the token (embedding row, residual) reduce the
         // partials of every head block.
         if (hasA || hasH) {
