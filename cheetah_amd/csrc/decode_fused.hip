@@ -859,6 +859,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs a) {
                 stage_lds(xs, tb, H, ly.ln2, a.eps, sm.red);
             }
             mark(16 * l + 10);
+            if (myH) load_row(wE[0], ly.down + (size_t)gw * a.down_stride, nI);
             {
                 int nr = 0;
 #pragma unroll
@@ -885,7 +886,6 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs a) {
             mark(16 * l + 11);
 
             // ---- E: down + residual.
-            if (myH) load_row(wE[0], ly.down + (size_t)gw * a.down_stride, nI);
             if (l + 1 < a.L) load_wA(l + 1);
             if (hasH) {
                 if (!gather_lds(tb, a.act, I, tD, a.abort_flag)) return;
