@@ -68,7 +68,19 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--cpu-decode-steps", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-ops", action="store_true",
+                    help="skip the op-level attention / GEMV / GEMM measurements")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only copy 1 GiB device-to-device 3 times (calibrates rocprofv3 byte counters)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        from cheetah_amd import hip
+
+        src, dst = hip.DeviceBuffer(1 << 30), hip.DeviceBuffer(1 << 30)
+        for _ in range(3):
+            hip.copy(dst, src, 1 << 30)
+        print(json.dumps({"copy_calibration_bytes": 1 << 30, "copies": 3}))
+        return 0
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported "
                                    "(the decoder is not sharded)", "n_gpus": args.gpus}))
@@ -114,18 +126,32 @@ def main() -> int:
     decode_tok_s = args.steps * DECODE / dec
     prefill_tok_s = args.steps * PROMPT / pre
 
-    # Dominant decode kernel (gate/up GEMV with fused RMSNorm + SwiGLU), timed
-    # with HIP events on the model's stream, cycling the 24 layers' weights.
+    # The decode loop timed with HIP events on the model's stream: one launch
+    # of the persistent decode kernel runs all DECODE steps (the dominant and
+    # only kernel of the decode phase). Then the multi-kernel path's dominant
+    # GEMV (gate/up with fused RMSNorm + SwiGLU) alone, cycling the layers.
     g.clear_cache()
     first = g.forward_greedy(prompt, 0, chunk_rows=CHUNK)
     ms_step, gemv_ms, _ = g.time_decode(first, PROMPT, DECODE)
     H, I = shape.hidden_size, shape.intermediate_size
     gemv_bytes = 2 * I * H * 2 + H * 4 + H * 2 + I * 4  # gate+up BF16, hidden, gain, out
-    achieved = gemv_bytes / (gemv_ms * 1e-3) / 1e9
+    gemv_gbps = gemv_bytes / (gemv_ms * 1e-3) / 1e9
+    # Algorithmic bytes of one decode step at context c: every weight once
+    # (linear + tied head, BF16), the K/V rows of c positions read and one
+    # position written (24 layers x K,V x 2 KV heads x 64 x 2 B = 12,288 B
+    # per position).
     weight_bytes = (shape.linear_params() + shape.head_params()) * 2
-    ctx_mean = PROMPT + DECODE / 2
-    kv_bytes = shape.num_layers * 2 * shape.kv_dim * 2 * ctx_mean
-    step_bytes = weight_bytes + kv_bytes
+    kv_pos_bytes = shape.num_layers * 2 * shape.kv_dim * 2
+    ctx_sum = sum(p + 1 for p in range(PROMPT, PROMPT + DECODE))
+    launch_bytes = DECODE * weight_bytes + kv_pos_bytes * (ctx_sum + DECODE)
+    launch_ms = ms_step * DECODE
+    achieved = launch_bytes / (launch_ms * 1e-3) / 1e9
+    step_bytes = launch_bytes / DECODE
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "decode_flow_qwen2_0_5b_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
 
     golden_ok = None
     gpath = os.path.join(ROOT, "tests", "golden", "qwen2_0_5b_bf16kv_greedy.json")
@@ -157,22 +183,38 @@ def main() -> int:
         },
         "prefill_tok_s": round(prefill_tok_s, 1),
         "decode_ms_per_token": round(dec / (args.steps * DECODE) * 1e3, 4),
-        "decode_graph_ms_per_token": round(ms_step, 4),
+        "decode_event_ms_per_token": round(ms_step, 4),
         "decode_effective_gbps": round(step_bytes / (ms_step * 1e-3) / 1e9, 1),
         "decode_hbm_roofline_frac": round(step_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
         "greedy_first32_match_golden": golden_ok,
         "roofline": {
-            "kernel": "gemv_kernel<BF16> gate/up + SwiGLU (fused RMSNorm), 4864x896 x2",
+            "kernel": f"decode_flow_kernel (persistent decode: {DECODE} steps per launch, BF16 weights, "
+                      "BF16 paged KV)",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": traffic,
+            "bytes_per_launch": int(launch_bytes),
+            "avg_launch_ms": round(launch_ms, 3),
+        },
+        "graph_path_gemv": {
+            "kernel": "gemv_kernel<BF16> gate/up + SwiGLU (fused RMSNorm), 4864x896 x2",
+            "achieved_gbps": round(gemv_gbps, 1),
             "bytes_per_launch": gemv_bytes,
             "avg_launch_ms": round(gemv_ms, 5),
-            "traffic": None,
         },
     }
+    if not args.no_ops:
+        from cheetah_amd import opbench
+
+        g.close()
+        log("[bench] op-level attention ...")
+        ops = {"attention": opbench.attention()}
+        log("[bench] op-level GEMV / GEMM ...")
+        ops["gemv_gemm"] = opbench.gemv_gemm()
+        result["ops"] = ops
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (oracle) ...")
         result["cpu_baseline"] = cpu_baseline(shape, weights, prompt, args.cpu_decode_steps)

@@ -114,6 +114,14 @@ int cheetah_hip_download(void *dst, const void *src, size_t bytes) {
     return 0;
 }
 
+int cheetah_hip_copy(void *dst, const void *src, size_t bytes) {
+    CHIP_TRY(ensure_ready());
+    if (!dst || (!src && bytes)) return fail("HIP backend: copy with a null pointer.");
+    CHIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, g_stream));
+    CHIP_CHECK(hipStreamSynchronize(g_stream));
+    return 0;
+}
+
 int cheetah_hip_synchronize(void) {
     CHIP_TRY(ensure_ready());
     CHIP_CHECK(hipStreamSynchronize(g_stream));
@@ -192,9 +200,17 @@ int cheetah_hip_dequant_q4(const uint8_t *w, size_t rows, size_t cols, float *ou
     return launch_dequant(WMat{FMT_Q4, w, rows, cols}, out, g_stream);
 }
 
+static int attention_op(const float *q, const cheetah_hip_kv_view *kv, uint32_t q_heads, size_t rows, size_t offset,
+                        float *out);
+
 int cheetah_hip_attention(const float *q, const cheetah_hip_kv_view *kv, uint32_t q_heads, size_t rows,
                           size_t offset, float *out) {
     CHIP_TRY(ensure_ready());
+    return attention_op(q, kv, q_heads, rows, offset, out);
+}
+
+static int attention_op(const float *q, const cheetah_hip_kv_view *kv, uint32_t q_heads, size_t rows, size_t offset,
+                        float *out) {
     if (!q || !kv || !out) return fail("HIP backend: attention with a null pointer.");
     if (rows == 0) return fail("HIP backend: attention needs at least one query row.");
     static thread_local float *part = nullptr;
@@ -252,6 +268,60 @@ int cheetah_hip_time_gemv(uint32_t fmt, const void *const *w, size_t nbuf, size_
         j.w = WMat{(int)fmt, (const uint8_t *)w[i % nbuf], rows, cols};
         CHIP_TRY(launch_gemv(j, g_stream));
     }
+    CHIP_CHECK(hipEventRecord(e1, g_stream));
+    CHIP_CHECK(hipEventSynchronize(e1));
+    float total = 0.f;
+    CHIP_CHECK(hipEventElapsedTime(&total, e0, e1));
+    *ms = total / (float)iters;
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return 0;
+}
+
+int cheetah_hip_time_gemm(uint32_t fmt, const void *const *w, size_t nbuf, size_t rows, size_t cols,
+                          const float *x, size_t n, float *y, size_t iters, float *ms) {
+    CHIP_TRY(ensure_ready());
+    if (!w || nbuf == 0 || iters == 0 || !ms || !x || !y || n == 0)
+        return fail("HIP backend: time_gemm needs buffers, rows and iterations.");
+    if (fmt != FMT_BF16 && fmt != FMT_Q8 && fmt != FMT_Q4) return fail("HIP backend: unknown weight format.");
+    for (size_t i = 0; i < nbuf; ++i)
+        if (!w[i]) return fail("HIP backend: time_gemm with a null weight buffer.");
+    GemmJob j;
+    j.x = x;
+    j.n = n;
+    j.y = y;
+    hipEvent_t e0, e1;
+    CHIP_CHECK(hipEventCreate(&e0));
+    CHIP_CHECK(hipEventCreate(&e1));
+    for (size_t i = 0; i < nbuf; ++i) {
+        j.w = WMat{(int)fmt, (const uint8_t *)w[i], rows, cols};
+        CHIP_TRY(launch_gemm(j, g_stream));
+    }
+    CHIP_CHECK(hipEventRecord(e0, g_stream));
+    for (size_t i = 0; i < iters; ++i) {
+        j.w = WMat{(int)fmt, (const uint8_t *)w[i % nbuf], rows, cols};
+        CHIP_TRY(launch_gemm(j, g_stream));
+    }
+    CHIP_CHECK(hipEventRecord(e1, g_stream));
+    CHIP_CHECK(hipEventSynchronize(e1));
+    float total = 0.f;
+    CHIP_CHECK(hipEventElapsedTime(&total, e0, e1));
+    *ms = total / (float)iters;
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return 0;
+}
+
+int cheetah_hip_time_attention(const float *q, const cheetah_hip_kv_view *views, size_t nviews, uint32_t q_heads,
+                               size_t rows, size_t offset, float *out, size_t iters, float *ms) {
+    CHIP_TRY(ensure_ready());
+    if (!views || nviews == 0 || iters == 0 || !ms) return fail("HIP backend: time_attention needs views and iterations.");
+    for (size_t i = 0; i < nviews; ++i) CHIP_TRY(attention_op(q, &views[i], q_heads, rows, offset, out));
+    hipEvent_t e0, e1;
+    CHIP_CHECK(hipEventCreate(&e0));
+    CHIP_CHECK(hipEventCreate(&e1));
+    CHIP_CHECK(hipEventRecord(e0, g_stream));
+    for (size_t i = 0; i < iters; ++i) CHIP_TRY(attention_op(q, &views[i % nviews], q_heads, rows, offset, out));
     CHIP_CHECK(hipEventRecord(e1, g_stream));
     CHIP_CHECK(hipEventSynchronize(e1));
     float total = 0.f;

@@ -41,6 +41,8 @@
 // Math per phase is that of the multi-kernel path (gemv.hip, attention.hip,
 // misc.hip), i.e. the reference path of ops.rs / qwen2.rs; only f32
 // summation orders differ.
+#include <cstdlib>
+
 #include "decode_fused.hpp"
 #include "wunit.hpp"
 
@@ -983,7 +985,15 @@ int launch_one(const FusedArgs &a, int nb, hipStream_t s) {
         return fail("HIP backend: persistent decode needs more LDS than a block has.");
     void *args[] = {(void *)&a};
     CHIP_CHECK(hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    CHIP_CHECK(hipLaunchCooperativeKernel((const void *)k, dim3(nb), dim3(kThreads), args, (unsigned)lds, s));
+    // CHEETAH_HIP_FUSED_PLAIN_LAUNCH=1: an ordinary launch instead of the
+    // cooperative one (for tools that do not handle cooperative launches).
+    // One block per CU is co-resident on an otherwise idle device; were it
+    // not, the bounded polls time out and the call fails.
+    const char *plain = getenv("CHEETAH_HIP_FUSED_PLAIN_LAUNCH");
+    if (plain && plain[0] == '1')
+        CHIP_CHECK(hipLaunchKernel((const void *)k, dim3(nb), dim3(kThreads), args, (unsigned)lds, s));
+    else
+        CHIP_CHECK(hipLaunchCooperativeKernel((const void *)k, dim3(nb), dim3(kThreads), args, (unsigned)lds, s));
     return 0;
 }
 

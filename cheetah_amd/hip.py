@@ -55,6 +55,7 @@ SIGNATURES = {
     "cheetah_hip_free": (_c.c_int, [_VP]),
     "cheetah_hip_upload": (_c.c_int, [_VP, _VP, _SZ]),
     "cheetah_hip_download": (_c.c_int, [_VP, _VP, _SZ]),
+    "cheetah_hip_copy": (_c.c_int, [_VP, _VP, _SZ]),
     "cheetah_hip_synchronize": (_c.c_int, []),
     "cheetah_hip_gemv_bf16": (_c.c_int, [_VP, _SZ, _SZ, _VP, _VP]),
     "cheetah_hip_gemv_q8": (_c.c_int, [_VP, _SZ, _SZ, _VP, _VP]),
@@ -85,6 +86,9 @@ SIGNATURES = {
     "cheetah_hip_model_free": (None, [_VP]),
     "cheetah_hip_time_gemv": (_c.c_int, [_c.c_uint32, _c.POINTER(_VP), _SZ, _SZ, _SZ, _VP, _VP, _SZ, _F32P]),
     "cheetah_hip_time_decode": (_c.c_int, [_VP, _c.c_uint32, _SZ, _SZ, _F32P, _F32P, _U32P]),
+    "cheetah_hip_time_gemm": (_c.c_int, [_c.c_uint32, _c.POINTER(_VP), _SZ, _SZ, _SZ, _VP, _SZ, _VP, _SZ, _F32P]),
+    "cheetah_hip_time_attention": (_c.c_int, [_VP, _c.POINTER(KvView), _SZ, _c.c_uint32, _SZ, _SZ, _VP, _SZ,
+                                               _F32P]),
 }
 
 _lib = None
@@ -131,6 +135,13 @@ def device_name() -> str:
 
 def synchronize() -> None:
     check(lib().cheetah_hip_synchronize())
+
+
+def copy(dst: "DeviceBuffer", src: "DeviceBuffer", nbytes: int) -> None:
+    """Device-to-device copy of nbytes (cheetah_hip_copy)."""
+    if nbytes > min(dst.nbytes, src.nbytes):
+        raise ValueError("copy larger than a buffer")
+    check(lib().cheetah_hip_copy(dst.ptr, src.ptr, int(nbytes)))
 
 
 class DeviceBuffer:

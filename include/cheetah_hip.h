@@ -40,6 +40,10 @@ void *cheetah_hip_alloc(size_t bytes);
 int cheetah_hip_free(void *device_ptr);
 int cheetah_hip_upload(void *device_dst, const void *host_src, size_t bytes);
 int cheetah_hip_download(void *host_dst, const void *device_src, size_t bytes);
+/* Device-to-device copy. No counterpart in the reference; measurement
+ * helper (the plain copy whose byte counters calibrate the HBM traffic of
+ * the other kernels). */
+int cheetah_hip_copy(void *device_dst, const void *device_src, size_t bytes);
 int cheetah_hip_synchronize(void);
 
 /* ------------------------------------------------------------------------
@@ -184,6 +188,14 @@ void cheetah_hip_model_free(cheetah_hip_model *m);
  * milliseconds per launch in *ms. fmt: 1 = BF16, 4 = q8, 5 = q4. */
 int cheetah_hip_time_gemv(uint32_t fmt, const void *const *w, size_t nbuf, size_t rows, size_t cols,
                           const float *x, float *y, size_t iters, float *ms);
+/* Times `iters` launches of the op-level GEMM (n input rows) over `nbuf`
+ * rotating weight buffers; mean milliseconds per launch in *ms. */
+int cheetah_hip_time_gemm(uint32_t fmt, const void *const *w, size_t nbuf, size_t rows, size_t cols,
+                          const float *x, size_t n, float *y, size_t iters, float *ms);
+/* Times `iters` launches of cheetah_hip_attention over `nviews` rotating KV
+ * caches (views[i]); mean milliseconds per launch in *ms. */
+int cheetah_hip_time_attention(const float *q, const cheetah_hip_kv_view *views, size_t nviews, uint32_t q_heads,
+                               size_t rows, size_t offset, float *out, size_t iters, float *ms);
 /* Times `steps` greedy decode steps of a model already holding `offset`
  * cached positions (the decode graph replayed back to back), and the
  * model's largest GEMV alone over the same steps; both in ms per step. */
