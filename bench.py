@@ -61,6 +61,78 @@ def cpu_baseline(shape, weights, prompt, decode_steps: int):
     }
 
 
+def _golden(name):
+    path = os.path.join(ROOT, "tests", "golden", name)
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f)
+
+
+def large_workload(args) -> int:
+    """One timed pass of a large decoder (no warmup: each phase is long and
+    the kernels are already built); decode tok/s is `value`."""
+    from cheetah_amd import configs, hip, workloads
+
+    hip.init(0)
+    MFMA_PEAK = 2500.0
+    if args.workload == "llama3-8b-q4":
+        shape = configs.LLAMA3_8B
+        g, info = workloads.llama3_8b_q4(decode_steps=256)
+        lin_bytes = sum(hip.buffer_bytes("q4", r, c) for layer in range(shape.num_layers)
+                        for _, r, c in shape.linear_units(layer))
+        weight_bytes = lin_bytes + shape.head_params() * 2
+        ctx_mid = 8192 + 128
+        pre_flops = sum(workloads.prefill_flops(shape, 512, off) for off in range(0, 8192, 512))
+        pre_s = info["prefill_s"]
+        gold = _golden("llama3_8b_q4_bf16kv_greedy.json")
+        workload = ("llama3-8b architecture (32 layers, hidden 4096, 32/8 heads, hd 128, ffn 14336, vocab 128256), "
+                    "Q4 linears quantized on the device from seeded BF16 weights, BF16 head, BF16 paged KV; "
+                    "8192-token prompt in 512-row chunks, then 256 greedy decode steps, batch 1")
+        extra = {"prefill_tok_s": info["prefill_tok_s"]}
+    else:
+        shape = configs.QWEN2_7B
+        g, info = workloads.qwen2_7b_32k(decode_steps=128)
+        weight_bytes = (shape.linear_params() + shape.head_params()) * 2
+        ctx_mid = 32768 + 64
+        pre_flops = sum(workloads.prefill_flops(shape, 1024, off) for off in range(0, 32768, 1024))
+        pre_s = info["turn1_prefill_s"]
+        gold = _golden("qwen2_7b_32k_greedy.json")
+        workload = ("qwen2-7b architecture (28 layers, hidden 3584, 28/4 heads, hd 128, ffn 18944, vocab 152064), "
+                    "BF16 weights and paged KV; turn 1: 32768-token prompt in 1024-row chunks + KV snapshot; "
+                    "turn 2: restore 30720 positions, 2048-token suffix in 1024-row chunks, 128 greedy decodes")
+        extra = {"turn1_prefill_tok_s": info["turn1_prefill_tok_s"], "turn2_prefill_tok_s": info["turn2_prefill_tok_s"],
+                 "snapshot_s": info["snapshot_s"], "restore_s": info["restore_s"]}
+    step_bytes = workloads.decode_bytes(shape, ctx_mid, weight_bytes)
+    ms_tok = 1e3 / info["decode_tok_s"]
+    gbps = step_bytes / (ms_tok * 1e-3) / 1e9
+    tflops = pre_flops / pre_s / 1e12
+    match = None
+    if gold is not None:
+        n = min(32, len(gold["tokens"]))
+        match = info["tokens"][:n] == gold["tokens"][:n]
+    result = {
+        "metric": METRIC, "value": info["decode_tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": 1, "warmup": 0,
+        "ms_per_step": round((info.get("prefill_s", 0) + info.get("turn1_prefill_s", 0) + info.get("turn2_prefill_s", 0)
+                              + info["decode_s"]) * 1e3, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q4 weights, bf16 activations" if args.workload == "llama3-8b-q4" else "bf16",
+        "data": "synthetic: seeded random-init weights (normal 0.02), seeded uniform token ids",
+        "config": {"workload": workload, "global_batch": 1, "parallelism": "none (1 GPU)"},
+        **extra,
+        "decode_ms_per_token": round(ms_tok, 4),
+        "decode_effective_gbps": round(gbps, 1), "decode_hbm_roofline_frac": round(gbps / HBM_PEAK_GBPS, 4),
+        "decode_bytes_per_token": int(step_bytes),
+        "prefill_tflops": round(tflops, 2), "prefill_mfma_frac": round(tflops / MFMA_PEAK, 4),
+        "prefill_flops": pre_flops,
+        "greedy_first32_match_golden": match,
+        "load": {"synth_s": info.get("synth_s"), "upload_s": info.get("upload_s")},
+    }
+    g.close()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -70,6 +142,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-ops", action="store_true",
                     help="skip the op-level attention / GEMV / GEMM measurements")
+    ap.add_argument("--workload", default="qwen2-0.5b", choices=["qwen2-0.5b", "llama3-8b-q4", "qwen2-7b-32k"],
+                    help="qwen2-0.5b (the headline line); the two large decoders print their own line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy 1 GiB device-to-device 3 times (calibrates rocprofv3 byte counters)")
     args = ap.parse_args()
@@ -85,6 +159,9 @@ def main() -> int:
         print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported "
                                    "(the decoder is not sharded)", "n_gpus": args.gpus}))
         return 2
+
+    if args.workload != "qwen2-0.5b":
+        return large_workload(args)
 
     import numpy as np
 

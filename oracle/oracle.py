@@ -78,6 +78,8 @@ def lib():
         L.ref_silu_multiply.argtypes = [_F32P, _F32P, _SZ]
         L.ref_softmax.argtypes = [_F32P, _SZ]
         L.ref_attention.argtypes = [_F32P, _F32P, _SZ, _F32P, _F32P, _SZ, _SZ, _SZ, _SZ, _SZ]
+        L.ref_attention_rows.argtypes = [_F32P, _F32P, _SZ, _SZ, _F32P, _F32P, _SZ, _SZ, _SZ, _SZ]
+        L.ref_gemm_quant.argtypes = [_U8P, ctypes.c_uint32, _SZ, _SZ, _F32P, _SZ, _F32P]
         L.ref_set_threads.argtypes = [ctypes.c_int]
         L.ref_get_threads.restype = ctypes.c_int
         L.ref_model_create.argtypes = [ctypes.POINTER(RefConfig), ctypes.c_uint32, ctypes.c_int]
@@ -171,6 +173,16 @@ def gemv_quant(buffer: np.ndarray, rows: int, cols: int, x, fmt: str) -> np.ndar
     return y
 
 
+def gemm_quant(buffer: np.ndarray, rows: int, cols: int, x, fmt: str) -> np.ndarray:
+    """n tokens at once (x [n, cols] -> y [n, rows]); bit-identical to per-token gemv_quant."""
+    x = _f32(x).reshape(-1, cols)
+    y = np.empty((x.shape[0], rows), np.float32)
+    buf = np.ascontiguousarray(buffer, dtype=np.uint8)
+    lib().ref_gemm_quant(_p(buf, _U8P), 4 if fmt == "q8" else 5, rows, cols, _p(x, _F32P), x.shape[0],
+                         _p(y, _F32P))
+    return y
+
+
 def dequant(buffer: np.ndarray, rows: int, cols: int, fmt: str) -> np.ndarray:
     """Every dequantized value scale * code (Q8Matrix/Q4Matrix::dequant_value)."""
     buf = np.ascontiguousarray(buffer, dtype=np.uint8)
@@ -224,6 +236,22 @@ def attention(keys, values, q, q_heads: int, kv_heads: int, head_dim: int, posit
     out = np.zeros(q_heads * head_dim, np.float32)
     lib().ref_attention(_p(k, _F32P), _p(v, _F32P), cache_len, _p(qq, _F32P), _p(out, _F32P), q_heads, kv_heads,
                         head_dim, position, sliding_window)
+    return out
+
+
+def attention_rows(keys, values, q, q_heads: int, kv_heads: int, head_dim: int, offset: int,
+                   sliding_window: int = 0) -> np.ndarray:
+    """One chunk: keys/values f32 [offset + rows, kv_heads, head_dim], q [rows, q_heads*head_dim]; row r
+    attends over the first offset + r + 1 positions."""
+    k = _f32(keys)
+    v = _f32(values)
+    qq = _f32(q).reshape(-1, q_heads * head_dim)
+    rows = qq.shape[0]
+    if k.size != (offset + rows) * kv_heads * head_dim:
+        raise ValueError("cache does not hold offset + rows positions")
+    out = np.zeros_like(qq)
+    lib().ref_attention_rows(_p(k, _F32P), _p(v, _F32P), offset, rows, _p(qq, _F32P), _p(out, _F32P), q_heads,
+                             kv_heads, head_dim, sliding_window)
     return out
 
 

@@ -351,21 +351,95 @@ void ref_gemv_q4(const uint8_t *buffer, size_t rows, size_t cols, const float *x
     });
 }
 
+}  // extern "C"
+
+namespace {
+
+// Per-token gemv_q8 / gemv_q4 (ops.rs:544-630; the reference's linear_batch
+// runs one gemv per token for quantized units, ops.rs:1244-1326) evaluated
+// for many tokens at once. Vector lanes hold different tokens; each token's
+// sum is still the sequential fold over columns from 0.0, with
+// w = scale * code rounded once, then w * x and the add rounded separately,
+// so every output is bit-identical to ref_gemv_q* on that token alone.
+template <int FMT>
+void gemm_quant_tokens(const uint8_t *buffer, size_t rows, size_t cols, const float *x, size_t n, float *y) {
+    constexpr size_t TG = 16;  // tokens per group (two AVX2 vectors)
+    constexpr size_t RB = 4;   // weight rows per block
+    const size_t row_bytes = FMT == 4 ? (cols + 3) / 4 * 4 : ref_q4_row_stride(cols);
+    const size_t head = rows * 4;
+    const size_t groups = (n + TG - 1) / TG;
+    std::vector<float> xt(groups * cols * TG, 0.0f);  // [group][col][TG]
+    for (size_t t = 0; t < n; ++t)
+        for (size_t c = 0; c < cols; ++c) xt[(t / TG) * cols * TG + c * TG + t % TG] = x[t * cols + c];
+    const size_t blocks = (rows + RB - 1) / RB;
+    pool().parallel_for(blocks, [&](size_t b) {
+        const size_t r0 = b * RB, nr = std::min(RB, rows - r0);
+        std::vector<float> w(RB * cols, 0.0f);
+        for (size_t i = 0; i < nr; ++i) {
+            const float scale = load_f32(buffer + (r0 + i) * 4);
+            const uint8_t *row = buffer + head + (r0 + i) * row_bytes;
+            for (size_t c = 0; c < cols; ++c) {
+                const float code = FMT == 4 ? (float)(int8_t)row[c] : (float)q4_code(row[c / 2], c);
+                w[i * cols + c] = scale * code;
+            }
+        }
+        alignas(32) float lanes[TG];
+        for (size_t g = 0; g < groups; ++g) {
+            __m256 acc[RB][2];
+            for (size_t i = 0; i < RB; ++i) acc[i][0] = acc[i][1] = _mm256_setzero_ps();
+            const float *xg = xt.data() + g * cols * TG;
+            for (size_t c = 0; c < cols; ++c) {
+                const __m256 x0 = _mm256_loadu_ps(xg + c * TG), x1 = _mm256_loadu_ps(xg + c * TG + 8);
+                for (size_t i = 0; i < RB; ++i) {
+                    const __m256 wv = _mm256_broadcast_ss(&w[i * cols + c]);
+                    acc[i][0] = _mm256_add_ps(acc[i][0], _mm256_mul_ps(wv, x0));
+                    acc[i][1] = _mm256_add_ps(acc[i][1], _mm256_mul_ps(wv, x1));
+                }
+            }
+            for (size_t i = 0; i < nr; ++i) {
+                _mm256_store_ps(lanes, acc[i][0]);
+                _mm256_store_ps(lanes + 8, acc[i][1]);
+                for (size_t t = 0; t < TG && g * TG + t < n; ++t) y[(g * TG + t) * rows + r0 + i] = lanes[t];
+            }
+        }
+    });
+}
+
+}  // namespace
+
+extern "C" {
+
+// n tokens through gemv_q8 (fmt 4) or gemv_q4 (fmt 5), bit-identical to n
+// separate ref_gemv_q* calls; y is [n][rows].
+void ref_gemm_quant(const uint8_t *buffer, uint32_t fmt, size_t rows, size_t cols, const float *x, size_t n,
+                    float *y) {
+    if (n == 1) {
+        if (fmt == 4) ref_gemv_q8(buffer, rows, cols, x, y);
+        else ref_gemv_q4(buffer, rows, cols, x, y);
+        return;
+    }
+    if (fmt == 4) gemm_quant_tokens<4>(buffer, rows, cols, x, n, y);
+    else gemm_quant_tokens<5>(buffer, rows, cols, x, n, y);
+}
+
 // q8.rs:91-125 quantize: scale = max|w| / 127 (1.0 for a zero row).
 int ref_quantize_q8(const float *values, size_t rows, size_t cols, uint8_t *out, size_t out_len) {
     if (out_len != ref_q8_buffer_bytes(rows, cols))
         return fail("Q8 quantization output buffer has the wrong length.");
     std::memset(out, 0, out_len);
     const size_t row_bytes = (cols + 3) / 4 * 4;
-    for (size_t r = 0; r < rows; ++r) {
-        const float *v = values + r * cols;
-        float max_abs = 0.0f;
-        for (size_t c = 0; c < cols; ++c) max_abs = std::fmax(max_abs, std::fabs(v[c]));
-        float scale = max_abs > 0.0f ? max_abs / 127.0f : 1.0f;
-        std::memcpy(out + r * 4, &scale, 4);
-        for (size_t c = 0; c < cols; ++c)
-            out[rows * 4 + r * row_bytes + c] = (uint8_t)quant_code(v[c], scale, 127.0f);
-    }
+    // Rows are independent, so they are quantized in parallel blocks.
+    pool().parallel_for((rows + 63) / 64, [&](size_t blk) {
+        for (size_t r = blk * 64; r < std::min(rows, blk * 64 + 64); ++r) {
+            const float *v = values + r * cols;
+            float max_abs = 0.0f;
+            for (size_t c = 0; c < cols; ++c) max_abs = std::fmax(max_abs, std::fabs(v[c]));
+            float scale = max_abs > 0.0f ? max_abs / 127.0f : 1.0f;
+            std::memcpy(out + r * 4, &scale, 4);
+            for (size_t c = 0; c < cols; ++c)
+                out[rows * 4 + r * row_bytes + c] = (uint8_t)quant_code(v[c], scale, 127.0f);
+        }
+    });
     return 0;
 }
 
@@ -375,17 +449,19 @@ int ref_quantize_q4(const float *values, size_t rows, size_t cols, uint8_t *out,
         return fail("Q4 quantization output buffer has the wrong length.");
     std::memset(out, 0, out_len);
     const size_t row_bytes = ref_q4_row_stride(cols);
-    for (size_t r = 0; r < rows; ++r) {
-        const float *v = values + r * cols;
-        float max_abs = 0.0f;
-        for (size_t c = 0; c < cols; ++c) max_abs = std::fmax(max_abs, std::fabs(v[c]));
-        float scale = max_abs > 0.0f ? max_abs / 7.0f : 1.0f;
-        std::memcpy(out + r * 4, &scale, 4);
-        for (size_t c = 0; c < cols; ++c) {
-            int8_t q = quant_code(v[c], scale, 7.0f);
-            out[rows * 4 + r * row_bytes + c / 2] |= (uint8_t)(((uint8_t)q & 0x0F) << ((c % 2) * 4));
+    pool().parallel_for((rows + 63) / 64, [&](size_t blk) {
+        for (size_t r = blk * 64; r < std::min(rows, blk * 64 + 64); ++r) {
+            const float *v = values + r * cols;
+            float max_abs = 0.0f;
+            for (size_t c = 0; c < cols; ++c) max_abs = std::fmax(max_abs, std::fabs(v[c]));
+            float scale = max_abs > 0.0f ? max_abs / 7.0f : 1.0f;
+            std::memcpy(out + r * 4, &scale, 4);
+            for (size_t c = 0; c < cols; ++c) {
+                int8_t q = quant_code(v[c], scale, 7.0f);
+                out[rows * 4 + r * row_bytes + c / 2] |= (uint8_t)(((uint8_t)q & 0x0F) << ((c % 2) * 4));
+            }
         }
-    }
+    });
     return 0;
 }
 
@@ -500,6 +576,125 @@ extern "C" void ref_attention(const float *keys, const float *values, size_t cac
         for (size_t h = 0; h < q_heads; ++h) run(h);
 }
 
+namespace {
+
+// Keys regrouped as [kv_head][block of 8 positions][head_dim][8] (the last
+// block zero-padded), so that 8 positions' scores sit in one vector's lanes.
+size_t block_keys(const float *keys, size_t len, size_t kv_heads, size_t hd, std::vector<float> &kt) {
+    const size_t blocks = (len + 7) / 8;
+    kt.assign(kv_heads * blocks * hd * 8, 0.0f);
+    const size_t kv_dim = kv_heads * hd, span = 64;
+    const size_t items = (blocks + span - 1) / span;
+    pool().parallel_for(kv_heads * items, [&](size_t it) {
+        const size_t h = it / items, b0 = (it % items) * span, b1 = std::min(blocks, b0 + span);
+        for (size_t b = b0; b < b1; ++b) {
+            float *dst = kt.data() + (h * blocks + b) * hd * 8;
+            for (size_t j = 0; j < 8 && b * 8 + j < len; ++j) {
+                const float *src = keys + (b * 8 + j) * kv_dim + h * hd;
+                for (size_t d = 0; d < hd; ++d) dst[d * 8 + j] = src[d];
+            }
+        }
+    });
+    return blocks;
+}
+
+constexpr size_t kTile = 8;  // (row, head) pairs of one KV head per tile
+
+// attention_head (ops.rs:1424-1467) for up to 8 (row, head) pairs that share
+// a KV head, so each key block and value row is loaded once per tile. Per
+// pair the arithmetic is the scalar code's: every score is the sequential
+// fold over head_dim from -0.0 (product, then add, each rounded) times
+// 1/sqrt(hd); the same softmax; every output dim the sequential fold over
+// positions of w * v from 0.0. Positions a pair does not see get w = 0,
+// whose product +-0 leaves a finite fold unchanged, like the reference's
+// `w == 0` skip.
+struct TilePair {
+    const float *q;
+    float *out;
+    size_t len, window_start;
+};
+
+void attention_tile(const float *kt_head, const float *values, const TilePair *pairs, size_t np, size_t kv_dim,
+                    size_t kv_base, size_t hd, float scale) {
+    size_t max_len = 0, min_ws = SIZE_MAX;
+    for (size_t j = 0; j < np; ++j) {
+        max_len = std::max(max_len, pairs[j].len);
+        min_ws = std::min(min_ws, pairs[j].window_start);
+    }
+    thread_local std::vector<float> scores, zeros;
+    scores.assign(kTile * max_len, -INFINITY);
+    zeros.assign(hd, 0.0f);
+    const float *qs[kTile];
+    for (size_t j = 0; j < kTile; ++j) qs[j] = j < np ? pairs[j].q : zeros.data();
+    alignas(32) float lanes[kTile][8];
+    for (size_t b = min_ws / 8; b < (max_len + 7) / 8; ++b) {
+        __m256 acc[kTile];
+        for (size_t j = 0; j < kTile; ++j) acc[j] = _mm256_set1_ps(kSumInit);
+        const float *k = kt_head + b * hd * 8;
+        for (size_t d = 0; d < hd; ++d) {
+            const __m256 kv = _mm256_loadu_ps(k + d * 8);
+            for (size_t j = 0; j < kTile; ++j)
+                acc[j] = _mm256_add_ps(acc[j], _mm256_mul_ps(kv, _mm256_broadcast_ss(qs[j] + d)));
+        }
+        for (size_t j = 0; j < kTile; ++j) _mm256_store_ps(lanes[j], acc[j]);
+        for (size_t j = 0; j < np; ++j)
+            for (size_t l = 0; l < 8; ++l) {
+                const size_t pos = b * 8 + l;
+                if (pos >= pairs[j].window_start && pos < pairs[j].len)
+                    scores[j * max_len + pos] = lanes[j][l] * scale;
+            }
+    }
+    for (size_t j = 0; j < np; ++j) {
+        float *sj = scores.data() + j * max_len;
+        ref_softmax(sj, pairs[j].len);
+        for (size_t pos = pairs[j].len; pos < max_len; ++pos) sj[pos] = 0.0f;
+    }
+    for (size_t j = np; j < kTile; ++j)
+        for (size_t pos = 0; pos < max_len; ++pos) scores[j * max_len + pos] = 0.0f;
+    for (size_t dc = 0; dc < hd; dc += 8) {
+        __m256 acc[kTile];
+        for (size_t j = 0; j < kTile; ++j) acc[j] = _mm256_setzero_ps();
+        for (size_t pos = min_ws; pos < max_len; ++pos) {
+            const __m256 v = _mm256_loadu_ps(values + pos * kv_dim + kv_base + dc);
+            for (size_t j = 0; j < kTile; ++j)
+                acc[j] = _mm256_add_ps(acc[j], _mm256_mul_ps(_mm256_broadcast_ss(&scores[j * max_len + pos]), v));
+        }
+        for (size_t j = 0; j < np; ++j) _mm256_storeu_ps(pairs[j].out + dc, acc[j]);
+    }
+}
+
+}  // namespace
+
+extern "C" void ref_attention_rows(const float *keys, const float *values, size_t offset, size_t rows,
+                                   const float *q, float *out, size_t q_heads, size_t kv_heads, size_t head_dim,
+                                   size_t sliding_window) {
+    if (rows == 0) return;
+    const size_t kv_dim = kv_heads * head_dim, group = q_heads / kv_heads, qd = q_heads * head_dim;
+    if (head_dim % 8 != 0) {  // the tiles work in 8-dim slices; other widths take the per-row code
+        for (size_t r = 0; r < rows; ++r)
+            ref_attention(keys, values, offset + r + 1, q + r * qd, out + r * qd, q_heads, kv_heads, head_dim,
+                          offset + r, sliding_window);
+        return;
+    }
+    std::vector<float> kt;
+    const size_t blocks = block_keys(keys, offset + rows, kv_heads, head_dim, kt);
+    const float scale = 1.0f / std::sqrt((float)head_dim);
+    const size_t pairs_per_head = rows * group, tiles = (pairs_per_head + kTile - 1) / kTile;
+    pool().parallel_for(kv_heads * tiles, [&](size_t it) {
+        const size_t kvh = it / tiles, p0 = (it % tiles) * kTile;
+        const size_t np = std::min(kTile, pairs_per_head - p0);
+        TilePair pairs[kTile];
+        for (size_t j = 0; j < np; ++j) {
+            const size_t r = (p0 + j) / group, h = kvh * group + (p0 + j) % group;
+            const size_t position = offset + r, len = position + 1;
+            size_t ws = sliding_window == 0 ? 0 : (len > sliding_window ? len - sliding_window : 0);
+            pairs[j] = TilePair{q + r * qd + h * head_dim, out + r * qd + h * head_dim, len, std::min(ws, len - 1)};
+        }
+        attention_tile(kt.data() + kvh * blocks * head_dim * 8, values, pairs, np, kv_dim, kvh * head_dim,
+                       head_dim, scale);
+    });
+}
+
 // ===========================================================================
 // Model: OpsToolbox state + the qwen2/llama forward assembly.
 // ===========================================================================
@@ -599,17 +794,16 @@ int linear_rows(ref_model *m, const std::string &unit, size_t rows, size_t cols,
                 return fail("Linear unit '" + unit + "' does not match its " + std::to_string(rows) + "x" +
                             std::to_string(cols) + " shape.");
             std::vector<float> values(count);
-            for (size_t i = 0; i < count; ++i) values[i] = scalar_at(*u, i);
+            pool().parallel_for((count + (1 << 20) - 1) >> 20, [&](size_t b) {
+                for (size_t i = b << 20; i < std::min(count, (b + 1) << 20); ++i) values[i] = scalar_at(*u, i);
+            });
             std::vector<uint8_t> buf(m->quant_format == 4 ? ref_q8_buffer_bytes(rows, cols)
                                                           : ref_q4_buffer_bytes(rows, cols));
             if (m->quant_format == 4) ref_quantize_q8(values.data(), rows, cols, buf.data(), buf.size());
             else ref_quantize_q4(values.data(), rows, cols, buf.data(), buf.size());
             it = m->quant.emplace(unit, std::move(buf)).first;
         }
-        for (size_t t = 0; t < n; ++t) {
-            if (m->quant_format == 4) ref_gemv_q8(it->second.data(), rows, cols, x + t * cols, y + t * rows);
-            else ref_gemv_q4(it->second.data(), rows, cols, x + t * cols, y + t * rows);
-        }
+        ref_gemm_quant(it->second.data(), m->quant_format, rows, cols, x, n, y);
         return 0;
     }
     if (u->dtype == 1) {
@@ -649,15 +843,18 @@ int forward_layer_chunk(ref_model *m, size_t layer, size_t offset, size_t rows) 
     add_bias_rows(m, p + "self_attn.q_proj", m->q.data(), rows, qd);
     add_bias_rows(m, p + "self_attn.k_proj", m->k.data(), rows, kvd);
     add_bias_rows(m, p + "self_attn.v_proj", m->v.data(), rows, kvd);
-    for (size_t r = 0; r < rows; ++r) {
-        size_t pos = offset + r;
-        ref_rope_heads(m->q.data() + r * qd, c.q_heads, c.head_dim, c.rotary_dim, pos, c.rope_theta);
-        ref_rope_heads(m->k.data() + r * kvd, c.kv_heads, c.head_dim, c.rotary_dim, pos, c.rope_theta);
-        cache_append(m, layer, m->k.data() + r * kvd, m->v.data() + r * kvd);
-        size_t cache_len = m->kv_k[layer].size() / kvd;
-        ref_attention(m->kv_k[layer].data(), m->kv_v[layer].data(), cache_len, m->q.data() + r * qd,
-                      m->attn_out.data() + r * qd, c.q_heads, c.kv_heads, c.head_dim, pos, c.sliding_window);
-    }
+    // The reference ropes, appends and attends row by row (qwen2.rs:314-343).
+    // Row r reads only cache positions <= offset + r and the appended K/V do
+    // not depend on attention outputs, so the rows are roped in parallel,
+    // appended in order, then attended in parallel with identical results.
+    pool().parallel_for(rows, [&](size_t r) {
+        ref_rope_heads(m->q.data() + r * qd, c.q_heads, c.head_dim, c.rotary_dim, offset + r, c.rope_theta);
+        ref_rope_heads(m->k.data() + r * kvd, c.kv_heads, c.head_dim, c.rotary_dim, offset + r, c.rope_theta);
+    });
+    for (size_t r = 0; r < rows; ++r) cache_append(m, layer, m->k.data() + r * kvd, m->v.data() + r * kvd);
+    if (m->kv_k[layer].size() / kvd != offset + rows) return fail("KV cache length does not match the offset.");
+    ref_attention_rows(m->kv_k[layer].data(), m->kv_v[layer].data(), offset, rows, m->q.data(),
+                       m->attn_out.data(), c.q_heads, c.kv_heads, c.head_dim, c.sliding_window);
     if (linear_rows(m, p + "self_attn.o_proj.weight", H, qd, m->attn_out.data(), rows, m->proj.data())) return -1;
     add_bias_rows(m, p + "self_attn.o_proj", m->proj.data(), rows, H);
     for (size_t i = 0; i < rows * H; ++i) m->hidden[i] = m->hidden[i] + m->proj[i];

@@ -35,6 +35,11 @@ void ref_gemv_q8(const uint8_t *buffer, size_t rows, size_t cols,
                  const float *x, float *y);
 void ref_gemv_q4(const uint8_t *buffer, size_t rows, size_t cols,
                  const float *x, float *y);
+/* n tokens through gemv_q8 (fmt 4) / gemv_q4 (fmt 5) at once; bit-identical
+ * to n per-token calls (the reference's linear_batch for quantized units,
+ * ops.rs:1244-1326). y is [n][rows]. */
+void ref_gemm_quant(const uint8_t *buffer, uint32_t fmt, size_t rows, size_t cols,
+                    const float *x, size_t n, float *y);
 size_t ref_q8_buffer_bytes(size_t rows, size_t cols);
 size_t ref_q4_buffer_bytes(size_t rows, size_t cols);
 size_t ref_q4_row_stride(size_t cols);
@@ -58,6 +63,12 @@ void ref_softmax(float *scores, size_t n);
 void ref_attention(const float *keys, const float *values, size_t cache_len,
                    const float *q, float *out, size_t q_heads, size_t kv_heads,
                    size_t head_dim, size_t position, size_t sliding_window);
+/* `rows` query rows of one chunk at positions offset..offset+rows-1 over a
+ * cache already holding offset+rows positions; row r sees the first
+ * offset+r+1. Bit-identical to ref_attention per row (ops.rs:1357-1467). */
+void ref_attention_rows(const float *keys, const float *values, size_t offset,
+                        size_t rows, const float *q, float *out, size_t q_heads,
+                        size_t kv_heads, size_t head_dim, size_t sliding_window);
 
 /* ---- model (src/chat/registrations/{qwen2,llama}.rs) ---- */
 typedef struct ref_config {

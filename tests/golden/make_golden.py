@@ -1,6 +1,6 @@
 """Writes the greedy-decode golden fixtures from the CPU oracle.
 
-Usage: python tests/golden/make_golden.py [qwen2_0_5b] [qwen2_0_5b_bf16kv]
+Usage: python tests/golden/make_golden.py [name ...]   (names: the MAKERS keys)
 
 Config 1: Qwen2-0.5B shape, seeded random-init BF16 weights (cheetah_amd.synth,
 seed 0), 512 seeded prompt tokens (seed 1) prefilled in chunks of 128, then
@@ -55,9 +55,86 @@ def make_qwen2_0_5b(steps=64, kv_bf16=False):
     }
 
 
+def _decode(m, logits, position, steps):
+    tokens, margins = [], []
+    for step in range(steps):
+        srt = np.sort(logits)
+        margins.append(float(srt[-1] - srt[-2]))
+        tok = greedy(logits)
+        tokens.append(tok)
+        if step + 1 < steps:
+            logits = m.forward([tok], position + step)
+    return tokens, margins
+
+
+def make_llama3_8b_q4(steps=40, kv_bf16=False):
+    """Config 4: Llama-3-8B shape, Q4 linears quantized from the seeded BF16
+    weights (q4.rs:126-161), BF16 embedding/head/norms; an 8192-token prompt
+    (seed 1) in 512-row chunks, then greedy decode."""
+    shape = configs.LLAMA3_8B
+    w = synth.make_weights(shape)
+    prompt = synth.make_tokens(shape.vocab_size, 8192, seed=1)
+    m = oracle.RefModel(shape, w, quant="q4", kv_bf16=kv_bf16)
+    t0 = time.time()
+    logits = m.forward(prompt, 0, chunk_rows=512)
+    t_prefill = time.time() - t0
+    head = logits[:2048].tolist()
+    t0 = time.time()
+    tokens, margins = _decode(m, logits, 8192, steps)
+    return {
+        "config": "llama3-8b q4 (linears), bf16 embedding/head/norms, weights seed 0, prompt seed 1",
+        "kv_cache": "bf16 (K/V rounded to nearest even on append)" if kv_bf16 else "f32 (reference)",
+        "prompt_len": 8192, "prompt_seed": 1, "chunk_rows": 512,
+        "tokens": tokens, "top2_margins": margins, "prefill_logits_head": head,
+        "oracle_threads": oracle.get_threads(),
+        "oracle_seconds": {"prefill": round(t_prefill, 3), "decode": round(time.time() - t0, 3)},
+    }
+
+
+def make_qwen2_7b_32k(steps=40):
+    """Config 5: Qwen2-7B shape, BF16 weights and BF16 KV. Turn 1: a
+    32768-token prompt (seed 1) in 1024-row chunks, KV snapshot. Turn 2: the
+    first 30720 prompt tokens + 2048 new ones (seed 2); the prefix is restored
+    from the snapshot (engine.rs:523-601 semantics), the suffix prefilled in
+    1024-row chunks, then greedy decode."""
+    shape = configs.QWEN2_7B
+    w = synth.make_weights(shape)
+    prompt1 = synth.make_tokens(shape.vocab_size, 32768, seed=1)
+    suffix = synth.make_tokens(shape.vocab_size, 2048, seed=2)
+    m = oracle.RefModel(shape, w, kv_bf16=True)
+    t0 = time.time()
+    logits1 = m.forward(prompt1, 0, chunk_rows=1024)
+    t_turn1 = time.time() - t0
+    snap = m.kv_snapshot()
+    m.clear_cache()
+    assert m.restore_kv_prefix(snap, 30720)
+    del snap
+    t0 = time.time()
+    logits2 = m.forward(suffix, 30720, chunk_rows=1024)
+    t_turn2 = time.time() - t0
+    t0 = time.time()
+    tokens, margins = _decode(m, logits2, 32768, steps)
+    srt = np.sort(logits1)
+    return {
+        "config": "qwen2-7b bf16, weights seed 0; turn 1 prompt seed 1 (32768), turn 2 = first 30720 + 2048 "
+                  "tokens of seed 2",
+        "kv_cache": "bf16 (K/V rounded to nearest even on append)",
+        "prompt_len": 32768, "prefix_reused": 30720, "suffix_len": 2048, "suffix_seed": 2, "chunk_rows": 1024,
+        "turn1_token": greedy(logits1), "turn1_margin": float(srt[-1] - srt[-2]),
+        "turn1_logits_head": logits1[:2048].tolist(), "turn2_logits_head": logits2[:2048].tolist(),
+        "tokens": tokens, "top2_margins": margins,
+        "oracle_threads": oracle.get_threads(),
+        "oracle_seconds": {"turn1_prefill": round(t_turn1, 3), "turn2_prefill": round(t_turn2, 3),
+                           "decode": round(time.time() - t0, 3)},
+    }
+
+
 MAKERS = {
     "qwen2_0_5b": make_qwen2_0_5b,
     "qwen2_0_5b_bf16kv": lambda: make_qwen2_0_5b(kv_bf16=True),
+    "llama3_8b_q4": make_llama3_8b_q4,
+    "llama3_8b_q4_bf16kv": lambda: make_llama3_8b_q4(kv_bf16=True),
+    "qwen2_7b_32k": make_qwen2_7b_32k,
 }
 
 if __name__ == "__main__":
@@ -67,4 +144,4 @@ if __name__ == "__main__":
         path = os.path.join(os.path.dirname(os.path.abspath(__file__)), f"{name}_greedy.json")
         with open(path, "w") as f:
             json.dump(data, f)
-        print(path, data["tokens"][:16], min(data["top2_margins"][:32]))
+        print(path, data["tokens"][:16], min(data["top2_margins"][:32]), data["oracle_seconds"], flush=True)

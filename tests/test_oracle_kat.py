@@ -268,3 +268,35 @@ def test_bf16_rounding_helper():
     # 1 + 2^-8 is a tie between 1.0 and 1+2^-7: rounds to even (1.0)
     assert bits.tolist()[:2] == [0x3F80, 0x3F80]
     assert bf16_to_f32(bits)[3] == -3.5
+
+
+@pytest.mark.parametrize("fmt", ["q8", "q4"])
+@pytest.mark.parametrize("rows,cols,n", [(1, 1, 2), (5, 17, 3), (13, 33, 17), (64, 100, 40), (9, 257, 33)])
+def test_multi_token_quant_gemm_matches_per_token_gemv_bit_exact(oracle, fmt, rows, cols, n):
+    # The reference runs quantized units one gemv per token (ops.rs:1244-1326);
+    # the oracle's many-token form must reproduce each of those bit for bit.
+    rng = np.random.default_rng(rows * 1000 + cols + n)
+    buf = oracle.quantize(rng.standard_normal((rows, cols)).astype(np.float32), fmt)
+    x = rng.standard_normal((n, cols)).astype(np.float32)
+    got = oracle.gemm_quant(buf, rows, cols, x, fmt)
+    for t in range(n):
+        ref = oracle.gemv_quant(buf, rows, cols, x[t], fmt)
+        assert np.array_equal(got[t].view(np.uint32), ref.view(np.uint32)), (t, got[t], ref)
+
+
+@pytest.mark.parametrize("qh,kvh,hd,offset,rows,window", [
+    (4, 2, 16, 0, 1, 0), (8, 2, 16, 0, 37, 0), (7, 1, 64, 29, 45, 0), (8, 8, 32, 100, 3, 0),
+    (4, 4, 16, 10, 50, 13), (28, 4, 128, 7, 9, 0)])
+def test_chunk_attention_matches_per_row_attention_bit_exact(oracle, qh, kvh, hd, offset, rows, window):
+    # qwen2.rs:314-343 attends row by row over the growing cache; the oracle's
+    # chunk form (blocked keys, rows in parallel) must give the same bits.
+    rng = np.random.default_rng(qh * 7 + offset + rows)
+    L = offset + rows
+    k = rng.standard_normal((L, kvh, hd)).astype(np.float32)
+    v = rng.standard_normal((L, kvh, hd)).astype(np.float32)
+    q = rng.standard_normal((rows, qh * hd)).astype(np.float32)
+    got = oracle.attention_rows(k, v, q, qh, kvh, hd, offset, sliding_window=window)
+    for r in range(rows):
+        n = offset + r + 1
+        ref = oracle.attention(k[:n], v[:n], q[r], qh, kvh, hd, position=offset + r, sliding_window=window)
+        assert np.array_equal(got[r].view(np.uint32), ref.view(np.uint32)), r
