@@ -16,9 +16,13 @@ int g_device = -1;
 hipStream_t g_stream = nullptr;
 std::string g_name = "hip-gfx950";
 size_t g_max_lds = 65536;
+int g_cus = 256;
+size_t g_lds_per_cu = 160 * 1024;
 }  // namespace
 
 size_t device_max_lds() { return g_max_lds; }
+int device_cus() { return g_cus; }
+size_t device_lds_per_cu() { return g_lds_per_cu; }
 
 void set_error(const std::string &message) { g_error = message; }
 const char *last_error() { return g_error.c_str(); }
@@ -55,6 +59,8 @@ int cheetah_hip_init(int device) {
                     "; this library is built for gfx950 (MI355X) only.");
     CHIP_CHECK(hipSetDevice(device));
     g_max_lds = prop.sharedMemPerBlock;
+    g_cus = prop.multiProcessorCount;
+    if (prop.maxSharedMemoryPerMultiProcessor > 0) g_lds_per_cu = prop.maxSharedMemoryPerMultiProcessor;
     CHIP_CHECK(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
     g_device = device;
     g_name = std::string("hip-") + arch.substr(0, 6) + " (" + prop.name + ")";

@@ -11,6 +11,11 @@
 // block. The first weight loads are issued before the prologue and the
 // stream is double-buffered in registers, so weight traffic starts at once
 // and overlaps the x staging.
+#include <algorithm>
+#include <mutex>
+#include <numeric>
+#include <vector>
+
 #include "kernels.hpp"
 #include "wunit.hpp"
 
@@ -203,6 +208,361 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(Args a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Aligned-unit GEMV: every row is streamed as 16-byte units from its
+// 16-byte-aligned-down start, even when the reference layout only aligns rows
+// to 4 bytes (Q4 rows of 2052 / 7172 bytes, Q8 rows of K rounded up to 4).
+// Bytes of a unit that lie outside the row (the previous row's tail or the
+// scale head before it; padding after it) meet zeros: x sits in LDS between
+// 32 zero floats on each side and the unit's x window is shifted by the row's
+// misalignment, which is a multiple of 4 floats (Q8: delta, Q4: 2 * delta for
+// delta in {0, 4, 8, 12}), so every x read stays a 16-byte LDS read. Rows of
+// one group share their misalignment: the R rows of a group are P apart,
+// P = 16 / gcd(stride mod 16, 16). The grid is persistent (occupancy-sized),
+// so each block stages x once and streams many row groups.
+// ---------------------------------------------------------------------------
+constexpr int kPad = 32;  // zero floats before and after x in LDS
+constexpr int kAThreads = 512;  // 8 waves share one x staging
+constexpr int kAWaves = kAThreads / 64;
+
+template <int FMT, int R, int KS, bool NORM, bool DUAL>
+__global__ __launch_bounds__(kAThreads) void gemv_aligned_kernel(Args a, int P) {
+    using U = Unit<FMT, 16>;
+    constexpr int E = U::E;
+    constexpr int D = 4;
+    constexpr int UNROLL = 2;
+    constexpr int GPB = kAWaves / KS;
+    constexpr int STEP = 64 * KS * UNROLL;
+    constexpr int NM = DUAL ? 2 : 1;
+    extern __shared__ float4 xs_v4[];  // 16-byte aligned
+    float *xs_all = (float *)xs_v4;
+    float *xs = xs_all + kPad;
+    __shared__ float red[kAWaves];
+    __shared__ float kred[kAWaves][NM * R];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int sub = wave % KS, gib = wave / KS;
+    const int klane = sub * 64 + lane;
+    const int K = a.K;
+    const int row_bytes = FMT == FMT_Q4 ? (K + 1) / 2 : (FMT == FMT_Q8 ? K : 2 * K);
+    const int blocks_of_rows = (a.rows + R * P - 1) / (R * P);
+    const int groups = blocks_of_rows * P;
+
+    const uint8_t *ap[NM][R];  // aligned-down row starts
+    int row_of[R];
+    int shift = 0, nfull = 0;
+    bool gvalid = false;
+    auto set_group = [&](int g) {
+        const int blk = g / P, ph = g % P;
+        const int row0 = blk * R * P + ph;
+        // The last block of rows can leave phases without a first row: such a
+        // group loads nothing and stores nothing.
+        gvalid = row0 < a.rows;
+        if (!gvalid) {
+            nfull = 0;
+            shift = 0;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                row_of[r] = a.rows;
+                ap[0][r] = a.w;
+                if constexpr (DUAL) ap[1][r] = a.w2;
+            }
+            return;
+        }
+        const uintptr_t p0 = (uintptr_t)(a.w + (size_t)row0 * a.stride);
+        const int delta = (int)(p0 & 15);
+        shift = delta * E / 16;
+        nfull = (delta + row_bytes) / 16;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int row = row0 + r * P;
+            row_of[r] = row;
+            const int rr = row < a.rows ? row : row0;  // same misalignment, always in bounds
+            ap[0][r] = a.w + (size_t)rr * a.stride - delta;
+            if constexpr (DUAL) ap[1][r] = a.w2 + (size_t)rr * a.stride - delta;
+        }
+    };
+    uint32_t cur[UNROLL][NM][R][D];
+    auto load_batch = [&](uint32_t (&buf)[UNROLL][NM][R][D], int u0) {
+#pragma unroll
+        for (int i = 0; i < UNROLL; ++i) {
+            const int u = u0 + 64 * KS * i;
+#pragma unroll
+            for (int m = 0; m < NM; ++m)
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    if (u < nfull) load_raw<16>(ap[m][r] + (size_t)u * 16, buf[i][m][r]);
+                    else buf[i][m][r][0] = buf[i][m][r][1] = buf[i][m][r][2] = buf[i][m][r][3] = 0u;
+                }
+        }
+    };
+
+    int g = blockIdx.x * GPB + gib;
+    const int gstride = gridDim.x * GPB;
+    // The first row group's first batch is in flight while x is staged.
+    if (g < groups) {
+        set_group(g);
+        load_batch(cur, klane);
+    }
+    for (int i = tid; i < kPad; i += kAThreads) {
+        xs_all[i] = 0.f;
+        xs[K + i] = 0.f;
+    }
+    // x (and the norm gain) come in as direct global->LDS copies, all issued
+    // before one wait, so staging costs one memory round trip.
+    float *gs = xs + K + kPad;  // gain as floats-of-bf16-pairs (NORM only)
+    const bool dma_x = ((uintptr_t)a.x % 16) == 0 && (K % 4) == 0;
+    const bool dma_g = NORM && ((uintptr_t)a.gain % 16) == 0 && (K % 8) == 0;
+    if (dma_x) {
+        for (int c = wave; c * 256 < K; c += kAWaves) {
+            const int f = c * 256 + lane * 4;
+            if (f < K) __builtin_amdgcn_global_load_lds(a.x + f, (__attribute__((address_space(3))) void *)(xs + c * 256), 16, 0, 0);
+        }
+    }
+    if (dma_g) {
+        for (int c = wave; c * 512 < K; c += kAWaves) {
+            const int f = c * 512 + lane * 8;
+            if (f < K) __builtin_amdgcn_global_load_lds(a.gain + f, (__attribute__((address_space(3))) void *)(gs + c * 256), 16, 0, 0);
+        }
+    }
+    if (!dma_x)
+        for (int i = tid; i < K; i += kAThreads) xs[i] = a.x[i];
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if constexpr (NORM) {
+        // RMSNorm (ops.rs:646-652): x * (inv * gain), inv = 1/sqrt(mean(x^2)+eps).
+        float ss = 0.f;
+        for (int i = tid; i < K; i += kAThreads) ss = fmaf(xs[i], xs[i], ss);
+        ss = wave_sum(ss);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        float total = 0.f;
+#pragma unroll
+        for (int w = 0; w < kAWaves; ++w) total += red[w];
+        const float inv = 1.0f / sqrtf(total / (float)K + a.eps);
+        const uint16_t *gl = (const uint16_t *)gs;
+        for (int i = tid; i < K; i += kAThreads)
+            xs[i] = xs[i] * (inv * bf16_f32(dma_g ? gl[i] : a.gain[i]));
+        __syncthreads();
+    }
+
+    // Every wave of the block runs the same number of iterations (the
+    // cross-wave K reduction below synchronizes the block).
+    const int iters = (groups - (int)blockIdx.x * GPB + gstride - 1) / gstride;
+    for (int it = 0; it < iters; ++it, g += gstride) {
+        const bool valid = g < groups && gvalid;
+        float acc[NM][R];
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[m][r] = 0.f;
+        if (valid) {
+            for (int u0 = klane; u0 < nfull; u0 += STEP) {
+                uint32_t nxt[UNROLL][NM][R][D];
+                const bool more = u0 + STEP < nfull;
+                if (more) load_batch(nxt, u0 + STEP);
+#pragma unroll
+                for (int i = 0; i < UNROLL; ++i) {
+                    const int u = u0 + 64 * KS * i;
+                    // One weight dword at a time: its E/4 x values (Q4 8,
+                    // Q8 4, BF16 2) are read once and shared by every row.
+                    const float *xu = xs + u * E - shift;
+#pragma unroll
+                    for (int d = 0; d < D; ++d) {
+                        constexpr int ED = E / 4;
+                        float xv[ED];
+                        if constexpr (ED >= 4) {
+#pragma unroll
+                            for (int q = 0; q < ED / 4; ++q) {
+                                const float4 t = ((const float4 *)(xu + d * ED))[q];
+                                xv[4 * q] = t.x;
+                                xv[4 * q + 1] = t.y;
+                                xv[4 * q + 2] = t.z;
+                                xv[4 * q + 3] = t.w;
+                            }
+                        } else {
+                            const float2 t = *(const float2 *)(xu + d * ED);
+                            xv[0] = t.x;
+                            xv[1] = t.y;
+                        }
+#pragma unroll
+                        for (int m = 0; m < NM; ++m)
+#pragma unroll
+                            for (int r = 0; r < R; ++r) {
+                                const uint32_t word = cur[i][m][r][d];
+                                if constexpr (FMT == FMT_Q4) {
+#pragma unroll
+                                    for (int n = 0; n < 8; ++n)
+                                        acc[m][r] = fmaf((float)(((int)(word << (28 - 4 * n))) >> 28), xv[n], acc[m][r]);
+                                } else if constexpr (FMT == FMT_Q8) {
+#pragma unroll
+                                    for (int b = 0; b < 4; ++b)
+                                        acc[m][r] = fmaf((float)(int)(int8_t)(word >> (8 * b)), xv[b], acc[m][r]);
+                                } else {
+                                    acc[m][r] = fmaf(bf16_lo(word), xv[0], acc[m][r]);
+                                    acc[m][r] = fmaf(bf16_hi(word), xv[1], acc[m][r]);
+                                }
+                            }
+                    }
+                }
+                if (more) {
+#pragma unroll
+                    for (int i = 0; i < UNROLL; ++i)
+#pragma unroll
+                        for (int m = 0; m < NM; ++m)
+#pragma unroll
+                            for (int r = 0; r < R; ++r)
+#pragma unroll
+                                for (int d = 0; d < D; ++d) cur[i][m][r][d] = nxt[i][m][r][d];
+                }
+            }
+            // Elements past the last whole unit (fewer than 16 bytes' worth).
+            for (int e = max(nfull * E - shift, 0) + klane; e < K; e += 64 * KS) {
+                const float xv = xs[e];
+#pragma unroll
+                for (int m = 0; m < NM; ++m)
+#pragma unroll
+                    for (int r = 0; r < R; ++r)
+                        acc[m][r] = fmaf(U::element(ap[m][r] + (shift * 16 / E), e), xv, acc[m][r]);
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[m][r] = wave_sum(acc[m][r]);
+        int orow[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) orow[r] = row_of[r];
+        // Prefetch the next group's first batch before the epilogue.
+        if (g + gstride < groups) {
+            set_group(g + gstride);
+            load_batch(cur, klane);
+        }
+        if constexpr (KS > 1) {
+            if (lane == 0) {
+#pragma unroll
+                for (int m = 0; m < NM; ++m)
+#pragma unroll
+                    for (int r = 0; r < R; ++r) kred[wave][m * R + r] = acc[m][r];
+            }
+            __syncthreads();
+            if (sub == 0) {
+#pragma unroll
+                for (int m = 0; m < NM; ++m)
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        float s = kred[wave][m * R + r];
+#pragma unroll
+                        for (int k = 1; k < KS; ++k) s += kred[wave + k][m * R + r];
+                        acc[m][r] = s;
+                    }
+            }
+            __syncthreads();
+        }
+        if (sub == 0 && valid) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int row = orow[r];
+                if (lane == r && row < a.rows) {
+                    float v = acc[0][r];
+                    if (a.sc) v = v * a.sc[row];
+                    if constexpr (DUAL) {
+                        float u = acc[1][r];
+                        if (a.sc2) u = u * a.sc2[row];
+                        // silu_multiply, ops.rs:743-747: g * (u / (1 + exp(-g))).
+                        a.y[row] = v * (u / (1.0f + expf(-v)));
+                    } else {
+                        if (a.bias) v = v + a.bias[row];
+                        if (a.epi == EPI_RESIDUAL) a.residual[row] = a.residual[row] + v;
+                        else a.y[row] = v;
+                    }
+                }
+            }
+        }
+    }
+}
+
+// Blocks of the aligned kernel one CU holds: waves per SIMD from the kernel's
+// VGPR count (512 per lane, granule 8), LDS from the device's per-CU size.
+template <class Kern>
+int aligned_blocks_per_cu(Kern kern, size_t lds) {
+    static std::mutex mu;
+    static std::vector<std::pair<const void *, int>> vgprs;
+    int regs = 0;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        for (auto &e : vgprs)
+            if (e.first == (const void *)kern) regs = e.second;
+        if (regs == 0) {
+            hipFuncAttributes attr{};
+            regs = hipFuncGetAttributes(&attr, (const void *)kern) == hipSuccess && attr.numRegs > 0 ? attr.numRegs
+                                                                                                     : 128;
+            vgprs.push_back({(const void *)kern, regs});
+        }
+    }
+    const int waves_per_simd = std::min(8, 512 / ((regs + 7) / 8 * 8));
+    const int by_waves = waves_per_simd * 4 / kAWaves;
+    const int by_lds = (int)(device_lds_per_cu() / (lds + 1024));
+    return std::max(1, std::min(by_waves, by_lds));
+}
+
+template <int FMT, int R, int KS, bool NORM, bool DUAL>
+int launch_aligned(const Args &a, int P, hipStream_t s) {
+    constexpr int GPB = kAWaves / KS;
+    const int groups = (a.rows + R * P - 1) / (R * P) * P;
+    const size_t lds = (size_t)(a.K + 2 * kPad) * sizeof(float) + (NORM ? (size_t)a.K * 2 + 16 : 0);
+    auto kern = gemv_aligned_kernel<FMT, R, KS, NORM, DUAL>;
+    const int cap = device_cus() * aligned_blocks_per_cu(kern, lds);
+    const int blocks = std::max(1, std::min((groups + GPB - 1) / GPB, cap));
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(kAThreads), lds, s, a, P);
+    CHIP_CHECK(hipGetLastError());
+    return 0;
+}
+
+template <int FMT, int R, bool NORM, bool DUAL>
+int pick_ks(const Args &a, int P, int ks, hipStream_t s) {
+    switch (ks) {
+        case 8: return launch_aligned<FMT, R, 8, NORM, DUAL>(a, P, s);
+        case 4: return launch_aligned<FMT, R, 4, NORM, DUAL>(a, P, s);
+        case 2: return launch_aligned<FMT, R, 2, NORM, DUAL>(a, P, s);
+        default: return launch_aligned<FMT, R, 1, NORM, DUAL>(a, P, s);
+    }
+}
+
+// Rows per wave (R) and waves per row group (KS, splitting K), as measured
+// on MI355X: one row per wave streams BF16 / Q8 best; Q4 (twice the
+// elements per byte) gains from sharing each x read between 2-4 rows once
+// there are enough rows to keep every wave slot busy. K is split only when
+// rows are too few for the wave slots, keeping >= 2 units per lane.
+template <int FMT, bool NORM, bool DUAL>
+int pick_aligned(const Args &a, int P, hipStream_t s) {
+    constexpr int E = Unit<FMT, 16>::E;
+    const int n_units = (a.K + E - 1) / E;
+    const long slots = (long)device_cus() * 16;
+    int R = 1;
+    if constexpr (FMT == FMT_Q4) R = a.rows >= 3 * slots && !DUAL ? 4 : (a.rows >= slots ? 2 : 1);
+    const long groups = (a.rows + R - 1) / R;
+    int ks = 1;
+    while (ks < 8 && groups * ks < slots && n_units >= 64 * 2 * ks * 2) ks *= 2;
+    if constexpr (FMT == FMT_Q4) {
+        if constexpr (!DUAL)
+            if (R == 4) return pick_ks<FMT, 4, NORM, DUAL>(a, P, ks, s);
+        if (R == 2) return pick_ks<FMT, 2, NORM, DUAL>(a, P, ks, s);
+    }
+    return pick_ks<FMT, 1, NORM, DUAL>(a, P, ks, s);
+}
+
+template <int FMT>
+int pick_aligned_mode(const Args &a, int P, bool norm, bool dual, hipStream_t s) {
+    if (norm) return dual ? pick_aligned<FMT, true, true>(a, P, s) : pick_aligned<FMT, true, false>(a, P, s);
+    return dual ? pick_aligned<FMT, false, true>(a, P, s) : pick_aligned<FMT, false, false>(a, P, s);
+}
+
+// ---------------------------------------------------------------------------
+// Dword fallback for layouts the aligned kernel does not take (BF16 rows not
+// 16-byte aligned: odd widths in small shapes).
+// ---------------------------------------------------------------------------
 template <int FMT, int UB, int R, int KS, bool NORM, bool DUAL>
 int launch_t(const Args &a, hipStream_t s) {
     constexpr int GPB = kWaves / KS;
@@ -215,30 +575,21 @@ int launch_t(const Args &a, hipStream_t s) {
     return 0;
 }
 
-// Rows per group and waves per group: enough waves to keep every CU busy
-// (~8 per CU) while each lane still streams at least two units.
-template <int FMT, int UB, bool NORM, bool DUAL>
-int pick_shape(const Args &a, hipStream_t s) {
-    constexpr int E = Unit<FMT, UB>::E;
-    const int n_units = a.K / E;
-    if (a.rows >= 16384) return launch_t<FMT, UB, 2, 1, NORM, DUAL>(a, s);
-    int ks = 1;
-    while (ks < 4 && a.rows * ks < 2048 && n_units >= 64 * ks * 2 * 2) ks *= 2;
-    if (ks == 4) return launch_t<FMT, UB, 1, 4, NORM, DUAL>(a, s);
-    if (ks == 2) return launch_t<FMT, UB, 1, 2, NORM, DUAL>(a, s);
-    return launch_t<FMT, UB, 1, 1, NORM, DUAL>(a, s);
-}
-
 template <int FMT, bool NORM, bool DUAL>
-int pick_ub(const Args &a, bool aligned16, hipStream_t s) {
-    if (aligned16) return pick_shape<FMT, 16, NORM, DUAL>(a, s);
-    return pick_shape<FMT, 4, NORM, DUAL>(a, s);
+int pick_shape(const Args &a, hipStream_t s) {
+    constexpr int E = Unit<FMT, 4>::E;
+    const int n_units = a.K / E;
+    int ks = 1;
+    while (ks < 4 && a.rows * ks < 2048 && n_units >= 64 * ks * 2 * 4) ks *= 2;
+    if (ks == 4) return launch_t<FMT, 4, 1, 4, NORM, DUAL>(a, s);
+    if (ks == 2) return launch_t<FMT, 4, 1, 2, NORM, DUAL>(a, s);
+    return launch_t<FMT, 4, 1, 1, NORM, DUAL>(a, s);
 }
 
 template <int FMT>
-int pick_mode(const Args &a, bool aligned16, bool norm, bool dual, hipStream_t s) {
-    if (norm) return dual ? pick_ub<FMT, true, true>(a, aligned16, s) : pick_ub<FMT, true, false>(a, aligned16, s);
-    return dual ? pick_ub<FMT, false, true>(a, aligned16, s) : pick_ub<FMT, false, false>(a, aligned16, s);
+int pick_mode(const Args &a, bool norm, bool dual, hipStream_t s) {
+    if (norm) return dual ? pick_shape<FMT, true, true>(a, s) : pick_shape<FMT, true, false>(a, s);
+    return dual ? pick_shape<FMT, false, true>(a, s) : pick_shape<FMT, false, false>(a, s);
 }
 
 }  // namespace
@@ -268,13 +619,30 @@ int launch_gemv(const GemvJob &job, hipStream_t s) {
     a.y = job.y;
     a.residual = job.residual;
     a.epi = job.epi;
-    const bool aligned16 =
-        a.stride % 16 == 0 && ((uintptr_t)a.w % 16) == 0 && (!dual || ((uintptr_t)a.w2 % 16) == 0);
     const bool norm = job.norm_gain != nullptr;
+    // The aligned kernel needs 4-byte-aligned rows whose misalignment is a
+    // multiple of 4 x floats (BF16: rows 16-byte aligned), gate and up
+    // misaligned alike, and x plus its padding in LDS.
+    const uintptr_t b0 = (uintptr_t)a.w;
+    const int bpe_mod = w.fmt == FMT_BF16 ? 16 : 4;
+    // The aligned-down start of the first row must not precede the buffer.
+    const bool aligned_ok = a.stride % bpe_mod == 0 && b0 % bpe_mod == 0 && (uintptr_t)w.base % 16 == 0 &&
+                            (!dual || ((uintptr_t)job.w2.base % 16 == 0 && ((uintptr_t)a.w2 - b0) % 16 == 0)) &&
+                            (size_t)(a.K + 2 * kPad) * sizeof(float) + (norm ? (size_t)a.K * 2 + 16 : 0) + 256 <=
+                                device_max_lds();
+    if (aligned_ok) {
+        const int sm = (int)(a.stride % 16);
+        const int P = sm == 0 ? 1 : 16 / std::gcd(sm, 16);
+        switch (w.fmt) {
+            case FMT_BF16: return pick_aligned_mode<FMT_BF16>(a, P, norm, dual, s);
+            case FMT_Q8: return pick_aligned_mode<FMT_Q8>(a, P, norm, dual, s);
+            case FMT_Q4: return pick_aligned_mode<FMT_Q4>(a, P, norm, dual, s);
+        }
+    }
     switch (w.fmt) {
-        case FMT_BF16: return pick_mode<FMT_BF16>(a, aligned16, norm, dual, s);
-        case FMT_Q8: return pick_mode<FMT_Q8>(a, aligned16, norm, dual, s);
-        case FMT_Q4: return pick_mode<FMT_Q4>(a, aligned16, norm, dual, s);
+        case FMT_BF16: return pick_mode<FMT_BF16>(a, norm, dual, s);
+        case FMT_Q8: return pick_mode<FMT_Q8>(a, norm, dual, s);
+        case FMT_Q4: return pick_mode<FMT_Q4>(a, norm, dual, s);
     }
     return fail("HIP backend: unknown weight format.");
 }

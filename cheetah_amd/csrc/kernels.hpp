@@ -8,6 +8,8 @@ namespace chip {
 
 // Largest LDS allocation one block may make (queried at init).
 size_t device_max_lds();
+int device_cus();
+size_t device_lds_per_cu();
 
 // ---------------------------------------------------------------------------
 // Weight matrix in device memory, in the reference's layout.

@@ -142,3 +142,32 @@ def attention(lengths=(1024, 4096, 16384), nbuf: int = 8, iters: int = 40, prefi
     for b in kbufs + vbufs + [table, qd, od, qp, op]:
         b.free()
     return res
+
+
+def main(argv=None) -> int:
+    """python -m cheetah_amd.opbench [attention] [gemv] [gemm]: one JSON line
+    per measurement (all three when no part is named)."""
+    import argparse
+    import json
+
+    ap = argparse.ArgumentParser()
+    ap.add_argument("parts", nargs="*", choices=["attention", "gemv", "gemm"])
+    ap.add_argument("--shapes", default="4096x4096,4096x14336,14336x4096")
+    ap.add_argument("--fmts", default="q8,q4")
+    args = ap.parse_args(argv)
+    parts = set(args.parts or ["attention", "gemv", "gemm"])
+    hip.init(0)
+    if "attention" in parts:
+        print(json.dumps({"attention": attention()}), flush=True)
+    if parts & {"gemv", "gemm"}:
+        shapes = tuple(tuple(int(v) for v in s.split("x")) for s in args.shapes.split(","))
+        for r in gemv_gemm(shapes=shapes, fmts=tuple(args.fmts.split(",")),
+                           gemm_iters=3 if "gemm" in parts else 1):
+            if "gemm" not in parts:
+                r = {k: v for k, v in r.items() if not k.startswith("gemm")}
+            print(json.dumps(r), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -52,7 +52,9 @@ class Pool {
     }
     int threads() const { return threads_; }
 
-    // Runs fn(i) for i in [0, n); the caller participates.
+    // Runs fn(i) for i in [0, n); the caller participates. Each call has its
+    // own job record, so a worker still leaving an earlier job can only
+    // touch that job's (exhausted) counters.
     void parallel_for(size_t n, const std::function<void(size_t)> &fn) {
         if (n == 0) return;
         if (threads_ == 1 || n == 1) {
@@ -60,28 +62,34 @@ class Pool {
             return;
         }
         std::unique_lock<std::mutex> call_lock(call_mutex_);
+        auto job = std::make_shared<Job>();
+        job->fn = &fn;
+        job->n = n;
         {
             std::lock_guard<std::mutex> lock(mutex_);
-            job_ = &fn;
-            job_n_ = n;
-            next_.store(0);
-            done_.store(0);
+            job_ = job;
             ++generation_;
         }
         cv_.notify_all();
-        run_items();
+        run_items(*job);
         std::unique_lock<std::mutex> lock(mutex_);
-        done_cv_.wait(lock, [&] { return done_.load() == n; });
-        job_ = nullptr;
+        done_cv_.wait(lock, [&] { return job->done.load() == job->n; });
+        job_.reset();
     }
 
   private:
-    void run_items() {
+    struct Job {
+        const std::function<void(size_t)> *fn = nullptr;
+        size_t n = 0;
+        std::atomic<size_t> next{0}, done{0};
+    };
+
+    void run_items(Job &job) {
         for (;;) {
-            size_t i = next_.fetch_add(1);
-            if (i >= job_n_) break;
-            (*job_)(i);
-            if (done_.fetch_add(1) + 1 == job_n_) {
+            const size_t i = job.next.fetch_add(1);
+            if (i >= job.n) break;
+            (*job.fn)(i);
+            if (job.done.fetch_add(1) + 1 == job.n) {
                 std::lock_guard<std::mutex> lock(mutex_);
                 done_cv_.notify_all();
             }
@@ -90,13 +98,15 @@ class Pool {
     void loop() {
         uint64_t seen = 0;
         for (;;) {
+            std::shared_ptr<Job> job;
             {
                 std::unique_lock<std::mutex> lock(mutex_);
                 cv_.wait(lock, [&] { return quit_ || (generation_ != seen && job_ != nullptr); });
                 if (quit_) return;
                 seen = generation_;
+                job = job_;
             }
-            run_items();
+            run_items(*job);
         }
     }
     void stop() {
@@ -113,9 +123,7 @@ class Pool {
     std::vector<std::thread> workers_;
     std::mutex mutex_, call_mutex_;
     std::condition_variable cv_, done_cv_;
-    const std::function<void(size_t)> *job_ = nullptr;
-    size_t job_n_ = 0;
-    std::atomic<size_t> next_{0}, done_{0};
+    std::shared_ptr<Job> job_;
     uint64_t generation_ = 0;
     bool quit_ = false;
 };
