@@ -1,4 +1,5 @@
 // Library lifecycle, device memory and the op-level C-ABI (include/cheetah_hip.h).
+#include <algorithm>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -239,7 +240,11 @@ static int attention_op(const float *q, const cheetah_hip_kv_view *kv, uint32_t 
     if (splits > (size_t)attention_max_splits()) splits = attention_max_splits();
     if (splits < 1) splits = 1;
     j.splits = (int)splits;
-    const size_t need = attention_part_floats(rows, (int)q_heads, (int)splits, (int)kv->head_dim);
+    j.prefill = rows > 1;
+    size_t need = attention_part_floats(rows, (int)q_heads, (int)splits, (int)kv->head_dim);
+    if (j.prefill && attention_prefill_on_mfma(j.g, (int)q_heads))
+        need = std::max(need, attention_part_floats(rows, (int)q_heads, attention_prefill_splits(offset + rows),
+                                                    (int)kv->head_dim));
     if (need > part_floats) {
         CHIP_CHECK(hipStreamSynchronize(g_stream));
         if (part) CHIP_CHECK(hipFree(part));
@@ -249,6 +254,7 @@ static int attention_op(const float *q, const cheetah_hip_kv_view *kv, uint32_t 
         part_floats = need;
     }
     j.part = part;
+    j.part_floats = part_floats;
     return launch_attention(j, g_stream);
 }
 

@@ -20,6 +20,8 @@
 // with its own causal length. The position base comes from a device word in
 // the decode graph (pos_dev) or from the host. K/V elements are BF16
 // (default) or f32.
+#include <algorithm>
+
 #include "kernels.hpp"
 
 namespace chip {
@@ -253,6 +255,299 @@ __global__ __launch_bounds__(kThreads) void attn_combine_kernel(const float *par
     }
 }
 
+// ---------------------------------------------------------------------------
+// Chunked prefill on the matrix cores (BF16 KV): flash attention with the
+// score and value products as v_mfma_f32_32x32x16_bf16.
+//
+// A block is 4 waves and one KV head; each wave owns 32 "M rows" = RW query
+// rows x G heads of the group (RW = 32 / G). Per 64-position tile:
+//   S^T = K Q^T  (A = K rows from LDS, B = Q^T kept in registers as hi/lo
+//                BF16 halves of the f32 query, so scores carry ~2^-17
+//                relative error); every lane ends up holding one M row's
+//                scores (column = lane % 32), so the online softmax (running
+//                max / sum, rescale) is lane-local plus one exchange with
+//                lane ^ 32.
+//   O^T += V^T P^T (A = V^T from LDS, B = P^T straight from the S^T
+//                registers, again as hi/lo BF16 halves).
+// K rows are staged in LDS with bits 2 and 3 of the position swapped, which
+// makes the S^T output registers exactly the B operand layout of the second
+// product (8 consecutive positions per lane), so P never moves between lanes.
+// V is staged transposed ([dim][position]).
+//
+// Splits are absolute position ranges of kSpan keys, so every row's result
+// depends only on its own position (the same bits however the prompt is
+// chunked); the splits of a row are merged in order by attn_merge2_kernel.
+// ---------------------------------------------------------------------------
+constexpr int kSpan = 2048;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// LDS row of a position within a 64-position tile (an involution).
+__device__ __forceinline__ int krow_of(int p) { return (p & ~12) | ((p & 4) << 1) | ((p & 8) >> 1); }
+
+// hi = bf16(v) and lo = bf16(v - hi) (hardware round-to-nearest-even
+// conversions), so hi + lo carries v to ~2^-17 relative error.
+__device__ __forceinline__ void split8(const float (&v)[8], bf16x8 &hi, bf16x8 &lo) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        hi[q] = (__bf16)v[q];
+        lo[q] = (__bf16)(v[q] - (float)hi[q]);
+    }
+}
+
+// Column of position p (0..63) in row d of the transposed V tile: groups of 8
+// positions are XOR-swizzled by the row's dim group, so the transposing
+// stores of one wave spread over the LDS banks while every 8-position group
+// stays one aligned 16-byte read.
+__device__ __forceinline__ int vcol(int d, int p) { return (((p >> 3) ^ ((d >> 3) & 7)) << 3) | (p & 7); }
+
+template <int HD, int G>
+__global__ __launch_bounds__(kThreads) void attn_prefill_kernel(AttnArgs a, int rows, int S) {
+    constexpr int RW = 32 / G, MV = RW * G;
+    constexpr int LDK = HD + 8, LDV = 64 + 8;
+    constexpr int KSTEPS = HD / 16, UT = HD / 32, KC = HD / 32;
+    __shared__ __attribute__((aligned(16))) uint16_t ks[2][64 * LDK];
+    __shared__ __attribute__((aligned(16))) uint16_t vt[2][HD * LDV];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = lane & 31, half = lane >> 5;
+    const int rb = blockIdx.x, g = blockIdx.y, split = blockIdx.z;
+    const int row = rb * 4 * RW + wave * RW + n / G;
+    const int head = g * G + n % G;
+    const bool rvalid = n < MV && row < rows;
+    // Positions fit in 32 bits (the KV capacity is checked on the host).
+    const int off = (int)a.offset;
+    const int my_pos = off + row;
+    const int first_pos = off + rb * 4 * RW;
+    const int ctx = off + min(rows, (rb + 1) * 4 * RW);
+    const int start = split * kSpan;
+    const int end = min(start + kSpan, ctx);
+    float *part = a.part + (((size_t)row * a.q_heads + head) * S + split) * (HD + 2);
+    if (start >= ctx) {  // block-uniform: no row of this block reaches the split
+        if (rvalid && half == 0) part[HD] = -INFINITY;
+        return;
+    }
+
+    // Q^T operands (B of S^T = K Q^T): lane holds Q[m = lane % 32][16 s + 8 half .. +8],
+    // pre-scaled by log2(e) / sqrt(HD) so scores come out in the exp2 domain.
+    bf16x8 qh[KSTEPS], ql[KSTEPS];
+    {
+        const float sl2 = (1.0f / sqrtf((float)HD)) * 1.44269504088896340736f;
+        const float *qp = a.q + (size_t)(rvalid ? row : 0) * a.q_stride + (size_t)head * HD + 8 * half;
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s) {
+            float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            if (rvalid) {
+                const f32x4 t0 = *(const f32x4 *)(qp + 16 * s), t1 = *(const f32x4 *)(qp + 16 * s + 4);
+                v[0] = t0[0] * sl2; v[1] = t0[1] * sl2; v[2] = t0[2] * sl2; v[3] = t0[3] * sl2;
+                v[4] = t1[0] * sl2; v[5] = t1[1] * sl2; v[6] = t1[2] * sl2; v[7] = t1[3] * sl2;
+            }
+            split8(v, qh[s], ql[s]);
+        }
+    }
+
+    const uint16_t *kbase = (const uint16_t *)a.k, *vbase = (const uint16_t *)a.v;
+    u32x4 kr[KC], vr[KC];
+    auto fetch = [&](int t0) {
+        const int page = a.page_table[t0 / a.page_size];
+        const int slot0 = t0 % a.page_size;
+        const size_t tile = (((size_t)page * a.kv_heads + g) * a.page_size + slot0) * HD;
+#pragma unroll
+        for (int c = 0; c < KC; ++c) {
+            const int idx = tid + kThreads * c, p = idx / (HD / 8), d0 = (idx % (HD / 8)) * 8;
+            if (t0 + p < end) {  // positions past the split end may be unwritten: zeros, never read
+                kr[c] = *(const u32x4 *)(kbase + tile + p * HD + d0);
+                vr[c] = *(const u32x4 *)(vbase + tile + p * HD + d0);
+            } else {
+                kr[c] = u32x4{0u, 0u, 0u, 0u};
+                vr[c] = u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+    };
+    auto store = [&](int b) {
+#pragma unroll
+        for (int c = 0; c < KC; ++c) {
+            const int idx = tid + kThreads * c, p = idx / (HD / 8), d0 = (idx % (HD / 8)) * 8;
+            *(u32x4 *)(&ks[b][krow_of(p) * LDK + d0]) = kr[c];
+            const int col = vcol(d0, p);
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                vt[b][(d0 + e) * LDV + col] = (uint16_t)((e & 1) ? (vr[c][e >> 1] >> 16) : (vr[c][e >> 1] & 0xFFFFu));
+        }
+    };
+
+    f32x16 oacc[UT];
+#pragma unroll
+    for (int u = 0; u < UT; ++u) oacc[u] = f32x16{};
+    float m2 = -INFINITY, l = 0.f;
+    fetch(start);
+    store(0);
+    __syncthreads();
+    int b = 0;
+    for (int t0 = start; t0 < end; t0 += 64) {
+        const bool more = t0 + 64 < end;
+        if (more) fetch(t0 + 64);
+        f32x16 sacc[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int s = 0; s < KSTEPS; ++s) {
+                const bf16x8 ka =
+                    __builtin_bit_cast(bf16x8, *(const u32x4 *)(&ks[b][(32 * tt + n) * LDK + 16 * s + 8 * half]));
+                sacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qh[s], sacc[tt], 0, 0, 0);
+                sacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, ql[s], sacc[tt], 0, 0, 0);
+            }
+        // Causal / split-end mask, only on tiles that reach past a row's
+        // position or past the split (block-uniform test).
+        if (t0 + 63 > first_pos || t0 + 64 > end) {
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int p = t0 + 32 * tt + krow_of(8 * (r >> 2) + 4 * half + (r & 3));
+                    if (p > my_pos || p >= end) sacc[tt][r] = -INFINITY;
+                }
+        }
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sacc[tt][r]);
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float mnew = fmaxf(m2, tmax);
+        // A row with every score so far masked keeps m = -inf; its terms are 0.
+        const float mref = mnew == -INFINITY ? 0.f : mnew;
+        const float alpha = __builtin_amdgcn_exp2f(m2 - mref);
+        float tsum = 0.f;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float pv = __builtin_amdgcn_exp2f(sacc[tt][r] - mref);
+                sacc[tt][r] = pv;
+                tsum += pv;
+            }
+        tsum += __shfl_xor(tsum, 32, 64);
+        l = l * alpha + tsum;
+        m2 = mnew;
+#pragma unroll
+        for (int u = 0; u < UT; ++u)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[u][r] *= alpha;
+        // O^T += V^T P^T over 4 steps of 16 positions.
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+            float pv[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) pv[j] = sacc[s4 >> 1][8 * (s4 & 1) + j];
+            bf16x8 bh, bl;
+            split8(pv, bh, bl);
+#pragma unroll
+            for (int u = 0; u < UT; ++u) {
+                const int d = 32 * u + n;
+                const bf16x8 va = __builtin_bit_cast(
+                    bf16x8, *(const u32x4 *)(&vt[b][d * LDV + vcol(d, 16 * s4 + 8 * half)]));
+                oacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, bh, oacc[u], 0, 0, 0);
+                oacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, bl, oacc[u], 0, 0, 0);
+            }
+        }
+        if (more) store(b ^ 1);
+        __syncthreads();
+        b ^= 1;
+    }
+    if (!rvalid) return;
+    // O^T registers: lane's M row, dims 32 u + 8 (r / 4) + 4 half + r % 4.
+    if (S == 1) {
+        const float inv = 1.0f / l;
+        float *o = a.out + (size_t)row * (size_t)a.q_heads * HD + (size_t)head * HD;
+#pragma unroll
+        for (int u = 0; u < UT; ++u)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                *(f32x4 *)(o + 32 * u + 8 * q + 4 * half) =
+                    f32x4{oacc[u][4 * q] * inv, oacc[u][4 * q + 1] * inv, oacc[u][4 * q + 2] * inv,
+                          oacc[u][4 * q + 3] * inv};
+    } else {
+#pragma unroll
+        for (int u = 0; u < UT; ++u)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                *(f32x4 *)(part + 32 * u + 8 * q + 4 * half) =
+                    f32x4{oacc[u][4 * q], oacc[u][4 * q + 1], oacc[u][4 * q + 2], oacc[u][4 * q + 3]};
+        if (half == 0) {
+            part[HD] = m2;
+            part[HD + 1] = l;
+        }
+    }
+}
+
+// Merges the splits of one (row, q head) of attn_prefill_kernel in split
+// order: maxima in the log2 domain, weights 2^(m_s - M), output
+// (sum_s w_s o_s) * (1 / sum_s w_s l_s). A row whose only non-empty split
+// gives w = 1 gets o * (1 / l), the bits the one-split kernel writes.
+template <int HD>
+__global__ __launch_bounds__(kThreads) void attn_merge2_kernel(const float *part, int S, int q_heads, float *out) {
+    constexpr int GR = kThreads / HD;
+    __shared__ float s_w[kMaxSplits];
+    __shared__ float s_inv;
+    __shared__ float s_o[GR][HD];
+    const int h = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+    const float *p = part + ((size_t)row * q_heads + h) * (size_t)S * (HD + 2);
+    if (tid < 64) {
+        const float m = tid < S ? p[(size_t)tid * (HD + 2) + HD] : -INFINITY;
+        const float M = wave_max(m);
+        const float w = m == -INFINITY ? 0.f : exp2f(m - M);
+        const float l = w != 0.f ? p[(size_t)tid * (HD + 2) + HD + 1] : 0.f;
+        const float L = wave_sum(w * l);
+        if (tid < S) s_w[tid] = w;
+        if (tid == 0) s_inv = 1.0f / L;
+    }
+    __syncthreads();
+    const int d = tid % HD, grp = tid / HD;
+    float o = 0.f;
+    for (int s = grp; s < S; s += GR) {
+        const float w = s_w[s];
+        if (w != 0.f) o = fmaf(w, p[(size_t)s * (HD + 2) + d], o);
+    }
+    s_o[grp][d] = o;
+    __syncthreads();
+    if (tid < HD) {
+        float sum = s_o[0][tid];
+#pragma unroll
+        for (int k = 1; k < GR; ++k) sum += s_o[k][tid];
+        out[((size_t)row * q_heads + h) * HD + tid] = sum * s_inv;
+    }
+}
+
+template <int HD, int G>
+int launch_prefill_hg(const AttnJob &j, const AttnArgs &a, int S, hipStream_t s) {
+    constexpr int RW = 32 / G;
+    const int rb = (int)((j.rows + 4 * RW - 1) / (4 * RW));
+    hipLaunchKernelGGL((attn_prefill_kernel<HD, G>), dim3(rb, j.g.kv_heads, S), dim3(kThreads), 0, s, a, (int)j.rows,
+                       S);
+    CHIP_CHECK(hipGetLastError());
+    if (S > 1) {
+        hipLaunchKernelGGL((attn_merge2_kernel<HD>), dim3(j.q_heads, j.rows), dim3(kThreads), 0, s, a.part, S,
+                           j.q_heads, a.out);
+        CHIP_CHECK(hipGetLastError());
+    }
+    return 0;
+}
+
+template <int HD>
+int launch_prefill_h(const AttnJob &j, const AttnArgs &a, int G, int S, hipStream_t s) {
+    switch (G) {
+        case 1: return launch_prefill_hg<HD, 1>(j, a, S, s);
+        case 2: return launch_prefill_hg<HD, 2>(j, a, S, s);
+        case 3: return launch_prefill_hg<HD, 3>(j, a, S, s);
+        case 4: return launch_prefill_hg<HD, 4>(j, a, S, s);
+        case 5: return launch_prefill_hg<HD, 5>(j, a, S, s);
+        case 6: return launch_prefill_hg<HD, 6>(j, a, S, s);
+        case 7: return launch_prefill_hg<HD, 7>(j, a, S, s);
+        case 8: return launch_prefill_hg<HD, 8>(j, a, S, s);
+    }
+    return fail("HIP backend: attention supports 1..8 query heads per KV head.");
+}
+
 template <int HD, int G, class KT>
 int launch_hgk(const AttnJob &j, const AttnArgs &a, hipStream_t s) {
     const dim3 grid(j.splits, j.g.kv_heads, j.rows);
@@ -298,9 +593,16 @@ size_t attention_part_floats(size_t rows, int q_heads, int splits, int head_dim)
 
 int attention_max_splits() { return kMaxSplits; }
 
+int attention_prefill_splits(size_t ctx) { return (int)std::max<size_t>(1, (ctx + kSpan - 1) / kSpan); }
+
+bool attention_prefill_on_mfma(const KvGeom &g, int q_heads) {
+    return !g.kv_f32 && (g.head_dim == 64 || g.head_dim == 128) && g.kv_heads > 0 && q_heads % g.kv_heads == 0 &&
+           q_heads / g.kv_heads <= 8;
+}
+
 int launch_attention(const AttnJob &j, hipStream_t s) {
     if (j.rows == 0) return 0;
-    if (!j.q || !j.out || !j.k || !j.v || !j.g.page_table || (j.splits > 1 && !j.part))
+    if (!j.q || !j.out || !j.k || !j.v || !j.g.page_table || (!j.prefill && j.splits > 1 && !j.part))
         return fail("HIP backend: attention is missing a buffer.");
     if (j.g.kv_heads <= 0 || j.q_heads <= 0 || j.q_heads % j.g.kv_heads)
         return fail("HIP backend: q_heads must be a multiple of kv_heads.");
@@ -322,6 +624,16 @@ int launch_attention(const AttnJob &j, hipStream_t s) {
     a.part = j.part;
     a.out = j.out;
     const int G = j.q_heads / j.g.kv_heads;
+    if (j.prefill && attention_prefill_on_mfma(j.g, j.q_heads)) {
+        if (j.pos_dev) return fail("HIP backend: prefill attention takes a host position.");
+        if (j.offset + j.rows > (size_t)INT32_MAX) return fail("HIP backend: prefill position out of range.");
+        const int S = attention_prefill_splits(j.offset + j.rows);
+        if (S > kMaxSplits) return fail("HIP backend: prefill context exceeds the attention split limit.");
+        if (S > 1 && (!j.part || j.part_floats < attention_part_floats(j.rows, j.q_heads, S, j.g.head_dim)))
+            return fail("HIP backend: prefill attention partial buffer too small.");
+        if (j.g.head_dim == 64) return launch_prefill_h<64>(j, a, G, S, s);
+        return launch_prefill_h<128>(j, a, G, S, s);
+    }
     if (j.g.head_dim == 64) return launch_h<64>(j, a, G, s);
     if (j.g.head_dim == 128) return launch_h<128>(j, a, G, s);
     return fail("HIP backend: attention supports head_dim 64 and 128.");

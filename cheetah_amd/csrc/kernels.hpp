@@ -121,10 +121,17 @@ struct AttnJob {
     const int32_t *pos_dev = nullptr;
     int splits = 1;
     float *part = nullptr;  // partial buffer (splits > 1)
+    // Chunked prefill (host offset): BF16 KV with head_dim 64/128 runs on the
+    // matrix cores with attention_prefill_splits(offset + rows) splits and
+    // ignores `splits`; part must then hold part_floats >= the partials.
+    bool prefill = false;
+    size_t part_floats = 0;
 };
 int launch_attention(const AttnJob &job, hipStream_t s);
 size_t attention_part_floats(size_t rows, int q_heads, int splits, int head_dim);
 int attention_max_splits();
+int attention_prefill_splits(size_t ctx);
+bool attention_prefill_on_mfma(const KvGeom &g, int q_heads);
 
 // Greedy argmax (ties -> last index, total order) of logits[n]; writes the
 // index to *out_token. When `step` is set (the device-side decode loop,

@@ -159,6 +159,7 @@ struct cheetah_hip_model {
     // activations
     float *hidden = nullptr, *normed = nullptr, *qkv = nullptr, *qrot = nullptr, *attn = nullptr, *act = nullptr;
     float *logits = nullptr, *part = nullptr;
+    size_t part_floats = 0;
     uint32_t *tokens_dev = nullptr, *next_dev = nullptr, *hist_dev = nullptr;
     int32_t *step_dev = nullptr;  // [0] = token, [1] = position
     void *argmax_scratch = nullptr;
@@ -547,8 +548,13 @@ int init_instance(cheetah_hip_model *m) {
     CHIP_TRY(m->mem.alloc(&m->qrot, R * qd));
     CHIP_TRY(m->mem.alloc(&m->act, R * c.intermediate_size));
     CHIP_TRY(m->mem.alloc(&m->logits, c.vocab_size));
-    const size_t part_rows = std::max(R * (size_t)kPrefillSplits, (size_t)attention_max_splits());
-    CHIP_TRY(m->mem.alloc(&m->part, part_rows * c.q_heads * (c.head_dim + 2)));
+    // Prefill partials: the fixed VALU split count, or the matrix-core
+    // kernel's span splits at full capacity; decode: attention_max_splits.
+    const size_t prefill_splits =
+        std::max((size_t)kPrefillSplits, (size_t)attention_prefill_splits(sh.kv_capacity));
+    const size_t part_rows = std::max(R * prefill_splits, (size_t)attention_max_splits());
+    m->part_floats = part_rows * c.q_heads * (c.head_dim + 2);
+    CHIP_TRY(m->mem.alloc(&m->part, m->part_floats));
     CHIP_TRY(m->mem.alloc(&m->tokens_dev, sh.kv_capacity));
     CHIP_TRY(m->mem.alloc(&m->next_dev, 1));
     CHIP_TRY(m->mem.alloc(&m->hist_dev, sh.kv_capacity + 1));
@@ -762,6 +768,8 @@ int enqueue_chunk(cheetah_hip_model *m, const uint32_t *tokens_dev, size_t rows,
         aj.offset = pos;
         aj.splits = (int)splits;
         aj.part = m->part;
+        aj.part_floats = m->part_floats;
+        aj.prefill = true;
         CHIP_TRY(launch_attention(aj, s));
         GemmJob o;
         o.w = L.o;
