@@ -278,7 +278,7 @@ __global__ __launch_bounds__(kThreads) void attn_combine_kernel(const float *par
 // depends only on its own position (the same bits however the prompt is
 // chunked); the splits of a row are merged in order by attn_merge2_kernel.
 // ---------------------------------------------------------------------------
-constexpr int kSpan = 2048;
+constexpr int kSpan = 1024;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -302,11 +302,13 @@ __device__ __forceinline__ void split8(const float (&v)[8], bf16x8 &hi, bf16x8 &
 __device__ __forceinline__ int vcol(int d, int p) { return (((p >> 3) ^ ((d >> 3) & 7)) << 3) | (p & 7); }
 
 template <int HD, int G>
-__global__ __launch_bounds__(kThreads) void attn_prefill_kernel(AttnArgs a, int rows, int S) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void attn_prefill_kernel(AttnArgs a, int rows, int S) {
     constexpr int RW = 32 / G, MV = RW * G;
-    constexpr int LDK = HD + 8, LDV = 64 + 8;
+    constexpr int LDV = 64 + 8;
     constexpr int KSTEPS = HD / 16, UT = HD / 32, KC = HD / 32;
-    __shared__ __attribute__((aligned(16))) uint16_t ks[2][64 * LDK];
+    constexpr int CPR = HD / 8;  // 16-byte chunks per K row
+    // K rows unpadded, chunk c of LDS row r stored at chunk c ^ (r % CPR).
+    __shared__ __attribute__((aligned(16))) uint16_t ks[2][64 * HD];
     __shared__ __attribute__((aligned(16))) uint16_t vt[2][HD * LDV];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 31, half = lane >> 5;
@@ -346,28 +348,38 @@ __global__ __launch_bounds__(kThreads) void attn_prefill_kernel(AttnArgs a, int 
     }
 
     const uint16_t *kbase = (const uint16_t *)a.k, *vbase = (const uint16_t *)a.v;
-    u32x4 kr[KC], vr[KC];
-    auto fetch = [&](int t0) {
+    u32x4 vr[KC];
+    // K: direct global->LDS copies. One wave instruction fills 1 KB = 64 / CPR
+    // LDS rows; lane i lands at byte 16 i, so it fetches the global chunk
+    // that the swizzle places there. Rows past the split end may hold stale
+    // bytes: their scores are masked before use.
+    auto fetch_k = [&](int t0, int b) {
         const int page = a.page_table[t0 / a.page_size];
-        const int slot0 = t0 % a.page_size;
-        const size_t tile = (((size_t)page * a.kv_heads + g) * a.page_size + slot0) * HD;
+        const size_t tile = (((size_t)page * a.kv_heads + g) * a.page_size + (t0 % a.page_size)) * HD;
+        constexpr int RPI = 64 / CPR;  // LDS rows per wave instruction
 #pragma unroll
         for (int c = 0; c < KC; ++c) {
-            const int idx = tid + kThreads * c, p = idx / (HD / 8), d0 = (idx % (HD / 8)) * 8;
-            if (t0 + p < end) {  // positions past the split end may be unwritten: zeros, never read
-                kr[c] = *(const u32x4 *)(kbase + tile + p * HD + d0);
-                vr[c] = *(const u32x4 *)(vbase + tile + p * HD + d0);
-            } else {
-                kr[c] = u32x4{0u, 0u, 0u, 0u};
-                vr[c] = u32x4{0u, 0u, 0u, 0u};
-            }
+            const int r0 = (wave + 4 * c) * RPI;  // first LDS row of this instruction
+            const int r = r0 + lane / CPR, cs = lane % CPR;
+            const int p = krow_of(r), chunk = cs ^ (r % CPR);
+            __builtin_amdgcn_global_load_lds(kbase + tile + (size_t)p * HD + chunk * 8,
+                                             (__attribute__((address_space(3))) void *)(&ks[b][r0 * HD]), 16, 0, 0);
         }
     };
-    auto store = [&](int b) {
+    auto fetch_v = [&](int t0) {
+        const int page = a.page_table[t0 / a.page_size];
+        const size_t tile = (((size_t)page * a.kv_heads + g) * a.page_size + (t0 % a.page_size)) * HD;
 #pragma unroll
         for (int c = 0; c < KC; ++c) {
-            const int idx = tid + kThreads * c, p = idx / (HD / 8), d0 = (idx % (HD / 8)) * 8;
-            *(u32x4 *)(&ks[b][krow_of(p) * LDK + d0]) = kr[c];
+            const int idx = tid + kThreads * c, p = idx / CPR, d0 = (idx % CPR) * 8;
+            // positions past the split end may be unwritten: zeros (p = 0 there)
+            vr[c] = t0 + p < end ? *(const u32x4 *)(vbase + tile + p * HD + d0) : u32x4{0u, 0u, 0u, 0u};
+        }
+    };
+    auto store_v = [&](int b) {
+#pragma unroll
+        for (int c = 0; c < KC; ++c) {
+            const int idx = tid + kThreads * c, p = idx / CPR, d0 = (idx % CPR) * 8;
             const int col = vcol(d0, p);
 #pragma unroll
             for (int e = 0; e < 8; ++e)
@@ -379,78 +391,90 @@ __global__ __launch_bounds__(kThreads) void attn_prefill_kernel(AttnArgs a, int 
 #pragma unroll
     for (int u = 0; u < UT; ++u) oacc[u] = f32x16{};
     float m2 = -INFINITY, l = 0.f;
-    fetch(start);
-    store(0);
+    fetch_k(start, 0);
+    fetch_v(start);
+    store_v(0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     int b = 0;
     for (int t0 = start; t0 < end; t0 += 64) {
         const bool more = t0 + 64 < end;
-        if (more) fetch(t0 + 64);
-        f32x16 sacc[2] = {f32x16{}, f32x16{}};
+        if (more) {
+            fetch_k(t0 + 64, b ^ 1);
+            fetch_v(t0 + 64);
+        }
+        // Two halves of 32 positions, each: S^T, online softmax, O^T update.
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
+        for (int tt = 0; tt < 2; ++tt) {
+            f32x16 sacc = f32x16{};
 #pragma unroll
             for (int s = 0; s < KSTEPS; ++s) {
+                const int r = 32 * tt + n;
                 const bf16x8 ka =
-                    __builtin_bit_cast(bf16x8, *(const u32x4 *)(&ks[b][(32 * tt + n) * LDK + 16 * s + 8 * half]));
-                sacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qh[s], sacc[tt], 0, 0, 0);
-                sacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, ql[s], sacc[tt], 0, 0, 0);
+                    __builtin_bit_cast(bf16x8, *(const u32x4 *)(&ks[b][r * HD + (((2 * s + half) ^ (r % CPR)) << 3)]));
+                sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qh[s], sacc, 0, 0, 0);
+                sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, ql[s], sacc, 0, 0, 0);
             }
-        // Causal / split-end mask, only on tiles that reach past a row's
-        // position or past the split (block-uniform test).
-        if (t0 + 63 > first_pos || t0 + 64 > end) {
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt)
+            // Causal / split-end mask, only where the half reaches past a
+            // row's position or past the split (block-uniform test).
+            const int h0 = t0 + 32 * tt;
+            if (h0 + 31 > first_pos || h0 + 32 > end) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int p = t0 + 32 * tt + krow_of(8 * (r >> 2) + 4 * half + (r & 3));
-                    if (p > my_pos || p >= end) sacc[tt][r] = -INFINITY;
+                    const int p = h0 + krow_of(8 * (r >> 2) + 4 * half + (r & 3));
+                    if (p > my_pos || p >= end) sacc[r] = -INFINITY;
                 }
-        }
-        float tmax = -INFINITY;
+            }
+            float tmax = -INFINITY;
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
+            for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sacc[r]);
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+            // Delayed rescaling: exponentials are taken against a reference
+            // max m2 that is raised only when a score exceeds it by more than
+            // 8 (log2 units), so p <= 256 and the O / l rescale is rare. Each
+            // row's steps depend only on its own scores.
+            const bool raise = tmax > m2 + 8.0f;
+            if (__any(raise)) {
+                const float mnew = raise ? tmax : m2;
+                const float alpha = __builtin_amdgcn_exp2f(m2 - mnew);  // 1 where not raised, 0 from -inf
+                l *= alpha;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sacc[tt][r]);
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        const float mnew = fmaxf(m2, tmax);
-        // A row with every score so far masked keeps m = -inf; its terms are 0.
-        const float mref = mnew == -INFINITY ? 0.f : mnew;
-        const float alpha = __builtin_amdgcn_exp2f(m2 - mref);
-        float tsum = 0.f;
+                for (int u = 0; u < UT; ++u)
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
+                    for (int r = 0; r < 16; ++r) oacc[u][r] *= alpha;
+                m2 = mnew;
+            }
+            // A row with every score so far masked keeps m2 = -inf; its terms are 0.
+            const float mref = m2 == -INFINITY ? 0.f : m2;
+            float tsum = 0.f;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const float pv = __builtin_amdgcn_exp2f(sacc[tt][r] - mref);
-                sacc[tt][r] = pv;
+                const float pv = __builtin_amdgcn_exp2f(sacc[r] - mref);
+                sacc[r] = pv;
                 tsum += pv;
             }
-        tsum += __shfl_xor(tsum, 32, 64);
-        l = l * alpha + tsum;
-        m2 = mnew;
+            tsum += __shfl_xor(tsum, 32, 64);
+            l += tsum;
+            // O^T += V^T P^T over 2 steps of 16 positions.
 #pragma unroll
-        for (int u = 0; u < UT; ++u)
+            for (int s2 = 0; s2 < 2; ++s2) {
+                float pv[8];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) oacc[u][r] *= alpha;
-        // O^T += V^T P^T over 4 steps of 16 positions.
+                for (int j = 0; j < 8; ++j) pv[j] = sacc[8 * s2 + j];
+                bf16x8 bh, bl;
+                split8(pv, bh, bl);
 #pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4) {
-            float pv[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) pv[j] = sacc[s4 >> 1][8 * (s4 & 1) + j];
-            bf16x8 bh, bl;
-            split8(pv, bh, bl);
-#pragma unroll
-            for (int u = 0; u < UT; ++u) {
-                const int d = 32 * u + n;
-                const bf16x8 va = __builtin_bit_cast(
-                    bf16x8, *(const u32x4 *)(&vt[b][d * LDV + vcol(d, 16 * s4 + 8 * half)]));
-                oacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, bh, oacc[u], 0, 0, 0);
-                oacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, bl, oacc[u], 0, 0, 0);
+                for (int u = 0; u < UT; ++u) {
+                    const int d = 32 * u + n;
+                    const bf16x8 va = __builtin_bit_cast(
+                        bf16x8, *(const u32x4 *)(&vt[b][d * LDV + vcol(d, 32 * tt + 16 * s2 + 8 * half)]));
+                    oacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, bh, oacc[u], 0, 0, 0);
+                    oacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, bl, oacc[u], 0, 0, 0);
+                }
             }
         }
-        if (more) store(b ^ 1);
+        if (more) store_v(b ^ 1);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         b ^= 1;
     }
@@ -481,41 +505,35 @@ __global__ __launch_bounds__(kThreads) void attn_prefill_kernel(AttnArgs a, int 
 }
 
 // Merges the splits of one (row, q head) of attn_prefill_kernel in split
-// order: maxima in the log2 domain, weights 2^(m_s - M), output
-// (sum_s w_s o_s) * (1 / sum_s w_s l_s). A row whose only non-empty split
-// gives w = 1 gets o * (1 / l), the bits the one-split kernel writes.
+// order, one wave per (row, head): maxima in the log2 domain, weights
+// 2^(m_s - M), output (sum_s w_s o_s) * (1 / sum_s w_s l_s). A row whose only
+// non-empty split gives w = 1 gets o * (1 / l), the bits the one-split
+// kernel writes.
 template <int HD>
-__global__ __launch_bounds__(kThreads) void attn_merge2_kernel(const float *part, int S, int q_heads, float *out) {
-    constexpr int GR = kThreads / HD;
-    __shared__ float s_w[kMaxSplits];
-    __shared__ float s_inv;
-    __shared__ float s_o[GR][HD];
-    const int h = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
-    const float *p = part + ((size_t)row * q_heads + h) * (size_t)S * (HD + 2);
-    if (tid < 64) {
-        const float m = tid < S ? p[(size_t)tid * (HD + 2) + HD] : -INFINITY;
-        const float M = wave_max(m);
-        const float w = m == -INFINITY ? 0.f : exp2f(m - M);
-        const float l = w != 0.f ? p[(size_t)tid * (HD + 2) + HD + 1] : 0.f;
-        const float L = wave_sum(w * l);
-        if (tid < S) s_w[tid] = w;
-        if (tid == 0) s_inv = 1.0f / L;
-    }
-    __syncthreads();
-    const int d = tid % HD, grp = tid / HD;
-    float o = 0.f;
-    for (int s = grp; s < S; s += GR) {
-        const float w = s_w[s];
-        if (w != 0.f) o = fmaf(w, p[(size_t)s * (HD + 2) + d], o);
-    }
-    s_o[grp][d] = o;
-    __syncthreads();
-    if (tid < HD) {
-        float sum = s_o[0][tid];
+__global__ __launch_bounds__(kThreads) void attn_merge2_kernel(const float *part, int S, int q_heads, int items,
+                                                              float *out) {
+    const int lane = threadIdx.x & 63;
+    const int item = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    if (item >= items) return;
+    const float *p = part + (size_t)item * (size_t)S * (HD + 2);
+    const float m = lane < S ? p[(size_t)lane * (HD + 2) + HD] : -INFINITY;
+    const float M = wave_max(m);
+    const float w = m == -INFINITY ? 0.f : exp2f(m - M);
+    const float L = wave_sum(w != 0.f ? w * p[(size_t)lane * (HD + 2) + HD + 1] : 0.f);
+    const float inv = 1.0f / L;
+    constexpr int DPL = HD / 64;  // dims per lane
+    float o[DPL];
 #pragma unroll
-        for (int k = 1; k < GR; ++k) sum += s_o[k][tid];
-        out[((size_t)row * q_heads + h) * HD + tid] = sum * s_inv;
+    for (int k = 0; k < DPL; ++k) o[k] = 0.f;
+    for (int s = 0; s < S; ++s) {
+        const float ws = __shfl(w, s, 64);
+        if (ws != 0.f) {
+#pragma unroll
+            for (int k = 0; k < DPL; ++k) o[k] = fmaf(ws, p[(size_t)s * (HD + 2) + lane + 64 * k], o[k]);
+        }
     }
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) out[(size_t)item * HD + lane + 64 * k] = o[k] * inv;
 }
 
 template <int HD, int G>
@@ -526,8 +544,9 @@ int launch_prefill_hg(const AttnJob &j, const AttnArgs &a, int S, hipStream_t s)
                        S);
     CHIP_CHECK(hipGetLastError());
     if (S > 1) {
-        hipLaunchKernelGGL((attn_merge2_kernel<HD>), dim3(j.q_heads, j.rows), dim3(kThreads), 0, s, a.part, S,
-                           j.q_heads, a.out);
+        const int items = (int)j.rows * j.q_heads;
+        hipLaunchKernelGGL((attn_merge2_kernel<HD>), dim3((items + 3) / 4), dim3(kThreads), 0, s, a.part, S,
+                           j.q_heads, items, a.out);
         CHIP_CHECK(hipGetLastError());
     }
     return 0;
