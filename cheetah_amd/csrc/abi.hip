@@ -156,6 +156,24 @@ int cheetah_hip_gemv_q4(const uint8_t *w, size_t rows, size_t cols, const float 
     return gemv_op(FMT_Q4, w, rows, cols, x, y);
 }
 
+// Split-K scratch of the op-level GEMM (grown on demand, per thread).
+static int gemm_scratch(size_t rows, size_t cols, size_t n, GemmJob &j) {
+    static thread_local float *ws = nullptr;
+    static thread_local size_t ws_floats = 0;
+    const size_t need = gemm_split_workspace_floats(rows, cols, n, false);
+    if (need > ws_floats) {
+        CHIP_CHECK(hipStreamSynchronize(g_stream));
+        if (ws) CHIP_CHECK(hipFree(ws));
+        ws = nullptr;
+        ws_floats = 0;
+        CHIP_CHECK(hipMalloc(&ws, need * sizeof(float)));
+        ws_floats = need;
+    }
+    j.ws = ws;
+    j.ws_floats = ws_floats;
+    return 0;
+}
+
 static int gemm_op(int fmt, const void *w, size_t rows, size_t cols, const float *x, size_t n, float *y) {
     CHIP_TRY(ensure_ready());
     if (!w || !x || !y) return fail("HIP backend: gemm with a null pointer.");
@@ -165,6 +183,7 @@ static int gemm_op(int fmt, const void *w, size_t rows, size_t cols, const float
     j.x = x;
     j.n = n;
     j.y = y;
+    CHIP_TRY(gemm_scratch(rows, cols, n, j));
     return launch_gemm(j, g_stream);
 }
 
@@ -302,6 +321,7 @@ int cheetah_hip_time_gemm(uint32_t fmt, const void *const *w, size_t nbuf, size_
     j.x = x;
     j.n = n;
     j.y = y;
+    CHIP_TRY(gemm_scratch(rows, cols, n, j));
     hipEvent_t e0, e1;
     CHIP_CHECK(hipEventCreate(&e0));
     CHIP_CHECK(hipEventCreate(&e1));

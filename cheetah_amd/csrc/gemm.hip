@@ -9,8 +9,19 @@
 // so two v_mfma_f32_32x32x16_bf16 per k-step carry x to ~2^-17 relative
 // error (f32 accumulation), instead of bf16's 2^-9.
 //
-// Tiling: a 256-thread block computes a 64 (tokens) x 64 (weight rows) tile
-// as 2 x 2 waves of 32 x 32; K advances 64 per LDS stage.
+// Tiling: a 256-thread block computes 64 or 128 tokens x 128 weight rows as
+// 2 x 2 waves (each 32 or 64 tokens x 64 rows); K advances 32 per LDS stage,
+// double-buffered, the next stage's global loads in flight during the MFMAs.
+//
+// Accumulation order: K is cut into chunks of a depth fixed by K alone; each
+// chunk is accumulated from zero and the chunk sums are folded left to right
+// (t = 0; t += c0; t += c1; ...). With many tiles a block folds its chunks in
+// registers; with few tiles every chunk is its own block (split-K) and a
+// reduce kernel folds the stored chunk sums in the same order. Both give the
+// same bits, so a token's outputs never depend on how many tokens share the
+// call (chunked prefill stays bit-exact however the prompt is cut).
+#include <algorithm>
+
 #include "kernels.hpp"
 
 namespace chip {
@@ -20,8 +31,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kThreads = 256;
-constexpr int BM = 64, BN = 64, BK = 64;
-constexpr int LDK = BK + 8;  // LDS row stride in bf16 (pad breaks bank conflicts)
+constexpr int BN = 128, BK = 32;
+constexpr int LDK = BK + 8;  // 80-byte LDS rows: 16 consecutive rows start on distinct bank groups
 
 struct GArgs {
     const uint8_t *w, *w2;
@@ -32,6 +43,9 @@ struct GArgs {
     const float *bias;
     float *y, *residual;
     int epi;
+    int chunk, nchunks;  // accumulation chunk depth (multiple of BK) and count
+    float *ws;           // split-K: [nchunks][M][N] chunk sums (a second set for the dual matrix)
+    int vec_x, vec_w;    // 16-byte global loads allowed
 };
 
 __device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) { return (uint32_t)lo | ((uint32_t)hi << 16); }
@@ -39,204 +53,353 @@ __device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) { return (ui
 // BF16 bits of a small integer code (exact).
 __device__ __forceinline__ uint16_t code_bf16(int code) { return (uint16_t)(__float_as_uint((float)code) >> 16); }
 
-// Stage a BN x BK tile of W (rows n0.., k0..) into LDS as BF16 bits.
-template <int FMT>
-__device__ __forceinline__ void stage_w(const GArgs &a, const uint8_t *w, int n0, int k0, uint16_t *ws) {
-    const int tid = threadIdx.x;
-    if constexpr (FMT == FMT_BF16) {
-        // 64 rows x 64 k = 64 x 128 B: 512 chunks of 16 B (8 k), 2 per thread.
+__device__ __forceinline__ bf16x8 frag(const uint16_t *base, int row, int k) {
+    return __builtin_bit_cast(bf16x8, *(const u32x4 *)(base + row * LDK + k));
+}
+
+// One stage's operands in flight: X as f32, W as raw reference bytes.
+template <int MT>
+struct Regs {
+    static constexpr int XV = 64 * MT * BK / 4 / kThreads;  // float4 per thread
+    f32x4 x[XV];
+    u32x4 w[2];   // BF16: 2 x 8 elements; Q8: w[0] = 16 codes; Q4: w[0].xy = 16 codes
+    u32x4 w2[2];  // dual matrix
+};
+
+template <int MT>
+__device__ __forceinline__ void load_x(const GArgs &a, int m0, int k0, Regs<MT> &r) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int c = tid + i * kThreads;
-            const int r = c >> 3, kc = (c & 7) * 8;
-            const int n = n0 + r, k = k0 + kc;
-            uint32_t v[4] = {0, 0, 0, 0};
-            if (n < a.N) {
-                const uint16_t *src = (const uint16_t *)(w + (size_t)n * a.stride) + k;
-                if (k + 8 <= a.K && (a.stride % 16) == 0) {
-                    u32x4 t = *(const u32x4 *)src;
-                    v[0] = t[0]; v[1] = t[1]; v[2] = t[2]; v[3] = t[3];
-                } else {
-                    uint16_t e[8];
-#pragma unroll
-                    for (int q = 0; q < 8; ++q) e[q] = (k + q < a.K) ? src[q] : 0;
-                    v[0] = pack2(e[0], e[1]); v[1] = pack2(e[2], e[3]);
-                    v[2] = pack2(e[4], e[5]); v[3] = pack2(e[6], e[7]);
-                }
-            }
-            *(u32x4 *)(ws + r * LDK + kc) = u32x4{v[0], v[1], v[2], v[3]};
-        }
-    } else if constexpr (FMT == FMT_Q8) {
-        // 64 rows x 64 codes: 256 chunks of 16 codes, 1 per thread.
-        const int r = tid >> 2, kc = (tid & 3) * 16;
-        const int n = n0 + r, k = k0 + kc;
-        uint16_t e[16];
-        if (n < a.N) {
-            const int8_t *src = (const int8_t *)(w + (size_t)n * a.stride) + k;
-            if (k + 16 <= a.K && (a.stride % 16) == 0 && ((uintptr_t)src % 16) == 0) {
-                u32x4 t = *(const u32x4 *)src;
-#pragma unroll
-                for (int q = 0; q < 16; ++q) e[q] = code_bf16((int)(int8_t)(t[q >> 2] >> (8 * (q & 3))));
+    for (int i = 0; i < Regs<MT>::XV; ++i) {
+        const int c = threadIdx.x + kThreads * i;
+        const int row = c >> 3, kc = (c & 7) * 4;
+        const int m = m0 + row, k = k0 + kc;
+        f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        if (m < a.M && k < a.K) {
+            const float *src = a.x + (size_t)m * a.K + k;
+            if (a.vec_x) {
+                v = *(const f32x4 *)src;
             } else {
 #pragma unroll
-                for (int q = 0; q < 16; ++q) e[q] = (k + q < a.K) ? code_bf16(src[q]) : 0;
+                for (int q = 0; q < 4; ++q) v[q] = k + q < a.K ? src[q] : 0.f;
             }
-        } else {
-#pragma unroll
-            for (int q = 0; q < 16; ++q) e[q] = 0;
         }
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-            *(u32x4 *)(ws + r * LDK + kc + 8 * h) =
-                u32x4{pack2(e[8 * h], e[8 * h + 1]), pack2(e[8 * h + 2], e[8 * h + 3]),
-                      pack2(e[8 * h + 4], e[8 * h + 5]), pack2(e[8 * h + 6], e[8 * h + 7])};
-    } else {
-        // Q4: 64 rows x 64 codes = 64 x 32 B; rows are only 4-byte aligned.
-        const int r = tid >> 2, kc = (tid & 3) * 16;
-        const int n = n0 + r, k = k0 + kc;
-        uint16_t e[16];
-        if (n < a.N) {
-            const uint8_t *src = w + (size_t)n * a.stride + (k >> 1);
-            if (k + 16 <= a.K) {
-                const uint32_t d0 = *(const uint32_t *)src, d1 = *(const uint32_t *)(src + 4);
-#pragma unroll
-                for (int q = 0; q < 8; ++q) {
-                    e[q] = code_bf16(((int)(d0 << (28 - 4 * q))) >> 28);
-                    e[8 + q] = code_bf16(((int)(d1 << (28 - 4 * q))) >> 28);
-                }
-            } else {
-#pragma unroll
-                for (int q = 0; q < 16; ++q) {
-                    int code = 0;
-                    if (k + q < a.K) {
-                        const uint8_t byte = src[q >> 1];
-                        const int nib = (q & 1) ? (byte >> 4) : (byte & 0xF);
-                        code = nib >= 8 ? nib - 16 : nib;
-                    }
-                    e[q] = code_bf16(code);
-                }
-            }
-        } else {
-#pragma unroll
-            for (int q = 0; q < 16; ++q) e[q] = 0;
-        }
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-            *(u32x4 *)(ws + r * LDK + kc + 8 * h) =
-                u32x4{pack2(e[8 * h], e[8 * h + 1]), pack2(e[8 * h + 2], e[8 * h + 3]),
-                      pack2(e[8 * h + 4], e[8 * h + 5]), pack2(e[8 * h + 6], e[8 * h + 7])};
+        r.x[i] = v;
     }
 }
 
-// Stage a BM x BK tile of X (f32) into LDS as hi / lo BF16 halves.
-__device__ __forceinline__ void stage_x(const GArgs &a, int m0, int k0, uint16_t *xh, uint16_t *xl) {
-    const int tid = threadIdx.x;
-    // 64 rows x 64 k f32 = 1024 chunks of 4 floats, 4 per thread.
+template <int MT>
+__device__ __forceinline__ void store_x(const Regs<MT> &r, uint16_t *xh, uint16_t *xl) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int c = tid + i * kThreads;
-        const int r = c >> 4, kc = (c & 15) * 4;
-        const int m = m0 + r, k = k0 + kc;
-        float v[4] = {0.f, 0.f, 0.f, 0.f};
-        if (m < a.M) {
-            const float *src = a.x + (size_t)m * a.K + k;
-            if (k + 4 <= a.K && (a.K % 4) == 0) {
-                f32x4 t = *(const f32x4 *)src;
-                v[0] = t[0]; v[1] = t[1]; v[2] = t[2]; v[3] = t[3];
-            } else {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) v[q] = (k + q < a.K) ? src[q] : 0.f;
-            }
-        }
+    for (int i = 0; i < Regs<MT>::XV; ++i) {
+        const int c = threadIdx.x + kThreads * i;
+        const int row = c >> 3, kc = (c & 7) * 4;
         uint16_t h[4], l[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            h[q] = f32_bf16_rne(v[q]);
-            l[q] = f32_bf16_rne(v[q] - bf16_f32(h[q]));
+            const __bf16 hb = (__bf16)r.x[i][q];
+            h[q] = __builtin_bit_cast(uint16_t, hb);
+            l[q] = __builtin_bit_cast(uint16_t, (__bf16)(r.x[i][q] - (float)hb));
         }
-        *(uint2 *)(xh + r * LDK + kc) = make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
-        *(uint2 *)(xl + r * LDK + kc) = make_uint2(pack2(l[0], l[1]), pack2(l[2], l[3]));
+        *(uint2 *)(xh + row * LDK + kc) = make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
+        *(uint2 *)(xl + row * LDK + kc) = make_uint2(pack2(l[0], l[1]), pack2(l[2], l[3]));
     }
 }
 
-__device__ __forceinline__ bf16x8 frag(const uint16_t *base, int row, int k) {
-    u32x4 t = *(const u32x4 *)(base + row * LDK + k);
-    return __builtin_bit_cast(bf16x8, t);
-}
-
-template <int FMT, bool DUAL>
-__global__ __launch_bounds__(kThreads) void gemm_kernel(GArgs a) {
-    __shared__ __attribute__((aligned(16))) uint16_t xh[BM * LDK];
-    __shared__ __attribute__((aligned(16))) uint16_t xl[BM * LDK];
-    __shared__ __attribute__((aligned(16))) uint16_t ws[BN * LDK];
-    __shared__ __attribute__((aligned(16))) uint16_t ws2[DUAL ? BN * LDK : 8];
-
-    const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
-    f32x16 acc = {}, acc2 = {};
-
-    for (int k0 = 0; k0 < a.K; k0 += BK) {
-        stage_x(a, m0, k0, xh, xl);
-        stage_w<FMT>(a, a.w, n0, k0, ws);
-        if constexpr (DUAL) stage_w<FMT>(a, a.w2, n0, k0, ws2);
-        __syncthreads();
+// W stage: BN rows x BK columns of the reference layout.
+template <int FMT>
+__device__ __forceinline__ void load_w(const GArgs &a, const uint8_t *w, int n0, int k0, u32x4 (&out)[2]) {
+    const int tid = threadIdx.x;
+    if constexpr (FMT == FMT_BF16) {
 #pragma unroll
-        for (int kk = 0; kk < BK; kk += 16) {
-            const int kf = kk + 8 * (lane >> 5);
-            const bf16x8 ah = frag(xh, wm + (lane & 31), kf);
-            const bf16x8 al = frag(xl, wm + (lane & 31), kf);
-            const bf16x8 b = frag(ws, wn + (lane & 31), kf);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, b, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, b, acc, 0, 0, 0);
-            if constexpr (DUAL) {
-                const bf16x8 b2 = frag(ws2, wn + (lane & 31), kf);
-                acc2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, b2, acc2, 0, 0, 0);
-                acc2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, b2, acc2, 0, 0, 0);
+        for (int j = 0; j < 2; ++j) {
+            const int c = tid + kThreads * j;
+            const int row = c >> 2, kc = (c & 3) * 8;
+            const int n = n0 + row, k = k0 + kc;
+            u32x4 v = {0u, 0u, 0u, 0u};
+            if (n < a.N && k < a.K) {
+                const uint16_t *src = (const uint16_t *)(w + (size_t)n * a.stride) + k;
+                if (a.vec_w) {
+                    v = *(const u32x4 *)src;
+                } else {
+                    uint16_t e[8];
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) e[q] = k + q < a.K ? src[q] : 0;
+                    v = u32x4{pack2(e[0], e[1]), pack2(e[2], e[3]), pack2(e[4], e[5]), pack2(e[6], e[7])};
+                }
+            }
+            out[j] = v;
+        }
+    } else {
+        // Q8 / Q4: 16 codes per thread, rows tid / 2, codes 16 (tid % 2) ..
+        const int row = tid >> 1, kc = (tid & 1) * 16;
+        const int n = n0 + row, k = k0 + kc;
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (n < a.N && k < a.K) {
+            const uint8_t *rp = w + (size_t)n * a.stride;
+            if constexpr (FMT == FMT_Q8) {
+                if (a.vec_w) {
+                    v = *(const u32x4 *)(rp + k);
+                } else {
+                    uint32_t d[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+                    for (int q = 0; q < 16; ++q)
+                        if (k + q < a.K) d[q >> 2] |= (uint32_t)rp[k + q] << (8 * (q & 3));
+                    v = u32x4{d[0], d[1], d[2], d[3]};
+                }
+            } else {
+                // Rows are 4-byte aligned; k is a multiple of 16, so the 8 code
+                // bytes are 8-byte aligned within the row.
+                if (k + 16 <= a.K) {
+                    const uint32_t *p = (const uint32_t *)(rp + (k >> 1));
+                    v = u32x4{p[0], p[1], 0u, 0u};
+                } else {
+                    uint32_t d[2] = {0u, 0u};
+                    for (int q = 0; q < 16 && k + q < a.K; ++q) {
+                        const uint8_t byte = rp[(k + q) >> 1];
+                        const uint32_t nib = ((k + q) & 1) ? (byte >> 4) : (byte & 0xF);
+                        d[q >> 3] |= nib << (4 * (q & 7));
+                    }
+                    v = u32x4{d[0], d[1], 0u, 0u};
+                }
             }
         }
-        __syncthreads();
-    }
-
-    // D layout of the 32x32 MFMA: column = lane % 32, row = 8*(r/4) + 4*(lane/32) + r%4.
-    const int n = n0 + wn + (lane & 31);
-    if (n >= a.N) return;
-    const float sc = a.sc ? a.sc[n] : 1.0f;
-    const float sc2 = (DUAL && a.sc2) ? a.sc2[n] : 1.0f;
-    const float b = a.bias ? a.bias[n] : 0.0f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (m >= a.M) continue;
-        float v = a.sc ? acc[r] * sc : acc[r];
-        const size_t o = (size_t)m * a.N + n;
-        if constexpr (DUAL) {
-            const float u = a.sc2 ? acc2[r] * sc2 : acc2[r];
-            a.y[o] = v * (u / (1.0f + expf(-v)));
-        } else {
-            if (a.bias) v = v + b;
-            if (a.epi == EPI_RESIDUAL) a.residual[o] = a.residual[o] + v;
-            else a.y[o] = v;
-        }
+        out[0] = v;
     }
 }
 
 template <int FMT>
-int launch_fmt(const GArgs &a, bool dual, hipStream_t s) {
-    dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM);
-    if (dual) hipLaunchKernelGGL((gemm_kernel<FMT, true>), grid, dim3(kThreads), 0, s, a);
-    else hipLaunchKernelGGL((gemm_kernel<FMT, false>), grid, dim3(kThreads), 0, s, a);
+__device__ __forceinline__ void store_w(const u32x4 (&in)[2], uint16_t *ws) {
+    const int tid = threadIdx.x;
+    if constexpr (FMT == FMT_BF16) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int c = tid + kThreads * j;
+            *(u32x4 *)(ws + (c >> 2) * LDK + (c & 3) * 8) = in[j];
+        }
+    } else {
+        const int row = tid >> 1, kc = (tid & 1) * 16;
+        uint16_t e[16];
+        if constexpr (FMT == FMT_Q8) {
+#pragma unroll
+            for (int q = 0; q < 16; ++q) e[q] = code_bf16((int)(int8_t)(in[0][q >> 2] >> (8 * (q & 3))));
+        } else {
+#pragma unroll
+            for (int q = 0; q < 16; ++q) e[q] = code_bf16(((int)(in[0][q >> 3] << (28 - 4 * (q & 7)))) >> 28);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            *(u32x4 *)(ws + row * LDK + kc + 8 * h) =
+                u32x4{pack2(e[8 * h], e[8 * h + 1]), pack2(e[8 * h + 2], e[8 * h + 3]),
+                      pack2(e[8 * h + 4], e[8 * h + 5]), pack2(e[8 * h + 6], e[8 * h + 7])};
+    }
+}
+
+// out = f(v * row scale (+ bias)); dual: SwiGLU of gate v and up u.
+template <bool DUAL>
+__device__ __forceinline__ void epilogue(const GArgs &a, int m, int n, float v, float u) {
+    if (a.sc) v = v * a.sc[n];
+    const size_t o = (size_t)m * a.N + n;
+    if constexpr (DUAL) {
+        if (a.sc2) u = u * a.sc2[n];
+        // silu_multiply, ops.rs:743-747: g * (u / (1 + exp(-g))).
+        a.y[o] = v * (u / (1.0f + expf(-v)));
+    } else {
+        if (a.bias) v = v + a.bias[n];
+        if (a.epi == EPI_RESIDUAL) a.residual[o] = a.residual[o] + v;
+        else a.y[o] = v;
+    }
+}
+
+// blockIdx: x = weight-row tile, y = token tile, z = chunk (split-K) or 0.
+template <int FMT, bool DUAL, int MT>
+__global__ __launch_bounds__(kThreads) void gemm_kernel(GArgs a, int split) {
+    constexpr int BM = 64 * MT;
+    __shared__ __attribute__((aligned(16))) uint16_t xh[2][BM * LDK];
+    __shared__ __attribute__((aligned(16))) uint16_t xl[2][BM * LDK];
+    __shared__ __attribute__((aligned(16))) uint16_t wsm[2][BN * LDK];
+    __shared__ __attribute__((aligned(16))) uint16_t wsm2[DUAL ? 2 : 1][DUAL ? BN * LDK : 8];
+
+    const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = (wave >> 1) * 32 * MT, wn = (wave & 1) * 64;
+    const int kbeg = split ? blockIdx.z * a.chunk : 0;
+    const int kend = split ? min(a.K, kbeg + a.chunk) : a.K;
+
+    f32x16 acc[MT][2], acc2[DUAL ? MT : 1][2], tot[MT][2], tot2[DUAL ? MT : 1][2];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            acc[i][j] = f32x16{};
+            tot[i][j] = f32x16{};
+            if constexpr (DUAL) {
+                acc2[i][j] = f32x16{};
+                tot2[i][j] = f32x16{};
+            }
+        }
+
+    Regs<MT> r;
+    load_x<MT>(a, m0, kbeg, r);
+    load_w<FMT>(a, a.w, n0, kbeg, r.w);
+    if constexpr (DUAL) load_w<FMT>(a, a.w2, n0, kbeg, r.w2);
+    store_x<MT>(r, xh[0], xl[0]);
+    store_w<FMT>(r.w, wsm[0]);
+    if constexpr (DUAL) store_w<FMT>(r.w2, wsm2[0]);
+    __syncthreads();
+    int b = 0;
+    for (int k0 = kbeg; k0 < kend; k0 += BK) {
+        const bool more = k0 + BK < kend;
+        if (more) {
+            load_x<MT>(a, m0, k0 + BK, r);
+            load_w<FMT>(a, a.w, n0, k0 + BK, r.w);
+            if constexpr (DUAL) load_w<FMT>(a, a.w2, n0, k0 + BK, r.w2);
+        }
+#pragma unroll
+        for (int ks = 0; ks < BK; ks += 16) {
+            const int kf = ks + 8 * (lane >> 5);
+            bf16x8 ah[MT], al[MT], bw[2], bw2[DUAL ? 2 : 1];
+#pragma unroll
+            for (int i = 0; i < MT; ++i) {
+                ah[i] = frag(xh[b], wm + 32 * i + (lane & 31), kf);
+                al[i] = frag(xl[b], wm + 32 * i + (lane & 31), kf);
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                bw[j] = frag(wsm[b], wn + 32 * j + (lane & 31), kf);
+                if constexpr (DUAL) bw2[j] = frag(wsm2[b], wn + 32 * j + (lane & 31), kf);
+            }
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bw[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bw[j], acc[i][j], 0, 0, 0);
+                    if constexpr (DUAL) {
+                        acc2[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bw2[j], acc2[i][j], 0, 0, 0);
+                        acc2[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bw2[j], acc2[i][j], 0, 0, 0);
+                    }
+                }
+        }
+        // Chunk end: fold the chunk sum into the running total (t += c).
+        if (k0 + BK >= kend || ((k0 + BK) % a.chunk) == 0) {
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    tot[i][j] += acc[i][j];
+                    acc[i][j] = f32x16{};
+                    if constexpr (DUAL) {
+                        tot2[i][j] += acc2[i][j];
+                        acc2[i][j] = f32x16{};
+                    }
+                }
+        }
+        if (more) {
+            store_x<MT>(r, xh[b ^ 1], xl[b ^ 1]);
+            store_w<FMT>(r.w, wsm[b ^ 1]);
+            if constexpr (DUAL) store_w<FMT>(r.w2, wsm2[b ^ 1]);
+        }
+        __syncthreads();
+        b ^= 1;
+    }
+    // D layout of the 32x32 MFMA: column = lane % 32, row = 8*(r/4) + 4*(lane/32) + r%4.
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int n = n0 + wn + 32 * j + (lane & 31);
+        if (n >= a.N) continue;
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int m = m0 + wm + 32 * i + 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
+                if (m >= a.M) continue;
+                const float v = tot[i][j][q];
+                const float u = DUAL ? tot2[DUAL ? i : 0][j][q] : 0.f;
+                if (split) {
+                    const size_t o = ((size_t)blockIdx.z * a.M + m) * a.N + n;
+                    a.ws[o] = v;
+                    if constexpr (DUAL) a.ws[(size_t)a.nchunks * a.M * a.N + o] = u;
+                } else {
+                    epilogue<DUAL>(a, m, n, v, u);
+                }
+            }
+    }
+}
+
+// Folds the stored chunk sums in chunk order (t = 0; t += c_z) and applies
+// the epilogue: the same bits as the in-register fold.
+template <bool DUAL>
+__global__ __launch_bounds__(kThreads) void gemm_reduce_kernel(GArgs a) {
+    const size_t MN = (size_t)a.M * a.N;
+    const size_t e = (size_t)blockIdx.x * kThreads + threadIdx.x;
+    if (e >= MN) return;
+    float v = 0.f, u = 0.f;
+    for (int z = 0; z < a.nchunks; ++z) {
+        v += a.ws[(size_t)z * MN + e];
+        if constexpr (DUAL) u += a.ws[((size_t)a.nchunks + z) * MN + e];
+    }
+    epilogue<DUAL>(a, (int)(e / a.N), (int)(e % a.N), v, u);
+}
+
+template <int FMT, bool DUAL, int MT>
+int launch_mt(const GArgs &a, bool split, hipStream_t s) {
+    constexpr int BM = 64 * MT;
+    const dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM, split ? a.nchunks : 1);
+    hipLaunchKernelGGL((gemm_kernel<FMT, DUAL, MT>), grid, dim3(kThreads), 0, s, a, split ? 1 : 0);
     CHIP_CHECK(hipGetLastError());
+    if (split) {
+        const size_t MN = (size_t)a.M * a.N;
+        hipLaunchKernelGGL((gemm_reduce_kernel<DUAL>), dim3((unsigned)((MN + kThreads - 1) / kThreads)),
+                           dim3(kThreads), 0, s, a);
+        CHIP_CHECK(hipGetLastError());
+    }
     return 0;
 }
 
+template <int FMT>
+int launch_fmt(const GArgs &a, bool dual, size_t ws_floats, hipStream_t s) {
+    const long n_tiles = (a.N + BN - 1) / BN;
+    const long tiles128 = n_tiles * ((a.M + 127) / 128), tiles64 = n_tiles * ((a.M + 63) / 64);
+    const long cus = device_cus();
+    // Many tiles: fold in registers (128-token tiles when they still fill
+    // the chip, dual always 64). Few tiles: split-K over the chunks when the
+    // workspace holds them.
+    const bool split = a.nchunks > 1 && tiles64 < cus && a.ws &&
+                       ws_floats >= gemm_workspace_floats(a.N, a.K, a.M, dual);
+    if (dual) {
+        if (split) return launch_mt<FMT, true, 1>(a, true, s);
+        return launch_mt<FMT, true, 1>(a, false, s);
+    }
+    if (!split && tiles128 >= cus) return launch_mt<FMT, false, 2>(a, false, s);
+    return launch_mt<FMT, false, 1>(a, split, s);
+}
+
 }  // namespace
+
+int gemm_chunk_depth(int K) {
+    const int want = std::max(256, (K + 15) / 16);
+    return (want + BK - 1) / BK * BK;
+}
+
+size_t gemm_workspace_floats(size_t N, size_t K, size_t M, bool dual) {
+    const int chunk = gemm_chunk_depth((int)K);
+    const size_t nchunks = (K + chunk - 1) / chunk;
+    if (nchunks <= 1) return 0;
+    return nchunks * M * N * (dual ? 2 : 1);
+}
+
+size_t gemm_split_workspace_floats(size_t N, size_t K, size_t m_max, bool dual) {
+    // The split path runs only while 64-token tiles leave CUs idle.
+    const size_t n_tiles = (N + BN - 1) / BN;
+    const size_t m_split = 64 * (((size_t)device_cus() + n_tiles - 1) / n_tiles);
+    return gemm_workspace_floats(N, K, std::min(m_max, m_split), dual);
+}
 
 int launch_gemm(const GemmJob &job, hipStream_t s) {
     const WMat &w = job.w;
     if (job.n == 0) return 0;
     if (!w.base || !job.x || w.rows == 0 || w.cols == 0) return fail("HIP backend: gemm needs a weight and an input.");
-    if (w.rows > (size_t)INT32_MAX || w.cols > (size_t)INT32_MAX || job.n > 65535u * BM)
+    if (w.rows > (size_t)INT32_MAX || w.cols > (size_t)INT32_MAX || job.n > 65535u * 64u)
         return fail("HIP backend: gemm shape too large.");
     const bool dual = job.epi == EPI_SWIGLU;
     if (dual && (!job.w2.base || job.w2.fmt != w.fmt || job.w2.rows != w.rows || job.w2.cols != w.cols))
@@ -256,10 +419,20 @@ int launch_gemm(const GemmJob &job, hipStream_t s) {
     a.y = job.y;
     a.residual = job.residual;
     a.epi = job.epi;
+    a.chunk = gemm_chunk_depth(a.K);
+    a.nchunks = (a.K + a.chunk - 1) / a.chunk;
+    a.ws = job.ws;
+    a.vec_x = (a.K % 4) == 0 && ((uintptr_t)job.x % 16) == 0;
+    const uintptr_t p1 = (uintptr_t)a.w, p2 = dual ? (uintptr_t)a.w2 : p1;
+    if (w.fmt == FMT_BF16) a.vec_w = a.stride % 16 == 0 && p1 % 16 == 0 && p2 % 16 == 0 && a.K % 8 == 0;
+    else if (w.fmt == FMT_Q8) a.vec_w = a.stride % 16 == 0 && p1 % 16 == 0 && p2 % 16 == 0 && a.K % 16 == 0;
+    else a.vec_w = 0;
+    if (w.fmt == FMT_Q4 && (a.stride % 4 != 0 || p1 % 4 != 0 || p2 % 4 != 0))
+        return fail("HIP backend: Q4 rows must be 4-byte aligned.");
     switch (w.fmt) {
-        case FMT_BF16: return launch_fmt<FMT_BF16>(a, dual, s);
-        case FMT_Q8: return launch_fmt<FMT_Q8>(a, dual, s);
-        case FMT_Q4: return launch_fmt<FMT_Q4>(a, dual, s);
+        case FMT_BF16: return launch_fmt<FMT_BF16>(a, dual, job.ws_floats, s);
+        case FMT_Q8: return launch_fmt<FMT_Q8>(a, dual, job.ws_floats, s);
+        case FMT_Q4: return launch_fmt<FMT_Q4>(a, dual, job.ws_floats, s);
     }
     return fail("HIP backend: unknown weight format.");
 }

@@ -52,8 +52,16 @@ struct GemmJob {
     float *y = nullptr;          // [n][rows]
     float *residual = nullptr;   // [n][rows]
     int epi = EPI_STORE;
+    // Optional split-K scratch; without room for the chunk sums the GEMM
+    // folds in registers (the same bits, fewer blocks).
+    float *ws = nullptr;
+    size_t ws_floats = 0;
 };
 int launch_gemm(const GemmJob &job, hipStream_t stream);
+int gemm_chunk_depth(int K);
+size_t gemm_workspace_floats(size_t N, size_t K, size_t M, bool dual);
+// Scratch the split path can use for any token count up to m_max.
+size_t gemm_split_workspace_floats(size_t N, size_t K, size_t m_max, bool dual);
 
 // ---------------------------------------------------------------------------
 // Quantization (bit-exact to q8.rs / q4.rs quantize) and dequantization.

@@ -19,6 +19,7 @@
 // residual}, LM head GEMV with fused final norm, argmax. The token and
 // position live in device memory, so the same graph replays every step and
 // the greedy loop can run back to back with no host round trip.
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -160,6 +161,8 @@ struct cheetah_hip_model {
     float *hidden = nullptr, *normed = nullptr, *qkv = nullptr, *qrot = nullptr, *attn = nullptr, *act = nullptr;
     float *logits = nullptr, *part = nullptr;
     size_t part_floats = 0;
+    float *gemm_ws = nullptr;  // split-K chunk sums of the prefill GEMMs
+    size_t gemm_ws_floats = 0;
     uint32_t *tokens_dev = nullptr, *next_dev = nullptr, *hist_dev = nullptr;
     int32_t *step_dev = nullptr;  // [0] = token, [1] = position
     void *argmax_scratch = nullptr;
@@ -555,6 +558,14 @@ int init_instance(cheetah_hip_model *m) {
     const size_t part_rows = std::max(R * prefill_splits, (size_t)attention_max_splits());
     m->part_floats = part_rows * c.q_heads * (c.head_dim + 2);
     CHIP_TRY(m->mem.alloc(&m->part, m->part_floats));
+    {
+        const size_t qd = sh.q_dim(), kvd = sh.kv_dim(), I = c.intermediate_size, H = c.hidden_size;
+        m->gemm_ws_floats = std::max({gemm_split_workspace_floats(qd + 2 * kvd, H, R, false),
+                                      gemm_split_workspace_floats(H, qd, R, false),
+                                      gemm_split_workspace_floats(I, H, R, true),
+                                      gemm_split_workspace_floats(H, I, R, false), (size_t)1});
+        CHIP_TRY(m->mem.alloc(&m->gemm_ws, m->gemm_ws_floats));
+    }
     CHIP_TRY(m->mem.alloc(&m->tokens_dev, sh.kv_capacity));
     CHIP_TRY(m->mem.alloc(&m->next_dev, 1));
     CHIP_TRY(m->mem.alloc(&m->hist_dev, sh.kv_capacity + 1));
@@ -753,6 +764,8 @@ int enqueue_chunk(cheetah_hip_model *m, const uint32_t *tokens_dev, size_t rows,
         qkv.n = rows;
         qkv.bias = L.qkv_bias;
         qkv.y = m->qkv;
+        qkv.ws = m->gemm_ws;
+        qkv.ws_floats = m->gemm_ws_floats;
         CHIP_TRY(launch_gemm(qkv, s));
         CHIP_TRY(launch_rope_append(m->qkv, m->qrot, rows, (int)c.q_heads, geom(m), L.kv, sh.rope_cos, sh.rope_sin,
                                     (int)c.rotary_dim, pos, nullptr, s));
@@ -778,6 +791,8 @@ int enqueue_chunk(cheetah_hip_model *m, const uint32_t *tokens_dev, size_t rows,
         o.bias = L.o_bias;
         o.residual = m->hidden;
         o.epi = EPI_RESIDUAL;
+        o.ws = m->gemm_ws;
+        o.ws_floats = m->gemm_ws_floats;
         CHIP_TRY(launch_gemm(o, s));
         CHIP_TRY(launch_rmsnorm_rows(m->hidden, L.ln2, c.rms_eps, rows, H, m->normed, s));
         GemmJob gu;
@@ -787,6 +802,8 @@ int enqueue_chunk(cheetah_hip_model *m, const uint32_t *tokens_dev, size_t rows,
         gu.n = rows;
         gu.y = m->act;
         gu.epi = EPI_SWIGLU;
+        gu.ws = m->gemm_ws;
+        gu.ws_floats = m->gemm_ws_floats;
         CHIP_TRY(launch_gemm(gu, s));
         GemmJob dn;
         dn.w = L.down;
@@ -794,6 +811,8 @@ int enqueue_chunk(cheetah_hip_model *m, const uint32_t *tokens_dev, size_t rows,
         dn.n = rows;
         dn.residual = m->hidden;
         dn.epi = EPI_RESIDUAL;
+        dn.ws = m->gemm_ws;
+        dn.ws_floats = m->gemm_ws_floats;
         CHIP_TRY(launch_gemm(dn, s));
     }
     if (last_chunk) {
