@@ -151,11 +151,13 @@ def main(argv=None) -> int:
     import json
 
     ap = argparse.ArgumentParser()
-    ap.add_argument("parts", nargs="*", choices=["attention", "gemv", "gemm"])
+    ap.add_argument("parts", nargs="*", help="attention, gemv and/or gemm")
     ap.add_argument("--shapes", default="4096x4096,4096x14336,14336x4096")
     ap.add_argument("--fmts", default="q8,q4")
     args = ap.parse_args(argv)
     parts = set(args.parts or ["attention", "gemv", "gemm"])
+    if parts - {"attention", "gemv", "gemm"}:
+        ap.error(f"unknown part(s): {sorted(parts - {'attention', 'gemv', 'gemm'})}")
     hip.init(0)
     if "attention" in parts:
         print(json.dumps({"attention": attention()}), flush=True)
