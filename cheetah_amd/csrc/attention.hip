@@ -55,6 +55,32 @@ __device__ __forceinline__ void load8(const float *p, float (&f)[8]) {
     f[4] = b[0]; f[5] = b[1]; f[6] = b[2]; f[7] = b[3];
 }
 
+// Eight consecutive K or V elements as loaded (converted to f32 at use), so
+// a whole tile can be in flight while the previous one computes.
+template <class KT>
+struct Raw8;
+template <>
+struct Raw8<uint16_t> {
+    u32x4 w;
+    __device__ void load(const uint16_t *p) { w = *(const u32x4 *)p; }
+    __device__ void get(float (&f)[8]) const {
+        f[0] = bf16_lo(w[0]); f[1] = bf16_hi(w[0]); f[2] = bf16_lo(w[1]); f[3] = bf16_hi(w[1]);
+        f[4] = bf16_lo(w[2]); f[5] = bf16_hi(w[2]); f[6] = bf16_lo(w[3]); f[7] = bf16_hi(w[3]);
+    }
+};
+template <>
+struct Raw8<float> {
+    f32x4 a, b;
+    __device__ void load(const float *p) {
+        a = *(const f32x4 *)p;
+        b = *(const f32x4 *)(p + 4);
+    }
+    __device__ void get(float (&f)[8]) const {
+        f[0] = a[0]; f[1] = a[1]; f[2] = a[2]; f[3] = a[3];
+        f[4] = b[0]; f[5] = b[1]; f[6] = b[2]; f[7] = b[3];
+    }
+};
+
 template <int HD, int G, class KT, bool DIRECT>
 __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
     constexpr int T = HD / 8;          // threads per position row (8 dims each)
@@ -106,18 +132,31 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
         l_run[i] = 0.f;
     }
 
-    for (long t0 = start; t0 < end; t0 += TP) {
-        const int page = a.page_table[t0 / a.page_size];
-        const long slot0 = t0 % a.page_size;
-        const size_t tile_off = (((size_t)page * a.kv_heads + g) * a.page_size + slot0) * HD;
+    // Tile t0 + TP is loaded while tile t0 computes.
+    Raw8<KT> ck[TP / P], cv[TP / P], nk[TP / P], nv[TP / P];
+    auto issue = [&](long t, Raw8<KT> (&kr)[TP / P], Raw8<KT> (&vr)[TP / P]) {
+        const int page = a.page_table[t / a.page_size];
+        const size_t tile_off = (((size_t)page * a.kv_heads + g) * a.page_size + t % a.page_size) * HD;
         const KT *kt = (const KT *)a.k + tile_off;
         const KT *vt = (const KT *)a.v + tile_off;
-        // V rows are independent of the scores: start their loads now.
-        float vf[TP / P][8];
 #pragma unroll
         for (int p = 0; p < TP / P; ++p) {
             const int pi = p * P + pg;
-            if (t0 + pi < end) load8(vt + (size_t)pi * HD + d8 * 8, vf[p]);
+            if (t + pi < end) {
+                kr[p].load(kt + (size_t)pi * HD + d8 * 8);
+                vr[p].load(vt + (size_t)pi * HD + d8 * 8);
+            }
+        }
+    };
+    issue(start, ck, cv);
+    for (long t0 = start; t0 < end; t0 += TP) {
+        const bool more = t0 + TP < end;
+        if (more) issue(t0 + TP, nk, nv);
+        float vf[TP / P][8], kf[TP / P][8];
+#pragma unroll
+        for (int p = 0; p < TP / P; ++p) {
+            ck[p].get(kf[p]);
+            cv[p].get(vf[p]);
         }
         // Scores of every head of the group for the tile's rows.
 #pragma unroll
@@ -128,12 +167,10 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
 #pragma unroll
             for (int j = 0; j < G; ++j) dot[j] = 0.f;
             if (valid) {
-                float kf[8];
-                load8(kt + (size_t)pi * HD + d8 * 8, kf);
 #pragma unroll
                 for (int j = 0; j < G; ++j)
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) dot[j] = fmaf(kf[e], qr[j][e], dot[j]);
+                    for (int e = 0; e < 8; ++e) dot[j] = fmaf(kf[p][e], qr[j][e], dot[j]);
             }
 #pragma unroll
             for (int j = 0; j < G; ++j) {
@@ -176,6 +213,13 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
 #pragma unroll
                     for (int e = 0; e < 8; ++e) acc[j][e] = fmaf(pj, vf[p][e], acc[j][e]);
                 }
+            }
+        }
+        if (more) {
+#pragma unroll
+            for (int p = 0; p < TP / P; ++p) {
+                ck[p] = nk[p];
+                cv[p] = nv[p];
             }
         }
         __syncthreads();
@@ -240,10 +284,21 @@ __global__ __launch_bounds__(kThreads) void attn_combine_kernel(const float *par
     }
     __syncthreads();
     const int d = tid % HD, grp = tid / HD;
+    // Every split value this thread folds is loaded first (one memory round
+    // trip), then folded in split order.
+    constexpr int PER = kMaxSplits / GR;
+    float v[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int s = grp + GR * i;
+        v[i] = s < S ? p[(size_t)s * (HD + 2) + d] : 0.f;
+    }
     float o = 0.f;
-    for (int s = grp; s < S; s += GR) {
-        const float w = s_w[s];
-        if (w != 0.f) o = fmaf(w, p[(size_t)s * (HD + 2) + d], o);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int s = grp + GR * i;
+        const float w = s < S ? s_w[s] : 0.f;
+        if (w != 0.f) o = fmaf(w, v[i], o);
     }
     s_o[grp][d] = o;
     __syncthreads();
