@@ -171,6 +171,21 @@ static int gemm_scratch(size_t rows, size_t cols, size_t n, GemmJob &j) {
     }
     j.ws = ws;
     j.ws_floats = ws_floats;
+    // x split into BF16 halves once per call.
+    static thread_local uint16_t *xs = nullptr;
+    static thread_local size_t xs_elems = 0;
+    const size_t elems = n * cols;
+    if (elems > xs_elems) {
+        CHIP_CHECK(hipStreamSynchronize(g_stream));
+        if (xs) CHIP_CHECK(hipFree(xs));
+        xs = nullptr;
+        xs_elems = 0;
+        CHIP_CHECK(hipMalloc(&xs, 2 * elems * sizeof(uint16_t) + 256));
+        xs_elems = elems;
+    }
+    CHIP_TRY(launch_split_bf16(j.x, elems, xs, xs + (elems + 127) / 128 * 128, g_stream));
+    j.xh = xs;
+    j.xl = xs + (elems + 127) / 128 * 128;
     return 0;
 }
 
@@ -332,6 +347,8 @@ int cheetah_hip_time_gemm(uint32_t fmt, const void *const *w, size_t nbuf, size_
     CHIP_CHECK(hipEventRecord(e0, g_stream));
     for (size_t i = 0; i < iters; ++i) {
         j.w = WMat{(int)fmt, (const uint8_t *)w[i % nbuf], rows, cols};
+        // The x split is part of every GEMM call on f32 activations: timed too.
+        CHIP_TRY(launch_split_bf16(x, n * cols, (uint16_t *)j.xh, (uint16_t *)j.xl, g_stream));
         CHIP_TRY(launch_gemm(j, g_stream));
     }
     CHIP_CHECK(hipEventRecord(e1, g_stream));

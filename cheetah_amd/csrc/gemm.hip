@@ -40,6 +40,7 @@ struct GArgs {
     size_t stride;
     int N, K, M;  // N = weight rows, K = cols, M = tokens
     const float *x;
+    const uint16_t *xh, *xl;  // x pre-split into hi / lo BF16 halves, [M][K] (or null)
     const float *bias;
     float *y, *residual;
     int epi;
@@ -61,7 +62,9 @@ __device__ __forceinline__ bf16x8 frag(const uint16_t *base, int row, int k) {
 template <int MT>
 struct Regs {
     static constexpr int XV = 64 * MT * BK / 4 / kThreads;  // float4 per thread
+    static constexpr int XB = 64 * MT * BK / 8 / kThreads;  // 8-element BF16 chunks per thread
     f32x4 x[XV];
+    u32x4 xh[XB], xl[XB];
     u32x4 w[2];   // BF16: 2 x 8 elements; Q8: w[0] = 16 codes; Q4: w[0].xy = 16 codes
     u32x4 w2[2];  // dual matrix
 };
@@ -84,6 +87,34 @@ __device__ __forceinline__ void load_x(const GArgs &a, int m0, int k0, Regs<MT> 
             }
         }
         r.x[i] = v;
+    }
+}
+
+// Pre-split x: BM x BK BF16 per half, 16-byte chunks (K % 8 == 0).
+template <int MT>
+__device__ __forceinline__ void load_xs(const GArgs &a, int m0, int k0, Regs<MT> &r) {
+#pragma unroll
+    for (int i = 0; i < Regs<MT>::XB; ++i) {
+        const int c = threadIdx.x + kThreads * i;
+        const int row = c >> 2, kc = (c & 3) * 8;
+        const int m = m0 + row, k = k0 + kc;
+        if (m < a.M && k < a.K) {
+            r.xh[i] = *(const u32x4 *)(a.xh + (size_t)m * a.K + k);
+            r.xl[i] = *(const u32x4 *)(a.xl + (size_t)m * a.K + k);
+        } else {
+            r.xh[i] = u32x4{0u, 0u, 0u, 0u};
+            r.xl[i] = u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+}
+
+template <int MT>
+__device__ __forceinline__ void store_xs(const Regs<MT> &r, uint16_t *xh, uint16_t *xl) {
+#pragma unroll
+    for (int i = 0; i < Regs<MT>::XB; ++i) {
+        const int c = threadIdx.x + kThreads * i;
+        *(u32x4 *)(xh + (c >> 2) * LDK + (c & 3) * 8) = r.xh[i];
+        *(u32x4 *)(xl + (c >> 2) * LDK + (c & 3) * 8) = r.xl[i];
     }
 }
 
@@ -211,7 +242,7 @@ __device__ __forceinline__ void epilogue(const GArgs &a, int m, int n, float v, 
 }
 
 // blockIdx: x = weight-row tile, y = token tile, z = chunk (split-K) or 0.
-template <int FMT, bool DUAL, int MT>
+template <int FMT, bool DUAL, int MT, bool PRE>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GArgs a, int split) {
     constexpr int BM = 64 * MT;
     __shared__ __attribute__((aligned(16))) uint16_t xh[2][BM * LDK];
@@ -239,10 +270,12 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GArgs a, int split) {
         }
 
     Regs<MT> r;
-    load_x<MT>(a, m0, kbeg, r);
+    if constexpr (PRE) load_xs<MT>(a, m0, kbeg, r);
+    else load_x<MT>(a, m0, kbeg, r);
     load_w<FMT>(a, a.w, n0, kbeg, r.w);
     if constexpr (DUAL) load_w<FMT>(a, a.w2, n0, kbeg, r.w2);
-    store_x<MT>(r, xh[0], xl[0]);
+    if constexpr (PRE) store_xs<MT>(r, xh[0], xl[0]);
+    else store_x<MT>(r, xh[0], xl[0]);
     store_w<FMT>(r.w, wsm[0]);
     if constexpr (DUAL) store_w<FMT>(r.w2, wsm2[0]);
     __syncthreads();
@@ -250,7 +283,8 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GArgs a, int split) {
     for (int k0 = kbeg; k0 < kend; k0 += BK) {
         const bool more = k0 + BK < kend;
         if (more) {
-            load_x<MT>(a, m0, k0 + BK, r);
+            if constexpr (PRE) load_xs<MT>(a, m0, k0 + BK, r);
+            else load_x<MT>(a, m0, k0 + BK, r);
             load_w<FMT>(a, a.w, n0, k0 + BK, r.w);
             if constexpr (DUAL) load_w<FMT>(a, a.w2, n0, k0 + BK, r.w2);
         }
@@ -295,7 +329,8 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GArgs a, int split) {
                 }
         }
         if (more) {
-            store_x<MT>(r, xh[b ^ 1], xl[b ^ 1]);
+            if constexpr (PRE) store_xs<MT>(r, xh[b ^ 1], xl[b ^ 1]);
+            else store_x<MT>(r, xh[b ^ 1], xl[b ^ 1]);
             store_w<FMT>(r.w, wsm[b ^ 1]);
             if constexpr (DUAL) store_w<FMT>(r.w2, wsm2[b ^ 1]);
         }
@@ -326,6 +361,184 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GArgs a, int split) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// BF16 weights with pre-split x: both operands reach LDS by direct
+// global->LDS copies (no registers), NS stages in flight in a ring, so the
+// MFMAs of one stage overlap the memory latency of the next NS - 1. Tiles
+// are unpadded 32-element (64-byte) rows; 16-byte chunk c of row r sits at
+// slot c ^ ((r / 4) % 4), which keeps the fragment reads of 16 consecutive
+// rows on distinct LDS banks. The MFMA order and the chunk folds are those of
+// gemm_kernel, so the results are the same bits.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 2) & 3); }
+
+template <bool DUAL>
+__global__ __launch_bounds__(kThreads) void gemm_reduce_kernel(GArgs a);
+
+// s_waitcnt immediate waiting until at most n vector-memory ops are pending.
+constexpr int vm_wait_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+
+template <bool DUAL, int MT, int NS>
+__global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GArgs a, int split) {
+    constexpr int BM = 64 * MT;
+    constexpr int XT = BM * BK, WT = BN * BK;                 // elements per tile
+    constexpr int STAGE = 2 * XT + (DUAL ? 2 : 1) * WT;       // elements per ring stage
+    constexpr int NI = STAGE / 512;                           // 1 KB copy instructions per stage
+    constexpr int IPW = NI / 4;                               // per wave
+    static_assert(NI % 4 == 0, "stage copies must split evenly over the waves");
+    extern __shared__ __attribute__((aligned(16))) uint16_t ring[];
+
+    const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = (wave >> 1) * 32 * MT, wn = (wave & 1) * 64;
+    const int kbeg = split ? blockIdx.z * a.chunk : 0;
+    const int kend = split ? min(a.K, kbeg + a.chunk) : a.K;
+    const int nst = (kend - kbeg) / BK;  // K % BK == 0 on this path
+
+    // Stage s's copies: instruction q covers 16 rows of one tile.
+    auto issue = [&](int st) {
+        const int k0 = kbeg + st * BK;
+        uint16_t *base = ring + (st % NS) * STAGE;
+#pragma unroll
+        for (int i = 0; i < IPW; ++i) {
+            const int q = wave + 4 * i;
+            int tile, grp;
+            if (q < BM / 16) { tile = 0; grp = q; }
+            else if (q < BM / 8) { tile = 1; grp = q - BM / 16; }
+            else if (q < BM / 8 + BN / 16) { tile = 2; grp = q - BM / 8; }
+            else { tile = 3; grp = q - BM / 8 - BN / 16; }
+            const int r = 16 * grp + (lane >> 2), c = swz(r, lane & 3);
+            const void *src;
+            if (tile < 2) {
+                const int m = min(m0 + r, a.M - 1);  // rows past M feed only unstored outputs
+                src = (tile == 0 ? a.xh : a.xl) + (size_t)m * a.K + k0 + 8 * c;
+            } else {
+                const int n = min(n0 + r, a.N - 1);
+                src = (tile == 2 ? a.w : a.w2) + (size_t)n * a.stride + (size_t)(k0 + 8 * c) * 2;
+            }
+            uint16_t *dst = base + (tile == 0 ? 0 : tile == 1 ? XT : tile == 2 ? 2 * XT : 2 * XT + WT) + 16 * grp * BK;
+            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+        }
+    };
+
+    f32x16 acc[MT][2], acc2[DUAL ? MT : 1][2], tot[MT][2], tot2[DUAL ? MT : 1][2];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            acc[i][j] = f32x16{};
+            tot[i][j] = f32x16{};
+            if constexpr (DUAL) {
+                acc2[i][j] = f32x16{};
+                tot2[i][j] = f32x16{};
+            }
+        }
+
+#pragma unroll
+    for (int st = 0; st < NS - 1; ++st)
+        if (st < nst) issue(st);
+    for (int st = 0; st < nst; ++st) {
+        if (st + NS - 1 < nst) issue(st + NS - 1);
+        // Stage st is complete once only the later stages' copies are pending.
+        if (st + NS - 1 < nst) __builtin_amdgcn_s_waitcnt(vm_wait_imm(IPW * (NS - 1)));
+        else __builtin_amdgcn_s_waitcnt(vm_wait_imm(0));
+        // A bare barrier: each wave has just waited for its own copies of
+        // stage st, and LDS is coherent within the CU. (A fenced barrier
+        // would also drain the later stages' copies.)
+        __builtin_amdgcn_s_barrier();
+        const uint16_t *xh = ring + (st % NS) * STAGE, *xl = xh + XT, *wt = xh + 2 * XT, *wt2 = wt + WT;
+#pragma unroll
+        for (int ks = 0; ks < BK; ks += 16) {
+            const int c = (ks >> 3) + (lane >> 5);
+            bf16x8 ah[MT], al[MT], bw[2], bw2[DUAL ? 2 : 1];
+#pragma unroll
+            for (int i = 0; i < MT; ++i) {
+                const int r = wm + 32 * i + (lane & 31);
+                ah[i] = __builtin_bit_cast(bf16x8, *(const u32x4 *)(xh + r * BK + 8 * swz(r, c)));
+                al[i] = __builtin_bit_cast(bf16x8, *(const u32x4 *)(xl + r * BK + 8 * swz(r, c)));
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int r = wn + 32 * j + (lane & 31);
+                bw[j] = __builtin_bit_cast(bf16x8, *(const u32x4 *)(wt + r * BK + 8 * swz(r, c)));
+                if constexpr (DUAL) bw2[j] = __builtin_bit_cast(bf16x8, *(const u32x4 *)(wt2 + r * BK + 8 * swz(r, c)));
+            }
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bw[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bw[j], acc[i][j], 0, 0, 0);
+                    if constexpr (DUAL) {
+                        acc2[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bw2[j], acc2[i][j], 0, 0, 0);
+                        acc2[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bw2[j], acc2[i][j], 0, 0, 0);
+                    }
+                }
+        }
+        const int k0 = kbeg + st * BK;
+        if (k0 + BK >= kend || ((k0 + BK) % a.chunk) == 0) {
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    tot[i][j] += acc[i][j];
+                    acc[i][j] = f32x16{};
+                    if constexpr (DUAL) {
+                        tot2[i][j] += acc2[i][j];
+                        acc2[i][j] = f32x16{};
+                    }
+                }
+        }
+        // The slot of stage st is refilled by the next iteration's copies; the
+        // fragments were already read into registers.
+        __builtin_amdgcn_s_waitcnt(vm_wait_imm(63) & ~(0xF << 8));  // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int n = n0 + wn + 32 * j + (lane & 31);
+        if (n >= a.N) continue;
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int m = m0 + wm + 32 * i + 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
+                if (m >= a.M) continue;
+                const float v = tot[i][j][q];
+                const float u = DUAL ? tot2[DUAL ? i : 0][j][q] : 0.f;
+                if (split) {
+                    const size_t o = ((size_t)blockIdx.z * a.M + m) * a.N + n;
+                    a.ws[o] = v;
+                    if constexpr (DUAL) a.ws[(size_t)a.nchunks * a.M * a.N + o] = u;
+                } else {
+                    epilogue<DUAL>(a, m, n, v, u);
+                }
+            }
+    }
+}
+
+template <bool DUAL, int MT>
+int launch_dma(const GArgs &a, bool split, hipStream_t s) {
+    constexpr int NS = 4, BM = 64 * MT;
+    constexpr size_t lds = (size_t)NS * (2 * BM * BK + (DUAL ? 2 : 1) * BN * BK) * sizeof(uint16_t);
+    static bool attr_set = false;
+    if (!attr_set) {
+        CHIP_CHECK(hipFuncSetAttribute((const void *)gemm_dma_kernel<DUAL, MT, NS>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        attr_set = true;
+    }
+    const dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM, split ? a.nchunks : 1);
+    hipLaunchKernelGGL((gemm_dma_kernel<DUAL, MT, NS>), grid, dim3(kThreads), lds, s, a, split ? 1 : 0);
+    CHIP_CHECK(hipGetLastError());
+    if (split) {
+        const size_t MN = (size_t)a.M * a.N;
+        hipLaunchKernelGGL((gemm_reduce_kernel<DUAL>), dim3((unsigned)((MN + kThreads - 1) / kThreads)),
+                           dim3(kThreads), 0, s, a);
+        CHIP_CHECK(hipGetLastError());
+    }
+    return 0;
+}
+
 // Folds the stored chunk sums in chunk order (t = 0; t += c_z) and applies
 // the epilogue: the same bits as the in-register fold.
 template <bool DUAL>
@@ -345,7 +558,8 @@ template <int FMT, bool DUAL, int MT>
 int launch_mt(const GArgs &a, bool split, hipStream_t s) {
     constexpr int BM = 64 * MT;
     const dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM, split ? a.nchunks : 1);
-    hipLaunchKernelGGL((gemm_kernel<FMT, DUAL, MT>), grid, dim3(kThreads), 0, s, a, split ? 1 : 0);
+    if (a.xh) hipLaunchKernelGGL((gemm_kernel<FMT, DUAL, MT, true>), grid, dim3(kThreads), 0, s, a, split ? 1 : 0);
+    else hipLaunchKernelGGL((gemm_kernel<FMT, DUAL, MT, false>), grid, dim3(kThreads), 0, s, a, split ? 1 : 0);
     CHIP_CHECK(hipGetLastError());
     if (split) {
         const size_t MN = (size_t)a.M * a.N;
@@ -366,15 +580,57 @@ int launch_fmt(const GArgs &a, bool dual, size_t ws_floats, hipStream_t s) {
     // workspace holds them.
     const bool split = a.nchunks > 1 && tiles64 < cus && a.ws &&
                        ws_floats >= gemm_workspace_floats(a.N, a.K, a.M, dual);
+    // BF16 weights with pre-split x stream both operands straight into LDS.
+    const bool dma = FMT == FMT_BF16 && a.xh && a.K % BK == 0 && a.stride % 16 == 0 &&
+                     ((uintptr_t)a.w % 16) == 0 && (!dual || ((uintptr_t)a.w2 % 16) == 0);
     if (dual) {
-        if (split) return launch_mt<FMT, true, 1>(a, true, s);
-        return launch_mt<FMT, true, 1>(a, false, s);
+        if (dma) return launch_dma<true, 1>(a, split, s);
+        return launch_mt<FMT, true, 1>(a, split, s);
     }
-    if (!split && tiles128 >= cus) return launch_mt<FMT, false, 2>(a, false, s);
+    if (!split && tiles128 >= cus) {
+        if (dma) return launch_dma<false, 2>(a, false, s);
+        return launch_mt<FMT, false, 2>(a, false, s);
+    }
+    if (dma) return launch_dma<false, 1>(a, split, s);
     return launch_mt<FMT, false, 1>(a, split, s);
 }
 
+// x -> hi = bf16(x), lo = bf16(x - hi), 4 elements per thread.
+__global__ __launch_bounds__(kThreads) void split_bf16_kernel(const float *x, size_t n, uint16_t *xh, uint16_t *xl) {
+    const size_t i = ((size_t)blockIdx.x * kThreads + threadIdx.x) * 4;
+    if (i >= n) return;
+    if (i + 4 <= n) {
+        const f32x4 v = *(const f32x4 *)(x + i);
+        uint16_t h[4], l[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const __bf16 hb = (__bf16)v[q];
+            h[q] = __builtin_bit_cast(uint16_t, hb);
+            l[q] = __builtin_bit_cast(uint16_t, (__bf16)(v[q] - (float)hb));
+        }
+        *(uint2 *)(xh + i) = make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
+        *(uint2 *)(xl + i) = make_uint2(pack2(l[0], l[1]), pack2(l[2], l[3]));
+    } else {
+        for (size_t q = i; q < n; ++q) {
+            const __bf16 hb = (__bf16)x[q];
+            xh[q] = __builtin_bit_cast(uint16_t, hb);
+            xl[q] = __builtin_bit_cast(uint16_t, (__bf16)(x[q] - (float)hb));
+        }
+    }
+}
+
 }  // namespace
+
+int launch_split_bf16(const float *x, size_t n, uint16_t *xh, uint16_t *xl, hipStream_t s) {
+    if (n == 0) return 0;
+    if (!x || !xh || !xl || ((uintptr_t)x % 16) || ((uintptr_t)xh % 8) || ((uintptr_t)xl % 8))
+        return fail("HIP backend: split needs 16-byte aligned input and 8-byte aligned halves.");
+    const size_t threads = (n + 3) / 4;
+    hipLaunchKernelGGL(split_bf16_kernel, dim3((unsigned)((threads + kThreads - 1) / kThreads)), dim3(kThreads), 0, s,
+                       x, n, xh, xl);
+    CHIP_CHECK(hipGetLastError());
+    return 0;
+}
 
 int gemm_chunk_depth(int K) {
     const int want = std::max(256, (K + 15) / 16);
@@ -423,6 +679,10 @@ int launch_gemm(const GemmJob &job, hipStream_t s) {
     a.nchunks = (a.K + a.chunk - 1) / a.chunk;
     a.ws = job.ws;
     a.vec_x = (a.K % 4) == 0 && ((uintptr_t)job.x % 16) == 0;
+    // Pre-split halves are used when every 8-element chunk is 16-byte aligned.
+    const bool pre = job.xh && job.xl && a.K % 8 == 0 && ((uintptr_t)job.xh % 16) == 0 && ((uintptr_t)job.xl % 16) == 0;
+    a.xh = pre ? job.xh : nullptr;
+    a.xl = pre ? job.xl : nullptr;
     const uintptr_t p1 = (uintptr_t)a.w, p2 = dual ? (uintptr_t)a.w2 : p1;
     if (w.fmt == FMT_BF16) a.vec_w = a.stride % 16 == 0 && p1 % 16 == 0 && p2 % 16 == 0 && a.K % 8 == 0;
     else if (w.fmt == FMT_Q8) a.vec_w = a.stride % 16 == 0 && p1 % 16 == 0 && p2 % 16 == 0 && a.K % 16 == 0;

@@ -56,8 +56,13 @@ struct GemmJob {
     // folds in registers (the same bits, fewer blocks).
     float *ws = nullptr;
     size_t ws_floats = 0;
+    // Optional x pre-split by launch_split_bf16 ([n][cols] each): the GEMM
+    // then stages BF16 halves instead of splitting x once per weight tile
+    // (the same bits).
+    const uint16_t *xh = nullptr, *xl = nullptr;
 };
 int launch_gemm(const GemmJob &job, hipStream_t stream);
+int launch_split_bf16(const float *x, size_t n, uint16_t *xh, uint16_t *xl, hipStream_t s);
 int gemm_chunk_depth(int K);
 size_t gemm_workspace_floats(size_t N, size_t K, size_t M, bool dual);
 // Scratch the split path can use for any token count up to m_max.

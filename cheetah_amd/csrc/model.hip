@@ -163,6 +163,7 @@ struct cheetah_hip_model {
     size_t part_floats = 0;
     float *gemm_ws = nullptr;  // split-K chunk sums of the prefill GEMMs
     size_t gemm_ws_floats = 0;
+    uint16_t *xh = nullptr, *xl = nullptr;  // a GEMM input split into BF16 halves, [R][max width]
     uint32_t *tokens_dev = nullptr, *next_dev = nullptr, *hist_dev = nullptr;
     int32_t *step_dev = nullptr;  // [0] = token, [1] = position
     void *argmax_scratch = nullptr;
@@ -565,6 +566,9 @@ int init_instance(cheetah_hip_model *m) {
                                       gemm_split_workspace_floats(I, H, R, true),
                                       gemm_split_workspace_floats(H, I, R, false), (size_t)1});
         CHIP_TRY(m->mem.alloc(&m->gemm_ws, m->gemm_ws_floats));
+        const size_t width = std::max({H, qd, I});
+        CHIP_TRY(m->mem.alloc(&m->xh, R * width));
+        CHIP_TRY(m->mem.alloc(&m->xl, R * width));
     }
     CHIP_TRY(m->mem.alloc(&m->tokens_dev, sh.kv_capacity));
     CHIP_TRY(m->mem.alloc(&m->next_dev, 1));
@@ -766,6 +770,9 @@ int enqueue_chunk(cheetah_hip_model *m, const uint32_t *tokens_dev, size_t rows,
         qkv.y = m->qkv;
         qkv.ws = m->gemm_ws;
         qkv.ws_floats = m->gemm_ws_floats;
+        CHIP_TRY(launch_split_bf16(m->normed, rows * (size_t)(H), m->xh, m->xl, s));
+        qkv.xh = m->xh;
+        qkv.xl = m->xl;
         CHIP_TRY(launch_gemm(qkv, s));
         CHIP_TRY(launch_rope_append(m->qkv, m->qrot, rows, (int)c.q_heads, geom(m), L.kv, sh.rope_cos, sh.rope_sin,
                                     (int)c.rotary_dim, pos, nullptr, s));
@@ -793,6 +800,9 @@ int enqueue_chunk(cheetah_hip_model *m, const uint32_t *tokens_dev, size_t rows,
         o.epi = EPI_RESIDUAL;
         o.ws = m->gemm_ws;
         o.ws_floats = m->gemm_ws_floats;
+        CHIP_TRY(launch_split_bf16(m->attn, rows * (size_t)(sh.q_dim()), m->xh, m->xl, s));
+        o.xh = m->xh;
+        o.xl = m->xl;
         CHIP_TRY(launch_gemm(o, s));
         CHIP_TRY(launch_rmsnorm_rows(m->hidden, L.ln2, c.rms_eps, rows, H, m->normed, s));
         GemmJob gu;
@@ -804,6 +814,9 @@ int enqueue_chunk(cheetah_hip_model *m, const uint32_t *tokens_dev, size_t rows,
         gu.epi = EPI_SWIGLU;
         gu.ws = m->gemm_ws;
         gu.ws_floats = m->gemm_ws_floats;
+        CHIP_TRY(launch_split_bf16(m->normed, rows * (size_t)(H), m->xh, m->xl, s));
+        gu.xh = m->xh;
+        gu.xl = m->xl;
         CHIP_TRY(launch_gemm(gu, s));
         GemmJob dn;
         dn.w = L.down;
@@ -813,6 +826,9 @@ int enqueue_chunk(cheetah_hip_model *m, const uint32_t *tokens_dev, size_t rows,
         dn.epi = EPI_RESIDUAL;
         dn.ws = m->gemm_ws;
         dn.ws_floats = m->gemm_ws_floats;
+        CHIP_TRY(launch_split_bf16(m->act, rows * (size_t)(c.intermediate_size), m->xh, m->xl, s));
+        dn.xh = m->xh;
+        dn.xl = m->xl;
         CHIP_TRY(launch_gemm(dn, s));
     }
     if (last_chunk) {

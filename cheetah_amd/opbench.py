@@ -44,8 +44,11 @@ def _replicas(host: np.ndarray, count: int) -> list:
 
 def quantized_weights(fmt: str, rows: int, cols: int, seed: int) -> np.ndarray:
     """A buffer in the reference layout: f32 scales uniform in [1e-3, 1e-2],
-    codes uniform over the format's range (Q8 [-127, 127], Q4 [-8, 7])."""
+    codes uniform over the format's range (Q8 [-127, 127], Q4 [-8, 7]); BF16:
+    normal(0, 0.02) rounded to BF16 (the synthetic model weights)."""
     rng = np.random.default_rng(seed)
+    if fmt == "bf16":
+        return _bf16_bits((rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)).view(np.uint8).reshape(-1)
     total = hip.buffer_bytes(fmt, rows, cols)
     stride = (total - rows * 4) // rows
     out = np.zeros(total, np.uint8)
