@@ -367,7 +367,10 @@ __global__ __launch_bounds__(kAThreads) void gemv_aligned_kernel(Args a, int P) 
                     const int u = u0 + 64 * KS * i;
                     // One weight dword at a time: its E/4 x values (Q4 8,
                     // Q8 4, BF16 2) are read once and shared by every row.
-                    const float *xu = xs + u * E - shift;
+                    // A unit past the row has zero weights (load_batch) and
+                    // reads the last unit's x: LDS past x + padding holds
+                    // whatever an earlier kernel left, and 0 * NaN is NaN.
+                    const float *xu = xs + min(u, nfull - 1) * E - shift;
 #pragma unroll
                     for (int d = 0; d < D; ++d) {
                         constexpr int ED = E / 4;
