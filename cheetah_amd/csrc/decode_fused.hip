@@ -4,8 +4,10 @@
 //
 // Per layer five phases, per step one more:
 //   A  QKV rows (fused RMSNorm, bias, RoPE); K/V rows appended to the pages
-//   B  GQA attention: one item = (KV head, run of positions), two-pass softmax
-//   C  attention partials merged in split order, o_proj + residual
+//   B  GQA attention: one item = (KV head, run of 128 positions), two-pass
+//      softmax, (output, max, sum) partials per q head
+//   C  every o_proj block merges all partials in split order itself, then
+//      o_proj + residual
 //   D  gate/up (fused RMSNorm) + SwiGLU
 //   E  down + residual
 //   H  LM head (fused final RMSNorm) + per-block argmax partials; blocks that
@@ -15,19 +17,31 @@
 // Phases are chained through the data. Every value one block hands to
 // another is a 64-bit word {f32 bits, tag}, where the tag names the phase
 // instance that produced it (launch base + step * (5L + 1) + 5 * layer +
-// phase). A consumer copies the words it needs into LDS with direct
-// global->LDS loads (16 bytes per lane, device-coherent sc1, many in flight,
-// no registers), checks the tags there, and re-loads only the 128-word
-// chunks that are still stale; aligned 8-byte stores are single-copy atomic,
-// so value and tag arrive together. A phase therefore starts as soon as its
-// own inputs exist. Producers write with device-scope relaxed atomic stores
-// (sc1), coherent across the XCDs' separate L2 caches, and so are the K/V
-// pages, which attention reads the same way into LDS. Weights are read-only
-// and use plain non-temporal loads.
+// phase). Aligned 8-byte stores are single-copy atomic, so value and tag
+// arrive together, and a consumer knows its inputs are complete when every
+// word it copied carries the expected tag.
 //
-// Each wave owns fixed rows of every projection and issues the loads of a
-// phase's weight rows into registers before it polls that phase's inputs,
-// so HBM streaming overlaps the wait for the producers.
+// Roles inside a block. Waves 0-6 (compute waves) own weight rows; wave 7
+// (the poll wave) owns no rows and does all cross-block input traffic: it
+// copies the tagged words a phase needs into LDS with direct global->LDS
+// loads (16 bytes per lane, device-coherent sc1, many in flight), re-loads
+// only the 128-word chunks still stale, and converts the words to the f32
+// vector the compute waves read (RMSNorm fused where the phase has one).
+// Vector memory operations of one wave complete in issue order, so a wave
+// that waited on polls behind outstanding weight loads would wait for those
+// loads too; with the split, polls never wait on weights and weights never
+// wait on polls. The waves meet only at LDS barriers that wait on LDS
+// traffic alone (s_waitcnt lgkmcnt(0); s_barrier), never on vector memory.
+//
+// Weight streaming. Each compute wave keeps its rows of every phase of the
+// next layer in flight: right after it uses phase X's rows of layer l it
+// issues phase X's rows of layer l + 1 (after the last layer: nothing, and
+// after the LM head all of layer 0 of the next step). The loads are buffer
+// loads issued on every path, with rows a wave does not own pointed past the
+// buffer's range (those lanes read nothing and return 0), so the compiler
+// counts outstanding loads exactly and each use waits only for its own rows.
+// The poll wave's LDS copies are written as inline assembly for the same
+// reason: the compiler would otherwise make every LDS read wait for them.
 //
 // Buffer reuse needs no barrier: a block polls a phase's inputs only in a
 // phase where it also produces outputs, and every buffer is rewritten only by
@@ -36,7 +50,12 @@
 // argmax partials; those alternate between two buffers by step parity.
 //
 // Every poll is bounded: on timeout a block raises the abort word, which all
-// polls watch, and every wave returns; the host then resets the tagged words.
+// polls watch, so every later poll gives up within a few rounds and the
+// launch runs to its end on stale values (no wave leaves early: an exit inside
+// the layer loop would add control-flow paths that make the compiler's waits
+// for weight rows conservative). The host sees the word, discards the steps
+// and resets the tagged words. The only data-dependent address, the token,
+// keeps its last good value when its poll gives up.
 //
 // Math per phase is that of the multi-kernel path (gemv.hip, attention.hip,
 // misc.hip), i.e. the reference path of ops.rs / qwen2.rs; only f32
@@ -51,10 +70,24 @@ namespace {
 
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
-constexpr int TP = 64;            // positions per KV page
-constexpr int kChunk = 128;       // tagged words per wave-wide 16-byte-per-lane load
-constexpr int kLdsBudget = 128 * 1024;  // dynamic LDS the layout may use
+constexpr int kCW = kWaves - 1;        // compute waves 0 .. kCW - 1
+constexpr int kSpareWave = kWaves - 1;  // owns no weight rows
+constexpr int TP = 64;                 // positions per KV page
+constexpr int kItemPos = 2 * TP;       // positions per attention item, at most
+// Positions per item for a K/V row size: two pages, or one when a row is
+// wider than 256 bytes (one item's K and V rows stay within 64 KB of LDS).
+__host__ __device__ constexpr int item_positions(int row_bytes) { return row_bytes <= 256 ? 2 * TP : TP; }
+constexpr int kChunk = 128;            // tagged words per wave-wide 16-byte-per-lane load
+constexpr int kMaxChunks = 128;        // largest gather: 16384 words
 constexpr long kSpinLimit = 1L << 20;
+constexpr uint32_t kNoRead = 0x80000000u;  // buffer offset past every range
+
+// The f32 vector the dot products read sits in LDS with every 8 elements
+// padded to 10 floats: a lane reads the 8 x values of its 16-byte weight unit
+// at a 40-byte stride, so the lanes of a quarter wave hit distinct banks (at
+// the unpadded 32-byte stride, lanes 8 apart share banks and seven waves
+// reading one vector serialise on the conflicts).
+__host__ __device__ constexpr int xpad(int i) { return (i >> 3) * 10 + (i & 7); }
 
 // threadIdx.x through an opaque copy: address arithmetic stays next to its
 // use inside the step loop instead of being hoisted out of it and held in
@@ -64,22 +97,30 @@ __device__ __forceinline__ int tid_here() {
     asm volatile("" : "+v"(t));
     return t;
 }
-// Global wave index, recomputed where used (same reason).
-__device__ __forceinline__ int gw_here() { return (int)blockIdx.x * kWaves + (tid_here() >> 6); }
+__device__ __forceinline__ int lane_here() { return tid_here() & 63; }
 
-__device__ __forceinline__ void stt(uint64_t *p, uint32_t bits, unsigned tag) {
-    __hip_atomic_store(p, ((uint64_t)tag << 32) | bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Global stores are written as inline assembly (the instructions the
+// compiler emits for device-scope relaxed atomic stores: sc1). Vector memory
+// loads complete in issue order but stores need not, and the compiler, seeing
+// both kinds outstanding, would make every wait for a weight row a wait for
+// everything; with stores out of its sight it waits for a row only until the
+// loads issued after that row remain, which in-order loads make exact.
+__device__ __forceinline__ void st_u64(uint64_t *p, uint64_t v) {
+    asm volatile("global_store_dwordx2 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
 }
+__device__ __forceinline__ void st_u32(void *p, uint32_t v) {
+    asm volatile("global_store_dword %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void st_u16(void *p, uint32_t v) {
+    asm volatile("global_store_short %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void stt(uint64_t *p, uint32_t bits, unsigned tag) { st_u64(p, ((uint64_t)tag << 32) | bits); }
 __device__ __forceinline__ void stf(uint64_t *p, float v, unsigned tag) { stt(p, __float_as_uint(v), tag); }
 __device__ __forceinline__ unsigned tag_of(uint64_t w) { return (unsigned)(w >> 32); }
 __device__ __forceinline__ float val_of(uint64_t w) { return __uint_as_float((uint32_t)w); }
 
-__device__ __forceinline__ void st_kv(uint16_t *p, float v) {
-    __hip_atomic_store(p, f32_bf16_rne(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_kv(float *p, float v) {
-    __hip_atomic_store((unsigned *)p, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+__device__ __forceinline__ void st_kv(uint16_t *p, float v) { st_u16(p, f32_bf16_rne(v)); }
+__device__ __forceinline__ void st_kv(float *p, float v) { st_u32(p, __float_as_uint(v)); }
 // The value a K/V element has once stored in the cache.
 template <class KT>
 __device__ __forceinline__ float kv_round(float v) {
@@ -90,169 +131,191 @@ __device__ __forceinline__ float kv_round(float v) {
 __device__ __forceinline__ bool aborted(const int *f) {
     return __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
 }
-__device__ __forceinline__ void raise_abort(int *f) {
-    __hip_atomic_store(f, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void raise_abort(int *f) { st_u32(f, 1u); }
+
+// Read-only values at a wave-uniform index through the constant address
+// space: scalar loads (counted apart from the vector loads of the weights).
+template <class T>
+__device__ __forceinline__ T ldc(const T *p, long i) {
+    return ((const __attribute__((address_space(4))) T *)p)[i];
+}
+__device__ __forceinline__ float ldc_bf16(const uint16_t *p, long i) {
+    const uint32_t w = ldc((const uint32_t *)p, i >> 1);
+    return (i & 1) ? bf16_hi(w) : bf16_lo(w);
 }
 
-// One layer's pointer table by value, read through the constant address
-// space: scalar loads into scalar registers, not re-read after every store
-// (a reference into global memory would be, as the stores might alias it).
-__device__ __forceinline__ FusedLayer load_layer(const FusedLayer *table, int l) {
-    typedef const __attribute__((address_space(4))) FusedLayer CLayer;
-    CLayer *p = (CLayer *)table + l;
-    FusedLayer o;
-    o.qkv = p->qkv;
-    o.o = p->o;
-    o.gate = p->gate;
-    o.up = p->up;
-    o.down = p->down;
-    o.qkv_sc = p->qkv_sc;
-    o.o_sc = p->o_sc;
-    o.gate_sc = p->gate_sc;
-    o.up_sc = p->up_sc;
-    o.down_sc = p->down_sc;
-    o.qkv_bias = p->qkv_bias;
-    o.o_bias = p->o_bias;
-    o.ln1 = p->ln1;
-    o.ln2 = p->ln2;
-    o.kc = p->kc;
-    o.vc = p->vc;
-    return o;
+typedef const __attribute__((address_space(4))) FusedArgs CArgs;
+typedef const __attribute__((address_space(4))) FusedLayer CLayer;
+
+// The launch's arguments, read where used: through an opaque copy of the
+// kernarg pointer, so that fields are re-read (scalar-cache hits) instead of
+// each being held in a scalar register for the whole launch.
+__device__ __forceinline__ CArgs *A() {
+    auto p = (const __attribute__((address_space(4))) char *)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(p));
+    return (CArgs *)p;
 }
+// Layer l's pointer table, read the same way.
+__device__ __forceinline__ CLayer *LY(int l) { return (CLayer *)A()->layers + l; }
+
+// LDS barrier that waits on LDS (and scalar) traffic only: outstanding
+// vector memory loads stay in flight across it.
+__device__ __forceinline__ void bar() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // 16 bytes per lane from global memory straight into LDS at lds + 16 * lane
-// (lds must be the same in every lane of the wave), device-coherent (sc1).
-__device__ __forceinline__ void dma16(const void *g, void *lds) {
-    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)lds, 16, 0, 16);
+// (lds the same in every lane), device-coherent (sc1). The low 32 bits of a
+// generic pointer into LDS are the LDS byte address.
+__device__ __forceinline__ void dma16(const void *g, const void *lds) {
+    const uint32_t l = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off sc1" ::"v"(g), "s"(l)
+                 : "memory", "m0");
 }
-__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+__device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// Copies tagged words src[0, n) into LDS dst[0, n) and waits until each
-// carries `tag`. Wave w loads chunks w, w + 4, ... (128 words each); after
-// each round only chunks with a stale word are loaded again. Block-wide:
-// starts with a barrier (dst may still be read by the previous phase) and
-// ends with one; false in every thread on timeout or abort.
-__device__ __forceinline__ bool gather_lds(uint64_t *dst, const uint64_t *src, int n, unsigned tag, int *abort_flag) {
-    const int tid = tid_here(), lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+// All waves: copies tagged words src[0, n) into LDS dst[0, n) and waits until
+// each carries `tag`. Wave w owns the 128-word chunks w, w + 8, ...: it loads
+// them with direct global->LDS copies and re-loads the stale ones until every
+// word of its chunks is fresh (its tag reads for eight chunks in flight at a
+// time); the caller's barrier then makes all of them visible to the block.
+// While a round finds nothing new (the producers are not there yet) the wave
+// only probes its first pending chunk, so waiting blocks do not flood the
+// memory system that the weight rows stream through. A wave's wait also
+// covers the weight rows it has in flight. On timeout the abort word is
+// raised and the wave moves on with what it has.
+__device__ void gather(uint64_t *dst, const uint64_t *src, int n, unsigned tag, int *abort_flag) {
+    const int lane = lane_here(), wave = __builtin_amdgcn_readfirstlane(tid_here() >> 6);
     const int chunks = (n + kChunk - 1) / kChunk;
-    __syncthreads();
-    uint64_t pend = 0;  // bit i: chunk wave + 4 i is stale
-    for (int c = wave, i = 0; c < chunks; c += kWaves, ++i) pend |= 1ull << i;
+    const int mine = chunks > wave ? (chunks - 1 - wave) / kWaves + 1 : 0;  // at most 16
+    const uint32_t *d32 = (const uint32_t *)dst;
+    uint32_t pend = (1u << mine) - 1;
+    bool probe = false;
     long spins = 0;
-    bool ok = true;
     while (pend) {
-        for (int c = wave, i = 0; c < chunks; c += kWaves, ++i)
-            if ((pend >> i) & 1) {
-                const int w = c * kChunk + lane * 2;
-                if (w < n) dma16(src + w, dst + c * kChunk);
+        const uint32_t issued = probe ? (pend & (0u - pend)) : pend;
+        for (uint32_t m = issued; m; m &= m - 1) {
+            const int c = wave + kWaves * __builtin_ctz(m), w = c * kChunk + lane * 2;
+            if (w < n) dma16(src + w, dst + c * kChunk);
+        }
+        wait_vm();
+        uint32_t still = 0;
+        for (int i0 = 0; i0 < mine; i0 += 8) {
+            uint32_t t0[8], t1[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int w = (wave + kWaves * min(i0 + j, mine - 1)) * kChunk + lane * 2;
+                t0[j] = d32[2 * w + 1];
+                t1[j] = d32[2 * w + 3];
             }
-        wait_dma();
-        uint64_t still = 0;
-        for (int c = wave, i = 0; c < chunks; c += kWaves, ++i)
-            if ((pend >> i) & 1) {
-                const int w = c * kChunk + lane * 2;
-                bool stale = w < n && tag_of(dst[w]) != tag;
-                stale |= w + 1 < n && tag_of(dst[w + 1]) != tag;
-                if (__any(stale)) still |= 1ull << i;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = i0 + j, w = (wave + kWaves * i) * kChunk + lane * 2;
+                const bool stale = (w < n && t0[j] != tag) || (w + 1 < n && t1[j] != tag);
+                if (i < mine && ((issued >> i) & 1) && __any(stale)) still |= 1u << i;
             }
-        pend = still;
+        }
+        // Chunks not issued this round stay pending.
+        const uint32_t next = still | (pend & ~issued);
+        probe = (still == issued);  // nothing issued came back fresh
+        pend = next;
         if (pend) {
             if (++spins > kSpinLimit || ((spins & 15) == 0 && aborted(abort_flag))) {
                 raise_abort(abort_flag);
-                ok = false;
-                break;
+                return;
             }
             __builtin_amdgcn_s_sleep(1);
         }
     }
-    return __syncthreads_and(ok);
 }
 
-// xs[i] = value of tb[i] (i < n); with a gain, RMSNorm'd in place as the
-// GEMV prologue does: x * (inv * g), inv = 1 / sqrt(mean(x^2) + eps)
-// (ops.rs:646-652). Block-wide; ends with a barrier.
-__device__ void stage_lds(float *xs, const uint64_t *tb, int n, const uint16_t *gain, float eps, float *red) {
-    const int tid = tid_here(), lane = tid & 63, wave = tid >> 6;
-    float ss = 0.f;
-    for (int i = tid; i < n; i += kThreads) {
-        const float v = val_of(tb[i]);
-        xs[i] = v;
-        ss = fmaf(v, v, ss);
+// Poll wave only: starts copying `bytes` (a multiple of 16) from global
+// memory into LDS; completion is awaited with wait_vm.
+__device__ __forceinline__ void dma_bytes(void *dst, const void *src, int bytes) {
+    const int lane = lane_here();
+    for (int c = 0; c < bytes; c += 1024) {
+        const int byte = c + lane * 16;
+        if (byte < bytes) dma16((const uint8_t *)src + byte, (uint8_t *)dst + c);
     }
-    if (gain) {
-        ss = wave_sum(ss);
-        if (lane == 0) red[wave] = ss;
-        __syncthreads();
-        float total = 0.f;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) total += red[w];
-        const float inv = 1.0f / sqrtf(total / (float)n + eps);
-        for (int i = tid; i < n; i += kThreads) xs[i] = xs[i] * (inv * bf16_f32(gain[i]));
-    }
-    __syncthreads();
 }
 
-// The embedding row, RMSNorm'd (layer 0's QKV input).
-__device__ void stage_embed(float *xs, const uint16_t *row, int n, const uint16_t *gain, float eps, float *red) {
-    const int tid = tid_here(), lane = tid & 63, wave = tid >> 6;
+// One wave: the RMSNorm scale of n values, inv = 1 / sqrt(mean(x^2) +
+// eps) (ops.rs:646-652); x the values of the tagged words src or the BF16
+// row src.
+template <bool BF16_SRC>
+__device__ __forceinline__ float wave_norm_scale(const void *src, int n, float eps) {
+    const int lane = lane_here();
     float ss = 0.f;
-    for (int i = tid; i < n; i += kThreads) {
-        const float v = bf16_f32(row[i]);
-        xs[i] = v;
+#pragma unroll 4
+    for (int i = lane; i < n; i += 64) {
+        float v;
+        if constexpr (BF16_SRC) v = bf16_f32(((const uint16_t *)src)[i]);
+        else v = val_of(((const uint64_t *)src)[i]);
         ss = fmaf(v, v, ss);
     }
     ss = wave_sum(ss);
-    if (lane == 0) red[wave] = ss;
-    __syncthreads();
-    float total = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) total += red[w];
-    const float inv = 1.0f / sqrtf(total / (float)n + eps);
-    for (int i = tid; i < n; i += kThreads) xs[i] = xs[i] * (inv * bf16_f32(gain[i]));
-    __syncthreads();
+    return 1.0f / sqrtf(ss / (float)n + eps);
 }
 
-// One weight row as 16-byte units, unit u in lane u % 64, slot u / 64.
-template <int N>
-__device__ __forceinline__ void load_row(u32x4 (&w)[N], const uint8_t *row, int n_units) {
-    const int lane = tid_here() & 63;
-#pragma unroll
-    for (int k = 0; k < N; ++k) {
-        const int u = lane + 64 * k;
-        if (u < n_units) w[k] = __builtin_nontemporal_load((const u32x4 *)(row + (size_t)u * 16));
+// All waves: xs[xpad(i)] = x[i], or x[i] * (inv * g[i]) with a BF16 gain row g
+// (the GEMV prologue's RMSNorm).
+template <bool BF16_SRC>
+__device__ __forceinline__ void block_stage(float *xs, const void *src, int n, const uint16_t *g, float inv) {
+#pragma unroll 4
+    for (int i = tid_here(); i < n; i += kThreads) {
+        float v;
+        if constexpr (BF16_SRC) v = bf16_f32(((const uint16_t *)src)[i]);
+        else v = val_of(((const uint64_t *)src)[i]);
+        xs[xpad(i)] = g ? v * (inv * bf16_f32(g[i])) : v;
     }
 }
 
-// Wave-wide dot products of R loaded rows (the first nr valid, nr uniform
-// across the wave) with xs; a unit's x values are read once for all rows.
-// Per row the summation order is fixed (unit, then element). Results land
-// in every lane.
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+__device__ __forceinline__ Rsrc rsrc(const void *base, size_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)bytes, 0x00020000);
+}
+
+// Compute waves: one weight row as 16-byte units (unit u in lane u % 64,
+// slot u / 64) by buffer loads issued whether or not the row is the wave's:
+// lanes without a unit of an owned row read past the range (nothing).
+template <int N>
+__device__ __forceinline__ void load_row(u32x4 (&w)[N], Rsrc r, uint32_t row_off, int n_units, bool valid) {
+    const int lane = lane_here();
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        const int u = lane + 64 * k;
+        const uint32_t off = valid && u < n_units ? row_off + (uint32_t)u * 16u : kNoRead;
+        w[k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
+    }
+}
+
+// Wave-wide dot products of R loaded rows with xs; a unit's x values are
+// read once for all rows. Per row the summation order is fixed (unit, then
+// element); results land in every lane. Branch-free: lanes past the row
+// (n_units) read a valid x at a clamped index while their weights are the
+// zeros of a load that read nothing, and rows a wave does not own are
+// computed from such zeros too, so every path consumes every loaded
+// register (a path that skipped one would make the compiler wait for its
+// load before reusing the register).
 template <int FMT, int R, int N>
-__device__ __forceinline__ void dot_rows(const u32x4 (&w)[R][N], const float *xs, int n_units, int nr,
-                                         float (&out)[R]) {
+__device__ __forceinline__ void dot_rows(const u32x4 (&w)[R][N], const float *xs, int n_units, float (&out)[R]) {
     using U = Unit<FMT, 16>;
-    const int lane = tid_here() & 63;
+    const int lane = lane_here();
     float acc[R];
 #pragma unroll
     for (int i = 0; i < R; ++i) acc[i] = 0.f;
 #pragma unroll
     for (int k = 0; k < N; ++k) {
-        const int u = lane + 64 * k;
-        if (u < n_units) {
-            float xv[U::E];
+        const int u = min(lane + 64 * k, n_units - 1);
+        float xv[U::E];
 #pragma unroll
-            for (int e = 0; e < U::E; ++e) xv[e] = xs[u * U::E + e];
+        for (int e = 0; e < U::E; ++e) xv[e] = xs[xpad(u * U::E + e)];
 #pragma unroll
-            for (int i = 0; i < R; ++i)
-                if (i < nr) {
-                    const uint32_t raw[4] = {w[i][k][0], w[i][k][1], w[i][k][2], w[i][k][3]};
-                    U::decode(raw, [&](int e, float v) { acc[i] = fmaf(v, xv[e], acc[i]); });
-                }
+        for (int i = 0; i < R; ++i) {
+            const uint32_t raw[4] = {w[i][k][0], w[i][k][1], w[i][k][2], w[i][k][3]};
+            U::decode(raw, [&](int e, float v) { acc[i] = fmaf(v, xv[e], acc[i]); });
         }
     }
 #pragma unroll
-    for (int i = 0; i < R; ++i) out[i] = i < nr ? wave_sum(acc[i]) : 0.f;
+    for (int i = 0; i < R; ++i) out[i] = wave_sum(acc[i]);
 }
 
 __device__ __forceinline__ int total_key(float f) {
@@ -265,118 +328,88 @@ __device__ __forceinline__ void better(int &key, uint32_t &idx, int k2, uint32_t
         idx = i2;
     }
 }
-
-constexpr int kStage = 64;  // outputs one block publishes per phase, at most
-
-struct Shm {
-    float red[kWaves];
-    int ikey[kWaves];
-    uint32_t iidx[kWaves];
-    // A phase's outputs of the block's waves, stored by one wave afterwards
-    // so that consecutive words leave in one coalesced run.
-    float outv[kStage];
-    int outi[kStage];   // destination word (QKV: index into the q/K/V words)
-    int outc[kStage];   // QKV: cache element (bit 30: V cache), or -1
-};
-
-// Stores vals[0, n) as the tagged words dst[0, n): one run by the first
-// threads. Block-wide; starts with a barrier (the values are staged by other
-// waves).
-__device__ __forceinline__ void publish(uint64_t *dst, const float *vals, int n, unsigned tag) {
-    __syncthreads();
-    const int tid = tid_here();
-    if (tid < n) stf(dst + tid, vals[tid], tag);
-}
-
-// Reduces (key, idx) over the block; the result lands in every thread.
-__device__ void block_best(int &key, uint32_t &idx, Shm &sm) {
-    const int tid = tid_here(), lane = tid & 63, wave = tid >> 6;
+__device__ __forceinline__ void wave_best(int &key, uint32_t &idx) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
         const int k2 = __shfl_xor(key, off, 64);
         const uint32_t i2 = __shfl_xor(idx, off, 64);
         better(key, idx, k2, i2);
     }
+}
+
+constexpr int kStage = 64;  // outputs one block publishes per phase, at most
+
+struct Shm {
+    int ikey[kWaves];
+    uint32_t iidx[kWaves];
+    int token;           // the step's sampled id
+    float out[kStage];   // a phase's outputs of the block, stored as one run
+};
+
+// Reduces (key, idx) over the block; the result lands in every thread.
+__device__ void block_best(int &key, uint32_t &idx, Shm &sm) {
+    const int lane = lane_here(), wave = tid_here() >> 6;
+    wave_best(key, idx);
     if (lane == 0) {
         sm.ikey[wave] = key;
         sm.iidx[wave] = idx;
     }
-    __syncthreads();
+    bar();
     key = sm.ikey[0];
     idx = sm.iidx[0];
     for (int w = 1; w < kWaves; ++w) better(key, idx, sm.ikey[w], sm.iidx[w]);
-    __syncthreads();
+    bar();
 }
 
-// Attention work-item geometry: T threads per position (8 elements each),
-// P positions per pass, CH positions per item (one 64-position page: many
-// small items keep each block's share of the attention short).
-template <int HD, class KT>
-struct AttnGeo {
-    static constexpr int T = HD / 8;
-    static constexpr int P = kThreads / T;
-    static constexpr int ROW = HD * (int)sizeof(KT);  // bytes of one K or V row
-    static constexpr int CH = TP;
-};
-
-template <int HD, int G, int CH>
+template <int HD, int G>
 struct AttnShm {
     static constexpr int GP = (G + 3) / 4 * 4;
-    float p[CH][GP];  // scores, then weights, of position x head
+    float p[kItemPos][GP];  // scores, then weights, of position x head
     float red[kWaves][G][HD];
     float m[G], l[G];
 };
 
 __host__ __device__ constexpr int round_up(int x, int m) { return (x + m - 1) / m * m; }
+__host__ __device__ constexpr int imax(int a, int b) { return a > b ? a : b; }
 
-// Dynamic LDS layout (byte offsets): tagged-word staging, the f32 vector,
-// merge weights. The staging area also holds one attention item's q/K/V:
-// the group's q and new K/V words first, then its K rows and V rows.
+// Dynamic LDS layout (byte offsets): tagged-word staging, the f32 vector the
+// compute waves read (also an attention item's q), one item's K and V rows,
+// the merge weights of every (split, q head) and 1 / sum per q head, the
+// next step's embedding row and a phase's RMSNorm gains (BF16).
 struct LdsLayout {
-    int qkw;    // words reserved for a group's q + new K/V
-    int tbw;    // staging words
-    int xs, total;
+    int tbw;  // staging words
+    int xs, kv, mw, emb, gain, total;
 };
 __host__ __device__ inline LdsLayout lds_layout(int H, int I, int nq, int hd, int G, int kv_bytes, int blocks,
                                                 int max_splits) {
     LdsLayout o{};
-    o.qkw = round_up((G + 2) * hd, kChunk);
-    int tbw = o.qkw + 2 * TP * hd * kv_bytes / 8;
-    tbw = tbw > H ? tbw : H;
-    tbw = tbw > I ? tbw : I;
-    tbw = tbw > 2 * blocks ? tbw : 2 * blocks;
-    const int parts = max_splits * G * (hd + 2);
-    tbw = tbw > parts ? tbw : parts;
+    int tbw = imax(imax(H, I), imax((G + 2) * hd, 2 * blocks));
+    tbw = imax(tbw, max_splits * nq * (hd + 2));
     o.tbw = round_up(tbw + 2, kChunk);
-    int xf = H > I ? H : I;
-    xf = xf > nq * hd ? xf : nq * hd;
+    const int xf = xpad(imax(imax(H, I), nq * hd)) + 10;
     o.xs = o.tbw * 8;
-    o.total = o.xs + xf * 4;
+    o.kv = o.xs + round_up(xf * 4, 16);
+    o.mw = o.kv + 2 * item_positions(hd * kv_bytes) * hd * kv_bytes;
+    o.emb = o.mw + round_up((max_splits + 1) * nq * 4, 16);
+    o.gain = o.emb + round_up(H * 2, 16);
+    o.total = o.gain + round_up(H * 2, 16);
     return o;
 }
 
-// Loads the cached K and V rows of positions [start, lim) of KV head g into
-// LDS (row p - start of each), 64-position pages at a time.
+// Poll wave only: starts the copies of the cached K and V rows of positions
+// [start, lim) of KV head g into LDS (row p - start of each); completion is
+// awaited with wait_vm.
 template <int HD, class KT>
-__device__ void load_kv_lds(uint8_t *k_lds, uint8_t *v_lds, const FusedArgs &a, const FusedLayer &ly, int g,
-                            long start, long lim) {
-    using Geo = AttnGeo<HD, KT>;
-    const int tid = tid_here(), lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    constexpr int NT = Geo::CH / TP;
-    int pages[NT];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) pages[t] = start + t * TP < lim ? a.page_table[(start + t * TP) / TP] : 0;
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        const long t0 = start + t * TP;
-        if (t0 >= lim) break;
-        const int page = pages[t];
-        const int bytes = (int)(min((long)TP, lim - t0)) * Geo::ROW;
-        const size_t off = (((size_t)page * a.kv_heads + g) * TP) * Geo::ROW;
-        const uint8_t *ks = (const uint8_t *)ly.kc + off, *vs = (const uint8_t *)ly.vc + off;
-        uint8_t *kd = k_lds + (t0 - start) * Geo::ROW, *vd = v_lds + (t0 - start) * Geo::ROW;
-        for (int c = wave * 1024; c < bytes; c += kWaves * 1024) {
+__device__ void load_kv_lds(uint8_t *k_lds, uint8_t *v_lds, int l, int g, long start, long lim) {
+    constexpr int ROW = HD * (int)sizeof(KT);
+    const int lane = lane_here();
+    for (long t0 = start; t0 < lim; t0 += TP) {
+        const int page = ldc(A()->page_table, t0 / TP);
+        const int bytes = (int)(min((long)TP, lim - t0)) * ROW;
+        const size_t off = (((size_t)page * A()->kv_heads + g) * TP) * ROW;
+        const uint8_t *ks = (const uint8_t *)LY(l)->kc + off, *vs = (const uint8_t *)LY(l)->vc + off;
+        uint8_t *kd = k_lds + (t0 - start) * ROW, *vd = v_lds + (t0 - start) * ROW;
+        for (int c = 0; c < bytes; c += 1024) {
             const int byte = c + lane * 16;
             if (byte < bytes) {
                 dma16(ks + byte, kd + c);
@@ -405,61 +438,21 @@ __device__ __forceinline__ void ld8(const KT *p, float (&f)[8]) {
     }
 }
 
-// Attention item (KV head g, positions [split * CH, ...)) for all G heads of
-// the group; writes (unnormalised output, max, sum) partials per q head.
-// With `late`, the cached rows are loaded only after the q gather (whose
-// tags prove every earlier position of this layer is written); otherwise
-// they were loaded into LDS beforehand.
+// One attention item, all waves: q (G heads, f32) in qs, nv K and V rows in
+// LDS; writes (unnormalised output, max, sum) per q head of the group to
+// part[j * (HD + 2) + ...] (compute waves store, so the poll wave has no
+// stores in flight when it polls next).
 template <int HD, int G, class KT>
-__device__ bool attn_item(const FusedArgs &a, const FusedLayer &ly, uint64_t *tb, int g, int split, int S, long pos,
-                          unsigned tA, unsigned tB, bool late, int qkw,
-                          AttnShm<HD, G, AttnGeo<HD, KT>::CH> &sh, uint64_t *tr) {
-    using Geo = AttnGeo<HD, KT>;
-    constexpr int T = Geo::T, P = Geo::P, CH = Geo::CH;
+__device__ void attn_compute(const float *qs, const uint8_t *k_lds, const uint8_t *v_lds, int nv, AttnShm<HD, G> &sh,
+                             uint64_t *part, unsigned tag, uint64_t *tr) {
+    constexpr int T = HD / 8, P = kThreads / T, ROW = HD * (int)sizeof(KT);
     const int tid = tid_here(), lane = tid & 63, wave = tid >> 6;
     const int d8 = tid % T, pg = tid / T;
     auto mark = [&](int ev) {
-        if (tr && tid == 0) tr[ev] = wall_clock64();
+        if (tr && tid == 0) st_u64(tr + ev, wall_clock64());
     };
-    const long ctx = pos + 1;
-    const long start = (long)split * CH;
-    const long end = min(start + CH, ctx);
-    const int nv = (int)(end - start);
-    uint8_t *k_lds = (uint8_t *)(tb + qkw), *v_lds = k_lds + CH * Geo::ROW;
-    if (!gather_lds(tb, a.qkvn + (size_t)g * (G + 2) * HD, (G + 2) * HD, tA, a.abort_flag)) return false;
-    if (late) {
-        load_kv_lds<HD, KT>(k_lds, v_lds, a, ly, g, start, min(end, pos));
-        wait_dma();
-        __syncthreads();
-    }
-    if (end == ctx) {
-        // The new position's K and V rows, as stored in the cache.
-        for (int i = tid; i < 2 * HD; i += kThreads) {
-            const float v = val_of(tb[G * HD + i]);
-            KT *row = (KT *)((i < HD ? k_lds : v_lds) + (size_t)(nv - 1) * Geo::ROW);
-            if constexpr (sizeof(KT) == 2) row[i % HD] = f32_bf16_rne(v);
-            else row[i % HD] = v;
-        }
-        __syncthreads();
-    }
-    mark(0);
-    // q as f32 in LDS (reusing the staging words it came in).
-    float *qs = (float *)tb;
-    __syncthreads();
-    {
-        float qv[(G * HD + kThreads - 1) / kThreads];
-#pragma unroll
-        for (int k = 0; k * kThreads < G * HD; ++k)
-            if (tid + k * kThreads < G * HD) qv[k] = val_of(tb[tid + k * kThreads]);
-        __syncthreads();
-#pragma unroll
-        for (int k = 0; k * kThreads < G * HD; ++k)
-            if (tid + k * kThreads < G * HD) qs[tid + k * kThreads] = qv[k];
-        __syncthreads();
-    }
     const float scale = 1.0f / sqrtf((float)HD);
     const int passes = (nv + P - 1) / P;
-#pragma unroll 2
     for (int ps = 0; ps < passes; ++ps) {
         const int pi = ps * P + pg;
         const bool valid = pi < nv;
@@ -468,7 +461,7 @@ __device__ bool attn_item(const FusedArgs &a, const FusedLayer &ly, uint64_t *tb
         for (int j = 0; j < G; ++j) dot[j] = 0.f;
         if (valid) {
             float kf[8];
-            ld8<KT>((const KT *)(k_lds + (size_t)pi * Geo::ROW) + d8 * 8, kf);
+            ld8<KT>((const KT *)(k_lds + (size_t)pi * ROW) + d8 * 8, kf);
 #pragma unroll
             for (int j = 0; j < G; ++j)
 #pragma unroll
@@ -480,7 +473,7 @@ __device__ bool attn_item(const FusedArgs &a, const FusedLayer &ly, uint64_t *tb
             if (d8 == 0 && valid) sh.p[pi][j] = s * scale;
         }
     }
-    __syncthreads();
+    bar();
     mark(1);
     for (int j = wave; j < G; j += kWaves) {
         float mx = -INFINITY;
@@ -498,11 +491,12 @@ __device__ bool attn_item(const FusedArgs &a, const FusedLayer &ly, uint64_t *tb
             sh.l[j] = sum;
         }
     }
-    __syncthreads();
+    bar();
     mark(2);
-    // Weighted V: lane owns DPL head dimensions, wave w positions w, w + 4,
-    // ...; the four waves' sums are added in wave order.
+    // Weighted V: lane owns DPL head dimensions, wave w positions w, w + 8,
+    // ...; the waves' sums are added in wave order.
     constexpr int DPL = HD / 64;
+    constexpr int GP = AttnShm<HD, G>::GP;
     float acc[G][DPL];
 #pragma unroll
     for (int j = 0; j < G; ++j)
@@ -510,7 +504,7 @@ __device__ bool attn_item(const FusedArgs &a, const FusedLayer &ly, uint64_t *tb
         for (int e = 0; e < DPL; ++e) acc[j][e] = 0.f;
 #pragma unroll 4
     for (int pi = wave; pi < nv; pi += kWaves) {
-        const KT *vrow = (const KT *)(v_lds + (size_t)pi * Geo::ROW) + lane * DPL;
+        const KT *vrow = (const KT *)(v_lds + (size_t)pi * ROW) + lane * DPL;
         float vf[DPL];
         if constexpr (sizeof(KT) == 2) {
             if constexpr (DPL == 1) {
@@ -524,9 +518,9 @@ __device__ bool attn_item(const FusedArgs &a, const FusedLayer &ly, uint64_t *tb
 #pragma unroll
             for (int e = 0; e < DPL; ++e) vf[e] = vrow[e];
         }
-        float pj[AttnShm<HD, G, CH>::GP];
+        float pj[GP];
 #pragma unroll
-        for (int j4 = 0; j4 < AttnShm<HD, G, CH>::GP; j4 += 4) {
+        for (int j4 = 0; j4 < GP; j4 += 4) {
             const f32x4 q4 = *(const f32x4 *)&sh.p[pi][j4];
             pj[j4] = q4[0];
             pj[j4 + 1] = q4[1];
@@ -542,406 +536,520 @@ __device__ bool attn_item(const FusedArgs &a, const FusedLayer &ly, uint64_t *tb
     for (int j = 0; j < G; ++j)
 #pragma unroll
         for (int e = 0; e < DPL; ++e) sh.red[wave][j][lane * DPL + e] = acc[j][e];
-    __syncthreads();
+    bar();
     mark(3);
-    // Partials of group g, split-major: [split][head of group][HD + 2].
-    uint64_t *gpart = a.part + (size_t)g * a.max_splits * G * (HD + 2);
-    uint64_t *part = gpart + (size_t)split * G * (HD + 2);
-    for (int t = tid; t < G * HD; t += kThreads) {
-        const int j = t / HD, d = t % HD;
-        float o = sh.red[0][j][d];
+    if (tid < kCW * 64) {
+        for (int t = tid; t < G * HD; t += kCW * 64) {
+            const int j = t / HD, d = t % HD;
+            float o = sh.red[0][j][d];
 #pragma unroll
-        for (int w = 1; w < kWaves; ++w) o += sh.red[w][j][d];
-        stf(part + (size_t)j * (HD + 2) + d, o, tB);
-    }
-    if (tid < G) {
-        stf(part + (size_t)tid * (HD + 2) + HD, sh.m[tid], tB);
-        stf(part + (size_t)tid * (HD + 2) + HD + 1, sh.l[tid], tB);
-    }
-    if (split != 0) return true;
-    // The split-0 item merges the group's S partials in split order
-    // (weights exp(m_s - M), sum L = sum_s w_s l_s) and publishes the
-    // group's attention output.
-    if (!gather_lds(tb, gpart, S * G * (HD + 2), tB, a.abort_flag)) return false;
-    if (tid < G) {
-        float M = -INFINITY;
-        for (int s = 0; s < S; ++s) M = fmaxf(M, val_of(tb[((size_t)s * G + tid) * (HD + 2) + HD]));
-        float L = 0.f;
-        for (int s = 0; s < S; ++s) {
-            const uint64_t *ps = tb + ((size_t)s * G + tid) * (HD + 2);
-            const float w = expf(val_of(ps[HD]) - M);
-            sh.p[s][tid] = w;
-            L = fmaf(w, val_of(ps[HD + 1]), L);
+            for (int w = 1; w < kWaves; ++w) o += sh.red[w][j][d];
+            stf(part + (size_t)j * (HD + 2) + d, o, tag);
         }
-        sh.l[tid] = 1.0f / L;
+        if (tid < G) {
+            stf(part + (size_t)tid * (HD + 2) + HD, sh.m[tid], tag);
+            stf(part + (size_t)tid * (HD + 2) + HD + 1, sh.l[tid], tag);
+        }
     }
-    __syncthreads();
-    for (int t = tid; t < G * HD; t += kThreads) {
-        const int j = t / HD, d = t % HD;
-        float o = 0.f;
-        for (int s = 0; s < S; ++s) o = fmaf(sh.p[s][j], val_of(tb[((size_t)s * G + j) * (HD + 2) + d]), o);
-        stf(a.attn + (size_t)(g * G + j) * HD + d, o * sh.l[j], tB);
-    }
-    return true;
+}
+
+// Keeps loaded rows in their registers across code that would otherwise
+// reuse them (the compiler then waits for their loads here).
+template <int R, int N>
+__device__ __forceinline__ void pin(u32x4 (&w)[R][N]) {
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+#pragma unroll
+        for (int k = 0; k < N; ++k) asm volatile("" : "+v"(w[i][k]));
 }
 
 // LM head rows gw, gw + W, ... of one wave against the final-normed hidden
-// state xs: logits, and the wave's best (key, index). Out of line, so that
-// its double-buffered rows are register-allocated apart from the layer loop.
+// state xs: logits, and the wave's best (key, index). Batches of HB rows, two
+// in flight; every batch issues HB rows of loads (rows past head_rows read
+// nothing), so the waits count exactly.
 template <int UHB>
-__device__ __noinline__ void head_dots(const uint16_t *head, float *logits, const float *xs, int H, int V, int gw,
-                                       int W, int head_rows, int &key, uint32_t &idx) {
-    constexpr int HB = 4;  // rows per batch, two batches in flight
-    const int lane = tid_here() & 63, nHB = H / 8;
-    const size_t stride = (size_t)H * 2;
+__device__ __forceinline__ void head_dots(const uint16_t *head, float *logits, const float *xs, int H, int V, int gw,
+                                          int W, int head_rows, int &key, uint32_t &idx) {
+    constexpr int HB = 4;
+    const int lane = lane_here(), nHB = H / 8;
+    const uint32_t stride = (uint32_t)H * 2;
+    const Rsrc r = rsrc(head, (size_t)V * stride);
     u32x4 hb[2][HB][UHB];
     const int nbat = (head_rows + HB - 1) / HB;
     auto issue = [&](u32x4 (&buf)[HB][UHB], int bi) {
 #pragma unroll
         for (int k = 0; k < HB; ++k) {
             const int i = bi * HB + k;
-            if (i < head_rows) load_row(buf[k], (const uint8_t *)head + (size_t)(gw + W * i) * stride, nHB);
+            load_row(buf[k], r, (uint32_t)(gw + W * i) * stride, nHB, i < head_rows);
         }
     };
     auto consume = [&](const u32x4 (&buf)[HB][UHB], int bi) {
-        const int nr = min(HB, head_rows - bi * HB);
+        const int nr = max(0, min(HB, head_rows - bi * HB));
         float y[HB];
-        dot_rows<FMT_BF16>(buf, xs, nHB, nr, y);
+        dot_rows<FMT_BF16>(buf, xs, nHB, y);
 #pragma unroll
         for (int k = 0; k < HB; ++k)
             if (k < nr) {
-                const uint32_t r = (uint32_t)(gw + W * (bi * HB + k));
-                if (lane == 0) logits[r] = y[k];
-                better(key, idx, total_key(y[k]), r);
+                const uint32_t row = (uint32_t)(gw + W * (bi * HB + k));
+                if (lane == 0) st_u32(logits + row, __float_as_uint(y[k]));
+                better(key, idx, total_key(y[k]), row);
             }
     };
     issue(hb[0], 0);
     for (int bi = 0; bi < nbat; bi += 2) {
-        if (bi + 1 < nbat) issue(hb[1], bi + 1);
+        issue(hb[1], bi + 1);
         consume(hb[0], bi);
-        if (bi + 2 < nbat) issue(hb[0], bi + 2);
-        if (bi + 1 < nbat) consume(hb[1], bi + 1);
+        issue(hb[0], bi + 2);
+        consume(hb[1], bi + 1);
     }
+    // The last batch issued (rows past the wave's, reading nothing) is
+    // retired here, so no later code inherits a wait for its registers.
+    pin(hb[0]);
 }
 
 // UH/UQ/UI: 16-byte units per lane of a row with H / q_heads*HD / I
-// columns; RGU: gate/up rows per wave; UHB: units per lane of a BF16 head row.
+// columns; RGU: gate/up rows per compute wave; UHB: units per lane of a BF16
+// head row. Shape values are re-read from the arguments where used (A()) and
+// block roles recomputed from them, so that little stays in scalar registers
+// across the step loop.
 template <int FMT, int HD, int G, class KT, int UH, int UQ, int UI, int RGU, int UHB>
-__global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs a) {
-    using Geo = AttnGeo<HD, KT>;
+__global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
     using U = Unit<FMT, 16>;
+    constexpr int ROW = HD * (int)sizeof(KT);
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ Shm sm;
-    __shared__ AttnShm<HD, G, Geo::CH> ash;
-    const int tid = tid_here(), lane = tid & 63, wave = tid >> 6;
-    const int NB = gridDim.x, W = NB * kWaves, b = blockIdx.x;
-    const int gw0 = b * kWaves + wave;
-    const int H = a.H, I = a.I, V = a.V;
-    const int qd = a.q_heads * HD, kvd = a.kv_heads * HD;
-    const int nH = H / U::E, nQ = qd / U::E, nI = I / U::E;
-    const int npairs = (qd + 2 * kvd) / 2;
-    const int half = a.rotary / 2;
-    const LdsLayout lay = lds_layout(H, I, a.q_heads, HD, G, (int)sizeof(KT), NB, a.max_splits);
+    __shared__ AttnShm<HD, G> ash;
+    const int lane = tid_here() & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid_here() >> 6);
+    const bool spare = wave == kSpareWave;
+    const int b = blockIdx.x;
     uint64_t *tb = (uint64_t *)lds;
-    float *xs = (float *)(lds + lay.xs);
 
-    const bool hasA = b * kWaves < npairs, myA = gw0 < npairs;
-    const bool hasH = b * kWaves < H, myH = gw0 < H;
-    // Gate/up rows: block b owns RB consecutive rows, wave w rows w, w + 8, ...
-    const int RB = (I + NB - 1) / NB;
-    const bool hasD = b * RB < I;
-    const int head_rows = gw0 < V ? (V - 1 - gw0) / W + 1 : 0;
-    const bool hasHead = b * kWaves < V;
-    // Blocks that own head rows write argmax partials. Blocks without would
-    // have nothing pacing them and could overwrite a step's partials before
-    // they are read, so they write none.
-    const int head_blocks = min(NB, (V + kWaves - 1) / kWaves);
-
-    int token = __hip_atomic_load(a.step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    long pos = __hip_atomic_load(a.step + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    float h_own = 0.f;
+    // Roles. o_proj and down rows: blocks [0, nhb), compute wave w of block b
+    // owns row kCW * b + w of both (the residual stays in its register). QKV
+    // pairs: the next nab blocks (the last ones when the grid is short).
+    // Gate/up: every block rb consecutive rows, wave w rows w, w + kCW, ...
+    // Attention items: the last blocks. LM head: every wave of every block.
+    auto npairs = [&]() { return (A()->q_heads + 2 * A()->kv_heads) * HD / 2; };
+    auto hasA = [&]() {
+        const int s0 = A()->a0;
+        return b >= s0 && b < s0 + A()->nab;
+    };
+    auto pairA = [&]() { return (b - A()->a0) * kCW + wave; };
+    auto myA = [&]() { return !spare && hasA() && pairA() < npairs(); };
+    auto hasH = [&]() { return b < A()->nhb; };
+    auto rowH = [&]() { return b * kCW + wave; };
+    auto myH = [&]() { return !spare && hasH() && rowH() < A()->H; };
+    auto hasD = [&]() { return b * A()->rb < A()->I; };
+    auto nrD = [&]() {
+        const int rb = A()->rb, I = A()->I;
+        int n = 0;
+#pragma unroll
+        for (int k = 0; k < RGU; ++k) {
+            const int j = wave + kCW * k;
+            n += !spare && j < rb && b * rb + j < I ? 1 : 0;
+        }
+        return n;
+    };
+    auto hasHead = [&]() { return b * kWaves < A()->V; };
 
     u32x4 wA[2][UH], wC[1][UQ], wD[2 * RGU][UH], wE[1][UI];
 
-    // QKV rows of layer l: issued one phase early (before the previous
-    // layer's down-phase wait, or before the argmax wait for layer 0).
-    auto load_wA = [&](int l) {
-        if (myA) {
-            const FusedLayer ly = load_layer(a.layers, l);
-            const int gw = gw_here();
-            load_row(wA[0], ly.qkv + (size_t)(2 * gw) * a.qkv_stride, nH);
-            load_row(wA[1], ly.qkv + (size_t)(2 * gw + 1) * a.qkv_stride, nH);
+    // Weight rows of layer l. Every wave issues the same loads at the same
+    // points (the spare wave's and those of rows a wave does not own read
+    // nothing), so no path through the loop has a different load count and
+    // the compiler's waits stay exact. Issue points: right after A the
+    // o_proj, gate/up and down rows of the layer (the o_proj/down blocks are
+    // idle while QKV and attention run, and a CU sustains only so many
+    // outstanding misses, so issuing later would stall the wave for the
+    // transfer), after D the next layer's QKV rows.
+    auto load_wA = [&](int l, bool valid) {
+        const size_t stride = A()->qkv_stride;
+        const int rows = (A()->q_heads + 2 * A()->kv_heads) * HD;
+        const Rsrc r = rsrc(LY(l)->qkv, (size_t)rows * stride);
+        const bool v = valid && myA();
+        const uint32_t off = (uint32_t)(2 * pairA()) * (uint32_t)stride;
+        load_row(wA[0], r, off, A()->H / U::E, v);
+        load_row(wA[1], r, off + (uint32_t)stride, A()->H / U::E, v);
+    };
+    auto load_wC = [&](int l, bool valid) {
+        const size_t stride = A()->o_stride;
+        const Rsrc r = rsrc(LY(l)->o, (size_t)A()->H * stride);
+        load_row(wC[0], r, (uint32_t)rowH() * (uint32_t)stride, A()->q_heads * HD / U::E, valid && myH());
+    };
+    auto load_wD = [&](int l, bool valid) {
+        const size_t stride = A()->gu_stride, bytes = (size_t)A()->I * stride;
+        const Rsrc rg = rsrc(LY(l)->gate, bytes), ru = rsrc(LY(l)->up, bytes);
+        const int n = nrD(), base = b * A()->rb + wave, nH = A()->H / U::E;
+#pragma unroll
+        for (int k = 0; k < RGU; ++k) {
+            const uint32_t off = (uint32_t)(base + kCW * k) * (uint32_t)stride;
+            load_row(wD[2 * k], rg, off, nH, valid && k < n);
+            load_row(wD[2 * k + 1], ru, off, nH, valid && k < n);
         }
     };
-    load_wA(0);
+    auto load_wE = [&](int l, bool valid) {
+        const size_t stride = A()->down_stride;
+        const Rsrc r = rsrc(LY(l)->down, (size_t)A()->H * stride);
+        load_row(wE[0], r, (uint32_t)rowH() * (uint32_t)stride, A()->I / U::E, valid && myH());
+    };
 
-    const int PH = fused_phases_per_step(a.L);
+    // Layer 0's inputs need the token: the embedding row (spare wave of QKV
+    // blocks, into LDS) and the residual element (compute waves of o/down
+    // blocks).
+    float h_own = 0.f, emb_r = 0.f;
+    auto fetch_embed = [&](int tok) {
+        if (spare && hasA()) dma_bytes(lds + A()->lds_emb, A()->embed + (size_t)tok * A()->H, A()->H * 2);
+        if (myH()) emb_r = ldc_bf16(A()->embed, (long)tok * A()->H + rowH());
+    };
+    // A phase's normed input: every wave computes the scale itself (same
+    // order, same value) and stages its share of xs.
+    auto stage_norm = [&](const void *src, bool bf16_src) {
+        const uint16_t *g = (const uint16_t *)(lds + A()->lds_gain);
+        float *xs = (float *)(lds + A()->lds_xs);
+        const int H = A()->H;
+        if (bf16_src) block_stage<true>(xs, src, H, g, wave_norm_scale<true>(src, H, A()->eps));
+        else block_stage<false>(xs, src, H, g, wave_norm_scale<false>(src, H, A()->eps));
+    };
+
+    int token = __builtin_amdgcn_readfirstlane(__hip_atomic_load(A()->step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    long pos = __builtin_amdgcn_readfirstlane(__hip_atomic_load(A()->step + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    load_wA(0, true);
+    fetch_embed(token);
+
     // A block is paced when it waited on the previous step's last layer (or
     // this is the launch's first step): only then are the cached K/V rows of
     // every earlier position written when it starts a step. Blocks with no
     // role in the previous step may run ahead and must not prefetch them.
-    const bool always_paced = hasA || hasH || hasD || hasHead;
     bool item_prev = false;
-    for (int s = 0; s < a.steps; ++s, ++pos) {
+    for (int s = 0; s < A()->steps; ++s, ++pos) {
+        const int L = A()->L;
         // Optional per-phase timestamps of one step (thread 0 of each block).
-        const bool traced = a.trace && s == a.trace_step;
+        const bool traced = A()->trace && s == A()->trace_step;
         auto mark = [&](int ev) {
-            if (traced && tid == 0) a.trace[(size_t)b * (16 * a.L + 3) + ev] = wall_clock64();
+            if (traced && tid_here() == 0) st_u64(A()->trace + (size_t)b * (16 * A()->L + 3) + ev, wall_clock64());
         };
-        const unsigned tb0 = a.tag0 + (unsigned)(s * PH);
+        const unsigned tb0 = A()->tag0 + (unsigned)(s * fused_phases_per_step(L));
+        // This block's attention item: KV head ig, positions [kv_start, kv_end).
         const long ctx = pos + 1;
-        const int S = (int)((ctx + Geo::CH - 1) / Geo::CH);
-        const int it = NB - 1 - b;
-        const bool hasB = it < a.kv_heads * S;
-        const int ig = hasB ? it / S : 0, isplit = hasB ? it % S : 0;
-        const bool paced = s == 0 || always_paced || item_prev;
+        constexpr int IP = item_positions(ROW);
+        const int S = (int)((ctx + IP - 1) / IP);
+        const int it = (int)gridDim.x - 1 - b;
+        const bool hasB = it < A()->kv_heads * S;
+        int ig = 0, isplit = it;  // it = ig * S + isplit, by subtraction (scalar)
+        while (hasB && isplit >= S) {
+            isplit -= S;
+            ++ig;
+        }
+        const bool paced = s == 0 || hasA() || hasH() || hasD() || hasHead() || item_prev;
         item_prev = hasB;
-        const float *cr = a.rope_cos + (size_t)pos * half;
-        const float *sr = a.rope_sin + (size_t)pos * half;
-        const int page = a.page_table[pos / TP];
-        const int slot = (int)(pos % TP);
-        const uint16_t *emb = a.embed + (size_t)token * H;
+        const long kv_start = (long)isplit * IP;
+        const long kv_end = min(kv_start + IP, ctx);
+        const long kv_lim = min(kv_end, pos);  // cached rows; the new one comes tagged
+        const int nv = (int)(kv_end - kv_start);
 
-        for (int l = 0; l < a.L; ++l) {
-            const FusedLayer ly = load_layer(a.layers, l);
-            const int gw = gw_here();
+        for (int l = 0; l < L; ++l) {
+            const bool more = l + 1 < L;
+            const int ln = more ? l + 1 : l;
             const unsigned tA = tb0 + 5 * l, tB = tA + 1, tC = tA + 2, tD = tA + 3, tE = tA + 4;
-            const long kv_start = (long)isplit * Geo::CH, kv_lim = min(kv_start + Geo::CH, pos);
-            // Weight rows of the o and gate/up phases go out right after the
-            // QKV phase (attention blocks: gate/up before attention, o after
-            // it), so they stream while attention runs; down rows go out
-            // before the down phase's input wait.
-            auto load_wD = [&]() {
-#pragma unroll
-                for (int k = 0; k < RGU; ++k) {
-                    const int j = (gw - b * kWaves) + kWaves * k, r = b * RB + j;
-                    if (j < RB && r < I) {
-                        load_row(wD[2 * k], ly.gate + (size_t)r * a.gu_stride, nH);
-                        load_row(wD[2 * k + 1], ly.up + (size_t)r * a.gu_stride, nH);
-                    }
-                }
-            };
-            auto load_wC = [&]() {
-                if (myH) load_row(wC[0], ly.o + (size_t)gw * a.o_stride, nQ);
-            };
             mark(16 * l);
+            uint8_t *k_lds = lds + A()->lds_kv, *v_lds = k_lds + IP * ROW;
+            float *xs = (float *)(lds + A()->lds_xs);
 
-            // ---- A: QKV pairs + RoPE + K/V append. Attention blocks without
-            // QKV rows start loading their cached K/V rows now.
-            const bool kv_early = hasB && !hasA && (l > 0 || paced);
-            if (kv_early) {
-                uint8_t *k_lds = (uint8_t *)(tb + lay.qkw);
-                load_kv_lds<HD, KT>(k_lds, k_lds + Geo::CH * Geo::ROW, a, ly, ig, kv_start, kv_lim);
-            }
-            if (hasB) load_wD();
-            if (hasA) {
-                if (l == 0) {
-                    stage_embed(xs, emb, H, ly.ln1, a.eps, sm.red);
-                } else {
-                    if (!gather_lds(tb, a.hid1, H, tA - 1, a.abort_flag)) return;
-                    stage_lds(xs, tb, H, ly.ln1, a.eps, sm.red);
-                }
+            // The attention item's cached rows start loading at once (spare
+            // wave: no weight rows in flight).
+            const bool kv_early = hasB && (l > 0 || paced);
+            if (spare && kv_early) load_kv_lds<HD, KT>(k_lds, v_lds, l, ig, kv_start, kv_lim);
+
+            // ---- A: QKV pairs + RoPE + K/V append.
+            if (hasA()) {
+                if (spare) dma_bytes(lds + A()->lds_gain, LY(l)->ln1, A()->H * 2);
+                if (l > 0) gather(tb, A()->hid1, A()->H, tA - 1, A()->abort_flag);
+                if (spare) wait_vm();
+                bar();
+                if (l == 0) stage_norm(lds + A()->lds_emb, true);
+                else stage_norm(tb, false);
+                bar();
             }
             mark(16 * l + 1);
-            if (myA) {
-                const int r0 = 2 * gw;
+            if (myA()) {
+                const int r0 = 2 * pairA();
                 float y[2];
-                dot_rows<FMT>(wA, xs, nH, 2, y);
+                dot_rows<FMT>(wA, xs, A()->H / U::E, y);
                 float v0 = y[0], v1 = y[1];
-                if (lane == 0) {
-                    if (ly.qkv_sc) {
-                        v0 = v0 * ly.qkv_sc[r0];
-                        v1 = v1 * ly.qkv_sc[r0 + 1];
+                if (const float *sc = LY(l)->qkv_sc) {
+                    v0 = v0 * ldc(sc, r0);
+                    v1 = v1 * ldc(sc, r0 + 1);
+                }
+                if (const float *bias = LY(l)->qkv_bias) {
+                    v0 = v0 + ldc(bias, r0);
+                    v1 = v1 + ldc(bias, r0 + 1);
+                }
+                const int qd = A()->q_heads * HD, kvd = A()->kv_heads * HD, kvh = A()->kv_heads;
+                const int rot = A()->rotary, half = rot / 2;
+                const int page = ldc(A()->page_table, pos / TP), slot = (int)(pos % TP);
+                int i0, i1, c0 = -1, c1 = -1;  // q/K/V word, cache element
+                if (r0 < qd + kvd) {
+                    const bool is_q = r0 < qd;
+                    const int base = is_q ? r0 : r0 - qd;
+                    const int h = base / HD, d0 = base % HD;
+                    int o0 = d0, o1 = d0 + 1;
+                    if (d0 < rot) {
+                        const int i = d0 / 2;
+                        const float c = ldc(A()->rope_cos, pos * half + i), sn = ldc(A()->rope_sin, pos * half + i);
+                        const float x1 = v0 * c - v1 * sn, x2 = v1 * c + v0 * sn;
+                        v0 = x1;
+                        v1 = x2;
+                        o0 = i;
+                        o1 = half + i;
                     }
-                    if (ly.qkv_bias) {
-                        v0 = v0 + ly.qkv_bias[r0];
-                        v1 = v1 + ly.qkv_bias[r0 + 1];
-                    }
-                    int i0, i1, c0 = -1, c1 = -1;  // q/K/V word, cache element
-                    if (r0 < qd + kvd) {
-                        const bool is_q = r0 < qd;
-                        const int base = is_q ? r0 : r0 - qd;
-                        const int h = base / HD, d0 = base % HD;
-                        int o0 = d0, o1 = d0 + 1;
-                        if (d0 < a.rotary) {
-                            const int i = d0 / 2;
-                            const float c = cr[i], sn = sr[i];
-                            const float x1 = v0 * c - v1 * sn, x2 = v1 * c + v0 * sn;
-                            v0 = x1;
-                            v1 = x2;
-                            o0 = i;
-                            o1 = half + i;
-                        }
-                        if (is_q) {
-                            const int q0 = (h / G) * (G + 2) * HD + (h % G) * HD;
-                            i0 = q0 + o0;
-                            i1 = q0 + o1;
-                        } else {
-                            const int k0 = h * (G + 2) * HD + G * HD;
-                            i0 = k0 + o0;
-                            i1 = k0 + o1;
-                            const int e0 = ((page * a.kv_heads + h) * TP + slot) * HD;
-                            c0 = e0 + o0;
-                            c1 = e0 + o1;
-                        }
+                    if (is_q) {
+                        const int q0 = (h / G) * (G + 2) * HD + (h % G) * HD;
+                        i0 = q0 + o0;
+                        i1 = q0 + o1;
                     } else {
-                        const int base = r0 - qd - kvd;
-                        const int h = base / HD, d0 = base % HD;
-                        const int v0i = h * (G + 2) * HD + (G + 1) * HD;
-                        i0 = v0i + d0;
-                        i1 = v0i + d0 + 1;
-                        const int e0 = ((page * a.kv_heads + h) * TP + slot) * HD;
-                        c0 = (e0 + d0) | (1 << 30);
-                        c1 = (e0 + d0 + 1) | (1 << 30);
+                        const int k0 = h * (G + 2) * HD + G * HD;
+                        i0 = k0 + o0;
+                        i1 = k0 + o1;
+                        const int e0 = ((page * kvh + h) * TP + slot) * HD;
+                        c0 = e0 + o0;
+                        c1 = e0 + o1;
                     }
-                    sm.outv[2 * wave] = v0;
-                    sm.outv[2 * wave + 1] = v1;
-                    sm.outi[2 * wave] = i0;
-                    sm.outi[2 * wave + 1] = i1;
-                    sm.outc[2 * wave] = c0;
-                    sm.outc[2 * wave + 1] = c1;
+                } else {
+                    const int base = r0 - qd - kvd;
+                    const int h = base / HD, d0 = base % HD;
+                    const int v0i = h * (G + 2) * HD + (G + 1) * HD;
+                    i0 = v0i + d0;
+                    i1 = v0i + d0 + 1;
+                    const int e0 = ((page * kvh + h) * TP + slot) * HD;
+                    c0 = (e0 + d0) | (1 << 30);
+                    c1 = (e0 + d0 + 1) | (1 << 30);
+                }
+                if (lane == 0) {
+                    if (c0 >= 0) {
+                        KT *cache = (KT *)((c0 >> 30) ? LY(l)->vc : LY(l)->kc);
+                        st_kv(cache + (c0 & ((1 << 30) - 1)), v0);
+                        st_kv(cache + (c1 & ((1 << 30) - 1)), v1);
+                    }
+                    uint64_t *qkvn = A()->qkvn;
+                    stf(qkvn + i0, c0 >= 0 ? kv_round<KT>(v0) : v0, tA);
+                    stf(qkvn + i1, c1 >= 0 ? kv_round<KT>(v1) : v1, tA);
                 }
             }
-            if (hasA) {
-                // The block's pairs leave as one run: q/K/V words (K/V as
-                // the cache holds them) and the K/V cache elements.
-                __syncthreads();
-                const int n = 2 * min(kWaves, npairs - b * kWaves);
-                if (tid < n) {
-                    const float v = sm.outv[tid];
-                    const int c = sm.outc[tid];
-                    if (c >= 0) {
-                        KT *cache = (KT *)((c >> 30) ? ly.vc : ly.kc);
-                        st_kv(cache + (c & ((1 << 30) - 1)), v);
-                    }
-                    stf(a.qkvn + sm.outi[tid], c >= 0 ? kv_round<KT>(v) : v, tA);
-                }
-            }
+            load_wC(l, true);
+            load_wD(l, true);
+            load_wE(l, true);
             mark(16 * l + 2);
-            if (!hasB) {
-                load_wC();
-                load_wD();
-            }
 
             // ---- B: attention item.
             if (hasB) {
-                if (hasA) {
-                    uint8_t *k_lds = (uint8_t *)(tb + lay.qkw);
-                    load_kv_lds<HD, KT>(k_lds, k_lds + Geo::CH * Geo::ROW, a, ly, ig, kv_start, kv_lim);
+                gather(tb, A()->qkvn + (size_t)ig * (G + 2) * HD, (G + 2) * HD, tA, A()->abort_flag);
+                if (!kv_early) {
+                    // Not paced: the cached rows are read only once the
+                    // block holds q (whose tags prove every earlier position
+                    // of this layer written); the spare wave owns no chunk of
+                    // the gather, so it waits at a barrier first.
+                    bar();
+                    if (spare) load_kv_lds<HD, KT>(k_lds, v_lds, l, ig, kv_start, kv_lim);
                 }
-                uint64_t *tr = traced ? a.trace + (size_t)b * (16 * a.L + 3) + 16 * l + 3 : nullptr;
-                if (!attn_item<HD, G, KT>(a, ly, tb, ig, isplit, S, pos, tA, tB, !hasA && !kv_early, lay.qkw, ash, tr))
-                    return;
-                load_wC();
+                if (spare) wait_vm();
+                bar();
+                // q as f32; the new position's K and V rows as stored in the cache.
+                for (int i = tid_here(); i < G * HD; i += kThreads) xs[i] = val_of(tb[i]);
+                if (kv_end == ctx)
+                    for (int i = tid_here(); i < 2 * HD; i += kThreads) {
+                        const float v = val_of(tb[G * HD + i]);
+                        KT *row = (KT *)((i < HD ? k_lds : v_lds) + (size_t)(nv - 1) * ROW);
+                        if constexpr (sizeof(KT) == 2) row[i % HD] = f32_bf16_rne(v);
+                        else row[i % HD] = v;
+                    }
+                bar();
+                mark(16 * l + 3);
+                uint64_t *tr = traced ? A()->trace + (size_t)b * (16 * A()->L + 3) + 16 * l + 3 : nullptr;
+                attn_compute<HD, G, KT>(xs, k_lds, v_lds, nv, ash,
+                                        A()->part + ((size_t)isplit * A()->q_heads + (size_t)ig * G) * (HD + 2), tB,
+                                        tr);
             }
             mark(16 * l + 7);
 
-            // ---- C: merge + o_proj + residual.
-            if (hasH) {
-                if (!gather_lds(tb, a.attn, qd, tB, a.abort_flag)) return;
-                stage_lds(xs, tb, qd, nullptr, 0.f, sm.red);
+            // ---- C: partials merged in split order (weights exp(m_s - M),
+            // sum L = sum_s w_s l_s), o_proj + residual. Wave w merges q
+            // heads w, w + 8, ...: lane s holds split s's max and sum, lanes
+            // hold head dimensions for the weighted sum.
+            if (hasH()) {
+                const int Q = A()->q_heads;
+                gather(tb, A()->part, S * Q * (HD + 2), tB, A()->abort_flag);
+                bar();
+                for (int h = wave; h < Q; h += kWaves) {
+                    const uint64_t *ph = tb + (size_t)h * (HD + 2);
+                    const size_t stride = (size_t)Q * (HD + 2);
+                    const float ms = lane < S ? val_of(ph[lane * stride + HD]) : -INFINITY;
+                    const float M = wave_max(ms);
+                    const float ws = lane < S ? expf(ms - M) : 0.f;
+                    const float lsum = lane < S ? val_of(ph[lane * stride + HD + 1]) : 0.f;
+                    float Ls = 0.f;
+                    for (int s2 = 0; s2 < S; ++s2) Ls = fmaf(lane_read(ws, s2), lane_read(lsum, s2), Ls);
+                    const float linv = 1.0f / Ls;
+#pragma unroll
+                    for (int e = 0; e < HD / 64; ++e) {
+                        const int d = lane + 64 * e;
+                        float o = 0.f;
+                        for (int s2 = 0; s2 < S; ++s2) o = fmaf(lane_read(ws, s2), val_of(ph[s2 * stride + d]), o);
+                        xs[xpad(h * HD + d)] = o * linv;
+                    }
+                }
+                bar();
             }
             mark(16 * l + 8);
-            if (myH) {
+            if (myH()) {
+                const int r = rowH();
                 float y[1];
-                dot_rows<FMT>(wC, xs, nQ, 1, y);
+                dot_rows<FMT>(wC, xs, A()->q_heads * HD / U::E, y);
+                mark(16 * l + 14);
                 float v = y[0];
-                if (ly.o_sc) v = v * ly.o_sc[gw];
-                if (ly.o_bias) v = v + ly.o_bias[gw];
-                const float old = l == 0 ? bf16_f32(emb[gw]) : h_own;
+                if (const float *sc = LY(l)->o_sc) v = v * ldc(sc, r);
+                if (const float *bias = LY(l)->o_bias) v = v + ldc(bias, r);
+                const float old = l == 0 ? emb_r : h_own;
                 h_own = old + v;
-                if (lane == 0) sm.outv[wave] = h_own;
+                if (lane == 0) sm.out[wave] = h_own;
             }
-            if (hasH) publish(a.hid0 + b * kWaves, sm.outv, min(kWaves, H - b * kWaves), tC);
+            // The block's rows leave as one coalesced run (one writer per
+            // line instead of one per wave).
+            if (hasH()) {
+                bar();
+                const int cnt = min(kCW, A()->H - b * kCW);
+                if (wave == 0 && lane < cnt) stf(A()->hid0 + b * kCW + lane, sm.out[lane], tC);
+            }
             mark(16 * l + 9);
 
             // ---- D: gate/up + SwiGLU.
-            if (hasD) {
-                if (!gather_lds(tb, a.hid0, H, tC, a.abort_flag)) return;
-                stage_lds(xs, tb, H, ly.ln2, a.eps, sm.red);
+            if (hasD()) {
+                if (spare) dma_bytes(lds + A()->lds_gain, LY(l)->ln2, A()->H * 2);
+                gather(tb, A()->hid0, A()->H, tC, A()->abort_flag);
+                if (spare) wait_vm();
+                bar();
+                stage_norm(tb, false);
+                bar();
             }
             mark(16 * l + 10);
-            if (myH) load_row(wE[0], ly.down + (size_t)gw * a.down_stride, nI);
             {
-                int nr = 0;
+                const int n = nrD();
+                if (n > 0) {
+                    float y[2 * RGU];
+                    dot_rows<FMT>(wD, xs, A()->H / U::E, y);
+                    const int base = b * A()->rb + wave;
 #pragma unroll
-                for (int k = 0; k < RGU; ++k) {
-                    const int j = wave + kWaves * k;
-                    nr += j < RB && b * RB + j < I ? 2 : 0;
-                }
-                float y[2 * RGU];
-                dot_rows<FMT>(wD, xs, nH, nr, y);
-#pragma unroll
-                for (int k = 0; k < RGU; ++k) {
-                    const int j = wave + kWaves * k, r = b * RB + j;
-                    if (j < RB && r < I) {
-                        float gv = y[2 * k], uv = y[2 * k + 1];
-                        if (ly.gate_sc) {
-                            gv = gv * ly.gate_sc[r];
-                            uv = uv * ly.up_sc[r];
+                    for (int k = 0; k < RGU; ++k)
+                        if (k < n) {
+                            const int r = base + kCW * k;
+                            float gv = y[2 * k], uv = y[2 * k + 1];
+                            if (const float *gs = LY(l)->gate_sc) {
+                                gv = gv * ldc(gs, r);
+                                uv = uv * ldc(LY(l)->up_sc, r);
+                            }
+                            if (lane == 0) sm.out[r - b * A()->rb] = gv * (uv / (1.0f + expf(-gv)));
                         }
-                        if (lane == 0) sm.outv[j] = gv * (uv / (1.0f + expf(-gv)));
-                    }
                 }
             }
-            if (hasD) publish(a.act + b * RB, sm.outv, min(RB, I - b * RB), tD);
+            if (hasD()) {
+                bar();
+                const int cnt = min(A()->rb, A()->I - b * A()->rb);
+                if (wave == 0 && lane < cnt) stf(A()->act + b * A()->rb + lane, sm.out[lane], tD);
+            }
+            load_wA(ln, more);
             mark(16 * l + 11);
 
             // ---- E: down + residual.
-            if (l + 1 < a.L) load_wA(l + 1);
-            if (hasH) {
-                if (!gather_lds(tb, a.act, I, tD, a.abort_flag)) return;
-                stage_lds(xs, tb, I, nullptr, 0.f, sm.red);
+            const int nI_e = A()->I / U::E;
+            const float *down_sc = LY(l)->down_sc;
+            uint64_t *hid1 = A()->hid1;
+            if (hasH()) {
+                gather(tb, A()->act, A()->I, tD, A()->abort_flag);
+                bar();
+                block_stage<false>(xs, tb, A()->I, nullptr, 0.f);
+                bar();
             }
             mark(16 * l + 12);
-            if (myH) {
+            if (myH()) {
+                const int r = rowH();
                 float y[1];
-                dot_rows<FMT>(wE, xs, nI, 1, y);
+                dot_rows<FMT>(wE, xs, nI_e, y);
+                mark(16 * l + 15);
                 float v = y[0];
-                if (ly.down_sc) v = v * ly.down_sc[gw];
+                if (down_sc) v = v * ldc(down_sc, r);
                 h_own = h_own + v;
-                if (lane == 0) sm.outv[wave] = h_own;
+                if (lane == 0) sm.out[wave] = h_own;
             }
-            if (hasH) publish(a.hid1 + b * kWaves, sm.outv, min(kWaves, H - b * kWaves), tE);
+            if (hasH()) {
+                bar();
+                const int cnt = min(kCW, A()->H - b * kCW);
+                if (wave == 0 && lane < cnt) stf(hid1 + b * kCW + lane, sm.out[lane], tE);
+            }
             mark(16 * l + 13);
         }
 
-        // ---- LM head (BF16, final norm fused) + argmax partials.
-        const unsigned tH = tb0 + 5 * a.L;
+        // ---- LM head (BF16, final norm fused) + argmax partials. The weight
+        // registers hold the last layer's no-op prefetches; pinned across the
+        // head, its row buffers live elsewhere, and no path from a head load
+        // reaches a layer's use of a weight register.
+        pin(wA);
+        pin(wC);
+        pin(wD);
+        pin(wE);
+        const unsigned tH = tb0 + 5 * L;
         int key = INT_MIN;
         uint32_t idx = 0;
-        if (hasHead) {
-            if (!gather_lds(tb, a.hid1, H, tH - 1, a.abort_flag)) return;
-            stage_lds(xs, tb, H, a.final_norm, a.eps, sm.red);
-            mark(16 * a.L);
-            head_dots<UHB>(a.head, a.logits, xs, H, V, gw_here(), W, head_rows, key, idx);
+        if (hasHead()) {
+            if (spare) dma_bytes(lds + A()->lds_gain, A()->final_norm, A()->H * 2);
+            gather(tb, A()->hid1, A()->H, tH - 1, A()->abort_flag);
+            if (spare) wait_vm();
+            bar();
+            stage_norm(tb, false);
+            bar();
+            mark(16 * L);
+            const int W = (int)gridDim.x * kWaves, gw0 = b * kWaves + wave, V = A()->V;
+            const int head_rows = gw0 < V ? (V - 1 - gw0) / W + 1 : 0;
+            head_dots<UHB>(A()->head, A()->logits, (const float *)(lds + A()->lds_xs), A()->H, V, gw0, W, head_rows,
+                           key, idx);
         }
         block_best(key, idx, sm);
-        mark(16 * a.L + 1);
-        uint64_t *am = a.am + (size_t)(s & 1) * NB * 2;
-        if (hasHead && tid == 0) {
+        pin(wA);
+        pin(wC);
+        pin(wD);
+        pin(wE);
+        mark(16 * L + 1);
+        uint64_t *am = A()->am + (size_t)(s & 1) * gridDim.x * 2;
+        if (hasHead() && tid_here() == 0) {
             stt(am + 2 * b, (uint32_t)key, tH);
             stt(am + 2 * b + 1, idx, tH);
         }
-        if (s + 1 < a.steps) load_wA(0);
+        const bool next = s + 1 < A()->steps;
+        load_wA(0, next);
         // Blocks that use the token (embedding row, residual) reduce the
-        // partials of every head block.
-        if (hasA || hasH) {
-            if (!gather_lds(tb, am, 2 * head_blocks, tH, a.abort_flag)) return;
-            key = INT_MIN;
-            idx = 0;
-            for (int i = tid; i < head_blocks; i += kThreads)
-                better(key, idx, (int)(uint32_t)tb[2 * i], (uint32_t)tb[2 * i + 1]);
-            block_best(key, idx, sm);
-            token = (int)idx;
-            if (b == 0 && tid == 0) {
-                if (pos + 1 < a.hist_cap)
-                    __hip_atomic_store(a.hist + pos + 1, idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store((uint32_t *)a.step, idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(a.step + 1, (int32_t)(pos + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // partials of every head block. A partial that never arrived (the
+        // poll gave up) still holds a valid row index.
+        if (hasA() || hasH()) {
+            const int head_blocks = A()->head_blocks;
+            gather(tb, am, 2 * head_blocks, tH, A()->abort_flag);
+            bar();
+            if (wave == 0) {
+                key = INT_MIN;
+                idx = 0;
+                for (int i = lane; i < head_blocks; i += 64)
+                    better(key, idx, (int)(uint32_t)tb[2 * i], (uint32_t)tb[2 * i + 1]);
+                wave_best(key, idx);
+                if (lane == 0) sm.token = (int)idx;
             }
+            bar();
+            token = __builtin_amdgcn_readfirstlane(sm.token);
+            if (b == 0 && tid_here() == 0) {
+                if (pos + 1 < A()->hist_cap) st_u32(A()->hist + pos + 1, (uint32_t)token);
+                st_u32(A()->step, (uint32_t)token);
+                st_u32(A()->step + 1, (uint32_t)(pos + 1));
+            }
+            if (next) fetch_embed(token);
         }
-        mark(16 * a.L + 2);
+        mark(16 * L + 2);
     }
 }
 
@@ -961,24 +1069,46 @@ int units_per_lane(int cols, int elems_per_unit) { return (cols / elems_per_unit
 
 const Variant *find_variant(int fmt, int H, int q_heads, int kv_heads, int hd, int I, int blocks) {
     if (kv_heads <= 0 || q_heads % kv_heads) return nullptr;
-    const int g = q_heads / kv_heads, E = fmt == FMT_Q8 ? 16 : 8, W = blocks * kWaves;
+    const int g = q_heads / kv_heads, E = fmt == FMT_Q8 ? 16 : 8, W = blocks * kCW;
     const int qd = q_heads * hd, kvd = kv_heads * hd;
     if (H % 8 || qd % E || H % E || I % E) return nullptr;
+    if (H > kMaxChunks * kChunk || I > kMaxChunks * kChunk) return nullptr;  // one gather each
     if ((qd + 2 * kvd) / 2 > W || H > W) return nullptr;
     for (const Variant &v : kVariants) {
         if (v.fmt != fmt || v.hd != hd || v.g != g) continue;
         if (units_per_lane(H, E) > v.uh || units_per_lane(qd, E) > v.uq || units_per_lane(I, E) > v.ui) continue;
         const int rb = (I + blocks - 1) / blocks;
-        if (rb > kStage || (rb + kWaves - 1) / kWaves > v.rgu || units_per_lane(H, 8) > v.uhb) continue;
+        if ((rb + kCW - 1) / kCW > v.rgu || rb > kStage || units_per_lane(H, 8) > v.uhb) continue;
         return &v;
     }
     return nullptr;
 }
 
+size_t static_lds_bytes(int hd, int g) {
+    size_t att = 0;
+    if (hd == 64 && g == 7) att = sizeof(AttnShm<64, 7>);
+    else if (hd == 64 && g == 2) att = sizeof(AttnShm<64, 2>);
+    else if (hd == 128 && g == 4) att = sizeof(AttnShm<128, 4>);
+    return sizeof(Shm) + att;
+}
+
 template <int FMT, int HD, int G, class KT, int UH, int UQ, int UI, int RGU, int UHB>
-int launch_one(const FusedArgs &a, int nb, hipStream_t s) {
+int launch_one(FusedArgs a, int nb, hipStream_t s) {
     auto k = decode_flow_kernel<FMT, HD, G, KT, UH, UQ, UI, RGU, UHB>;
-    const size_t lds = (size_t)lds_layout(a.H, a.I, a.q_heads, HD, G, (int)sizeof(KT), nb, a.max_splits).total;
+    const LdsLayout lay = lds_layout(a.H, a.I, a.q_heads, HD, G, (int)sizeof(KT), nb, a.max_splits);
+    a.lds_xs = lay.xs;
+    a.lds_kv = lay.kv;
+    a.lds_mw = lay.mw;
+    a.lds_emb = lay.emb;
+    a.lds_gain = lay.gain;
+    a.lds_total = lay.total;
+    const int npairs = (a.q_heads + 2 * a.kv_heads) * HD / 2;
+    a.nhb = (a.H + kCW - 1) / kCW;
+    a.nab = (npairs + kCW - 1) / kCW;
+    a.a0 = a.nhb + a.nab <= nb ? a.nhb : nb - a.nab;
+    a.rb = (a.I + nb - 1) / nb;
+    a.head_blocks = std::min(nb, (a.V + kWaves - 1) / kWaves);
+    const size_t lds = (size_t)lay.total;
     hipFuncAttributes attr{};
     CHIP_CHECK(hipFuncGetAttributes(&attr, (const void *)k));
     if (attr.sharedSizeBytes + lds > device_max_lds())
@@ -1008,9 +1138,7 @@ int launch_kt(const Variant &v, const FusedArgs &a, int nb, hipStream_t s) {
 }  // namespace
 
 int fused_positions_per_item(int head_dim, bool kv_f32) {
-    (void)head_dim;
-    (void)kv_f32;
-    return TP;
+    return item_positions(head_dim * (kv_f32 ? 4 : 2));
 }
 
 bool fused_decode_supported(int fmt, int H, int q_heads, int kv_heads, int head_dim, int I, bool aligned16,
@@ -1027,21 +1155,22 @@ int fused_decode_blocks() {
 
 int fused_max_splits(int H, int q_heads, int kv_heads, int head_dim, int I, bool kv_f32, int blocks,
                      size_t capacity) {
-    // Splits whose partials fit the LDS budget next to everything else.
-    const int kvb = kv_f32 ? 4 : 2;
-    const LdsLayout base = lds_layout(H, I, q_heads, head_dim, q_heads / kv_heads, kvb, blocks, 1);
-    const int G = q_heads / kv_heads;
-    const int spare_words = (kLdsBudget - (base.total - base.tbw * 8)) / 8 - kChunk - 2;
-    const int fit = std::min(spare_words / (G * (head_dim + 2)), TP);  // merge weights fill one LDS row per split
-    const size_t per_item = (size_t)fused_positions_per_item(head_dim, kv_f32);
+    // The most splits whose partials every o_proj block can hold in LDS next
+    // to everything else (capped by the grid and by `capacity` positions).
+    const int kvb = kv_f32 ? 4 : 2, G = q_heads / kv_heads;
+    const size_t budget = device_max_lds(), fixed = static_lds_bytes(head_dim, G);
+    const size_t per_item = (size_t)item_positions(head_dim * kvb);
     const size_t need = (capacity + per_item - 1) / per_item;
-    int ms = blocks / kv_heads;
-    ms = std::min(ms, fit);
-    ms = (int)std::min((size_t)ms, need);
-    return std::max(ms, 1);
+    // At most 64: the merge holds one split per lane.
+    int ms = (int)std::min({(size_t)(blocks / kv_heads), std::max<size_t>(need, 1), (size_t)64});
+    for (; ms >= 1; --ms) {
+        const LdsLayout lay = lds_layout(H, I, q_heads, head_dim, G, kvb, blocks, ms);
+        if (fixed + (size_t)lay.total <= budget && lay.tbw <= kMaxChunks * kChunk) return ms;
+    }
+    return 0;  // not even one split fits: no persistent kernel for this shape
 }
 
-int launch_decode_fused(const FusedArgs &a, int fmt, int head_dim, int group, bool kv_f32, hipStream_t s) {
+int launch_decode_fused(FusedArgs a, int fmt, int head_dim, int group, bool kv_f32, hipStream_t s) {
     const int nb = fused_decode_blocks();
     if (nb <= 0) return fail("HIP backend: cannot size the persistent decode grid.");
     const Variant *v = find_variant(fmt, a.H, a.q_heads, a.kv_heads, head_dim, a.I, nb);

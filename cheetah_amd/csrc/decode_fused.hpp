@@ -35,8 +35,7 @@ struct FusedArgs {
     float *logits;              // [V], the last step's
     uint64_t *hid0, *hid1;      // [H] residual stream after o_proj / after down
     uint64_t *qkvn;             // [kv_heads][(G + 2) * hd]: a group's rotated q heads, then its new K and V rows
-    uint64_t *part;             // [kv_heads][max_splits][G][hd + 2] attention partials (output, max, sum)
-    uint64_t *attn;             // [q_heads * hd] merged attention output
+    uint64_t *part;             // [max_splits][q_heads][hd + 2] attention partials (output, max, sum)
     uint64_t *act;              // [I] SwiGLU output
     uint64_t *am;               // [2][blocks][2] argmax partials (key, index) by step parity
     int *abort_flag;            // raised when a poll times out
@@ -45,6 +44,11 @@ struct FusedArgs {
     int max_splits;
     uint64_t *trace;            // null, or [blocks][16L + 3] phase-end timestamps
     int trace_step;             // the step traced
+    // Filled in by launch_decode_fused: dynamic LDS layout (byte offsets) and
+    // block roles (o/down blocks, first QKV block, QKV blocks, gate/up rows
+    // per block, blocks owning LM-head rows).
+    int lds_xs, lds_kv, lds_mw, lds_emb, lds_gain, lds_total;
+    int nhb, a0, nab, rb, head_blocks;
 };
 
 // Phases per decode step: 5 per layer (qkv, attention, o, gate/up, down) + head.
@@ -59,10 +63,11 @@ bool fused_decode_supported(int fmt, int H, int q_heads, int kv_heads, int head_
 int fused_decode_blocks();
 
 // Largest attention split count the kernel's LDS holds for this shape
-// (capped by the grid and by `capacity` positions).
+// (capped by the grid and by `capacity` positions); 0 if none fits.
 int fused_max_splits(int H, int q_heads, int kv_heads, int head_dim, int I, bool kv_f32, int blocks,
                      size_t capacity);
 
-int launch_decode_fused(const FusedArgs &a, int fmt, int head_dim, int group, bool kv_f32, hipStream_t s);
+// Fills in a.lds_* and launches (a is taken by value for that).
+int launch_decode_fused(FusedArgs a, int fmt, int head_dim, int group, bool kv_f32, hipStream_t s);
 
 }  // namespace chip

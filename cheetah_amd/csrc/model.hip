@@ -178,7 +178,7 @@ struct cheetah_hip_model {
     FusedLayer *fused_layers = nullptr;  // device [L]
     int fused_blocks = 0;
     int fused_max_splits = 0;
-    uint64_t *tagged = nullptr;  // hid0 | hid1 | qkvn | part | attn | act | am, tagged words
+    uint64_t *tagged = nullptr;  // hid0 | hid1 | qkvn | part | act | am, tagged words
     size_t tagged_words = 0;
     int32_t *abort_dev = nullptr;
     unsigned next_tag = 1;          // tag of the next launch's first phase
@@ -380,13 +380,13 @@ int finalize(cheetah_hip_model *m) {
 }
 
 // Sizes (words) of the tagged arrays in one allocation: hid0, hid1, qkvn,
-// part, attn, act, am; each rounded to an even count plus 2 words, so every array
+// part, act, am; each rounded to an even count plus 2 words, so every array
 // starts 16-byte aligned and a 16-byte read at its last word stays inside.
 std::vector<size_t> fused_tagged_sizes(const cheetah_hip_model *m) {
     const auto &c = m->sh->cfg;
     const size_t hd = c.head_dim, G = c.q_heads / c.kv_heads;
     const size_t raw[] = {c.hidden_size, c.hidden_size, c.kv_heads * (G + 2) * hd,
-                          (size_t)m->fused_max_splits * c.q_heads * (hd + 2), c.q_heads * hd, c.intermediate_size,
+                          (size_t)m->fused_max_splits * c.q_heads * (hd + 2), c.intermediate_size,
                           4 * (size_t)m->fused_blocks};
     std::vector<size_t> out;
     for (size_t n : raw) out.push_back((n + 1) / 2 * 2 + 2);
@@ -401,8 +401,18 @@ int init_fused(cheetah_hip_model *m) {
     const auto &c = sh.cfg;
     const Layer &L0 = sh.layers[0];
     auto aligned = [](const WMat &w) { return w.row_stride() % 16 == 0 && ((uintptr_t)w.payload() % 16) == 0; };
-    bool al = (uintptr_t)sh.head.base % 16 == 0;
-    for (const Layer &L : sh.layers) al = al && aligned(L.qkv) && aligned(L.o) && aligned(L.gate) && aligned(L.up) && aligned(L.down);
+    // The persistent kernel reads weight rows in 16-byte units through buffer
+    // resources (byte ranges below 2 GiB) and copies the embedding row and the
+    // RMSNorm gains into LDS 16 bytes at a time.
+    auto a16 = [](const void *p) { return (uintptr_t)p % 16 == 0; };
+    auto fits = [](const WMat &w, size_t rows) { return rows * w.row_stride() < (size_t(1) << 31); };
+    const size_t qkv_rows = c.q_heads * c.head_dim + 2 * c.kv_heads * c.head_dim;
+    bool al = a16(sh.head.base) && a16(sh.embed) && a16(sh.final_norm) &&
+              (size_t)c.vocab_size * c.hidden_size * 2 < (size_t(1) << 31);
+    for (const Layer &L : sh.layers)
+        al = al && aligned(L.qkv) && aligned(L.o) && aligned(L.gate) && aligned(L.up) && aligned(L.down) &&
+             a16(L.ln1) && a16(L.ln2) && fits(L.qkv, qkv_rows) && fits(L.o, c.hidden_size) &&
+             fits(L.gate, c.intermediate_size) && fits(L.up, c.intermediate_size) && fits(L.down, c.hidden_size);
     m->fused_blocks = fused_decode_blocks();
     // The kernel addresses one layer's K (or V) pool with 30-bit element
     // indices.
@@ -414,6 +424,10 @@ int init_fused(cheetah_hip_model *m) {
     m->fused_max_splits = fused_max_splits((int)c.hidden_size, (int)c.q_heads, (int)c.kv_heads, (int)c.head_dim,
                                            (int)c.intermediate_size, sh.kv_f32 != 0, m->fused_blocks,
                                            sh.kv_capacity);
+    if (m->fused_max_splits == 0) {
+        m->fused_ok = false;
+        return 0;
+    }
     std::vector<FusedLayer> fl(c.num_layers);
     for (uint32_t l = 0; l < c.num_layers; ++l) {
         const Layer &L = sh.layers[l];
@@ -490,7 +504,7 @@ int run_fused(cheetah_hip_model *m, size_t steps) {
     a.hist_cap = (long)sh.kv_capacity + 1;
     a.logits = m->logits;
     uint64_t *t = m->tagged;
-    uint64_t **dst[] = {&a.hid0, &a.hid1, &a.qkvn, &a.part, &a.attn, &a.act, &a.am};
+    uint64_t **dst[] = {&a.hid0, &a.hid1, &a.qkvn, &a.part, &a.act, &a.am};
     const std::vector<size_t> sizes = fused_tagged_sizes(m);
     for (size_t i = 0; i < sizes.size(); ++i) {
         *dst[i] = t;
