@@ -177,21 +177,17 @@ __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::
 // them with direct global->LDS copies and re-loads the stale ones until every
 // word of its chunks is fresh (its tag reads for eight chunks in flight at a
 // time); the caller's barrier then makes all of them visible to the block.
-// While a round finds nothing new (the producers are not there yet) the wave
-// only probes its first pending chunk, so waiting blocks do not flood the
-// memory system that the weight rows stream through. A wave's wait also
-// covers the weight rows it has in flight. On timeout the abort word is
-// raised and the wave moves on with what it has.
+// A wave's wait also covers the weight rows it has in flight. On timeout the
+// abort word is raised and the wave moves on with what it has.
 __device__ void gather(uint64_t *dst, const uint64_t *src, int n, unsigned tag, int *abort_flag) {
     const int lane = lane_here(), wave = __builtin_amdgcn_readfirstlane(tid_here() >> 6);
     const int chunks = (n + kChunk - 1) / kChunk;
     const int mine = chunks > wave ? (chunks - 1 - wave) / kWaves + 1 : 0;  // at most 16
     const uint32_t *d32 = (const uint32_t *)dst;
     uint32_t pend = (1u << mine) - 1;
-    bool probe = false;
     long spins = 0;
     while (pend) {
-        const uint32_t issued = probe ? (pend & (0u - pend)) : pend;
+        const uint32_t issued = pend;
         for (uint32_t m = issued; m; m &= m - 1) {
             const int c = wave + kWaves * __builtin_ctz(m), w = c * kChunk + lane * 2;
             if (w < n) dma16(src + w, dst + c * kChunk);
@@ -213,10 +209,7 @@ __device__ void gather(uint64_t *dst, const uint64_t *src, int n, unsigned tag, 
                 if (i < mine && ((issued >> i) & 1) && __any(stale)) still |= 1u << i;
             }
         }
-        // Chunks not issued this round stay pending.
-        const uint32_t next = still | (pend & ~issued);
-        probe = (still == issued);  // nothing issued came back fresh
-        pend = next;
+        pend = still;
         if (pend) {
             if (++spins > kSpinLimit || ((spins & 15) == 0 && aborted(abort_flag))) {
                 raise_abort(abort_flag);
@@ -658,7 +651,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
     // Weight rows of layer l. Every wave issues the same loads at the same
     // points (the spare wave's and those of rows a wave does not own read
     // nothing), so no path through the loop has a different load count and
-    // the compiler's waits stay exact. Issue points: right after A the
+    // the compiler's waits stay exact. Issue points: right after B the
     // o_proj, gate/up and down rows of the layer (the o_proj/down blocks are
     // idle while QKV and attention run, and a CU sustains only so many
     // outstanding misses, so issuing later would stall the wave for the
@@ -836,9 +829,6 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                     stf(qkvn + i1, c1 >= 0 ? kv_round<KT>(v1) : v1, tA);
                 }
             }
-            load_wC(l, true);
-            load_wD(l, true);
-            load_wE(l, true);
             mark(16 * l + 2);
 
             // ---- B: attention item.
@@ -870,6 +860,11 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                                         A()->part + ((size_t)isplit * A()->q_heads + (size_t)ig * G) * (HD + 2), tB,
                                         tr);
             }
+            // Attention blocks issue these after their item: rows in flight
+            // would hold back the item's q poll.
+            load_wC(l, true);
+            load_wD(l, true);
+            load_wE(l, true);
             mark(16 * l + 7);
 
             // ---- C: partials merged in split order (weights exp(m_s - M),
