@@ -172,7 +172,7 @@ struct cheetah_hip_model {
     float *logits_host = nullptr;     // pinned
     // Decode graphs, one per attention split count (the grid of a captured
     // launch is fixed; the split count follows the context length).
-    hipGraphExec_t graphs[65] = {};
+    std::vector<hipGraphExec_t> graphs = std::vector<hipGraphExec_t>(attention_max_splits() + 1, nullptr);
     // Persistent decode kernel state (decode_fused.hip).
     bool fused_ok = false;
     FusedLayer *fused_layers = nullptr;  // device [L]
@@ -730,6 +730,7 @@ bool graphs_enabled() {
 int launch_decode(cheetah_hip_model *m, size_t pos) {
     const int splits = decode_splits(pos + 1);
     if (!graphs_enabled()) return enqueue_decode(m, splits);
+    if (splits < 1 || (size_t)splits >= m->graphs.size()) return fail("HIP backend: decode split count out of range.");
     hipGraphExec_t &exec = m->graphs[splits];
     if (!exec) {
         hipGraph_t g = nullptr;

@@ -2,7 +2,8 @@
 
 * Llama-3-8B shape, Q4 linears, 8192-token prompt in 512-row chunks: the
   greedy ids of the first 32 decode steps equal the oracle's (the reference
-  semantics: f32 KV cache), and the prefill logits agree within 1e-2.
+  semantics: f32 KV cache), and the prefill logits agree within 1e-2; the
+  same with the device's BF16 KV cache against the oracle run with BF16 K/V.
 * Qwen2-7B shape, BF16, 32768-token prompt in 1024-row chunks, a KV snapshot,
   restore of the first 30720 positions, a 2048-token suffix and greedy decode:
   the same bars against the oracle run with a BF16 KV cache (the device's).
@@ -48,6 +49,23 @@ def test_llama3_8b_q4_8k_prefill_and_32_greedy_steps(hip):
 
     print("[large] llama3-8b q4, f32 KV, 8192-token prompt", flush=True)
     g, info = workloads.llama3_8b_q4(decode_steps=33, kv="f32")
+    try:
+        assert _rel(info["prefill_logits_head"], gold["prefill_logits_head"]) < 1e-2
+        assert info["tokens"][:32] == gold["tokens"][:32]
+    finally:
+        g.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.timeout(600)
+def test_llama3_8b_q4_8k_bf16_kv_32_greedy_steps(hip):
+    """The same workload with the device's BF16 KV cache, against the oracle
+    run that rounds K/V to BF16 on append."""
+    gold = _load("llama3_8b_q4_bf16kv_greedy.json")
+    from cheetah_amd import workloads
+
+    print("[large] llama3-8b q4, bf16 KV, 8192-token prompt", flush=True)
+    g, info = workloads.llama3_8b_q4(decode_steps=33, kv="bf16")
     try:
         assert _rel(info["prefill_logits_head"], gold["prefill_logits_head"]) < 1e-2
         assert info["tokens"][:32] == gold["tokens"][:32]
