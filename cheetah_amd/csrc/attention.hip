@@ -29,8 +29,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int TP = 64;  // positions per tile (page_size is a multiple of it)
-constexpr int kMaxSplits = 128;        // split-K decode / f32-KV prefill
-constexpr int kMaxPrefillSplits = 64;  // matrix-core prefill (one merge lane per split)
+constexpr int kMaxSplits = 64;
 
 struct AttnArgs {
     const float *q;
@@ -43,6 +42,18 @@ struct AttnArgs {
     float *part;
     float *out;
 };
+
+// Eight consecutive K or V elements of one row as f32.
+__device__ __forceinline__ void load8(const uint16_t *p, float (&f)[8]) {
+    const u32x4 w = *(const u32x4 *)p;
+    f[0] = bf16_lo(w[0]); f[1] = bf16_hi(w[0]); f[2] = bf16_lo(w[1]); f[3] = bf16_hi(w[1]);
+    f[4] = bf16_lo(w[2]); f[5] = bf16_hi(w[2]); f[6] = bf16_lo(w[3]); f[7] = bf16_hi(w[3]);
+}
+__device__ __forceinline__ void load8(const float *p, float (&f)[8]) {
+    const f32x4 a = *(const f32x4 *)p, b = *(const f32x4 *)(p + 4);
+    f[0] = a[0]; f[1] = a[1]; f[2] = a[2]; f[3] = a[3];
+    f[4] = b[0]; f[5] = b[1]; f[6] = b[2]; f[7] = b[3];
+}
 
 // Eight consecutive K or V elements as loaded (converted to f32 at use), so
 // a whole tile can be in flight while the previous one computes.
@@ -251,53 +262,37 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
     }
 }
 
-// Merge the splits of one (row, q head) in split order. Every load is issued
-// up front (one memory round trip): each thread's split values, and in wave 0
-// every split's max and denominator. Wave 0 turns the maxima into weights
-// w_s = exp(m_s - M) and 1 / sum_s w_s l_s; then thread group k folds
-// w_s * o_s[d] over its splits s = k, k + GR, ... in order, skipping empty
-// splits, and the GR group sums are added in group order.
+// Merge the splits of one (row, q head) in split order: one wave turns the
+// split maxima into weights w_s = exp(m_s - M) and 1 / sum_s w_s l_s, then
+// all threads sum w_s * o_s[d] over the non-empty splits.
 template <int HD>
 __global__ __launch_bounds__(kThreads) void attn_combine_kernel(const float *part, int S, int q_heads, float *out) {
     constexpr int GR = kThreads / HD;  // split groups
-    constexpr int PER = kMaxSplits / GR;
-    constexpr int WPL = kMaxSplits / 64;
     __shared__ float s_w[kMaxSplits];
     __shared__ float s_inv;
     __shared__ float s_o[GR][HD];
     const int h = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
     const float *p = part + ((size_t)row * q_heads + h) * (size_t)S * (HD + 2);
+    if (tid < 64) {
+        const float m = tid < S ? p[(size_t)tid * (HD + 2) + HD] : -INFINITY;
+        const float M = wave_max(m);
+        const float w = m == -INFINITY ? 0.f : expf(m - M);
+        const float l = w != 0.f ? p[(size_t)tid * (HD + 2) + HD + 1] : 0.f;
+        const float L = wave_sum(w * l);
+        if (tid < S) s_w[tid] = w;
+        if (tid == 0) s_inv = 1.0f / L;
+    }
+    __syncthreads();
     const int d = tid % HD, grp = tid / HD;
+    // Every split value this thread folds is loaded first (one memory round
+    // trip), then folded in split order.
+    constexpr int PER = kMaxSplits / GR;
     float v[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
         const int s = grp + GR * i;
         v[i] = s < S ? p[(size_t)s * (HD + 2) + d] : 0.f;
     }
-    if (tid < 64) {
-        float m[WPL], l[WPL];
-#pragma unroll
-        for (int i = 0; i < WPL; ++i) {
-            const int s = tid + 64 * i;
-            m[i] = s < S ? p[(size_t)s * (HD + 2) + HD] : -INFINITY;
-            l[i] = s < S ? p[(size_t)s * (HD + 2) + HD + 1] : 0.f;
-        }
-        float mx = m[0];
-#pragma unroll
-        for (int i = 1; i < WPL; ++i) mx = fmaxf(mx, m[i]);
-        const float M = wave_max(mx);
-        float wl = 0.f;
-#pragma unroll
-        for (int i = 0; i < WPL; ++i) {
-            const float w = m[i] == -INFINITY ? 0.f : expf(m[i] - M);
-            if (i == 0) wl = w != 0.f ? w * l[i] : 0.f;
-            else wl += w != 0.f ? w * l[i] : 0.f;
-            if (tid + 64 * i < S) s_w[tid + 64 * i] = w;
-        }
-        const float L = wave_sum(wl);
-        if (tid == 0) s_inv = 1.0f / L;
-    }
-    __syncthreads();
     float o = 0.f;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
@@ -707,7 +702,7 @@ int launch_attention(const AttnJob &j, hipStream_t s) {
         if (j.pos_dev) return fail("HIP backend: prefill attention takes a host position.");
         if (j.offset + j.rows > (size_t)INT32_MAX) return fail("HIP backend: prefill position out of range.");
         const int S = attention_prefill_splits(j.offset + j.rows);
-        if (S > kMaxPrefillSplits) return fail("HIP backend: prefill context exceeds the attention split limit.");
+        if (S > kMaxSplits) return fail("HIP backend: prefill context exceeds the attention split limit.");
         if (S > 1 && (!j.part || j.part_floats < attention_part_floats(j.rows, j.q_heads, S, j.g.head_dim)))
             return fail("HIP backend: prefill attention partial buffer too small.");
         if (j.g.head_dim == 64) return launch_prefill_h<64>(j, a, G, S, s);
