@@ -605,13 +605,14 @@ __device__ __forceinline__ void head_dots(const uint16_t *head, float *logits, c
 // head row. Shape values are re-read from the arguments where used (A()) and
 // block roles recomputed from them, so that little stays in scalar registers
 // across the step loop.
-template <int FMT, int HD, int G, class KT, int UH, int UQ, int UI, int RGU, int UHB>
+template <int FMT, int HD, int G, class KT, int UH, int UQ, int UI, int RGU, int UHB, bool HS>
 __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
     using U = Unit<FMT, 16>;
     constexpr int ROW = HD * (int)sizeof(KT);
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ Shm sm;
-    __shared__ AttnShm<HD, G> ash;
+    constexpr int GI = HS ? 1 : G;  // q heads per attention item
+    __shared__ AttnShm<HD, GI> ash;
     const int lane = tid_here() & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid_here() >> 6);
     const bool spare = wave == kSpareWave;
@@ -727,9 +728,12 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
         const long ctx = pos + 1;
         constexpr int IP = item_positions(ROW);
         const int S = (int)((ctx + IP - 1) / IP);
+        // With HS every q head of a group is an item of its own:
+        // it = (ig * S + isplit) * G + ih; otherwise it = ig * S + isplit.
         const int it = (int)gridDim.x - 1 - b;
-        const bool hasB = it < A()->kv_heads * S;
-        int ig = 0, isplit = it;  // it = ig * S + isplit, by subtraction (scalar)
+        const bool hasB = it < A()->kv_heads * S * (G / GI);
+        const int ih = HS ? it % G : 0;
+        int ig = 0, isplit = HS ? it / G : it;  // by subtraction (scalar)
         while (hasB && isplit >= S) {
             isplit -= S;
             ++ig;
@@ -844,8 +848,9 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                 }
                 if (spare) wait_vm();
                 bar();
-                // q as f32; the new position's K and V rows as stored in the cache.
-                for (int i = tid_here(); i < G * HD; i += kThreads) xs[i] = val_of(tb[i]);
+                // q (the item's heads) as f32; the new position's K and V rows
+                // as stored in the cache.
+                for (int i = tid_here(); i < GI * HD; i += kThreads) xs[i] = val_of(tb[ih * HD + i]);
                 if (kv_end == ctx)
                     for (int i = tid_here(); i < 2 * HD; i += kThreads) {
                         const float v = val_of(tb[G * HD + i]);
@@ -856,9 +861,9 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                 bar();
                 mark(16 * l + 3);
                 uint64_t *tr = traced ? A()->trace + (size_t)b * (16 * A()->L + 3) + 16 * l + 3 : nullptr;
-                attn_compute<HD, G, KT>(xs, k_lds, v_lds, nv, ash,
-                                        A()->part + ((size_t)isplit * A()->q_heads + (size_t)ig * G) * (HD + 2), tB,
-                                        tr);
+                attn_compute<HD, GI, KT>(
+                    xs, k_lds, v_lds, nv, ash,
+                    A()->part + ((size_t)isplit * A()->q_heads + (size_t)ig * G + ih) * (HD + 2), tB, tr);
             }
             // Attention blocks issue these after their item: rows in flight
             // would hold back the item's q poll.
@@ -1087,9 +1092,9 @@ size_t static_lds_bytes(int hd, int g) {
     return sizeof(Shm) + att;
 }
 
-template <int FMT, int HD, int G, class KT, int UH, int UQ, int UI, int RGU, int UHB>
+template <int FMT, int HD, int G, class KT, int UH, int UQ, int UI, int RGU, int UHB, bool HS>
 int launch_one(FusedArgs a, int nb, hipStream_t s) {
-    auto k = decode_flow_kernel<FMT, HD, G, KT, UH, UQ, UI, RGU, UHB>;
+    auto k = decode_flow_kernel<FMT, HD, G, KT, UH, UQ, UI, RGU, UHB, HS>;
     const LdsLayout lay = lds_layout(a.H, a.I, a.q_heads, HD, G, (int)sizeof(KT), nb, a.max_splits);
     a.lds_xs = lay.xs;
     a.lds_kv = lay.kv;
@@ -1122,12 +1127,23 @@ int launch_one(FusedArgs a, int nb, hipStream_t s) {
     return 0;
 }
 
-template <class KT>
+template <class KT, bool HS>
 int launch_kt(const Variant &v, const FusedArgs &a, int nb, hipStream_t s) {
-    if (v.hd == 64 && v.g == 7) return launch_one<FMT_BF16, 64, 7, KT, 2, 2, 10, 3, 2>(a, nb, s);
-    if (v.hd == 64 && v.g == 2) return launch_one<FMT_BF16, 64, 2, KT, 1, 1, 1, 1, 1>(a, nb, s);
-    if (v.hd == 128 && v.g == 4) return launch_one<FMT_BF16, 128, 4, KT, 1, 2, 2, 1, 1>(a, nb, s);
+    if (v.hd == 64 && v.g == 7) return launch_one<FMT_BF16, 64, 7, KT, 2, 2, 10, 3, 2, HS>(a, nb, s);
+    if (v.hd == 64 && v.g == 2) return launch_one<FMT_BF16, 64, 2, KT, 1, 1, 1, 1, 1, HS>(a, nb, s);
+    if (v.hd == 128 && v.g == 4) return launch_one<FMT_BF16, 128, 4, KT, 1, 2, 2, 1, 1, HS>(a, nb, s);
     return fail("HIP backend: no persistent decode kernel for this shape.");
+}
+
+// Attention items one per (KV head, split, q head) when they all fit the
+// grid at the launch's longest context (CHEETAH_HIP_FUSED_HEAD_SPLIT=0: one
+// per (KV head, split), all q heads of the group).
+bool head_split(const FusedArgs &a, int group, int head_dim, bool kv_f32, int nb) {
+    const char *e = getenv("CHEETAH_HIP_FUSED_HEAD_SPLIT");
+    if (e && e[0] == '0') return false;
+    const long ip = item_positions(head_dim * (kv_f32 ? 4 : 2));
+    const long S = (a.ctx_end + ip - 1) / ip;
+    return group > 1 && (long)a.kv_heads * S * group <= (long)nb;
 }
 
 }  // namespace
@@ -1170,7 +1186,9 @@ int launch_decode_fused(FusedArgs a, int fmt, int head_dim, int group, bool kv_f
     if (nb <= 0) return fail("HIP backend: cannot size the persistent decode grid.");
     const Variant *v = find_variant(fmt, a.H, a.q_heads, a.kv_heads, head_dim, a.I, nb);
     if (!v || v->g != group) return fail("HIP backend: no persistent decode kernel for this shape.");
-    return kv_f32 ? launch_kt<float>(*v, a, nb, s) : launch_kt<uint16_t>(*v, a, nb, s);
+    const bool hs = head_split(a, group, head_dim, kv_f32, nb);
+    if (kv_f32) return hs ? launch_kt<float, true>(*v, a, nb, s) : launch_kt<float, false>(*v, a, nb, s);
+    return hs ? launch_kt<uint16_t, true>(*v, a, nb, s) : launch_kt<uint16_t, false>(*v, a, nb, s);
 }
 
 }  // namespace chip

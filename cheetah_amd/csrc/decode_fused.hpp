@@ -42,6 +42,7 @@ struct FusedArgs {
     unsigned tag0;              // tag of step 0, phase 0 of this launch
     int steps;
     int max_splits;
+    long ctx_end;               // context length after the launch's last step
     uint64_t *trace;            // null, or [blocks][16L + 3] phase-end timestamps
     int trace_step;             // the step traced
     // Filled in by launch_decode_fused: dynamic LDS layout (byte offsets) and

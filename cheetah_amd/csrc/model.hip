@@ -467,9 +467,9 @@ bool fused_fits(const cheetah_hip_model *m, size_t offset, size_t steps) {
 }
 
 // Runs `steps` decode steps in one persistent launch from the token and
-// position in step_dev; leaves the last step's logits in m->logits, its
+// position (`offset`, also in step_dev); leaves the last step's logits in m->logits, its
 // argmax in next_dev and every sampled id in hist_dev. Waits for the launch.
-int run_fused(cheetah_hip_model *m, size_t steps) {
+int run_fused(cheetah_hip_model *m, size_t offset, size_t steps) {
     Shared &sh = *m->sh;
     const auto &c = sh.cfg;
     const unsigned per_step = (unsigned)fused_phases_per_step((int)c.num_layers);
@@ -513,6 +513,7 @@ int run_fused(cheetah_hip_model *m, size_t steps) {
     a.abort_flag = m->abort_dev;
     a.tag0 = m->next_tag;
     a.steps = (int)steps;
+    a.ctx_end = (long)(offset + steps);
     a.max_splits = m->fused_max_splits;
     // CHEETAH_HIP_FUSED_TRACE=<file>: per-phase timestamps of the launch's
     // last step, one line per block (wall clock ticks).
@@ -900,7 +901,7 @@ int run_forward(cheetah_hip_model *m, const uint32_t *tokens, size_t n, size_t o
     CHIP_TRY(reserve_positions(m, n));
     if (n == 1) {
         CHIP_TRY(write_step(m, tokens[0], offset));
-        if (fused_fits(m, offset, 1)) CHIP_TRY(run_fused(m, 1));
+        if (fused_fits(m, offset, 1)) CHIP_TRY(run_fused(m, offset, 1));
         else CHIP_TRY(launch_decode(m, offset));
     } else {
         CHIP_CHECK(hipStreamSynchronize(m->stream));  // tokens_host reuse
@@ -1039,7 +1040,7 @@ int cheetah_hip_decode_greedy(cheetah_hip_model *m, uint32_t token, size_t offse
     CHIP_TRY(validate_decode(m, token, offset, steps));
     CHIP_TRY(reserve_positions(m, steps));
     CHIP_TRY(write_step(m, token, offset));
-    if (fused_fits(m, offset, steps)) CHIP_TRY(run_fused(m, steps));
+    if (fused_fits(m, offset, steps)) CHIP_TRY(run_fused(m, offset, steps));
     else
         for (size_t i = 0; i < steps; ++i) CHIP_TRY(launch_decode(m, offset + i));
     CHIP_CHECK(hipMemcpyAsync(tokens_out, m->hist_dev + offset + 1, steps * sizeof(uint32_t), hipMemcpyDeviceToHost,
@@ -1061,7 +1062,7 @@ int cheetah_hip_time_decode(cheetah_hip_model *m, uint32_t token, size_t offset,
     CHIP_CHECK(hipEventCreate(&e1));
     CHIP_CHECK(hipEventRecord(e0, m->stream));
     if (fused_fits(m, offset, steps)) {
-        CHIP_TRY(run_fused(m, steps));  // waits for the launch
+        CHIP_TRY(run_fused(m, offset, steps));  // waits for the launch
     } else {
         for (size_t i = 0; i < steps; ++i) CHIP_TRY(launch_decode(m, offset + i));
     }
