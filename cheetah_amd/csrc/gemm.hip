@@ -43,6 +43,7 @@ struct GArgs {
     const uint16_t *xh, *xl;  // x pre-split into hi / lo BF16 halves, [M][K] (or null)
     const float *bias;
     float *y, *residual;
+    uint16_t *yh, *yl;  // SwiGLU: the output also as BF16 halves (or null)
     int epi;
     int chunk, nchunks;  // accumulation chunk depth (multiple of BK) and count
     float *ws;           // split-K: [nchunks][M][N] chunk sums (a second set for the dual matrix)
@@ -233,7 +234,13 @@ __device__ __forceinline__ void epilogue(const GArgs &a, int m, int n, float v, 
     if constexpr (DUAL) {
         if (a.sc2) u = u * a.sc2[n];
         // silu_multiply, ops.rs:743-747: g * (u / (1 + exp(-g))).
-        a.y[o] = v * (u / (1.0f + expf(-v)));
+        const float g = v * (u / (1.0f + expf(-v)));
+        a.y[o] = g;
+        if (a.yh) {
+            const __bf16 hb = (__bf16)g;
+            a.yh[o] = __builtin_bit_cast(uint16_t, hb);
+            a.yl[o] = __builtin_bit_cast(uint16_t, (__bf16)(g - (float)hb));
+        }
     } else {
         if (a.bias) v = v + a.bias[n];
         if (a.epi == EPI_RESIDUAL) a.residual[o] = a.residual[o] + v;
@@ -674,6 +681,9 @@ int launch_gemm(const GemmJob &job, hipStream_t s) {
     a.bias = job.bias;
     a.y = job.y;
     a.residual = job.residual;
+    if (!job.yh != !job.yl) return fail("HIP backend: gemm output halves need both BF16 buffers or neither.");
+    a.yh = dual ? job.yh : nullptr;
+    a.yl = dual ? job.yl : nullptr;
     a.epi = job.epi;
     a.chunk = gemm_chunk_depth(a.K);
     a.nchunks = (a.K + a.chunk - 1) / a.chunk;

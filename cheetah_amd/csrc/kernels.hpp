@@ -60,6 +60,9 @@ struct GemmJob {
     // then stages BF16 halves instead of splitting x once per weight tile
     // (the same bits).
     const uint16_t *xh = nullptr, *xl = nullptr;
+    // EPI_SWIGLU only, optional: the output also as BF16 halves ([n][rows]
+    // each, the bits launch_split_bf16 would give), for the next GEMM.
+    uint16_t *yh = nullptr, *yl = nullptr;
 };
 int launch_gemm(const GemmJob &job, hipStream_t stream);
 int launch_split_bf16(const float *x, size_t n, uint16_t *xh, uint16_t *xl, hipStream_t s);
@@ -81,8 +84,10 @@ int launch_dequant(const WMat &w, float *out, hipStream_t s);
 int launch_embed(const uint16_t *table, size_t hidden, const uint32_t *tokens, size_t rows, float *out,
                  hipStream_t s);
 // out[i][:] = rmsnorm(x[i][:]) * gain (rows of width n)
+// Row-wise RMSNorm; with xh / xl also the normed rows as BF16 halves (the
+// bits launch_split_bf16 would give), the MFMA GEMM's input.
 int launch_rmsnorm_rows(const float *x, const uint16_t *gain, float eps, size_t rows, size_t n, float *out,
-                        hipStream_t s);
+                        hipStream_t s, uint16_t *xh = nullptr, uint16_t *xl = nullptr);
 
 // Paged KV cache of one layer: [pages][kv_heads][page_size][head_dim]
 // elements, BF16 (default) or f32 (the reference's own cache precision).

@@ -18,7 +18,7 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(const uint16_t *table, 
 
 // rmsnorm (ops.rs:646-652): x * (inv * gain), inv = 1 / sqrt(mean(x^2) + eps).
 __global__ __launch_bounds__(kThreads) void rmsnorm_rows_kernel(const float *x, const uint16_t *gain, float eps, int n,
-                                                                float *out) {
+                                                                float *out, uint16_t *xh, uint16_t *xl) {
     __shared__ float red[kThreads / 64];
     const float *src = x + (size_t)blockIdx.x * n;
     float *dst = out + (size_t)blockIdx.x * n;
@@ -29,7 +29,16 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_rows_kernel(const float *x, 
     __syncthreads();
     const float total = red[0] + red[1] + red[2] + red[3];
     const float inv = 1.0f / sqrtf(total / (float)n + eps);
-    for (int i = threadIdx.x; i < n; i += kThreads) dst[i] = src[i] * (inv * bf16_f32(gain[i]));
+    for (int i = threadIdx.x; i < n; i += kThreads) {
+        const float v = src[i] * (inv * bf16_f32(gain[i]));
+        dst[i] = v;
+        if (xh) {
+            const size_t o = (size_t)blockIdx.x * n + i;
+            const __bf16 hb = (__bf16)v;
+            xh[o] = __builtin_bit_cast(uint16_t, hb);
+            xl[o] = __builtin_bit_cast(uint16_t, (__bf16)(v - (float)hb));
+        }
+    }
 }
 
 // rope_heads (ops.rs:693-740) with the angle's cos/sin read from a table the
@@ -164,9 +173,10 @@ int launch_embed(const uint16_t *table, size_t hidden, const uint32_t *tokens, s
 }
 
 int launch_rmsnorm_rows(const float *x, const uint16_t *gain, float eps, size_t rows, size_t n, float *out,
-                        hipStream_t s) {
+                        hipStream_t s, uint16_t *xh, uint16_t *xl) {
     if (rows == 0) return 0;
-    hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(rows), dim3(kThreads), 0, s, x, gain, eps, (int)n, out);
+    if (!xh != !xl) return fail("HIP backend: rmsnorm needs both BF16 halves or neither.");
+    hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(rows), dim3(kThreads), 0, s, x, gain, eps, (int)n, out, xh, xl);
     CHIP_CHECK(hipGetLastError());
     return 0;
 }

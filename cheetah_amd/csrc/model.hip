@@ -164,6 +164,7 @@ struct cheetah_hip_model {
     float *gemm_ws = nullptr;  // split-K chunk sums of the prefill GEMMs
     size_t gemm_ws_floats = 0;
     uint16_t *xh = nullptr, *xl = nullptr;  // a GEMM input split into BF16 halves, [R][max width]
+    uint16_t *ah = nullptr, *al = nullptr;  // the SwiGLU output as BF16 halves, [R][intermediate]
     uint32_t *tokens_dev = nullptr, *next_dev = nullptr, *hist_dev = nullptr;
     int32_t *step_dev = nullptr;  // [0] = token, [1] = position
     void *argmax_scratch = nullptr;
@@ -584,6 +585,8 @@ int init_instance(cheetah_hip_model *m) {
         const size_t width = std::max({H, qd, I});
         CHIP_TRY(m->mem.alloc(&m->xh, R * width));
         CHIP_TRY(m->mem.alloc(&m->xl, R * width));
+        CHIP_TRY(m->mem.alloc(&m->ah, R * I));
+        CHIP_TRY(m->mem.alloc(&m->al, R * I));
     }
     CHIP_TRY(m->mem.alloc(&m->tokens_dev, sh.kv_capacity));
     CHIP_TRY(m->mem.alloc(&m->next_dev, 1));
@@ -777,7 +780,8 @@ int enqueue_chunk(cheetah_hip_model *m, const uint32_t *tokens_dev, size_t rows,
     const size_t splits = kPrefillSplits;
     for (uint32_t l = 0; l < c.num_layers; ++l) {
         Layer &L = sh.layers[l];
-        CHIP_TRY(launch_rmsnorm_rows(m->hidden, L.ln1, c.rms_eps, rows, H, m->normed, s));
+        // The normed rows come with their BF16 halves (the GEMM's input).
+        CHIP_TRY(launch_rmsnorm_rows(m->hidden, L.ln1, c.rms_eps, rows, H, m->normed, s, m->xh, m->xl));
         GemmJob qkv;
         qkv.w = L.qkv;
         qkv.x = m->normed;
@@ -786,7 +790,6 @@ int enqueue_chunk(cheetah_hip_model *m, const uint32_t *tokens_dev, size_t rows,
         qkv.y = m->qkv;
         qkv.ws = m->gemm_ws;
         qkv.ws_floats = m->gemm_ws_floats;
-        CHIP_TRY(launch_split_bf16(m->normed, rows * (size_t)(H), m->xh, m->xl, s));
         qkv.xh = m->xh;
         qkv.xl = m->xl;
         CHIP_TRY(launch_gemm(qkv, s));
@@ -820,7 +823,7 @@ int enqueue_chunk(cheetah_hip_model *m, const uint32_t *tokens_dev, size_t rows,
         o.xh = m->xh;
         o.xl = m->xl;
         CHIP_TRY(launch_gemm(o, s));
-        CHIP_TRY(launch_rmsnorm_rows(m->hidden, L.ln2, c.rms_eps, rows, H, m->normed, s));
+        CHIP_TRY(launch_rmsnorm_rows(m->hidden, L.ln2, c.rms_eps, rows, H, m->normed, s, m->xh, m->xl));
         GemmJob gu;
         gu.w = L.gate;
         gu.w2 = L.up;
@@ -830,9 +833,10 @@ int enqueue_chunk(cheetah_hip_model *m, const uint32_t *tokens_dev, size_t rows,
         gu.epi = EPI_SWIGLU;
         gu.ws = m->gemm_ws;
         gu.ws_floats = m->gemm_ws_floats;
-        CHIP_TRY(launch_split_bf16(m->normed, rows * (size_t)(H), m->xh, m->xl, s));
         gu.xh = m->xh;
         gu.xl = m->xl;
+        gu.yh = m->ah;  // the down projection's input halves
+        gu.yl = m->al;
         CHIP_TRY(launch_gemm(gu, s));
         GemmJob dn;
         dn.w = L.down;
@@ -842,9 +846,8 @@ int enqueue_chunk(cheetah_hip_model *m, const uint32_t *tokens_dev, size_t rows,
         dn.epi = EPI_RESIDUAL;
         dn.ws = m->gemm_ws;
         dn.ws_floats = m->gemm_ws_floats;
-        CHIP_TRY(launch_split_bf16(m->act, rows * (size_t)(c.intermediate_size), m->xh, m->xl, s));
-        dn.xh = m->xh;
-        dn.xl = m->xl;
+        dn.xh = m->ah;
+        dn.xl = m->al;
         CHIP_TRY(launch_gemm(dn, s));
     }
     if (last_chunk) {
