@@ -44,6 +44,7 @@ struct GArgs {
     const float *bias;
     float *y, *residual;
     uint16_t *yh, *yl;  // SwiGLU: the output also as BF16 halves (or null)
+    int defer;          // split-K: leave the chunk sums for the caller
     int epi;
     int chunk, nchunks;  // accumulation chunk depth (multiple of BK) and count
     float *ws;           // split-K: [nchunks][M][N] chunk sums (a second set for the dual matrix)
@@ -537,7 +538,7 @@ int launch_dma(const GArgs &a, bool split, hipStream_t s) {
     const dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM, split ? a.nchunks : 1);
     hipLaunchKernelGGL((gemm_dma_kernel<DUAL, MT, NS>), grid, dim3(kThreads), lds, s, a, split ? 1 : 0);
     CHIP_CHECK(hipGetLastError());
-    if (split) {
+    if (split && !a.defer) {
         const size_t MN = (size_t)a.M * a.N;
         hipLaunchKernelGGL((gemm_reduce_kernel<DUAL>), dim3((unsigned)((MN + kThreads - 1) / kThreads)),
                            dim3(kThreads), 0, s, a);
@@ -568,7 +569,7 @@ int launch_mt(const GArgs &a, bool split, hipStream_t s) {
     if (a.xh) hipLaunchKernelGGL((gemm_kernel<FMT, DUAL, MT, true>), grid, dim3(kThreads), 0, s, a, split ? 1 : 0);
     else hipLaunchKernelGGL((gemm_kernel<FMT, DUAL, MT, false>), grid, dim3(kThreads), 0, s, a, split ? 1 : 0);
     CHIP_CHECK(hipGetLastError());
-    if (split) {
+    if (split && !a.defer) {
         const size_t MN = (size_t)a.M * a.N;
         hipLaunchKernelGGL((gemm_reduce_kernel<DUAL>), dim3((unsigned)((MN + kThreads - 1) / kThreads)),
                            dim3(kThreads), 0, s, a);
@@ -578,7 +579,7 @@ int launch_mt(const GArgs &a, bool split, hipStream_t s) {
 }
 
 template <int FMT>
-int launch_fmt(const GArgs &a, bool dual, size_t ws_floats, hipStream_t s) {
+int launch_fmt(const GArgs &a, bool dual, size_t ws_floats, hipStream_t s, bool &split_out) {
     const long n_tiles = (a.N + BN - 1) / BN;
     const long tiles128 = n_tiles * ((a.M + 127) / 128), tiles64 = n_tiles * ((a.M + 63) / 64);
     const long cus = device_cus();
@@ -587,6 +588,7 @@ int launch_fmt(const GArgs &a, bool dual, size_t ws_floats, hipStream_t s) {
     // workspace holds them.
     const bool split = a.nchunks > 1 && tiles64 < cus && a.ws &&
                        ws_floats >= gemm_workspace_floats(a.N, a.K, a.M, dual);
+    split_out = split;
     // BF16 weights with pre-split x stream both operands straight into LDS.
     const bool dma = FMT == FMT_BF16 && a.xh && a.K % BK == 0 && a.stride % 16 == 0 &&
                      ((uintptr_t)a.w % 16) == 0 && (!dual || ((uintptr_t)a.w2 % 16) == 0);
@@ -684,6 +686,8 @@ int launch_gemm(const GemmJob &job, hipStream_t s) {
     if (!job.yh != !job.yl) return fail("HIP backend: gemm output halves need both BF16 buffers or neither.");
     a.yh = dual ? job.yh : nullptr;
     a.yl = dual ? job.yl : nullptr;
+    a.defer = job.deferred && job.epi == EPI_RESIDUAL ? 1 : 0;
+    if (job.deferred) *job.deferred = 0;
     a.epi = job.epi;
     a.chunk = gemm_chunk_depth(a.K);
     a.nchunks = (a.K + a.chunk - 1) / a.chunk;
@@ -699,12 +703,16 @@ int launch_gemm(const GemmJob &job, hipStream_t s) {
     else a.vec_w = 0;
     if (w.fmt == FMT_Q4 && (a.stride % 4 != 0 || p1 % 4 != 0 || p2 % 4 != 0))
         return fail("HIP backend: Q4 rows must be 4-byte aligned.");
+    bool split = false;
+    int rc = -1;
     switch (w.fmt) {
-        case FMT_BF16: return launch_fmt<FMT_BF16>(a, dual, job.ws_floats, s);
-        case FMT_Q8: return launch_fmt<FMT_Q8>(a, dual, job.ws_floats, s);
-        case FMT_Q4: return launch_fmt<FMT_Q4>(a, dual, job.ws_floats, s);
+        case FMT_BF16: rc = launch_fmt<FMT_BF16>(a, dual, job.ws_floats, s, split); break;
+        case FMT_Q8: rc = launch_fmt<FMT_Q8>(a, dual, job.ws_floats, s, split); break;
+        case FMT_Q4: rc = launch_fmt<FMT_Q4>(a, dual, job.ws_floats, s, split); break;
+        default: return fail("HIP backend: unknown weight format.");
     }
-    return fail("HIP backend: unknown weight format.");
+    if (rc == 0 && a.defer && split) *job.deferred = a.nchunks;
+    return rc;
 }
 
 }  // namespace chip

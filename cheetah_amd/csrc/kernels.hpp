@@ -63,6 +63,11 @@ struct GemmJob {
     // EPI_SWIGLU only, optional: the output also as BF16 halves ([n][rows]
     // each, the bits launch_split_bf16 would give), for the next GEMM.
     uint16_t *yh = nullptr, *yl = nullptr;
+    // EPI_RESIDUAL only, optional: when the GEMM splits K, leave the chunk
+    // sums in ws ([*deferred][n][rows]) for the caller's reduction
+    // (launch_residual_rmsnorm_rows) and set *deferred to the chunk count;
+    // 0 when the GEMM applied its epilogue itself.
+    int *deferred = nullptr;
 };
 int launch_gemm(const GemmJob &job, hipStream_t stream);
 int launch_split_bf16(const float *x, size_t n, uint16_t *xh, uint16_t *xl, hipStream_t s);
@@ -88,6 +93,15 @@ int launch_embed(const uint16_t *table, size_t hidden, const uint32_t *tokens, s
 // bits launch_split_bf16 would give), the MFMA GEMM's input.
 int launch_rmsnorm_rows(const float *x, const uint16_t *gain, float eps, size_t rows, size_t n, float *out,
                         hipStream_t s, uint16_t *xh = nullptr, uint16_t *xl = nullptr);
+// A deferred residual GEMM's reduction fused with the next RMSNorm: per row
+// m and column i, v = sum over chunks z (in order) of ws[z][m][i], times
+// sc[i], plus bias[i] (each optional), hidden[m][i] += v; then, with a gain,
+// the row RMSNorm of hidden into out (and BF16 halves when xh / xl are set).
+// The same operations as the GEMM's split-K reduction then
+// launch_rmsnorm_rows.
+int launch_residual_rmsnorm_rows(const float *ws, int nchunks, const float *sc, const float *bias, float *hidden,
+                                 size_t rows, size_t n, const uint16_t *gain, float eps, float *out, hipStream_t s,
+                                 uint16_t *xh = nullptr, uint16_t *xl = nullptr);
 
 // Paged KV cache of one layer: [pages][kv_heads][page_size][head_dim]
 // elements, BF16 (default) or f32 (the reference's own cache precision).

@@ -41,6 +41,57 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_rows_kernel(const float *x, 
     }
 }
 
+// A residual GEMM's split-K reduction (chunk sums folded in order, then the
+// epilogue of gemm_reduce_kernel: row scale, bias, residual add) fused with
+// the row RMSNorm that follows it; the norm's sum of squares runs over the
+// same per-thread order as rmsnorm_rows_kernel, so every output has the bits
+// of the two separate kernels.
+__global__ __launch_bounds__(kThreads) void residual_rmsnorm_rows_kernel(const float *ws, int nchunks, const float *sc,
+                                                                         const float *bias, float *hidden, int rows,
+                                                                         int n, const uint16_t *gain, float eps,
+                                                                         float *out, uint16_t *xh, uint16_t *xl) {
+    __shared__ float red[kThreads / 64];
+    const int m = blockIdx.x;
+    const size_t MN = (size_t)rows * n;
+    float *h = hidden + (size_t)m * n;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += kThreads) {
+        const size_t e = (size_t)m * n + i;
+        // Eight chunk sums loaded at a time, folded in chunk order.
+        float v = 0.f;
+        for (int z0 = 0; z0 < nchunks; z0 += 8) {
+            float t[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) t[j] = z0 + j < nchunks ? ws[(size_t)(z0 + j) * MN + e] : 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (z0 + j < nchunks) v += t[j];
+        }
+        if (sc) v = v * sc[i];
+        if (bias) v = v + bias[i];
+        const float r = h[i] + v;
+        h[i] = r;
+        ss = fmaf(r, r, ss);
+    }
+    if (!gain) return;
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float total = red[0] + red[1] + red[2] + red[3];
+    const float inv = 1.0f / sqrtf(total / (float)n + eps);
+    float *dst = out + (size_t)m * n;
+    for (int i = threadIdx.x; i < n; i += kThreads) {
+        const float v = h[i] * (inv * bf16_f32(gain[i]));
+        dst[i] = v;
+        if (xh) {
+            const size_t o = (size_t)m * n + i;
+            const __bf16 hb = (__bf16)v;
+            xh[o] = __builtin_bit_cast(uint16_t, hb);
+            xl[o] = __builtin_bit_cast(uint16_t, (__bf16)(v - (float)hb));
+        }
+    }
+}
+
 // rope_heads (ops.rs:693-740) with the angle's cos/sin read from a table the
 // host filled with the same libm powf/sinf/cosf the reference calls, so q and
 // k come out bit-identical to the CPU path for identical inputs; then
@@ -177,6 +228,19 @@ int launch_rmsnorm_rows(const float *x, const uint16_t *gain, float eps, size_t 
     if (rows == 0) return 0;
     if (!xh != !xl) return fail("HIP backend: rmsnorm needs both BF16 halves or neither.");
     hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(rows), dim3(kThreads), 0, s, x, gain, eps, (int)n, out, xh, xl);
+    CHIP_CHECK(hipGetLastError());
+    return 0;
+}
+
+int launch_residual_rmsnorm_rows(const float *ws, int nchunks, const float *sc, const float *bias, float *hidden,
+                                 size_t rows, size_t n, const uint16_t *gain, float eps, float *out, hipStream_t s,
+                                 uint16_t *xh, uint16_t *xl) {
+    if (rows == 0) return 0;
+    if (!ws || nchunks <= 0 || !hidden || (gain && !out)) return fail("HIP backend: residual norm is missing a buffer.");
+    if (!xh != !xl) return fail("HIP backend: rmsnorm needs both BF16 halves or neither.");
+    if (rows > (size_t)INT32_MAX || n > (size_t)INT32_MAX) return fail("HIP backend: residual norm shape too large.");
+    hipLaunchKernelGGL(residual_rmsnorm_rows_kernel, dim3((unsigned)rows), dim3(kThreads), 0, s, ws, nchunks, sc, bias,
+                       hidden, (int)rows, (int)n, gain, eps, out, xh, xl);
     CHIP_CHECK(hipGetLastError());
     return 0;
 }

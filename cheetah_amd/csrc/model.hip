@@ -778,10 +778,18 @@ int enqueue_chunk(cheetah_hip_model *m, const uint32_t *tokens_dev, size_t rows,
     // depend on how the prompt was cut into chunks (KV continuation stays
     // bit-exact, decoder.rs:1710-1728).
     const size_t splits = kPrefillSplits;
+    // A residual GEMM that split K leaves its chunk sums in gemm_ws; the
+    // reduction then runs fused with the RMSNorm that reads its output.
+    int down_chunks = 0;
+    const float *down_sc = nullptr;
     for (uint32_t l = 0; l < c.num_layers; ++l) {
         Layer &L = sh.layers[l];
         // The normed rows come with their BF16 halves (the GEMM's input).
-        CHIP_TRY(launch_rmsnorm_rows(m->hidden, L.ln1, c.rms_eps, rows, H, m->normed, s, m->xh, m->xl));
+        if (down_chunks)
+            CHIP_TRY(launch_residual_rmsnorm_rows(m->gemm_ws, down_chunks, down_sc, nullptr, m->hidden, rows, H, L.ln1,
+                                                  c.rms_eps, m->normed, s, m->xh, m->xl));
+        else
+            CHIP_TRY(launch_rmsnorm_rows(m->hidden, L.ln1, c.rms_eps, rows, H, m->normed, s, m->xh, m->xl));
         GemmJob qkv;
         qkv.w = L.qkv;
         qkv.x = m->normed;
@@ -822,8 +830,14 @@ int enqueue_chunk(cheetah_hip_model *m, const uint32_t *tokens_dev, size_t rows,
         CHIP_TRY(launch_split_bf16(m->attn, rows * (size_t)(sh.q_dim()), m->xh, m->xl, s));
         o.xh = m->xh;
         o.xl = m->xl;
+        int o_chunks = 0;
+        o.deferred = &o_chunks;
         CHIP_TRY(launch_gemm(o, s));
-        CHIP_TRY(launch_rmsnorm_rows(m->hidden, L.ln2, c.rms_eps, rows, H, m->normed, s, m->xh, m->xl));
+        if (o_chunks)
+            CHIP_TRY(launch_residual_rmsnorm_rows(m->gemm_ws, o_chunks, L.o.scales(), L.o_bias, m->hidden, rows, H,
+                                                  L.ln2, c.rms_eps, m->normed, s, m->xh, m->xl));
+        else
+            CHIP_TRY(launch_rmsnorm_rows(m->hidden, L.ln2, c.rms_eps, rows, H, m->normed, s, m->xh, m->xl));
         GemmJob gu;
         gu.w = L.gate;
         gu.w2 = L.up;
@@ -848,8 +862,13 @@ int enqueue_chunk(cheetah_hip_model *m, const uint32_t *tokens_dev, size_t rows,
         dn.ws_floats = m->gemm_ws_floats;
         dn.xh = m->ah;
         dn.xl = m->al;
+        dn.deferred = &down_chunks;
+        down_sc = L.down.scales();
         CHIP_TRY(launch_gemm(dn, s));
     }
+    if (down_chunks)
+        CHIP_TRY(launch_residual_rmsnorm_rows(m->gemm_ws, down_chunks, down_sc, nullptr, m->hidden, rows, H, nullptr,
+                                              0.f, nullptr, s));
     if (last_chunk) {
         // Final norm of the last row only, fused into the LM head GEMV
         // (qwen2.rs:227-232 then lm_head, ops.rs:1513-1563).
