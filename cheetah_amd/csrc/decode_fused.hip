@@ -4,8 +4,9 @@
 //
 // Per layer five phases, per step one more:
 //   A  QKV rows (fused RMSNorm, bias, RoPE); K/V rows appended to the pages
-//   B  GQA attention: one item = (KV head, run of 128 positions), two-pass
-//      softmax, (output, max, sum) partials per q head
+//   B  GQA attention: one item = (KV head, run of 128 positions, q head) when
+//      those items fit the grid, else (KV head, run) with all q heads of the
+//      group; two-pass softmax, (output, max, sum) partials per q head
 //   C  every o_proj block merges all partials in split order itself, then
 //      o_proj + residual
 //   D  gate/up (fused RMSNorm) + SwiGLU
@@ -22,26 +23,26 @@
 // word it copied carries the expected tag.
 //
 // Roles inside a block. Waves 0-6 (compute waves) own weight rows; wave 7
-// (the poll wave) owns no rows and does all cross-block input traffic: it
-// copies the tagged words a phase needs into LDS with direct global->LDS
-// loads (16 bytes per lane, device-coherent sc1, many in flight), re-loads
-// only the 128-word chunks still stale, and converts the words to the f32
-// vector the compute waves read (RMSNorm fused where the phase has one).
-// Vector memory operations of one wave complete in issue order, so a wave
-// that waited on polls behind outstanding weight loads would wait for those
-// loads too; with the split, polls never wait on weights and weights never
-// wait on polls. The waves meet only at LDS barriers that wait on LDS
-// traffic alone (s_waitcnt lgkmcnt(0); s_barrier), never on vector memory.
+// (the spare wave) owns none and copies the attention item's cached K/V rows
+// and the RMSNorm gains into LDS. Every wave polls: a phase's tagged input
+// words are split into 128-word chunks, wave w copies chunks w, w + 8, ...
+// into LDS with direct global->LDS loads (16 bytes per lane, device-coherent
+// sc1), checks their tags there and re-loads only the stale ones; all waves
+// then stage the f32 vector the dots read (RMSNorm fused where the phase has
+// one). The waves meet only at LDS barriers that wait on LDS traffic alone
+// (s_waitcnt lgkmcnt(0); s_barrier), never on vector memory.
 //
-// Weight streaming. Each compute wave keeps its rows of every phase of the
-// next layer in flight: right after it uses phase X's rows of layer l it
-// issues phase X's rows of layer l + 1 (after the last layer: nothing, and
-// after the LM head all of layer 0 of the next step). The loads are buffer
-// loads issued on every path, with rows a wave does not own pointed past the
-// buffer's range (those lanes read nothing and return 0), so the compiler
-// counts outstanding loads exactly and each use waits only for its own rows.
-// The poll wave's LDS copies are written as inline assembly for the same
-// reason: the compiler would otherwise make every LDS read wait for them.
+// Weight streaming. Weight rows live in registers. A layer's o_proj, gate/up
+// and down rows are issued right after its attention phase (the o_proj/down
+// blocks idle while QKV and attention run), the next layer's QKV rows right
+// after gate/up, and layer 0's after the LM head. Issuing a phase's rows just
+// before its dot would stall the dot: a CU holds only so many outstanding
+// misses. The loads are buffer loads issued on every path, with rows a wave
+// does not own pointed past the buffer's range (those lanes read nothing and
+// return 0), so the compiler counts outstanding loads exactly and each use
+// waits only for its own rows. The LDS copies and the hand-off stores are
+// inline assembly for the same reason: the compiler would otherwise make
+// LDS reads and later loads wait for them.
 //
 // Buffer reuse needs no barrier: a block polls a phase's inputs only in a
 // phase where it also produces outputs, and every buffer is rewritten only by
