@@ -31,6 +31,10 @@ constexpr int kThreads = 256;
 constexpr int TP = 64;  // positions per tile (page_size is a multiple of it)
 constexpr int kMaxSplits = 64;
 
+// Block barrier that waits on LDS traffic only (outstanding global loads
+// stay in flight across it).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 struct AttnArgs {
     const float *q;
     long q_stride;
@@ -132,31 +136,32 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
         l_run[i] = 0.f;
     }
 
-    // Tile t0 + TP is loaded while tile t0 computes.
-    Raw8<KT> ck[TP / P], cv[TP / P], nk[TP / P], nv[TP / P];
+    // K/V tiles ping-pong between two register sets: tile t0 + TP loads while
+    // tile t0 computes. A position past `end` reads the row at end - 1 (the
+    // compute masks it), and the tile barriers wait on LDS only, so the loads
+    // of the next tile stay in flight across the current tile's barriers.
+    Raw8<KT> bk[2][TP / P], bv[2][TP / P];
+    const long last_tile = start + (end - 1 - start) / TP * TP;
     auto issue = [&](long t, Raw8<KT> (&kr)[TP / P], Raw8<KT> (&vr)[TP / P]) {
+        t = min(t, last_tile);
         const int page = a.page_table[t / a.page_size];
         const size_t tile_off = (((size_t)page * a.kv_heads + g) * a.page_size + t % a.page_size) * HD;
         const KT *kt = (const KT *)a.k + tile_off;
         const KT *vt = (const KT *)a.v + tile_off;
+        const int rmax = (int)(end - 1 - t);
 #pragma unroll
         for (int p = 0; p < TP / P; ++p) {
-            const int pi = p * P + pg;
-            if (t + pi < end) {
-                kr[p].load(kt + (size_t)pi * HD + d8 * 8);
-                vr[p].load(vt + (size_t)pi * HD + d8 * 8);
-            }
+            const int r = min(p * P + pg, rmax);
+            kr[p].load(kt + (size_t)r * HD + d8 * 8);
+            vr[p].load(vt + (size_t)r * HD + d8 * 8);
         }
     };
-    issue(start, ck, cv);
-    for (long t0 = start; t0 < end; t0 += TP) {
-        const bool more = t0 + TP < end;
-        if (more) issue(t0 + TP, nk, nv);
+    auto tile = [&](long t0, const Raw8<KT> (&kc)[TP / P], const Raw8<KT> (&vc)[TP / P]) {
         float vf[TP / P][8], kf[TP / P][8];
 #pragma unroll
         for (int p = 0; p < TP / P; ++p) {
-            ck[p].get(kf[p]);
-            cv[p].get(vf[p]);
+            kc[p].get(kf[p]);
+            vc[p].get(vf[p]);
         }
         // Scores of every head of the group for the tile's rows.
 #pragma unroll
@@ -178,7 +183,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
                 if (d8 == 0) s_p[j][pi] = valid ? sum * scale : -INFINITY;
             }
         }
-        __syncthreads();
+        lds_barrier();
         // Online softmax per head: one wave per head, one lane per position.
 #pragma unroll
         for (int i = 0; i < JW; ++i) {
@@ -195,7 +200,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
                 if (lane == 0) s_alpha[j] = alpha;
             }
         }
-        __syncthreads();
+        lds_barrier();
         // acc = acc * alpha + sum_p p * V[p].
 #pragma unroll
         for (int j = 0; j < G; ++j) {
@@ -215,14 +220,21 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
                 }
             }
         }
-        if (more) {
-#pragma unroll
-            for (int p = 0; p < TP / P; ++p) {
-                ck[p] = nk[p];
-                cv[p] = nv[p];
-            }
+        lds_barrier();
+    };
+    issue(start, bk[0], bv[0]);
+    if (end - start <= TP) {
+        tile(start, bk[0], bv[0]);
+    } else {
+        // Issued whether or not the tile exists (a tile past the split reads
+        // the split's last tile again), so the compiler counts the loads
+        // exactly and each tile waits only for its own.
+        for (long t0 = start; t0 < end; t0 += 2 * TP) {
+            issue(t0 + TP, bk[1], bv[1]);
+            tile(t0, bk[0], bv[0]);
+            issue(t0 + 2 * TP, bk[0], bv[0]);
+            if (t0 + TP < end) tile(t0 + TP, bk[1], bv[1]);
         }
-        __syncthreads();
     }
     // Reduce acc over the position groups: lanes d8, d8+T, ... of a wave,
     // then across the 4 waves through LDS.
