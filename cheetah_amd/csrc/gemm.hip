@@ -249,6 +249,57 @@ __device__ __forceinline__ void epilogue(const GArgs &a, int m, int n, float v, 
     }
 }
 
+// The epilogue for one lane's outputs of a finished tile: column n per j,
+// rows m = mbase + 32 i + 8 (q / 4) + 4 (lane / 32) + q % 4. The column's scale
+// and bias, then a 32-row block's residuals, are loaded before any store (one
+// wait instead of one per output); each output's arithmetic is epilogue's.
+template <bool DUAL, int MT>
+__device__ __forceinline__ void epilogue_tile(const GArgs &a, const f32x16 (&tot)[MT][2],
+                                              const f32x16 (&tot2)[DUAL ? MT : 1][2], int mbase, int nbase, int lane) {
+    const bool resid = !DUAL && a.epi == EPI_RESIDUAL;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int n = nbase + 32 * j + (lane & 31);
+        if (n >= a.N) continue;
+        const float scn = a.sc ? a.sc[n] : 1.0f;
+        const float sc2n = DUAL && a.sc2 ? a.sc2[n] : 1.0f;
+        const float bn = !DUAL && a.bias ? a.bias[n] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+            float res[16];
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int m = mbase + 32 * i + 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
+                res[q] = resid && m < a.M ? a.residual[(size_t)m * a.N + n] : 0.0f;
+            }
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int m = mbase + 32 * i + 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
+                if (m >= a.M) continue;
+                const size_t o = (size_t)m * a.N + n;
+                float v = tot[i][j][q];
+                if (a.sc) v = v * scn;
+                if constexpr (DUAL) {
+                    float u = tot2[i][j][q];
+                    if (a.sc2) u = u * sc2n;
+                    // silu_multiply, ops.rs:743-747: g * (u / (1 + exp(-g))).
+                    const float g = v * (u / (1.0f + expf(-v)));
+                    a.y[o] = g;
+                    if (a.yh) {
+                        const __bf16 hb = (__bf16)g;
+                        a.yh[o] = __builtin_bit_cast(uint16_t, hb);
+                        a.yl[o] = __builtin_bit_cast(uint16_t, (__bf16)(g - (float)hb));
+                    }
+                } else {
+                    if (a.bias) v = v + bn;
+                    if (resid) a.residual[o] = res[q] + v;
+                    else a.y[o] = v;
+                }
+            }
+        }
+    }
+}
+
 // blockIdx: x = weight-row tile, y = token tile, z = chunk (split-K) or 0.
 template <int FMT, bool DUAL, int MT, bool PRE>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GArgs a, int split) {
@@ -346,6 +397,10 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GArgs a, int split) {
         b ^= 1;
     }
     // D layout of the 32x32 MFMA: column = lane % 32, row = 8*(r/4) + 4*(lane/32) + r%4.
+    if (!split) {
+        epilogue_tile<DUAL, MT>(a, tot, tot2, m0 + wm, n0 + wn, lane);
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int n = n0 + wn + 32 * j + (lane & 31);
@@ -356,15 +411,9 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GArgs a, int split) {
             for (int q = 0; q < 16; ++q) {
                 const int m = m0 + wm + 32 * i + 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
                 if (m >= a.M) continue;
-                const float v = tot[i][j][q];
-                const float u = DUAL ? tot2[DUAL ? i : 0][j][q] : 0.f;
-                if (split) {
-                    const size_t o = ((size_t)blockIdx.z * a.M + m) * a.N + n;
-                    a.ws[o] = v;
-                    if constexpr (DUAL) a.ws[(size_t)a.nchunks * a.M * a.N + o] = u;
-                } else {
-                    epilogue<DUAL>(a, m, n, v, u);
-                }
+                const size_t o = ((size_t)blockIdx.z * a.M + m) * a.N + n;
+                a.ws[o] = tot[i][j][q];
+                if constexpr (DUAL) a.ws[(size_t)a.nchunks * a.M * a.N + o] = tot2[i][j][q];
             }
     }
 }
@@ -502,6 +551,10 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GArgs a, int split) 
         __builtin_amdgcn_s_waitcnt(vm_wait_imm(63) & ~(0xF << 8));  // lgkmcnt(0)
         __builtin_amdgcn_s_barrier();
     }
+    if (!split) {
+        epilogue_tile<DUAL, MT>(a, tot, tot2, m0 + wm, n0 + wn, lane);
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int n = n0 + wn + 32 * j + (lane & 31);
@@ -512,15 +565,9 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GArgs a, int split) 
             for (int q = 0; q < 16; ++q) {
                 const int m = m0 + wm + 32 * i + 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
                 if (m >= a.M) continue;
-                const float v = tot[i][j][q];
-                const float u = DUAL ? tot2[DUAL ? i : 0][j][q] : 0.f;
-                if (split) {
-                    const size_t o = ((size_t)blockIdx.z * a.M + m) * a.N + n;
-                    a.ws[o] = v;
-                    if constexpr (DUAL) a.ws[(size_t)a.nchunks * a.M * a.N + o] = u;
-                } else {
-                    epilogue<DUAL>(a, m, n, v, u);
-                }
+                const size_t o = ((size_t)blockIdx.z * a.M + m) * a.N + n;
+                a.ws[o] = tot[i][j][q];
+                if constexpr (DUAL) a.ws[(size_t)a.nchunks * a.M * a.N + o] = tot2[i][j][q];
             }
     }
 }
