@@ -73,13 +73,36 @@ struct Staged {
     std::vector<uint64_t> shape;
 };
 
+constexpr int kLayerMats = 5;  // qkv, o, gate, up, down
+
 struct Layer {
     WMat qkv, o, gate, up, down;
     float *qkv_bias = nullptr;  // f32 [q_dim + 2 kv_dim] (zeros when absent)
     float *o_bias = nullptr;    // f32 [hidden] or null
     uint16_t *ln1 = nullptr, *ln2 = nullptr;
     KvLayer kv;
+    // Host tier: pinned copy of a matrix whose device buffer was released
+    // (its WMat base is then null); indexed like mat(). Null when resident.
+    uint8_t *host[kLayerMats] = {};
+    WMat &mat(int i) {
+        WMat *w[] = {&qkv, &o, &gate, &up, &down};
+        return *w[i];
+    }
+    const WMat &mat(int i) const { return const_cast<Layer *>(this)->mat(i); }
+    bool streamed() const {
+        for (const uint8_t *h : host)
+            if (h) return true;
+        return false;
+    }
 };
+
+// Byte offset of matrix i in a feed slot (each matrix 256-byte aligned, the
+// alignment of its own device buffer).
+size_t slot_offset(const Layer &L, int i) {
+    size_t off = 0;
+    for (int j = 0; j < i; ++j) off += (L.mat(j).bytes() + 255) / 256 * 256;
+    return off;
+}
 
 // Weights, rope table and KV pool: shared by a model, its clones and
 // snapshots.
@@ -103,6 +126,9 @@ struct Shared {
     std::vector<int> refs;
     std::vector<int> free_list;
     hipStream_t copy_stream = nullptr;
+    int host_mats = 0;       // layer matrices on the host tier
+    unsigned epoch = 0;      // bumped whenever a weight's device address changes
+    size_t slot_bytes = 0;   // one layer's matrices, as a feed slot holds them
 
     int q_dim() const { return (int)(cfg.q_heads * cfg.head_dim); }
     int kv_dim() const { return (int)(cfg.kv_heads * cfg.head_dim); }
@@ -114,6 +140,9 @@ struct Shared {
         }
         for (auto &kv : staged)
             if (kv.second.dev) (void)hipFree(kv.second.dev);
+        for (Layer &L : layers)
+            for (uint8_t *h : L.host)
+                if (h) (void)hipHostFree(h);
     }
 
     int page_alloc() {
@@ -184,9 +213,29 @@ struct cheetah_hip_model {
     int32_t *abort_dev = nullptr;
     unsigned next_tag = 1;          // tag of the next launch's first phase
     int32_t *abort_host = nullptr;  // pinned
+    unsigned epoch = 0;             // the weight epoch the graphs and layer table were built for
+    // Host-tier feed: layer l's streamed matrices are copied from pinned
+    // host memory into slot l % 2 on feed_stream, one streamed layer ahead
+    // of the compute stream. ready[k] marks a finished copy into slot k,
+    // released[k] the end of the last kernel reading it; fed[k] is the
+    // layer rebased onto the slot.
+    hipStream_t feed_stream = nullptr;
+    uint8_t *slot[2] = {};
+    int slot_layer[2] = {-1, -1};
+    unsigned slot_epoch[2] = {};
+    hipEvent_t ready[2] = {}, released[2] = {};
+    Layer fed[2];
 
     ~cheetah_hip_model() {
         if (stream) (void)hipStreamSynchronize(stream);
+        if (feed_stream) {
+            (void)hipStreamSynchronize(feed_stream);
+            (void)hipStreamDestroy(feed_stream);
+        }
+        for (int k = 0; k < 2; ++k) {
+            if (ready[k]) (void)hipEventDestroy(ready[k]);
+            if (released[k]) (void)hipEventDestroy(released[k]);
+        }
         for (hipGraphExec_t g : graphs)
             if (g) (void)hipGraphExecDestroy(g);
         if (stream) (void)hipStreamDestroy(stream);
@@ -345,6 +394,7 @@ int finalize(cheetah_hip_model *m) {
             kv.second.dev = nullptr;
         }
     sh.staged.clear();
+    sh.slot_bytes = slot_offset(sh.layers[0], kLayerMats);  // every layer has the same shapes
 
     // RoPE table: angle = pos * theta^(-2i/rotary_dim), with libm powf/sinf/
     // cosf exactly as rope_in_place computes it (ops.rs:702-707).
@@ -394,6 +444,22 @@ std::vector<size_t> fused_tagged_sizes(const cheetah_hip_model *m) {
     return out;
 }
 
+// The persistent kernel's per-layer pointer table (device addresses of the
+// weights as they are now; a host-tier matrix has none and the kernel is not
+// used while one exists).
+int upload_fused_layers(cheetah_hip_model *m) {
+    const Shared &sh = *m->sh;
+    std::vector<FusedLayer> fl(sh.cfg.num_layers);
+    for (uint32_t l = 0; l < sh.cfg.num_layers; ++l) {
+        const Layer &L = sh.layers[l];
+        fl[l] = FusedLayer{L.qkv.payload(), L.o.payload(), L.gate.payload(), L.up.payload(), L.down.payload(),
+                           L.qkv.scales(), L.o.scales(), L.gate.scales(), L.up.scales(), L.down.scales(),
+                           L.qkv_bias, L.o_bias, L.ln1, L.ln2, L.kv.k, L.kv.v};
+    }
+    CHIP_CHECK(hipMemcpy(m->fused_layers, fl.data(), fl.size() * sizeof(FusedLayer), hipMemcpyHostToDevice));
+    return 0;
+}
+
 // Persistent decode state of one instance: the per-layer pointer table and
 // the tagged hand-off words. Sets fused_ok when the model's shape and layout
 // have a persistent kernel; otherwise decode keeps the graph path.
@@ -429,15 +495,8 @@ int init_fused(cheetah_hip_model *m) {
         m->fused_ok = false;
         return 0;
     }
-    std::vector<FusedLayer> fl(c.num_layers);
-    for (uint32_t l = 0; l < c.num_layers; ++l) {
-        const Layer &L = sh.layers[l];
-        fl[l] = FusedLayer{L.qkv.payload(), L.o.payload(), L.gate.payload(), L.up.payload(), L.down.payload(),
-                           L.qkv.scales(), L.o.scales(), L.gate.scales(), L.up.scales(), L.down.scales(),
-                           L.qkv_bias, L.o_bias, L.ln1, L.ln2, L.kv.k, L.kv.v};
-    }
-    CHIP_TRY(m->mem.alloc(&m->fused_layers, fl.size()));
-    CHIP_CHECK(hipMemcpy(m->fused_layers, fl.data(), fl.size() * sizeof(FusedLayer), hipMemcpyHostToDevice));
+    CHIP_TRY(m->mem.alloc(&m->fused_layers, c.num_layers));
+    CHIP_TRY(upload_fused_layers(m));
     m->tagged_words = 0;
     for (size_t n : fused_tagged_sizes(m)) m->tagged_words += n;
     CHIP_TRY(m->mem.alloc(&m->tagged, m->tagged_words));
@@ -460,7 +519,8 @@ bool fused_enabled(const cheetah_hip_model *m) {
 // [offset, offset + steps): the attention items of the longest context must
 // fit the grid.
 bool fused_fits(const cheetah_hip_model *m, size_t offset, size_t steps) {
-    if (!fused_enabled(m)) return false;
+    // The persistent kernel reads every layer from HBM in place.
+    if (!fused_enabled(m) || m->sh->host_mats) return false;
     const Shared &sh = *m->sh;
     const size_t per_item = (size_t)fused_positions_per_item((int)sh.cfg.head_dim, sh.kv_f32 != 0);
     const size_t ctx = offset + steps;
@@ -561,6 +621,13 @@ int init_instance(cheetah_hip_model *m) {
     const auto &c = sh.cfg;
     const size_t H = c.hidden_size, qd = sh.q_dim(), kvd = sh.kv_dim(), R = sh.max_chunk;
     CHIP_CHECK(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
+    CHIP_CHECK(hipStreamCreateWithFlags(&m->feed_stream, hipStreamNonBlocking));
+    for (int k = 0; k < 2; ++k) {
+        CHIP_CHECK(hipEventCreateWithFlags(&m->ready[k], hipEventDisableTiming));
+        CHIP_CHECK(hipEventCreateWithFlags(&m->released[k], hipEventDisableTiming));
+        CHIP_CHECK(hipEventRecord(m->released[k], m->stream));
+    }
+    m->epoch = sh.epoch;
     CHIP_TRY(m->mem.alloc(&m->hidden, R * H));
     CHIP_TRY(m->mem.alloc(&m->normed, R * H));
     CHIP_TRY(m->mem.alloc(&m->qkv, R * (qd + 2 * kvd)));
@@ -651,6 +718,81 @@ KvGeom geom(const cheetah_hip_model *m) {
     return KvGeom{m->page_dev, kPageSize, (int)C(m).kv_heads, (int)C(m).head_dim, m->sh->kv_f32};
 }
 
+// Copies layer l's host-tier matrices into slot l % 2 on the feed stream,
+// after the last kernel that read the slot, and rebases fed[l % 2] onto it.
+int feed_issue(cheetah_hip_model *m, uint32_t l) {
+    Shared &sh = *m->sh;
+    const int k = (int)(l & 1);
+    if (!m->slot[k]) CHIP_TRY(m->mem.alloc(&m->slot[k], sh.slot_bytes));
+    const Layer &src = sh.layers[l];
+    Layer &dst = m->fed[k];
+    dst = src;
+    CHIP_CHECK(hipStreamWaitEvent(m->feed_stream, m->released[k], 0));
+    for (int i = 0; i < kLayerMats; ++i) {
+        if (!src.host[i]) continue;
+        uint8_t *at = m->slot[k] + slot_offset(src, i);
+        CHIP_CHECK(hipMemcpyAsync(at, src.host[i], src.mat(i).bytes(), hipMemcpyHostToDevice, m->feed_stream));
+        dst.mat(i).base = at;
+    }
+    CHIP_CHECK(hipEventRecord(m->ready[k], m->feed_stream));
+    m->slot_layer[k] = (int)l;
+    m->slot_epoch[k] = sh.epoch;
+    return 0;
+}
+
+bool slot_holds(const cheetah_hip_model *m, uint32_t l) {
+    const int k = (int)(l & 1);
+    return m->slot_layer[k] == (int)l && m->slot_epoch[k] == m->sh->epoch;
+}
+
+// The layer as the kernels enqueued next read it: the shared layer when all
+// of its matrices are resident, else its copy rebased onto the feed slot,
+// with the compute stream waiting for the slot's copy.
+int layer_begin(cheetah_hip_model *m, uint32_t l, hipStream_t s, const Layer **out) {
+    const Layer &L = m->sh->layers[l];
+    *out = &L;
+    if (!L.streamed()) return 0;
+    if (!slot_holds(m, l)) CHIP_TRY(feed_issue(m, l));
+    CHIP_CHECK(hipStreamWaitEvent(s, m->ready[l & 1], 0));
+    *out = &m->fed[l & 1];
+    return 0;
+}
+
+// After layer l's kernels: releases its slot and starts the copy of the next
+// streamed layer (wrapping to the first one, for the next step), so the
+// transfer overlaps the compute in between. A slot that already holds its
+// layer is kept, so two streamed layers of different parity stay in place.
+int layer_end(cheetah_hip_model *m, uint32_t l, hipStream_t s) {
+    const Shared &sh = *m->sh;
+    if (!sh.host_mats) return 0;
+    if (sh.layers[l].streamed()) CHIP_CHECK(hipEventRecord(m->released[l & 1], s));
+    const uint32_t n = sh.cfg.num_layers;
+    for (uint32_t d = 1; d <= n; ++d) {
+        const uint32_t next = (l + d) % n;
+        if (!sh.layers[next].streamed()) continue;
+        if (!slot_holds(m, next)) CHIP_TRY(feed_issue(m, next));
+        break;
+    }
+    return 0;
+}
+
+// Brings an instance up to the current weight epoch: captured graphs and the
+// persistent kernel's table hold device addresses that page_in / evict have
+// changed.
+int refresh_weights(cheetah_hip_model *m) {
+    const Shared &sh = *m->sh;
+    if (m->epoch == sh.epoch) return 0;
+    CHIP_CHECK(hipStreamSynchronize(m->stream));
+    for (hipGraphExec_t &g : m->graphs)
+        if (g) {
+            (void)hipGraphExecDestroy(g);
+            g = nullptr;
+        }
+    if (m->fused_ok && !sh.host_mats) CHIP_TRY(upload_fused_layers(m));
+    m->epoch = sh.epoch;
+    return 0;
+}
+
 // Attention splits of a decode step over `ctx` keys: ~128 positions each.
 int decode_splits(size_t ctx) {
     const size_t s = (ctx + 127) / 128;
@@ -665,7 +807,9 @@ int enqueue_decode(cheetah_hip_model *m, int splits) {
     const int32_t *pos = m->step_dev + 1;
     CHIP_TRY(launch_embed(sh.embed, c.hidden_size, (const uint32_t *)m->step_dev, 1, m->hidden, s));
     for (uint32_t l = 0; l < c.num_layers; ++l) {
-        Layer &L = sh.layers[l];
+        const Layer *Lp = nullptr;
+        CHIP_TRY(layer_begin(m, l, s, &Lp));
+        const Layer &L = *Lp;
         GemvJob qkv;
         qkv.w = L.qkv;
         qkv.x = m->hidden;
@@ -711,6 +855,7 @@ int enqueue_decode(cheetah_hip_model *m, int splits) {
         dn.residual = m->hidden;
         dn.epi = EPI_RESIDUAL;
         CHIP_TRY(launch_gemv(dn, s));
+        CHIP_TRY(layer_end(m, l, s));
     }
     GemvJob head;
     head.w = sh.head;
@@ -733,7 +878,9 @@ bool graphs_enabled() {
 // already hold it): the captured graph for the step's split count.
 int launch_decode(cheetah_hip_model *m, size_t pos) {
     const int splits = decode_splits(pos + 1);
-    if (!graphs_enabled()) return enqueue_decode(m, splits);
+    // Host-tier weights are fed by copies ordered with events on a second
+    // stream: those steps run eagerly.
+    if (!graphs_enabled() || m->sh->host_mats) return enqueue_decode(m, splits);
     if (splits < 1 || (size_t)splits >= m->graphs.size()) return fail("HIP backend: decode split count out of range.");
     hipGraphExec_t &exec = m->graphs[splits];
     if (!exec) {
@@ -783,7 +930,9 @@ int enqueue_chunk(cheetah_hip_model *m, const uint32_t *tokens_dev, size_t rows,
     int down_chunks = 0;
     const float *down_sc = nullptr;
     for (uint32_t l = 0; l < c.num_layers; ++l) {
-        Layer &L = sh.layers[l];
+        const Layer *Lp = nullptr;
+        CHIP_TRY(layer_begin(m, l, s, &Lp));
+        const Layer &L = *Lp;
         // The normed rows come with their BF16 halves (the GEMM's input).
         if (down_chunks)
             CHIP_TRY(launch_residual_rmsnorm_rows(m->gemm_ws, down_chunks, down_sc, nullptr, m->hidden, rows, H, L.ln1,
@@ -862,9 +1011,14 @@ int enqueue_chunk(cheetah_hip_model *m, const uint32_t *tokens_dev, size_t rows,
         dn.ws_floats = m->gemm_ws_floats;
         dn.xh = m->ah;
         dn.xl = m->al;
-        dn.deferred = &down_chunks;
+        // A streamed layer's scales live in its feed slot, which is reused
+        // once the layer ends: its reduction runs inside the layer (the same
+        // chunk order, so the same bits).
+        dn.deferred = L.streamed() ? nullptr : &down_chunks;
+        down_chunks = 0;
         down_sc = L.down.scales();
         CHIP_TRY(launch_gemm(dn, s));
+        CHIP_TRY(layer_end(m, l, s));
     }
     if (down_chunks)
         CHIP_TRY(launch_residual_rmsnorm_rows(m->gemm_ws, down_chunks, down_sc, nullptr, m->hidden, rows, H, nullptr,
@@ -918,6 +1072,7 @@ int validate_decode(const cheetah_hip_model *m, uint32_t token, size_t offset, s
 int run_forward(cheetah_hip_model *m, const uint32_t *tokens, size_t n, size_t offset, size_t chunk_rows) {
     CHIP_TRY(check_model(m));
     CHIP_TRY(validate(m, tokens, n, offset));
+    CHIP_TRY(refresh_weights(m));
     if (chunk_rows == 0) chunk_rows = 256;
     chunk_rows = std::min(chunk_rows, m->sh->max_chunk);
     CHIP_TRY(reserve_positions(m, n));
@@ -939,6 +1094,34 @@ int run_forward(cheetah_hip_model *m, const uint32_t *tokens, size_t n, size_t o
     }
     m->len = offset + n;
     return 0;
+}
+
+// A per-layer linear weight's unit id -> (layer, matrix index of
+// Layer::mat); q, k and v all name the fused qkv matrix. False for every
+// other id (embedding, norms, biases, head, unknown names).
+bool parse_layer_unit(const Shared &sh, const char *id, uint32_t *layer, int *mat) {
+    static const char *const names[] = {"self_attn.q_proj.weight", "self_attn.k_proj.weight",
+                                        "self_attn.v_proj.weight", "self_attn.o_proj.weight",
+                                        "mlp.gate_proj.weight",    "mlp.up_proj.weight",
+                                        "mlp.down_proj.weight"};
+    static const int index[] = {0, 0, 0, 1, 2, 3, 4};
+    const std::string s(id), prefix = "model.layers.";
+    if (s.compare(0, prefix.size(), prefix) != 0) return false;
+    size_t end = prefix.size();
+    while (end < s.size() && s[end] >= '0' && s[end] <= '9') ++end;
+    const size_t digits = end - prefix.size();
+    if (digits == 0 || digits > 9 || end >= s.size() || s[end] != '.') return false;
+    if (digits > 1 && s[prefix.size()] == '0') return false;
+    const unsigned long l = std::stoul(s.substr(prefix.size(), digits));
+    if (l >= sh.cfg.num_layers) return false;
+    const std::string rest = s.substr(end + 1);
+    for (int i = 0; i < 7; ++i)
+        if (rest == names[i]) {
+            *layer = (uint32_t)l;
+            *mat = index[i];
+            return true;
+        }
+    return false;
 }
 
 int read_logits(cheetah_hip_model *m, float *logits_out) {
@@ -1060,6 +1243,7 @@ int cheetah_hip_decode_greedy(cheetah_hip_model *m, uint32_t token, size_t offse
     if (steps == 0) return 0;
     if (!tokens_out) return fail("HIP backend: null tokens_out.");
     CHIP_TRY(validate_decode(m, token, offset, steps));
+    CHIP_TRY(refresh_weights(m));
     CHIP_TRY(reserve_positions(m, steps));
     CHIP_TRY(write_step(m, token, offset));
     if (fused_fits(m, offset, steps)) CHIP_TRY(run_fused(m, offset, steps));
@@ -1077,6 +1261,7 @@ int cheetah_hip_time_decode(cheetah_hip_model *m, uint32_t token, size_t offset,
     CHIP_TRY(check_model(m));
     if (steps == 0 || !ms_per_step) return fail("HIP backend: time_decode needs steps and an output.");
     CHIP_TRY(validate_decode(m, token, offset, steps));
+    CHIP_TRY(refresh_weights(m));
     CHIP_TRY(reserve_positions(m, steps));
     CHIP_TRY(write_step(m, token, offset));
     hipEvent_t e0, e1;
@@ -1096,7 +1281,8 @@ int cheetah_hip_time_decode(cheetah_hip_model *m, uint32_t token, size_t offset,
     if (tokens_out)
         CHIP_CHECK(hipMemcpy(tokens_out, m->hist_dev + offset + 1, steps * sizeof(uint32_t), hipMemcpyDeviceToHost));
     m->len = offset + steps;
-    if (gemv_ms) {
+    if (gemv_ms && m->sh->host_mats) *gemv_ms = 0.f;  // the kernel alone needs every layer in HBM
+    if (gemv_ms && !m->sh->host_mats) {
         // The dominant GEMV of the step (gate/up, SwiGLU epilogue, fused norm)
         // timed alone on the same stream, cycling through the layers so each
         // launch streams weights that are not cache resident.
@@ -1124,6 +1310,70 @@ int cheetah_hip_time_decode(cheetah_hip_model *m, uint32_t token, size_t offset,
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
     return 0;
+}
+
+int cheetah_hip_evict_unit(cheetah_hip_model *m, const char *unit_id) {
+    CHIP_TRY(check_model(m));
+    if (!unit_id) return fail("HIP backend: null unit id.");
+    Shared &sh = *m->sh;
+    uint32_t l = 0;
+    int i = 0;
+    if (!parse_layer_unit(sh, unit_id, &l, &i)) return 0;
+    Layer &L = sh.layers[l];
+    if (L.host[i]) return 1;
+    WMat &w = L.mat(i);
+    // No kernel of any instance sharing these weights may still read them.
+    CHIP_CHECK(hipDeviceSynchronize());
+    uint8_t *h = nullptr;
+    CHIP_CHECK(hipHostMalloc((void **)&h, w.bytes(), hipHostMallocDefault));
+    const hipError_t e = hipMemcpy(h, w.base, w.bytes(), hipMemcpyDeviceToHost);
+    if (e != hipSuccess) {
+        (void)hipHostFree(h);
+        return fail(std::string("HIP backend: evict copy failed: ") + hipGetErrorString(e));
+    }
+    sh.mem.release((void *)w.base);
+    w.base = nullptr;
+    L.host[i] = h;
+    ++sh.host_mats;
+    ++sh.epoch;
+    return 1;
+}
+
+int cheetah_hip_page_in_unit(cheetah_hip_model *m, const char *unit_id, int32_t tier) {
+    (void)tier;  // every page-in lands in HBM
+    CHIP_TRY(check_model(m));
+    if (!unit_id) return fail("HIP backend: null unit id.");
+    Shared &sh = *m->sh;
+    uint32_t l = 0;
+    int i = 0;
+    if (!parse_layer_unit(sh, unit_id, &l, &i)) return 0;
+    Layer &L = sh.layers[l];
+    if (!L.host[i]) return 1;
+    WMat &w = L.mat(i);
+    // No feed copy may still read the host copy.
+    CHIP_CHECK(hipDeviceSynchronize());
+    uint8_t *d = nullptr;
+    CHIP_TRY(sh.mem.alloc(&d, w.bytes()));
+    const hipError_t e = hipMemcpy(d, L.host[i], w.bytes(), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        sh.mem.release(d);
+        return fail(std::string("HIP backend: page-in copy failed: ") + hipGetErrorString(e));
+    }
+    (void)hipHostFree(L.host[i]);
+    L.host[i] = nullptr;
+    w.base = d;
+    --sh.host_mats;
+    ++sh.epoch;
+    return 1;
+}
+
+int cheetah_hip_unit_tier(const cheetah_hip_model *m, const char *unit_id) {
+    CHIP_TRY(check_model(m));
+    if (!unit_id) return fail("HIP backend: null unit id.");
+    uint32_t l = 0;
+    int i = 0;
+    if (!parse_layer_unit(*m->sh, unit_id, &l, &i)) return 0;
+    return m->sh->layers[l].host[i] ? 2 : 1;
 }
 
 void cheetah_hip_clear_cache(cheetah_hip_model *m) {

@@ -84,6 +84,9 @@ SIGNATURES = {
     "cheetah_hip_restore_kv_prefix": (_c.c_int, [_VP, _VP, _SZ]),
     "cheetah_hip_snapshot_free": (None, [_VP]),
     "cheetah_hip_model_free": (None, [_VP]),
+    "cheetah_hip_evict_unit": (_c.c_int, [_VP, _c.c_char_p]),
+    "cheetah_hip_page_in_unit": (_c.c_int, [_VP, _c.c_char_p, _c.c_int32]),
+    "cheetah_hip_unit_tier": (_c.c_int, [_VP, _c.c_char_p]),
     "cheetah_hip_time_gemv": (_c.c_int, [_c.c_uint32, _c.POINTER(_VP), _SZ, _SZ, _SZ, _VP, _VP, _SZ, _F32P]),
     "cheetah_hip_time_decode": (_c.c_int, [_VP, _c.c_uint32, _SZ, _SZ, _F32P, _F32P, _U32P]),
     "cheetah_hip_time_gemm": (_c.c_int, [_c.c_uint32, _c.POINTER(_VP), _SZ, _SZ, _SZ, _VP, _SZ, _VP, _SZ, _F32P]),
@@ -380,6 +383,31 @@ class HipForward:
     def restore_kv_prefix(self, snapshot: Snapshot, positions: int) -> bool:
         check(lib().cheetah_hip_restore_kv_prefix(self._h, snapshot._h, positions))
         return True
+
+    def page_in_unit(self, unit_id: str, tier: int = 0) -> bool:
+        """AntTierControl::page_in_unit (registry.rs:89): moves a per-layer
+        linear weight back into HBM; True when the id names one (tier is
+        ignored, as every reference implementation ignores it)."""
+        rc = lib().cheetah_hip_page_in_unit(self._h, unit_id.encode(), int(tier))
+        if rc < 0:
+            raise HipError(_err())
+        return rc == 1
+
+    def evict_unit(self, unit_id: str) -> bool:
+        """AntTierControl::evict_unit (registry.rs:91): releases a per-layer
+        linear weight's HBM buffer, keeping a pinned host copy that forwards
+        stream one layer ahead; True when the id names one."""
+        rc = lib().cheetah_hip_evict_unit(self._h, unit_id.encode())
+        if rc < 0:
+            raise HipError(_err())
+        return rc == 1
+
+    def unit_tier(self, unit_id: str) -> int:
+        """1 = HBM, 2 = pinned host memory, 0 = not a movable unit."""
+        rc = lib().cheetah_hip_unit_tier(self._h, unit_id.encode())
+        if rc < 0:
+            raise HipError(_err())
+        return rc
 
     def close(self) -> None:
         if getattr(self, "_h", None) and _lib is not None:

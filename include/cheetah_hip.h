@@ -180,6 +180,32 @@ int cheetah_hip_restore_kv_prefix(cheetah_hip_model *m, const cheetah_hip_snapsh
 void cheetah_hip_snapshot_free(cheetah_hip_snapshot *s);
 void cheetah_hip_model_free(cheetah_hip_model *m);
 
+/* Ant tier control (AntTierControl::page_in_unit / evict_unit,
+ * registry.rs:87-93; called from engine.rs:1210-1226). The movable units
+ * are the per-layer linear weights, model.layers.{l}.self_attn.{q,k,v,o}_proj
+ * .weight and model.layers.{l}.mlp.{gate,up,down}_proj.weight; q, k and v
+ * name one fused matrix and move together.
+ *   evict:   the device buffer is released and a pinned host copy becomes
+ *            authoritative (vulkan/transformer.rs:578-583). Forwards keep
+ *            working: each such layer's matrices are copied into one of two
+ *            device slots on a second stream, one streamed layer ahead of
+ *            the compute, with the same kernels reading them there (results
+ *            are bit-identical). While any unit is evicted, decode runs the
+ *            per-kernel path (no persistent kernel, no captured graph).
+ *   page_in: the unit returns to HBM and its host copy is freed; `tier` is
+ *            accepted and ignored, as every reference implementation does
+ *            (vulkan/transformer.rs:572-576).
+ * Both return 1 when the id names a movable unit (also when it already sits
+ * in the requested tier), 0 for any other id, -1 on error. They wait for the
+ * device to go idle and change weights shared with every clone: they must
+ * not overlap a forward on any instance sharing them. */
+int cheetah_hip_evict_unit(cheetah_hip_model *m, const char *unit_id);
+int cheetah_hip_page_in_unit(cheetah_hip_model *m, const char *unit_id, int32_t tier);
+/* Where a unit sits: 1 = HBM, 2 = pinned host memory, 0 = not a movable
+ * unit, -1 on error. Has no reference counterpart (the reference's Ant
+ * bookkeeping tracks tiers on the engine side); for tests and monitoring. */
+int cheetah_hip_unit_tier(const cheetah_hip_model *m, const char *unit_id);
+
 /* ------------------------------------------------------------------------
  * Measurement hooks (events on the stream the kernels run on).
  * ---------------------------------------------------------------------- */
