@@ -61,6 +61,36 @@ def cpu_baseline(shape, weights, prompt, decode_steps: int):
     }
 
 
+def host_tier(g, shape, prompt, resident_tokens, decode_steps: int = 32):
+    """One generation with every layer's linear weights evicted to pinned
+    host memory (Ant tier control, engine.rs:1210-1226): each forward streams
+    all layers' matrices over PCIe into the feed slots, so this is the
+    host-to-device copy rate, not an HBM figure. Pages everything back in."""
+    names = ["self_attn.q_proj", "self_attn.o_proj", "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj"]
+    units = [f"model.layers.{l}.{n}.weight" for l in range(shape.num_layers) for n in names]
+    for u in units:
+        assert g.evict_unit(u), u
+    g.clear_cache()
+    t0 = time.perf_counter()
+    first = g.forward_greedy(prompt, 0, chunk_rows=CHUNK)
+    t1 = time.perf_counter()
+    rest = g.decode_greedy(first, len(prompt), decode_steps)
+    t2 = time.perf_counter()
+    toks = [first] + rest.tolist()
+    for u in units:
+        assert g.page_in_unit(u, 0), u
+    streamed = shape.linear_params() * 2  # BF16 bytes of every layer's matrices
+    dec_s = (t2 - t1) / decode_steps
+    return {
+        "layers_on_host": shape.num_layers,
+        "streamed_bytes_per_forward": streamed,
+        "decode_tok_s": round(1.0 / dec_s, 2),
+        "prefill_tok_s": round(len(prompt) / (t1 - t0), 1),
+        "h2d_gbps_decode": round(streamed / dec_s / 1e9, 1),
+        "tokens_match_resident": toks == resident_tokens[:decode_steps + 1],
+    }
+
+
 def _golden(name):
     path = os.path.join(ROOT, "tests", "golden", name)
     if not os.path.exists(path):
@@ -140,6 +170,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--cpu-decode-steps", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-residency", action="store_true",
+                    help="skip the host-tier (evicted weights) generation")
     ap.add_argument("--no-ops", action="store_true",
                     help="skip the op-level attention / GEMV / GEMM measurements")
     ap.add_argument("--workload", default="qwen2-0.5b", choices=["qwen2-0.5b", "llama3-8b-q4", "qwen2-7b-32k"],
@@ -283,6 +315,8 @@ def main() -> int:
             "avg_launch_ms": round(gemv_ms, 5),
         },
     }
+    if not args.no_residency:
+        result["host_tier"] = host_tier(g, shape, prompt, tokens)
     if not args.no_ops:
         from cheetah_amd import opbench
 

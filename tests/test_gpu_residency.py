@@ -140,3 +140,32 @@ def test_page_in_restores_the_persistent_decode(hip, monkeypatch):
     assert got[1] == want[1]
     assert np.array_equal(bits(got[2]), bits(want[2]))
     g.close()
+
+
+@pytest.mark.parametrize("quant", [None, "q8"])
+def test_prepared_dir_with_ant_plan(hip, tmp_path, quant, monkeypatch):
+    """A prepared directory (units manifest + safetensors shards + config.json)
+    loads into the same model as the in-memory weights, and an Ant plan that
+    places a layer in RAM starts it evicted with the same logits."""
+    from cheetah_amd import prepared
+    monkeypatch.setenv("CHEETAH_HIP_FUSED", "0")
+    shape = configs.TINY_LLAMA
+    w = weights(shape)
+    prepared.write_prepared(str(tmp_path), w, prepared.hf_config(shape), shards=2)
+    prompt = synth.make_tokens(shape.vocab_size, 90, seed=23)
+    kw = dict(quant=quant, kv_capacity=512, max_chunk_rows=64)
+    ref = hip.HipForward(shape, w, **kw)
+    want = run(ref, prompt, 16, 64)
+    ref.close()
+    plan = {unit(1, n): "ram" for n in ALL}
+    plan[unit(0, "mlp.up_proj")] = "vram"
+    for p in (None, plan):
+        g = prepared.load(str(tmp_path), plan=p, **kw)
+        assert g.shape.replace(name=shape.name) == shape
+        assert g.unit_tier(unit(1, "mlp.down_proj")) == (2 if p else 1)
+        assert g.unit_tier(unit(0, "mlp.up_proj")) == 1
+        got = run(g, prompt, 16, 64)
+        assert np.array_equal(bits(got[0]), bits(want[0]))
+        assert got[1] == want[1]
+        assert np.array_equal(bits(got[2]), bits(want[2]))
+        g.close()
