@@ -230,7 +230,13 @@ __global__ __launch_bounds__(kAThreads) void gemv_aligned_kernel(Args a, int P) 
     using U = Unit<FMT, 16>;
     constexpr int E = U::E;
     constexpr int D = 4;
-    constexpr int UNROLL = 2;
+    // Units per lane per iteration. A Q4 row is half the bytes of a Q8 row, so
+    // two units per lane would cover a whole 4096-column row in one
+    // iteration: every wave would load, then compute, with nothing to
+    // overlap. One unit leaves a second iteration whose loads fly during the
+    // first one's FMAs (measured 8-17 % faster on 4096-14336-wide rows). A
+    // lane's units are taken in the same order either way.
+    constexpr int UNROLL = FMT == FMT_Q4 ? 1 : 2;
     constexpr int GPB = kAWaves / KS;
     constexpr int STEP = 64 * KS * UNROLL;
     constexpr int NM = DUAL ? 2 : 1;
