@@ -225,18 +225,11 @@ constexpr int kPad = 32;  // zero floats before and after x in LDS
 constexpr int kAThreads = 512;  // 8 waves share one x staging
 constexpr int kAWaves = kAThreads / 64;
 
-template <int FMT, int R, int KS, bool NORM, bool DUAL>
+template <int FMT, int R, int KS, bool NORM, bool DUAL, int UNROLL>
 __global__ __launch_bounds__(kAThreads) void gemv_aligned_kernel(Args a, int P) {
     using U = Unit<FMT, 16>;
     constexpr int E = U::E;
     constexpr int D = 4;
-    // Units per lane per iteration. A Q4 row is half the bytes of a Q8 row, so
-    // two units per lane would cover a whole 4096-column row in one
-    // iteration: every wave would load, then compute, with nothing to
-    // overlap. One unit leaves a second iteration whose loads fly during the
-    // first one's FMAs (measured 8-17 % faster on 4096-14336-wide rows). A
-    // lane's units are taken in the same order either way.
-    constexpr int UNROLL = FMT == FMT_Q4 ? 1 : 2;
     constexpr int GPB = kAWaves / KS;
     constexpr int STEP = 64 * KS * UNROLL;
     constexpr int NM = DUAL ? 2 : 1;
@@ -516,12 +509,12 @@ int aligned_blocks_per_cu(Kern kern, size_t lds) {
     return std::max(1, std::min(by_waves, by_lds));
 }
 
-template <int FMT, int R, int KS, bool NORM, bool DUAL>
+template <int FMT, int R, int KS, bool NORM, bool DUAL, int UNROLL>
 int launch_aligned(const Args &a, int P, hipStream_t s) {
     constexpr int GPB = kAWaves / KS;
     const int groups = (a.rows + R * P - 1) / (R * P) * P;
     const size_t lds = (size_t)(a.K + 2 * kPad) * sizeof(float) + (NORM ? (size_t)a.K * 2 + 16 : 0);
-    auto kern = gemv_aligned_kernel<FMT, R, KS, NORM, DUAL>;
+    auto kern = gemv_aligned_kernel<FMT, R, KS, NORM, DUAL, UNROLL>;
     const int cap = device_cus() * aligned_blocks_per_cu(kern, lds);
     const int blocks = std::max(1, std::min((groups + GPB - 1) / GPB, cap));
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(kAThreads), lds, s, a, P);
@@ -529,14 +522,26 @@ int launch_aligned(const Args &a, int P, hipStream_t s) {
     return 0;
 }
 
-template <int FMT, int R, bool NORM, bool DUAL>
-int pick_ks(const Args &a, int P, int ks, hipStream_t s) {
+template <int FMT, int R, bool NORM, bool DUAL, int UNROLL>
+int pick_ks_un(const Args &a, int P, int ks, hipStream_t s) {
     switch (ks) {
-        case 8: return launch_aligned<FMT, R, 8, NORM, DUAL>(a, P, s);
-        case 4: return launch_aligned<FMT, R, 4, NORM, DUAL>(a, P, s);
-        case 2: return launch_aligned<FMT, R, 2, NORM, DUAL>(a, P, s);
-        default: return launch_aligned<FMT, R, 1, NORM, DUAL>(a, P, s);
+        case 8: return launch_aligned<FMT, R, 8, NORM, DUAL, UNROLL>(a, P, s);
+        case 4: return launch_aligned<FMT, R, 4, NORM, DUAL, UNROLL>(a, P, s);
+        case 2: return launch_aligned<FMT, R, 2, NORM, DUAL, UNROLL>(a, P, s);
+        default: return launch_aligned<FMT, R, 1, NORM, DUAL, UNROLL>(a, P, s);
     }
+}
+
+// Units per lane per iteration (UNROLL). With two, a row of up to ~1,000
+// 16-byte units (a 4096-column Q4 row is 128) takes one or two iterations:
+// the waves load, then compute, with little to overlap. One unit per
+// iteration puts the next unit's loads in flight during the current FMAs:
+// measured 3-17 % faster on such rows, 3-14 % slower on 18,944-column BF16 /
+// Q8 rows. A lane takes its units in the same order either way (same bits).
+template <int FMT, int R, bool NORM, bool DUAL>
+int pick_ks(const Args &a, int P, int ks, int n_units, hipStream_t s) {
+    if (n_units / ks <= 1024) return pick_ks_un<FMT, R, NORM, DUAL, 1>(a, P, ks, s);
+    return pick_ks_un<FMT, R, NORM, DUAL, 2>(a, P, ks, s);
 }
 
 // Rows per wave (R) and waves per row group (KS, splitting K), as measured
@@ -556,10 +561,10 @@ int pick_aligned(const Args &a, int P, hipStream_t s) {
     while (ks < 8 && groups * ks < slots && n_units >= 64 * 2 * ks * 2) ks *= 2;
     if constexpr (FMT == FMT_Q4) {
         if constexpr (!DUAL)
-            if (R == 4) return pick_ks<FMT, 4, NORM, DUAL>(a, P, ks, s);
-        if (R == 2) return pick_ks<FMT, 2, NORM, DUAL>(a, P, ks, s);
+            if (R == 4) return pick_ks<FMT, 4, NORM, DUAL>(a, P, ks, n_units, s);
+        if (R == 2) return pick_ks<FMT, 2, NORM, DUAL>(a, P, ks, n_units, s);
     }
-    return pick_ks<FMT, 1, NORM, DUAL>(a, P, ks, s);
+    return pick_ks<FMT, 1, NORM, DUAL>(a, P, ks, n_units, s);
 }
 
 template <int FMT>
