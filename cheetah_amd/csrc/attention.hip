@@ -47,18 +47,6 @@ struct AttnArgs {
     float *out;
 };
 
-// Eight consecutive K or V elements of one row as f32.
-__device__ __forceinline__ void load8(const uint16_t *p, float (&f)[8]) {
-    const u32x4 w = *(const u32x4 *)p;
-    f[0] = bf16_lo(w[0]); f[1] = bf16_hi(w[0]); f[2] = bf16_lo(w[1]); f[3] = bf16_hi(w[1]);
-    f[4] = bf16_lo(w[2]); f[5] = bf16_hi(w[2]); f[6] = bf16_lo(w[3]); f[7] = bf16_hi(w[3]);
-}
-__device__ __forceinline__ void load8(const float *p, float (&f)[8]) {
-    const f32x4 a = *(const f32x4 *)p, b = *(const f32x4 *)(p + 4);
-    f[0] = a[0]; f[1] = a[1]; f[2] = a[2]; f[3] = a[3];
-    f[4] = b[0]; f[5] = b[1]; f[6] = b[2]; f[7] = b[3];
-}
-
 // Eight consecutive K or V elements as loaded (converted to f32 at use), so
 // a whole tile can be in flight while the previous one computes.
 template <class KT>

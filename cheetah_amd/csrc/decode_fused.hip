@@ -117,7 +117,6 @@ __device__ __forceinline__ void st_u16(void *p, uint32_t v) {
 }
 __device__ __forceinline__ void stt(uint64_t *p, uint32_t bits, unsigned tag) { st_u64(p, ((uint64_t)tag << 32) | bits); }
 __device__ __forceinline__ void stf(uint64_t *p, float v, unsigned tag) { stt(p, __float_as_uint(v), tag); }
-__device__ __forceinline__ unsigned tag_of(uint64_t w) { return (unsigned)(w >> 32); }
 __device__ __forceinline__ float val_of(uint64_t w) { return __uint_as_float((uint32_t)w); }
 
 __device__ __forceinline__ void st_kv(uint16_t *p, float v) { st_u16(p, f32_bf16_rne(v)); }
