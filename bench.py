@@ -9,6 +9,12 @@ with argmax on the device). `value` is decode tokens/s of the whole job;
 prefill tokens/s, the decode step's effective HBM rate and the dominant
 kernel's roofline are reported beside it, with the CPU oracle (a C++
 restatement of the reference's native AVX2 backend) timed on this host.
+
+Beside it: the same generation through the per-step ModelForward::forward
+path (logits to the host), with the reference's f32 KV cache, the greedy
+ids against the oracle's goldens (BF16-KV run and reference semantics), the
+Llama-3-8B Q4 (8K prompt) and Qwen2-7B (32K prompt, prefix reuse) decoders
+as `large`, and the op-level attention / GEMV / GEMM figures as `ops`.
 """
 from __future__ import annotations
 
@@ -32,14 +38,46 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+def host_cpus():
+    """The host cores this process may run on: the CPU model, the logical
+    CPUs in its affinity mask and the physical cores they belong to (sysfs
+    core_id per package). The reference sizes its pool to physical cores
+    (num_cpus::get_physical, engine.rs:859)."""
+    logical = sorted(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else list(range(os.cpu_count() or 1))
+    cores = set()
+    for c in logical:
+        base = f"/sys/devices/system/cpu/cpu{c}/topology/"
+        try:
+            with open(base + "physical_package_id") as f:
+                pkg = f.read().strip()
+            with open(base + "core_id") as f:
+                core = f.read().strip()
+            cores.add((pkg, core))
+        except OSError:
+            cores.add(("?", str(c)))
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "logical_cpus": len(logical), "physical_cores": len(cores),
+            "machine_logical_cpus": os.cpu_count()}
+
+
 def cpu_baseline(shape, weights, prompt, decode_steps: int):
     """The CPU oracle on a bounded sample of the same workload: the full
-    512-token prefill (128-row chunks) and `decode_steps` greedy decodes."""
+    512-token prefill (128-row chunks) and `decode_steps` greedy decodes, on
+    a pool of one thread per physical core this process may use."""
     import numpy as np
 
     from oracle import oracle
 
-    threads = max(1, min(16, os.cpu_count() or 1))
+    cpus = host_cpus()
+    threads = max(1, cpus["physical_cores"])
     oracle.set_threads(threads)
     m = oracle.RefModel(shape, weights)
     t0 = time.perf_counter()
@@ -56,8 +94,13 @@ def cpu_baseline(shape, weights, prompt, decode_steps: int):
         "kind": "port",
         "sample": f"decode tok/s over {decode_steps} greedy steps after the full {PROMPT}-token prefill "
                   f"(prefill {PROMPT / (t1 - t0):.1f} tok/s); C++ restatement of the reference native "
-                  f"AVX2 path, {threads} threads",
+                  f"AVX2 path, one thread per physical core ({threads})",
         "prefill_tok_s": round(PROMPT / (t1 - t0), 3),
+        "threads": threads,
+        "cores_physical": cpus["physical_cores"],
+        "logical_cpus": cpus["logical_cpus"],
+        "machine_logical_cpus": cpus["machine_logical_cpus"],
+        "cpu_model": cpus["cpu_model"],
     }
 
 
@@ -99,14 +142,34 @@ def _golden(name):
         return json.load(f)
 
 
-def large_workload(args) -> int:
+LARGE = {
+    "llama3-8b-q4": ("llama3-8b architecture (32 layers, hidden 4096, 32/8 heads, hd 128, ffn 14336, vocab 128256), "
+                     "Q4 linears quantized on the device from seeded BF16 weights, BF16 head, BF16 paged KV; "
+                     "8192-token prompt in 512-row chunks, then 256 greedy decode steps, batch 1"),
+    "qwen2-7b-32k": ("qwen2-7b architecture (28 layers, hidden 3584, 28/4 heads, hd 128, ffn 18944, vocab 152064), "
+                     "BF16 weights and paged KV; turn 1: 32768-token prompt in 1024-row chunks + KV snapshot; "
+                     "turn 2: restore 30720 positions, 2048-token suffix in 1024-row chunks, 128 greedy decodes"),
+}
+MFMA_PEAK_TFLOPS = 2500.0
+
+
+def _match32(tokens, gold):
+    if gold is None:
+        return None
+    n = min(32, len(gold["tokens"]))
+    return tokens[:n] == gold["tokens"][:n]
+
+
+def measure_large(name: str) -> dict:
     """One timed pass of a large decoder (no warmup: each phase is long and
-    the kernels are already built); decode tok/s is `value`."""
+    the kernels are already built). Decode tok/s with the device's BF16 KV
+    cache, prefill tok/s, their roofline fractions, and the greedy ids
+    against the oracle's goldens: the BF16-KV run and the reference
+    semantics (f32 KV)."""
     from cheetah_amd import configs, hip, workloads
 
     hip.init(0)
-    MFMA_PEAK = 2500.0
-    if args.workload == "llama3-8b-q4":
+    if name == "llama3-8b-q4":
         shape = configs.LLAMA3_8B
         g, info = workloads.llama3_8b_q4(decode_steps=256)
         lin_bytes = sum(hip.buffer_bytes("q4", r, c) for layer in range(shape.num_layers)
@@ -115,10 +178,8 @@ def large_workload(args) -> int:
         ctx_mid = 8192 + 128
         pre_flops = sum(workloads.prefill_flops(shape, 512, off) for off in range(0, 8192, 512))
         pre_s = info["prefill_s"]
-        gold = _golden("llama3_8b_q4_bf16kv_greedy.json")
-        workload = ("llama3-8b architecture (32 layers, hidden 4096, 32/8 heads, hd 128, ffn 14336, vocab 128256), "
-                    "Q4 linears quantized on the device from seeded BF16 weights, BF16 head, BF16 paged KV; "
-                    "8192-token prompt in 512-row chunks, then 256 greedy decode steps, batch 1")
+        gold_bf16 = _golden("llama3_8b_q4_bf16kv_greedy.json")
+        gold_ref = _golden("llama3_8b_q4_greedy.json")
         extra = {"prefill_tok_s": info["prefill_tok_s"]}
     else:
         shape = configs.QWEN2_7B
@@ -127,38 +188,44 @@ def large_workload(args) -> int:
         ctx_mid = 32768 + 64
         pre_flops = sum(workloads.prefill_flops(shape, 1024, off) for off in range(0, 32768, 1024))
         pre_s = info["turn1_prefill_s"]
-        gold = _golden("qwen2_7b_32k_greedy.json")
-        workload = ("qwen2-7b architecture (28 layers, hidden 3584, 28/4 heads, hd 128, ffn 18944, vocab 152064), "
-                    "BF16 weights and paged KV; turn 1: 32768-token prompt in 1024-row chunks + KV snapshot; "
-                    "turn 2: restore 30720 positions, 2048-token suffix in 1024-row chunks, 128 greedy decodes")
-        extra = {"turn1_prefill_tok_s": info["turn1_prefill_tok_s"], "turn2_prefill_tok_s": info["turn2_prefill_tok_s"],
+        gold_bf16 = _golden("qwen2_7b_32k_greedy.json")
+        gold_ref = _golden("qwen2_7b_32k_f32kv_greedy.json")
+        extra = {"prefill_tok_s": info["turn1_prefill_tok_s"], "turn2_prefill_tok_s": info["turn2_prefill_tok_s"],
                  "snapshot_s": info["snapshot_s"], "restore_s": info["restore_s"]}
+    g.close()
     step_bytes = workloads.decode_bytes(shape, ctx_mid, weight_bytes)
     ms_tok = 1e3 / info["decode_tok_s"]
     gbps = step_bytes / (ms_tok * 1e-3) / 1e9
     tflops = pre_flops / pre_s / 1e12
-    match = None
-    if gold is not None:
-        n = min(32, len(gold["tokens"]))
-        match = info["tokens"][:n] == gold["tokens"][:n]
-    result = {
-        "metric": METRIC, "value": info["decode_tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": 1, "warmup": 0,
-        "ms_per_step": round((info.get("prefill_s", 0) + info.get("turn1_prefill_s", 0) + info.get("turn2_prefill_s", 0)
-                              + info["decode_s"]) * 1e3, 3),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "q4 weights, bf16 activations" if args.workload == "llama3-8b-q4" else "bf16",
-        "data": "synthetic: seeded random-init weights (normal 0.02), seeded uniform token ids",
-        "config": {"workload": workload, "global_batch": 1, "parallelism": "none (1 GPU)"},
+    return {
+        "workload": LARGE[name],
+        "decode_tok_s": info["decode_tok_s"],
         **extra,
+        "wall_ms": round((info.get("prefill_s", 0) + info.get("turn1_prefill_s", 0) + info.get("turn2_prefill_s", 0)
+                          + info["decode_s"]) * 1e3, 3),
         "decode_ms_per_token": round(ms_tok, 4),
         "decode_effective_gbps": round(gbps, 1), "decode_hbm_roofline_frac": round(gbps / HBM_PEAK_GBPS, 4),
         "decode_bytes_per_token": int(step_bytes),
-        "prefill_tflops": round(tflops, 2), "prefill_mfma_frac": round(tflops / MFMA_PEAK, 4),
+        "prefill_tflops": round(tflops, 2), "prefill_mfma_frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
         "prefill_flops": pre_flops,
-        "greedy_first32_match_golden": match,
+        "kv_cache": "bf16",
+        "greedy_first32_match_bf16kv_oracle": _match32(info["tokens"], gold_bf16),
+        "greedy_first32_match_reference": _match32(info["tokens"], gold_ref),
         "load": {"synth_s": info.get("synth_s"), "upload_s": info.get("upload_s")},
     }
-    g.close()
+
+
+def large_workload(args) -> int:
+    """The large decoder's own line: decode tok/s is `value`."""
+    r = measure_large(args.workload)
+    result = {
+        "metric": METRIC, "value": r["decode_tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": 1, "warmup": 0,
+        "ms_per_step": r["wall_ms"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q4 weights, bf16 activations" if args.workload == "llama3-8b-q4" else "bf16",
+        "data": "synthetic: seeded random-init weights (normal 0.02), seeded uniform token ids",
+        "config": {"workload": r["workload"], "global_batch": 1, "parallelism": "none (1 GPU)"},
+        **{k: v for k, v in r.items() if k not in ("workload", "decode_tok_s", "wall_ms")},
+    }
     print(json.dumps(result), flush=True)
     return 0
 
@@ -174,6 +241,8 @@ def main() -> int:
                     help="skip the host-tier (evicted weights) generation")
     ap.add_argument("--no-ops", action="store_true",
                     help="skip the op-level attention / GEMV / GEMM measurements")
+    ap.add_argument("--no-large", action="store_true",
+                    help="skip the Llama-3-8B Q4 and Qwen2-7B 32K sub-measurements")
     ap.add_argument("--workload", default="qwen2-0.5b", choices=["qwen2-0.5b", "llama3-8b-q4", "qwen2-7b-32k"],
                     help="qwen2-0.5b (the headline line); the two large decoders print their own line")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -262,12 +331,47 @@ def main() -> int:
         with open(tpath) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
 
-    golden_ok = None
-    gpath = os.path.join(ROOT, "tests", "golden", "qwen2_0_5b_bf16kv_greedy.json")
-    if os.path.exists(gpath):
-        with open(gpath) as f:
-            gold = json.load(f)["tokens"]
-        golden_ok = tokens[:32] == gold[:32]
+    gold_bf16 = _golden("qwen2_0_5b_bf16kv_greedy.json")
+    gold_ref = _golden("qwen2_0_5b_greedy.json")
+    departure = None
+    if gold_ref is not None:
+        departure = next((i for i in range(min(len(tokens), len(gold_ref["tokens"])))
+                          if tokens[i] != gold_ref["tokens"][i]), None)
+
+    # The ModelForward contract path: one cheetah_hip_forward per decode step
+    # returning the vocabulary's logits to the host, greedy argmax on the host
+    # (ties to the last index), as Engine::generate_inner samples
+    # (engine.rs:1918-1935, 2247-2253).
+    def per_step_generation():
+        g.clear_cache()
+        logits = g.forward(prompt, 0, chunk_rows=CHUNK)
+        out = []
+        t0 = time.perf_counter()
+        for step in range(DECODE):
+            tok = int(len(logits) - 1 - np.argmax(logits[::-1]))
+            out.append(tok)
+            logits = g.forward(np.array([tok], np.uint32), PROMPT + step)
+        return time.perf_counter() - t0, out
+
+    per_step_generation()
+    ps_s, ps_tokens = per_step_generation()
+    log("[bench] per-step forward path timed")
+
+    # The reference's own KV precision (f32 cache): decode rate and token
+    # identity with the reference's greedy ids.
+    g32 = hip.HipForward(shape, weights, kv_capacity=2048, max_chunk_rows=CHUNK, kv="f32")
+
+    def generation32():
+        g32.clear_cache()
+        first = g32.forward_greedy(prompt, 0, chunk_rows=CHUNK)
+        t1 = time.perf_counter()
+        rest = g32.decode_greedy(first, PROMPT, DECODE)
+        return time.perf_counter() - t1, [first] + rest.tolist()
+
+    generation32()
+    f32_s, f32_tokens = generation32()
+    g32.close()
+    log("[bench] f32-KV generation timed")
 
     result = {
         "metric": METRIC,
@@ -295,7 +399,20 @@ def main() -> int:
         "decode_event_ms_per_token": round(ms_step, 4),
         "decode_effective_gbps": round(step_bytes / (ms_step * 1e-3) / 1e9, 1),
         "decode_hbm_roofline_frac": round(step_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-        "greedy_first32_match_golden": golden_ok,
+        "kv_cache": "bf16",
+        "greedy_first32_match_bf16kv_oracle": _match32(tokens, gold_bf16),
+        "greedy_first32_match_reference": _match32(tokens, gold_ref),
+        "reference_departure": None if departure is None else {
+            "step": departure, "reference_top2_margin": round(gold_ref["top2_margins"][departure], 5)},
+        "f32_kv": {
+            "decode_tok_s": round(DECODE / f32_s, 2),
+            "greedy_first32_match_reference": _match32(f32_tokens, gold_ref),
+        },
+        "forward_per_step": {
+            "path": "cheetah_hip_forward per decode step, logits to the host, host argmax (ModelForward::forward)",
+            "decode_tok_s": round(DECODE / ps_s, 2),
+            "tokens_match_device_greedy": ps_tokens == tokens[:DECODE],
+        },
         "roofline": {
             "kernel": f"decode_flow_kernel (persistent decode: {DECODE} steps per launch, BF16 weights, "
                       "BF16 paged KV)",
@@ -317,6 +434,12 @@ def main() -> int:
     }
     if not args.no_residency:
         result["host_tier"] = host_tier(g, shape, prompt, tokens)
+    if not args.no_large:
+        g.close()
+        result["large"] = {}
+        for name in LARGE:
+            log(f"[bench] {name} ...")
+            result["large"][name.replace("-", "_")] = measure_large(name)
     if not args.no_ops:
         from cheetah_amd import opbench
 

@@ -244,16 +244,29 @@ int cheetah_hip_dequant_q4(const uint8_t *w, size_t rows, size_t cols, float *ou
 static int attention_op(const float *q, const cheetah_hip_kv_view *kv, uint32_t q_heads, size_t rows, size_t offset,
                         float *out);
 
+// Argument checks of the attention entry points, made before any device call
+// (the split count below divides by kv_heads).
+static int check_attention_args(const float *q, const cheetah_hip_kv_view *kv, uint32_t q_heads, size_t rows,
+                                const float *out) {
+    if (!q || !kv || !out) return fail("HIP backend: attention with a null pointer.");
+    if (rows == 0) return fail("HIP backend: attention needs at least one query row.");
+    if (kv->kv_heads == 0 || q_heads == 0 || q_heads % kv->kv_heads)
+        return fail("HIP backend: q_heads must be a multiple of kv_heads.");
+    if (kv->head_dim == 0 || kv->page_size == 0)
+        return fail("HIP backend: attention needs a non-zero head_dim and page size.");
+    return 0;
+}
+
 int cheetah_hip_attention(const float *q, const cheetah_hip_kv_view *kv, uint32_t q_heads, size_t rows,
                           size_t offset, float *out) {
+    CHIP_TRY(check_attention_args(q, kv, q_heads, rows, out));
     CHIP_TRY(ensure_ready());
     return attention_op(q, kv, q_heads, rows, offset, out);
 }
 
 static int attention_op(const float *q, const cheetah_hip_kv_view *kv, uint32_t q_heads, size_t rows, size_t offset,
                         float *out) {
-    if (!q || !kv || !out) return fail("HIP backend: attention with a null pointer.");
-    if (rows == 0) return fail("HIP backend: attention needs at least one query row.");
+    CHIP_TRY(check_attention_args(q, kv, q_heads, rows, out));
     static thread_local float *part = nullptr;
     static thread_local size_t part_floats = 0;
     AttnJob j;

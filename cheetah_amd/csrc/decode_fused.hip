@@ -164,15 +164,25 @@ __device__ __forceinline__ void bar() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_
 
 // 16 bytes per lane from global memory straight into LDS at lds + 16 * lane
 // (lds the same in every lane), device-coherent (sc1). The low 32 bits of a
-// generic pointer into LDS are the LDS byte address. m0 is a reserved register
-// the compiler does not let an asm clobber list claim (it warns and drops the
-// entry); this is sound only because no compiler-generated code in this file
-// uses m0 (the built kernels reference it only inside these asm blocks), so
-// compiler-managed LDS DMA must not be mixed into this kernel.
+// generic pointer into LDS are the LDS byte address. The copy takes its LDS
+// base from m0, a register the compiler reserves (an asm clobber list cannot
+// claim it), so the block saves m0 into a scalar temporary and restores it
+// after the copy has issued: whatever value compiler-generated code keeps in
+// m0 survives. (The compiler's own global_load_lds builtin would manage m0,
+// but it makes every later LDS read wait for all vector loads in flight,
+// weight rows included.)
 __device__ __forceinline__ void dma16(const void *g, const void *lds) {
     const uint32_t l = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off sc1" ::"v"(g), "s"(l)
-                 : "memory", "m0");
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, off sc1\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(g), "s"(l)
+        : "memory");
 }
 __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 

@@ -679,13 +679,29 @@ int reserve_positions(cheetah_hip_model *m, size_t n) {
         return fail("HIP backend: KV cache capacity of " + std::to_string(sh.kv_capacity) +
                     " positions exceeded (needs " + std::to_string(end) + ").");
     bool changed = false;
+    // Shared pages this instance copied away from. Each keeps this instance's
+    // reference until the copies reading it have finished: released earlier,
+    // another holder could see itself as the only one and write the page in
+    // place while the copy still reads it.
+    std::vector<int> copied_from;
+    auto release_copied = [&]() {
+        if (copied_from.empty()) return hipSuccess;
+        const hipError_t e = hipStreamSynchronize(m->stream);
+        if (e == hipSuccess)
+            for (int p : copied_from) sh.page_unref(p);
+        copied_from.clear();
+        return e;
+    };
     const size_t first = m->len / kPageSize, last = (end - 1) / kPageSize;
     for (size_t lp = first; lp <= last; ++lp) {
         if (lp < m->pages.size()) {
             const int p = m->pages[lp];
             if (sh.page_refs(p) > 1) {  // copy on write
                 const int np = sh.page_alloc();
-                if (np < 0) return fail("HIP backend: KV page pool exhausted.");
+                if (np < 0) {
+                    CHIP_CHECK(release_copied());
+                    return fail("HIP backend: KV page pool exhausted.");
+                }
                 for (auto &L : sh.layers) {
                     const size_t pb = sh.page_bytes();
                     uint8_t *k = (uint8_t *)L.kv.k, *v = (uint8_t *)L.kv.v;
@@ -694,13 +710,16 @@ int reserve_positions(cheetah_hip_model *m, size_t n) {
                     CHIP_CHECK(hipMemcpyAsync(v + (size_t)np * pb, v + (size_t)p * pb, pb, hipMemcpyDeviceToDevice,
                                               m->stream));
                 }
-                sh.page_unref(p);
+                copied_from.push_back(p);
                 m->pages[lp] = np;
                 changed = true;
             }
         } else {
             const int np = sh.page_alloc();
-            if (np < 0) return fail("HIP backend: KV page pool exhausted.");
+            if (np < 0) {
+                CHIP_CHECK(release_copied());
+                return fail("HIP backend: KV page pool exhausted.");
+            }
             m->pages.push_back(np);
             changed = true;
         }
@@ -711,6 +730,7 @@ int reserve_positions(cheetah_hip_model *m, size_t n) {
                                   hipMemcpyHostToDevice, m->stream));
         CHIP_CHECK(hipStreamSynchronize(m->stream));  // page_host is pageable
     }
+    CHIP_CHECK(release_copied());
     return 0;
 }
 
@@ -1432,6 +1452,49 @@ int cheetah_hip_restore_kv_prefix(cheetah_hip_model *m, const cheetah_hip_snapsh
         CHIP_CHECK(hipStreamSynchronize(m->stream));
     }
     m->len = keep;
+    return 0;
+}
+
+int cheetah_hip_kv_download(const cheetah_hip_model *m, uint32_t layer, size_t pos_begin, size_t n, float *k_out,
+                            float *v_out) {
+    CHIP_TRY(check_model(m));
+    const Shared &sh = *m->sh;
+    const cheetah_hip_config &c = sh.cfg;
+    if (layer >= c.num_layers) return fail("HIP backend: kv_download layer out of range.");
+    if (pos_begin > m->len || n > m->len - pos_begin)
+        return fail("HIP backend: kv_download range exceeds the cached length " + std::to_string(m->len) + ".");
+    if (n == 0) return 0;
+    if (!k_out || !v_out) return fail("HIP backend: kv_download with a null output.");
+    CHIP_CHECK(hipStreamSynchronize(m->stream));
+    const size_t hd = c.head_dim, kvh = c.kv_heads, eb = sh.kv_f32 ? 4 : 2;
+    const size_t pb = sh.page_bytes();
+    std::vector<uint8_t> page(pb);
+    const KvLayer &kv = sh.layers[layer].kv;
+    for (int which = 0; which < 2; ++which) {
+        const uint8_t *pool = (const uint8_t *)(which ? kv.v : kv.k);
+        float *out = which ? v_out : k_out;
+        for (size_t lp = pos_begin / kPageSize; lp <= (pos_begin + n - 1) / kPageSize; ++lp) {
+            CHIP_CHECK(hipMemcpy(page.data(), pool + (size_t)m->pages[lp] * pb, pb, hipMemcpyDeviceToHost));
+            const size_t p0 = std::max(pos_begin, lp * kPageSize);
+            const size_t p1 = std::min(pos_begin + n, (lp + 1) * kPageSize);
+            for (size_t p = p0; p < p1; ++p)
+                for (size_t h = 0; h < kvh; ++h) {
+                    const uint8_t *src = page.data() + ((h * kPageSize + p % kPageSize) * hd) * eb;
+                    float *dst = out + ((p - pos_begin) * kvh + h) * hd;
+                    for (size_t d = 0; d < hd; ++d) {
+                        uint32_t bits;
+                        if (eb == 4) {
+                            std::memcpy(&bits, src + d * 4, 4);
+                        } else {
+                            uint16_t b16;
+                            std::memcpy(&b16, src + d * 2, 2);
+                            bits = (uint32_t)b16 << 16;  // BF16 widening is exact
+                        }
+                        std::memcpy(dst + d, &bits, 4);
+                    }
+                }
+        }
+    }
     return 0;
 }
 

@@ -83,6 +83,7 @@ SIGNATURES = {
     "cheetah_hip_kv_snapshot": (_c.c_int, [_VP, _c.POINTER(_VP), _c.POINTER(_SZ)]),
     "cheetah_hip_restore_kv_prefix": (_c.c_int, [_VP, _VP, _SZ]),
     "cheetah_hip_snapshot_free": (None, [_VP]),
+    "cheetah_hip_kv_download": (_c.c_int, [_VP, _c.c_uint32, _SZ, _SZ, _F32P, _F32P]),
     "cheetah_hip_model_free": (None, [_VP]),
     "cheetah_hip_evict_unit": (_c.c_int, [_VP, _c.c_char_p]),
     "cheetah_hip_page_in_unit": (_c.c_int, [_VP, _c.c_char_p, _c.c_int32]),
@@ -383,6 +384,16 @@ class HipForward:
     def restore_kv_prefix(self, snapshot: Snapshot, positions: int) -> bool:
         check(lib().cheetah_hip_restore_kv_prefix(self._h, snapshot._h, positions))
         return True
+
+    def kv_rows(self, layer: int, pos_begin: int, n: int):
+        """Cached K and V of positions [pos_begin, pos_begin + n) of one
+        layer as f32 [n, kv_heads, head_dim] (the reference's cache rows)."""
+        shp = (n, self.shape.kv_heads, self.shape.head_dim)
+        k = np.empty(shp, np.float32)
+        v = np.empty(shp, np.float32)
+        check(lib().cheetah_hip_kv_download(self._h, layer, pos_begin, n, k.ctypes.data_as(_F32P),
+                                            v.ctypes.data_as(_F32P)))
+        return k, v
 
     def page_in_unit(self, unit_id: str, tier: int = 0) -> bool:
         """AntTierControl::page_in_unit (registry.rs:89): moves a per-layer

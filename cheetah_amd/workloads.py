@@ -5,9 +5,10 @@ optional prefix restore, chunked prompt forward, snapshot, greedy loop).
 * Llama-3-8B shape, Q4 linears (quantized on the device from the seeded BF16
   weights, bit-exact to q4.rs:126-161), BF16 embedding/head/norms: an
   8192-token prompt in 512-row chunks, then greedy decode.
-* Qwen2-7B shape, BF16 weights, BF16 KV: turn 1 a 32768-token prompt in
-  1024-row chunks and a KV snapshot; turn 2 restores the first 30720
-  positions, prefills a 2048-token suffix in 1024-row chunks, then decodes.
+* Qwen2-7B shape, BF16 weights, BF16 (or f32) KV: turn 1 a 32768-token
+  prompt in 1024-row chunks and a KV snapshot; turn 2 restores the first
+  30720 positions, prefills a 2048-token suffix in 1024-row chunks, then
+  decodes.
 
 Each runner returns the sampled tokens and wall-clock phase timings
 (synchronous forwards, so host time covers the device work).
@@ -49,19 +50,19 @@ def llama3_8b_q4(g=None, decode_steps: int = 256, prompt_len: int = 8192, chunk:
     info.update({
         "prefill_s": round(t_pre, 4), "prefill_tok_s": round(prompt_len / t_pre, 1),
         "decode_s": round(t_dec, 4), "decode_tok_s": round((decode_steps - 1) / t_dec, 2),
-        "tokens": tokens, "prefill_logits_head": logits[:2048],
+        "tokens": tokens, "prefill_logits": logits,
     })
     return g, info
 
 
 def qwen2_7b_32k(g=None, decode_steps: int = 128, prompt_len: int = 32768, reuse: int = 30720,
-                 suffix_len: int = 2048, chunk: int = 1024):
+                 suffix_len: int = 2048, chunk: int = 1024, kv: str = "bf16"):
     shape = configs.QWEN2_7B
     info = {}
     if g is None:
         # The page pool holds the turn-1 snapshot (prompt_len positions) and
         # the pages turn 2 writes past the shared prefix.
-        g, info = load(shape, kv="bf16", kv_capacity=prompt_len + suffix_len + decode_steps + 64,
+        g, info = load(shape, kv=kv, kv_capacity=prompt_len + suffix_len + decode_steps + 64,
                        max_chunk_rows=chunk)
     prompt1 = synth.make_tokens(shape.vocab_size, prompt_len, seed=1)
     suffix = synth.make_tokens(shape.vocab_size, suffix_len, seed=2)
@@ -78,7 +79,7 @@ def qwen2_7b_32k(g=None, decode_steps: int = 128, prompt_len: int = 32768, reuse
         "snapshot_s": round(t_snap, 4), "restore_s": round(t_restore, 4),
         "turn2_prefill_s": round(t_turn2, 4), "turn2_prefill_tok_s": round(suffix_len / t_turn2, 1),
         "decode_s": round(t_dec, 4), "decode_tok_s": round((decode_steps - 1) / t_dec, 2),
-        "turn1_token": tok1, "turn1_logits_head": logits1[:2048], "turn2_logits_head": logits2[:2048],
+        "turn1_token": tok1, "turn1_logits": logits1, "turn2_logits": logits2,
         "tokens": [first] + rest.tolist(),
     })
     return g, info

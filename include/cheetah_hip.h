@@ -178,6 +178,13 @@ size_t cheetah_hip_kv_len(const cheetah_hip_model *m);
 int cheetah_hip_kv_snapshot(const cheetah_hip_model *m, cheetah_hip_snapshot **out, size_t *positions);
 int cheetah_hip_restore_kv_prefix(cheetah_hip_model *m, const cheetah_hip_snapshot *s, size_t positions);
 void cheetah_hip_snapshot_free(cheetah_hip_snapshot *s);
+/* Cached K and V rows of positions [pos_begin, pos_begin + n) of one layer,
+ * written to host buffers of n * kv_heads * head_dim floats each in the
+ * reference's per-layer cache layout [pos][kv_head][dim] (ops.rs:995-999,
+ * the rows KvSnapshot carries, registry.rs:48-55). BF16 pages widen exactly.
+ * Waits for the model's queued work. */
+int cheetah_hip_kv_download(const cheetah_hip_model *m, uint32_t layer, size_t pos_begin, size_t n, float *k_out,
+                            float *v_out);
 void cheetah_hip_model_free(cheetah_hip_model *m);
 
 /* Ant tier control (AntTierControl::page_in_unit / evict_unit,

@@ -76,6 +76,7 @@ def lib():
         L.ref_rope_in_place.argtypes = [_F32P, _SZ, _SZ, _SZ, ctypes.c_float]
         L.ref_rope_heads.argtypes = [_F32P, _SZ, _SZ, _SZ, _SZ, ctypes.c_float]
         L.ref_silu_multiply.argtypes = [_F32P, _F32P, _SZ]
+        L.ref_round_bf16.argtypes = [_F32P, _F32P, _SZ]
         L.ref_softmax.argtypes = [_F32P, _SZ]
         L.ref_attention.argtypes = [_F32P, _F32P, _SZ, _F32P, _F32P, _SZ, _SZ, _SZ, _SZ, _SZ]
         L.ref_attention_rows.argtypes = [_F32P, _F32P, _SZ, _SZ, _F32P, _F32P, _SZ, _SZ, _SZ, _SZ]
@@ -211,6 +212,15 @@ def rope_heads(values, heads: int, head_dim: int, rotary_dim: int, position: int
     v = _f32(values).copy()
     lib().ref_rope_heads(_p(v, _F32P), heads, head_dim, rotary_dim, position, theta)
     return v
+
+
+def round_bf16(values) -> np.ndarray:
+    """The BF16-KV mode's rounding of a K/V element (nearest, ties to even),
+    widened back to f32."""
+    x = _f32(values).reshape(-1)
+    out = np.empty_like(x)
+    lib().ref_round_bf16(_p(x, _F32P), _p(out, _F32P), x.size)
+    return out.reshape(np.shape(values))
 
 
 def silu_multiply(gate, up) -> np.ndarray:

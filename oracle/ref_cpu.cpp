@@ -757,6 +757,9 @@ float scalar_at(const Unit &u, size_t index) {
     return load_f32(u.bytes + 4 * index);
 }
 
+// The BF16-KV mode's cache element (the reference's cache is f32,
+// ops.rs:995-999): f32 -> BF16 round to nearest, ties to even, on the bit
+// pattern (finite inputs; the overflow past the largest BF16 gives inf).
 inline float round_bf16(float f) {
     uint32_t u;
     std::memcpy(&u, &f, 4);
@@ -764,6 +767,14 @@ inline float round_bf16(float f) {
     std::memcpy(&f, &u, 4);
     return f;
 }
+
+}  // namespace
+
+extern "C" void ref_round_bf16(const float *in, float *out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = round_bf16(in[i]);
+}
+
+namespace {
 
 // ops.rs:1102-1106 rmsnorm against `{unit}.weight`.
 int norm_rows(ref_model *m, const std::string &unit, float *x, size_t rows) {

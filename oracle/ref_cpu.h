@@ -57,6 +57,9 @@ void ref_rope_in_place(float *values, size_t heads, size_t head_dim,
 void ref_rope_heads(float *values, size_t heads, size_t head_dim,
                     size_t rotary_dim, size_t position, float theta);
 void ref_silu_multiply(float *gate, const float *up, size_t n);
+/* The BF16-KV mode's rounding of each appended K/V element (f32 -> BF16,
+ * nearest, ties to even), as values widened back to f32. */
+void ref_round_bf16(const float *in, float *out, size_t n);
 void ref_softmax(float *scores, size_t n);
 /* GQA attention of one query position over a contiguous f32 cache laid out
  * [pos][kv_head][head_dim] (ops.rs:1357-1467). */

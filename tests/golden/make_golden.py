@@ -91,8 +91,17 @@ def make_llama3_8b_q4(steps=40, kv_bf16=False):
     }
 
 
-def make_qwen2_7b_32k(steps=40):
-    """Config 5: Qwen2-7B shape, BF16 weights and BF16 KV. Turn 1: a
+def _vocab_sample(logits):
+    """Every 64th logit plus the top 16 (index, value): a full-vocabulary check
+    that stays a few KB."""
+    top = np.argsort(logits)[::-1][:16]
+    return {"stride64": logits[::64].tolist(), "top16_ids": top.tolist(),
+            "top16_values": logits[top].tolist()}
+
+
+def make_qwen2_7b_32k(steps=40, kv_bf16=True):
+    """Config 5: Qwen2-7B shape, BF16 weights, BF16 KV (kv_bf16) or the
+    reference's f32 KV (ops.rs:995-999). Turn 1: a
     32768-token prompt (seed 1) in 1024-row chunks, KV snapshot. Turn 2: the
     first 30720 prompt tokens + 2048 new ones (seed 2); the prefix is restored
     from the snapshot (engine.rs:523-601 semantics), the suffix prefilled in
@@ -101,7 +110,8 @@ def make_qwen2_7b_32k(steps=40):
     w = synth.make_weights(shape)
     prompt1 = synth.make_tokens(shape.vocab_size, 32768, seed=1)
     suffix = synth.make_tokens(shape.vocab_size, 2048, seed=2)
-    m = oracle.RefModel(shape, w, kv_bf16=True)
+    m = oracle.RefModel(shape, w, kv_bf16=kv_bf16)
+    del w
     t0 = time.time()
     logits1 = m.forward(prompt1, 0, chunk_rows=1024)
     t_turn1 = time.time() - t0
@@ -118,10 +128,11 @@ def make_qwen2_7b_32k(steps=40):
     return {
         "config": "qwen2-7b bf16, weights seed 0; turn 1 prompt seed 1 (32768), turn 2 = first 30720 + 2048 "
                   "tokens of seed 2",
-        "kv_cache": "bf16 (K/V rounded to nearest even on append)",
+        "kv_cache": "bf16 (K/V rounded to nearest even on append)" if kv_bf16 else "f32 (reference)",
         "prompt_len": 32768, "prefix_reused": 30720, "suffix_len": 2048, "suffix_seed": 2, "chunk_rows": 1024,
         "turn1_token": greedy(logits1), "turn1_margin": float(srt[-1] - srt[-2]),
         "turn1_logits_head": logits1[:2048].tolist(), "turn2_logits_head": logits2[:2048].tolist(),
+        "turn1_vocab_sample": _vocab_sample(logits1), "turn2_vocab_sample": _vocab_sample(logits2),
         "tokens": tokens, "top2_margins": margins,
         "oracle_threads": oracle.get_threads(),
         "oracle_seconds": {"turn1_prefill": round(t_turn1, 3), "turn2_prefill": round(t_turn2, 3),
@@ -135,9 +146,12 @@ MAKERS = {
     "llama3_8b_q4": make_llama3_8b_q4,
     "llama3_8b_q4_bf16kv": lambda: make_llama3_8b_q4(kv_bf16=True),
     "qwen2_7b_32k": make_qwen2_7b_32k,
+    "qwen2_7b_32k_f32kv": lambda: make_qwen2_7b_32k(kv_bf16=False),
 }
 
 if __name__ == "__main__":
+    if os.environ.get("CHEETAH_REF_THREADS"):
+        oracle.set_threads(int(os.environ["CHEETAH_REF_THREADS"]))
     which = sys.argv[1:] or list(MAKERS)
     for name in which:
         data = MAKERS[name]()

@@ -70,3 +70,22 @@ def test_host_wrapper_rejects_non_bf16_units():
     obj.shape = configs.TINY_QWEN2
     with pytest.raises(hip.HipError, match="not BF16"):
         obj.set_unit("model.norm.weight", np.zeros(4, np.float32))
+
+
+def test_attention_rejects_bad_geometry_before_device_work(lib):
+    # Every argument error comes back as -1 with a sentence before any device
+    # call (also without an initialized device): kv_heads == 0 used to reach
+    # a division by zero while sizing the split grid.
+    from cheetah_amd import hip
+    dummy = ctypes.c_void_p(16)
+    for kvh, hd, ps, q_heads, msg in [(0, 64, 64, 4, b"multiple of kv_heads"),
+                                      (2, 64, 64, 3, b"multiple of kv_heads"),
+                                      (2, 64, 64, 0, b"multiple of kv_heads"),
+                                      (2, 0, 64, 4, b"non-zero head_dim"),
+                                      (2, 64, 0, 4, b"non-zero head_dim")]:
+        view = hip.KvView(16, 16, 16, ps, kvh, hd)
+        assert lib.cheetah_hip_attention(dummy, ctypes.byref(view), q_heads, 1, 0, dummy) == -1
+        assert msg in lib.cheetah_hip_last_error(), (kvh, hd, ps, q_heads)
+    view = hip.KvView(16, 16, 16, 64, 2, 64)
+    assert lib.cheetah_hip_attention(dummy, ctypes.byref(view), 4, 0, 0, dummy) == -1
+    assert b"at least one query row" in lib.cheetah_hip_last_error()

@@ -1,12 +1,18 @@
 """Full-size decoder parity on the GPU against the oracle's golden runs.
 
-* Llama-3-8B shape, Q4 linears, 8192-token prompt in 512-row chunks: the
-  greedy ids of the first 32 decode steps equal the oracle's (the reference
-  semantics: f32 KV cache), and the prefill logits agree within 1e-2; the
-  same with the device's BF16 KV cache against the oracle run with BF16 K/V.
+Two KV precisions, two different claims:
+* f32 KV cache: the reference's own semantics (ops.rs:995-999). The device
+  must reproduce the reference's greedy tokens for the first 32 decode
+  steps and its logits within 1e-2.
+* BF16 KV cache (the served and timed default): a deliberate precision
+  change. The device must reproduce the oracle run that rounds K/V to BF16
+  on append; where that run departs from the reference's tokens, the test
+  pins the step and the reference's top-2 margin there.
+
+Workloads:
+* Llama-3-8B shape, Q4 linears, 8192-token prompt in 512-row chunks.
 * Qwen2-7B shape, BF16, 32768-token prompt in 1024-row chunks, a KV snapshot,
-  restore of the first 30720 positions, a 2048-token suffix and greedy decode:
-  the same bars against the oracle run with a BF16 KV cache (the device's).
+  restore of the first 30720 positions, a 2048-token suffix, greedy decode.
 
 The goldens come from tests/golden/make_golden.py (the oracle on this
 container's CPU; hours of CPU time, so they are committed fixtures).
@@ -41,16 +47,32 @@ def _rel(got, ref):
     return float(np.max(np.abs(got - ref)) / max(np.max(np.abs(ref)), 1e-30))
 
 
+def _check_logits(got, head, sample=None):
+    """First 2048 logits, and where the golden has them, every 64th logit of
+    the whole vocabulary plus the golden's top 16, all within 1e-2."""
+    got = np.asarray(got, np.float32)
+    assert _rel(got[: len(head)], head) < 1e-2
+    if sample:
+        assert _rel(got[::64], sample["stride64"]) < 1e-2
+        top = np.array(sample["top16_ids"])
+        assert _rel(got[top], sample["top16_values"]) < 1e-2
+
+
+def _first_departure(got, ref):
+    return next((i for i in range(min(len(got), len(ref))) if got[i] != ref[i]), None)
+
+
 @pytest.mark.gpu
 @pytest.mark.timeout(600)
-def test_llama3_8b_q4_8k_prefill_and_32_greedy_steps(hip):
+def test_llama3_8b_q4_8k_f32_kv_matches_reference(hip):
     gold = _load("llama3_8b_q4_greedy.json")
+    assert gold["kv_cache"].startswith("f32")
     from cheetah_amd import workloads
 
     print("[large] llama3-8b q4, f32 KV, 8192-token prompt", flush=True)
     g, info = workloads.llama3_8b_q4(decode_steps=33, kv="f32")
     try:
-        assert _rel(info["prefill_logits_head"], gold["prefill_logits_head"]) < 1e-2
+        _check_logits(info["prefill_logits"], gold["prefill_logits_head"], gold.get("prefill_vocab_sample"))
         assert info["tokens"][:32] == gold["tokens"][:32]
     finally:
         g.close()
@@ -59,32 +81,69 @@ def test_llama3_8b_q4_8k_prefill_and_32_greedy_steps(hip):
 @pytest.mark.gpu
 @pytest.mark.timeout(600)
 def test_llama3_8b_q4_8k_bf16_kv_32_greedy_steps(hip):
-    """The same workload with the device's BF16 KV cache, against the oracle
-    run that rounds K/V to BF16 on append."""
+    """The device's BF16 KV cache against the oracle run that rounds K/V to
+    BF16 on append: same 32 tokens. That run departs from the reference
+    (f32 KV) at decode step 6, where the reference's top-2 margin is 0.030:
+    BF16 K/V is not token-exact against the reference on this config."""
     gold = _load("llama3_8b_q4_bf16kv_greedy.json")
+    ref = _load("llama3_8b_q4_greedy.json")
     from cheetah_amd import workloads
 
     print("[large] llama3-8b q4, bf16 KV, 8192-token prompt", flush=True)
     g, info = workloads.llama3_8b_q4(decode_steps=33, kv="bf16")
     try:
-        assert _rel(info["prefill_logits_head"], gold["prefill_logits_head"]) < 1e-2
+        _check_logits(info["prefill_logits"], gold["prefill_logits_head"], gold.get("prefill_vocab_sample"))
+        _check_logits(info["prefill_logits"], ref["prefill_logits_head"], ref.get("prefill_vocab_sample"))
+        assert info["tokens"][:32] == gold["tokens"][:32]
+        first = _first_departure(info["tokens"][:32], ref["tokens"][:32])
+        print(f"[large] bf16-KV tokens depart from the reference at step {first}, reference top-2 margin "
+              f"{ref['top2_margins'][first]:.4f}", flush=True)
+        assert first == 6
+        assert abs(ref["top2_margins"][first] - 0.0301) < 1e-3
+    finally:
+        g.close()
+
+
+def _qwen2_7b(hip, kv, gold):
+    from cheetah_amd import workloads
+
+    print(f"[large] qwen2-7b bf16 weights, {kv} KV, 32768-token prompt, restore 30720 + 2048", flush=True)
+    g, info = workloads.qwen2_7b_32k(decode_steps=33, kv=kv)
+    try:
+        assert info["turn1_token"] == gold["turn1_token"]
+        _check_logits(info["turn1_logits"], gold["turn1_logits_head"], gold.get("turn1_vocab_sample"))
+        _check_logits(info["turn2_logits"], gold["turn2_logits_head"], gold.get("turn2_vocab_sample"))
         assert info["tokens"][:32] == gold["tokens"][:32]
     finally:
         g.close()
+    return info
 
 
 @pytest.mark.gpu
-@pytest.mark.timeout(600)
-def test_qwen2_7b_32k_prefill_prefix_reuse_and_32_greedy_steps(hip):
-    gold = _load("qwen2_7b_32k_greedy.json")
-    from cheetah_amd import workloads
+@pytest.mark.timeout(900)
+def test_qwen2_7b_32k_f32_kv_matches_reference(hip):
+    """Reference semantics (f32 KV) at 32K context: the turn-1 token, both
+    turns' logits within 1e-2 and the first 32 decode ids equal the CPU
+    path's."""
+    gold = _load("qwen2_7b_32k_f32kv_greedy.json")
+    assert gold["kv_cache"].startswith("f32")
+    _qwen2_7b(hip, "f32", gold)
 
-    print("[large] qwen2-7b bf16, 32768-token prompt, restore 30720 + 2048", flush=True)
-    g, info = workloads.qwen2_7b_32k(decode_steps=33)
-    try:
-        assert info["turn1_token"] == gold["turn1_token"]
-        assert _rel(info["turn1_logits_head"], gold["turn1_logits_head"]) < 1e-2
-        assert _rel(info["turn2_logits_head"], gold["turn2_logits_head"]) < 1e-2
-        assert info["tokens"][:32] == gold["tokens"][:32]
-    finally:
-        g.close()
+
+@pytest.mark.gpu
+@pytest.mark.timeout(900)
+def test_qwen2_7b_32k_bf16_kv_32_greedy_steps(hip):
+    """The BF16 cache against the oracle run with BF16 K/V; where the
+    reference-semantics golden exists, the departure from it is recorded and
+    must sit at a near-tie of the reference (top-2 margin below 0.05)."""
+    gold = _load("qwen2_7b_32k_greedy.json")
+    info = _qwen2_7b(hip, "bf16", gold)
+    path = os.path.join(GOLDEN, "qwen2_7b_32k_f32kv_greedy.json")
+    if os.path.exists(path):
+        with open(path) as f:
+            ref = json.load(f)
+        first = _first_departure(info["tokens"][:32], ref["tokens"][:32])
+        if first is not None:
+            print(f"[large] bf16-KV tokens depart from the reference at step {first}, reference top-2 margin "
+                  f"{ref['top2_margins'][first]:.4f}", flush=True)
+            assert ref["top2_margins"][first] < 0.05

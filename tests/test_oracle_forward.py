@@ -77,9 +77,30 @@ def test_token_validation_errors(oracle):
         m.forward(np.array([1000], np.uint32), 0)
 
 
-def numpy_forward(shape, w, tokens):
+def rne_bf16(values) -> np.ndarray:
+    """Round to the nearest BF16, ties to the even BF16, chosen by comparing
+    float64 distances to the two BF16 neighbours of each f32 value (an
+    independent statement of the rule: no bit-pattern carry trick)."""
+    x = np.ascontiguousarray(values, np.float32)
+    bits = x.view(np.uint32).astype(np.uint64)
+    toward0 = (bits & 0xFFFF0000).astype(np.uint32)
+    away = (toward0.astype(np.uint64) + 0x10000).astype(np.uint32)
+    lo = toward0.view(np.float32).astype(np.float64)
+    with np.errstate(over="ignore", invalid="ignore"):
+        hi = away.view(np.float32).astype(np.float64)
+        # Past the largest BF16 the upper neighbour is 2^128 (stored as inf).
+        hi = np.where((away & 0x7FFFFFFF) == 0x7F800000, np.copysign(2.0 ** 128, x.astype(np.float64)), hi)
+        d_lo = np.abs(x.astype(np.float64) - lo)
+        d_hi = np.abs(hi - x.astype(np.float64))
+    odd = ((toward0 >> 16) & 1) == 1
+    pick_hi = (bits & 0xFFFF != 0) & ((d_hi < d_lo) | ((d_hi == d_lo) & odd))
+    return np.where(pick_hi, away, toward0).view(np.float32)
+
+
+def numpy_forward(shape, w, tokens, kv_bf16=False):
     """float64 tensor-math forward of the qwen2/llama block
-    (decoder.rs:1367-1433 helper pattern)."""
+    (decoder.rs:1367-1433 helper pattern); kv_bf16 rounds every cached K and
+    V element (after RoPE) to BF16, as the BF16-KV cache stores it."""
     f = lambda name: synth.bf16_to_f32(w[name]).astype(np.float64)
     H, hd = shape.hidden_size, shape.head_dim
     n = len(tokens)
@@ -113,6 +134,9 @@ def numpy_forward(shape, w, tokens):
             v += f(p + "self_attn.v_proj.bias")
         q, k = rope(q, shape.q_heads), rope(k, shape.kv_heads)
         v = v.reshape(n, shape.kv_heads, hd)
+        if kv_bf16:
+            k = rne_bf16(k).astype(np.float64)
+            v = rne_bf16(v).astype(np.float64)
         out = np.zeros((n, shape.q_heads, hd))
         for h in range(shape.q_heads):
             s = q[:, h] @ k[:, h // G].T / math.sqrt(hd)
@@ -157,3 +181,53 @@ def test_quantized_forward_uses_quantize_then_gemv(oracle, fmt):
     a = mq.forward(toks, 0)
     b = mf.forward(toks, 0)
     assert np.max(np.abs(a - b)) < 1e-4 * max(1.0, np.max(np.abs(b)))
+
+
+def test_round_bf16_matches_nearest_even(oracle):
+    """The oracle's BF16-KV rounding (a bit-pattern carry) against the
+    distance-based statement above, on hand-picked cases and on random bit
+    patterns of every exponent."""
+    eps8 = 2.0 ** -8  # half a BF16 ulp at 1.0
+    cases = {
+        1.0 + eps8: 1.0,                         # tie, even neighbour below
+        1.0 + 3 * eps8: 1.0 + 4 * eps8,          # tie, even neighbour above
+        1.0 + eps8 + 2.0 ** -20: 1.0 + 2 * eps8, # just past the tie
+        -(1.0 + eps8): -1.0,
+        -(1.0 + 3 * eps8): -(1.0 + 4 * eps8),
+        65504.0: 65536.0,
+        float(np.finfo(np.float32).max): np.inf,  # past the largest BF16
+        -float(np.finfo(np.float32).max): -np.inf,
+        2.0 ** -130: 2.0 ** -130,                # subnormal, exact in BF16
+        0.0: 0.0,
+    }
+    src = np.array(list(cases), np.float32)
+    got = oracle.round_bf16(src)
+    assert np.array_equal(got, np.array(list(cases.values()), np.float32)), (src, got)
+    assert oracle.round_bf16(np.array([-0.0], np.float32)).view(np.uint32)[0] == 0x80000000
+    rng = np.random.default_rng(0)
+    bits = rng.integers(0, 2 ** 32, 200_000, dtype=np.uint64).astype(np.uint32)
+    bits = bits[(bits & 0x7F800000) != 0x7F800000]  # finite values only
+    x = bits.view(np.float32)
+    assert np.array_equal(oracle.round_bf16(x).view(np.uint32), rne_bf16(x).view(np.uint32))
+    # The rounding is idempotent and leaves BF16 values alone.
+    r = oracle.round_bf16(x)
+    assert np.array_equal(oracle.round_bf16(r).view(np.uint32), r.view(np.uint32))
+
+
+@pytest.mark.parametrize("shape", [configs.TINY_QWEN2, configs.TINY_LLAMA], ids=lambda s: s.name)
+def test_bf16_kv_forward_matches_float64_with_rounded_cache(oracle, shape):
+    """The oracle's BF16-KV mode against the float64 forward whose cached K
+    and V are rounded to BF16: agreement within 1e-5 of the largest logit
+    (measured ~5e-7), while the same float64 forward without the rounding
+    lies ~1e-3 away, so a dropped or partial (K-only) rounding fails here."""
+    w = synth.make_weights(shape)
+    m = oracle.RefModel(shape, w, kv_bf16=True)
+    toks = synth.make_tokens(shape.vocab_size, 23, seed=9)
+    got = m.forward(toks, 0, chunk_rows=8).astype(np.float64)
+    exp = numpy_forward(shape, w, toks, kv_bf16=True)
+    unrounded = numpy_forward(shape, w, toks, kv_bf16=False)
+    scale = max(1.0, np.max(np.abs(exp)))
+    err = np.max(np.abs(got - exp)) / scale
+    err_unrounded = np.max(np.abs(got - unrounded)) / scale
+    assert err < 1e-5, err
+    assert err_unrounded > 100 * err, (err, err_unrounded)
