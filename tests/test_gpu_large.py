@@ -82,9 +82,13 @@ def test_llama3_8b_q4_8k_f32_kv_matches_reference(hip):
 @pytest.mark.timeout(600)
 def test_llama3_8b_q4_8k_bf16_kv_32_greedy_steps(hip):
     """The device's BF16 KV cache against the oracle run that rounds K/V to
-    BF16 on append: same 32 tokens. That run departs from the reference
-    (f32 KV) at decode step 6, where the reference's top-2 margin is 0.030:
-    BF16 K/V is not token-exact against the reference on this config."""
+    BF16 on append: prefill logits within 1e-2 and the same 32 tokens.
+
+    Against the reference (f32 KV) the BF16 cache misses both bars on this
+    config, and the test pins by how much: the prefill logits differ by
+    ~2.5e-2 relative (8K positions of BF16-rounded K/V; the 1e-2 bar is met
+    only by the f32 cache, test above), and the tokens depart at decode step
+    6, where the reference's top-2 margin is 0.030."""
     gold = _load("llama3_8b_q4_bf16kv_greedy.json")
     ref = _load("llama3_8b_q4_greedy.json")
     from cheetah_amd import workloads
@@ -93,8 +97,11 @@ def test_llama3_8b_q4_8k_bf16_kv_32_greedy_steps(hip):
     g, info = workloads.llama3_8b_q4(decode_steps=33, kv="bf16")
     try:
         _check_logits(info["prefill_logits"], gold["prefill_logits_head"], gold.get("prefill_vocab_sample"))
-        _check_logits(info["prefill_logits"], ref["prefill_logits_head"], ref.get("prefill_vocab_sample"))
         assert info["tokens"][:32] == gold["tokens"][:32]
+        head = ref["prefill_logits_head"]
+        vs_ref = _rel(info["prefill_logits"][: len(head)], head)
+        print(f"[large] bf16-KV prefill logits vs the reference: {vs_ref:.4f} relative", flush=True)
+        assert 1e-2 < vs_ref < 5e-2
         first = _first_departure(info["tokens"][:32], ref["tokens"][:32])
         print(f"[large] bf16-KV tokens depart from the reference at step {first}, reference top-2 margin "
               f"{ref['top2_margins'][first]:.4f}", flush=True)
