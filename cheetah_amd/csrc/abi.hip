@@ -9,7 +9,18 @@
 
 namespace chip {
 
+// Scratch of cheetah_hip_attention_noalloc: the split partials of one call
+// (rows * q_heads * splits * (head_dim + 2) floats), at most 48 MiB, held by
+// every device the library runs on until the process ends. Host code never
+// passes `scratch` itself to a kernel (on the host it names a stand-in, not
+// device memory): it uses the device address hipGetSymbolAddress returned at
+// cheetah_hip_init, kept per device in g_scratch.
+constexpr size_t kNoAllocScratchFloats = (size_t)12 << 20;
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
 namespace {
+constexpr int kMaxDevices = 64;
+float *g_scratch[kMaxDevices] = {};
 thread_local std::string g_error;
 std::mutex g_mutex;
 bool g_ready = false;
@@ -59,6 +70,13 @@ int cheetah_hip_init(int device) {
         return fail("HIP backend: device " + std::to_string(device) + " is " + arch +
                     "; this library is built for gfx950 (MI355X) only.");
     CHIP_CHECK(hipSetDevice(device));
+    if (device >= kMaxDevices) return fail("HIP backend: device index above the supported 64.");
+    if (!g_scratch[device]) {
+        void *p = nullptr;
+        CHIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return fail("HIP backend: no device address for the attention scratch.");
+        g_scratch[device] = (float *)p;
+    }
     g_max_lds = prop.sharedMemPerBlock;
     g_cus = prop.multiProcessorCount;
     if (prop.maxSharedMemoryPerMultiProcessor > 0) g_lds_per_cu = prop.maxSharedMemoryPerMultiProcessor;
@@ -264,11 +282,9 @@ int cheetah_hip_attention(const float *q, const cheetah_hip_kv_view *kv, uint32_
     return attention_op(q, kv, q_heads, rows, offset, out);
 }
 
-static int attention_op(const float *q, const cheetah_hip_kv_view *kv, uint32_t q_heads, size_t rows, size_t offset,
-                        float *out) {
-    CHIP_TRY(check_attention_args(q, kv, q_heads, rows, out));
-    static thread_local float *part = nullptr;
-    static thread_local size_t part_floats = 0;
+// The job of one attention call and the partial floats it needs.
+static AttnJob attention_job(const float *q, const cheetah_hip_kv_view *kv, uint32_t q_heads, size_t rows,
+                             size_t offset, float *out, size_t *need_floats) {
     AttnJob j;
     j.q = q;
     j.q_stride = (size_t)q_heads * kv->head_dim;
@@ -292,6 +308,17 @@ static int attention_op(const float *q, const cheetah_hip_kv_view *kv, uint32_t 
     if (j.prefill && attention_prefill_on_mfma(j.g, (int)q_heads))
         need = std::max(need, attention_part_floats(rows, (int)q_heads, attention_prefill_splits(offset + rows),
                                                     (int)kv->head_dim));
+    *need_floats = need;
+    return j;
+}
+
+static int attention_op(const float *q, const cheetah_hip_kv_view *kv, uint32_t q_heads, size_t rows, size_t offset,
+                        float *out) {
+    CHIP_TRY(check_attention_args(q, kv, q_heads, rows, out));
+    static thread_local float *part = nullptr;
+    static thread_local size_t part_floats = 0;
+    size_t need = 0;
+    AttnJob j = attention_job(q, kv, q_heads, rows, offset, out, &need);
     if (need > part_floats) {
         CHIP_CHECK(hipStreamSynchronize(g_stream));
         if (part) CHIP_CHECK(hipFree(part));
@@ -302,6 +329,25 @@ static int attention_op(const float *q, const cheetah_hip_kv_view *kv, uint32_t 
     }
     j.part = part;
     j.part_floats = part_floats;
+    return launch_attention(j, g_stream);
+}
+
+int cheetah_hip_attention_noalloc(const float *q, const cheetah_hip_kv_view *kv, uint32_t q_heads, size_t rows,
+                                  size_t offset, float *out) {
+    CHIP_TRY(check_attention_args(q, kv, q_heads, rows, out));
+    CHIP_TRY(ensure_ready());
+    float *part = g_scratch[g_device];
+    if (!part) return fail("HIP backend: the attention scratch has no device address.");
+    size_t need = 0;
+    AttnJob j = attention_job(q, kv, q_heads, rows, offset, out, &need);
+    if (need > kNoAllocScratchFloats)
+        return fail("HIP backend: attention_noalloc needs " + std::to_string(need * sizeof(float)) +
+                    " bytes of split partials; its scratch holds " +
+                    std::to_string(kNoAllocScratchFloats * sizeof(float)) + ".");
+    // Every partial a launch reads was written by a split of the same launch
+    // first: nothing in the scratch has to start at zero.
+    j.part = part;
+    j.part_floats = kNoAllocScratchFloats;
     return launch_attention(j, g_stream);
 }
 

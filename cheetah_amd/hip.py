@@ -70,6 +70,7 @@ SIGNATURES = {
     "cheetah_hip_dequant_q8": (_c.c_int, [_VP, _SZ, _SZ, _VP]),
     "cheetah_hip_dequant_q4": (_c.c_int, [_VP, _SZ, _SZ, _VP]),
     "cheetah_hip_attention": (_c.c_int, [_VP, _c.POINTER(KvView), _c.c_uint32, _SZ, _SZ, _VP]),
+    "cheetah_hip_attention_noalloc": (_c.c_int, [_VP, _c.POINTER(KvView), _c.c_uint32, _SZ, _SZ, _VP]),
     "cheetah_hip_model_create": (_VP, [_c.POINTER(Config), _c.c_uint32, _c.c_uint32, _SZ, _SZ]),
     "cheetah_hip_model_set_unit": (_c.c_int, [_VP, _c.c_char_p, _VP, _SZ, _c.c_uint32,
                                               _c.POINTER(_c.c_uint64), _SZ]),
@@ -264,14 +265,16 @@ def paged_kv(keys_bf16: np.ndarray, values_bf16: np.ndarray, page_size: int = 64
 
 
 def attention(q: np.ndarray, kp: np.ndarray, vp: np.ndarray, table: np.ndarray, q_heads: int, rows: int,
-              offset: int) -> np.ndarray:
-    """q: f32 [rows, q_heads*hd]; kp/vp: BF16 pages; table: int32 page table."""
+              offset: int, noalloc: bool = False) -> np.ndarray:
+    """q: f32 [rows, q_heads*hd]; kp/vp: BF16 pages; table: int32 page table.
+    noalloc: through cheetah_hip_attention_noalloc (fixed device scratch)."""
     _, kvh, ps, hd = kp.shape
     qd = DeviceBuffer.from_array(np.ascontiguousarray(q, np.float32))
     kd, vd, td = DeviceBuffer.from_array(kp), DeviceBuffer.from_array(vp), DeviceBuffer.from_array(table)
     od = DeviceBuffer(rows * q_heads * hd * 4)
     view = KvView(kd.ptr, vd.ptr, td.ptr, ps, kvh, hd)
-    check(lib().cheetah_hip_attention(qd.ptr, _c.byref(view), q_heads, rows, offset, od.ptr))
+    fn = lib().cheetah_hip_attention_noalloc if noalloc else lib().cheetah_hip_attention
+    check(fn(qd.ptr, _c.byref(view), q_heads, rows, offset, od.ptr))
     return od.download(np.float32, rows * q_heads * hd).reshape(rows, q_heads * hd)
 
 

@@ -105,6 +105,17 @@ typedef struct cheetah_hip_kv_view {
  * f32 [rows][q_heads*head_dim]. Decode is rows == 1. */
 int cheetah_hip_attention(const float *q, const cheetah_hip_kv_view *kv, uint32_t q_heads, size_t rows,
                           size_t offset, float *out);
+/* cheetah_hip_attention that allocates nothing. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). The split partials live in a fixed 48 MiB device array per GPU
+ * instead of a buffer the library grows on demand; a call that needs more
+ * (rows * q_heads * splits * (head_dim + 2) floats) is rejected with an
+ * error before any device work. Same kernels and split choice, so the same
+ * results as cheetah_hip_attention. Calls that overlap on one GPU share
+ * that array and race. */
+int cheetah_hip_attention_noalloc(const float *q, const cheetah_hip_kv_view *kv, uint32_t q_heads, size_t rows,
+                                  size_t offset, float *out);
 
 /* ------------------------------------------------------------------------
  * Model: the HIP implementation of ModelForward (registry.rs:57-85) for the
