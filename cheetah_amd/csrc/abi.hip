@@ -295,13 +295,7 @@ static AttnJob attention_job(const float *q, const cheetah_hip_kv_view *kv, uint
     j.q_heads = (int)q_heads;
     j.rows = rows;
     j.offset = offset;
-    // Split each row's keys so the grid covers the chip: ~2048 blocks.
-    const size_t ctx = offset + rows;
-    const size_t tiles = (ctx + 63) / 64;
-    size_t splits = (2048 + rows * kv->kv_heads - 1) / (rows * kv->kv_heads);
-    if (splits > tiles) splits = tiles;
-    if (splits > (size_t)attention_max_splits()) splits = attention_max_splits();
-    if (splits < 1) splits = 1;
+    const size_t splits = (size_t)attention_decode_splits(offset + rows, (int)kv->kv_heads, rows);
     j.splits = (int)splits;
     j.prefill = rows > 1;
     size_t need = attention_part_floats(rows, (int)q_heads, (int)splits, (int)kv->head_dim);

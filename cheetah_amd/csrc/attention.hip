@@ -29,7 +29,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int TP = 64;  // positions per tile (page_size is a multiple of it)
-constexpr int kMaxSplits = 64;
+constexpr int kMaxSplits = 128;
 
 // Block barrier that waits on LDS traffic only (outstanding global loads
 // stay in flight across it).
@@ -128,7 +128,9 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
     // tile t0 computes. A position past `end` reads the row at end - 1 (the
     // compute masks it), and the tile barriers wait on LDS only, so the loads
     // of the next tile stay in flight across the current tile's barriers.
-    Raw8<KT> bk[2][TP / P], bv[2][TP / P];
+    // (Four sets, three tiles in flight, measured slower: 254 registers.)
+    constexpr int NB = 2;
+    Raw8<KT> bk[NB][TP / P], bv[NB][TP / P];
     const long last_tile = start + (end - 1 - start) / TP * TP;
     auto issue = [&](long t, Raw8<KT> (&kr)[TP / P], Raw8<KT> (&vr)[TP / P]) {
         t = min(t, last_tile);
@@ -145,17 +147,14 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
         }
     };
     auto tile = [&](long t0, const Raw8<KT> (&kc)[TP / P], const Raw8<KT> (&vc)[TP / P]) {
-        float vf[TP / P][8], kf[TP / P][8];
-#pragma unroll
-        for (int p = 0; p < TP / P; ++p) {
-            kc[p].get(kf[p]);
-            vc[p].get(vf[p]);
-        }
-        // Scores of every head of the group for the tile's rows.
+        // Scores of every head of the group for the tile's rows (each K row
+        // widened to f32 where it is used).
 #pragma unroll
         for (int p = 0; p < TP / P; ++p) {
             const int pi = p * P + pg;
             const bool valid = t0 + pi < end;
+            float kf[8];
+            kc[p].get(kf);
             float dot[G];
 #pragma unroll
             for (int j = 0; j < G; ++j) dot[j] = 0.f;
@@ -163,7 +162,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
 #pragma unroll
                 for (int j = 0; j < G; ++j)
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) dot[j] = fmaf(kf[p][e], qr[j][e], dot[j]);
+                    for (int e = 0; e < 8; ++e) dot[j] = fmaf(kf[e], qr[j][e], dot[j]);
             }
 #pragma unroll
             for (int j = 0; j < G; ++j) {
@@ -200,11 +199,13 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
         for (int p = 0; p < TP / P; ++p) {
             const int pi = p * P + pg;
             if (t0 + pi < end) {
+                float vf[8];
+                vc[p].get(vf);
 #pragma unroll
                 for (int j = 0; j < G; ++j) {
                     const float pj = s_p[j][pi];
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) acc[j][e] = fmaf(pj, vf[p][e], acc[j][e]);
+                    for (int e = 0; e < 8; ++e) acc[j][e] = fmaf(pj, vf[e], acc[j][e]);
                 }
             }
         }
@@ -214,14 +215,15 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
     if (end - start <= TP) {
         tile(start, bk[0], bv[0]);
     } else {
-        // Issued whether or not the tile exists (a tile past the split reads
-        // the split's last tile again), so the compiler counts the loads
-        // exactly and each tile waits only for its own.
-        for (long t0 = start; t0 < end; t0 += 2 * TP) {
-            issue(t0 + TP, bk[1], bv[1]);
-            tile(t0, bk[0], bv[0]);
-            issue(t0 + 2 * TP, bk[0], bv[0]);
-            if (t0 + TP < end) tile(t0 + TP, bk[1], bv[1]);
+#pragma unroll
+        for (int b = 1; b < NB; ++b) issue(start + b * TP, bk[b], bv[b]);
+        for (long t0 = start; t0 < end; t0 += NB * TP) {
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const long tb = t0 + b * TP;
+                if (b == 0 || tb < end) tile(tb, bk[b], bv[b]);
+                issue(tb + NB * TP, bk[b], bv[b]);
+            }
         }
     }
     // Reduce acc over the position groups: lanes d8, d8+T, ... of a wave,
@@ -273,32 +275,40 @@ __global__ __launch_bounds__(kThreads) void attn_combine_kernel(const float *par
     __shared__ float s_o[GR][HD];
     const int h = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
     const float *p = part + ((size_t)row * q_heads + h) * (size_t)S * (HD + 2);
+    static_assert(kMaxSplits <= 128, "one wave holds two splits per lane");
     if (tid < 64) {
-        const float m = tid < S ? p[(size_t)tid * (HD + 2) + HD] : -INFINITY;
-        const float M = wave_max(m);
-        const float w = m == -INFINITY ? 0.f : expf(m - M);
-        const float l = w != 0.f ? p[(size_t)tid * (HD + 2) + HD + 1] : 0.f;
-        const float L = wave_sum(w * l);
-        if (tid < S) s_w[tid] = w;
+        const int s1 = tid + 64;
+        const float m0 = tid < S ? p[(size_t)tid * (HD + 2) + HD] : -INFINITY;
+        const float m1 = s1 < S ? p[(size_t)s1 * (HD + 2) + HD] : -INFINITY;
+        const float M = wave_max(fmaxf(m0, m1));
+        const float w0 = m0 == -INFINITY ? 0.f : expf(m0 - M);
+        const float w1 = m1 == -INFINITY ? 0.f : expf(m1 - M);
+        const float l0 = w0 != 0.f ? p[(size_t)tid * (HD + 2) + HD + 1] : 0.f;
+        const float l1 = w1 != 0.f ? p[(size_t)s1 * (HD + 2) + HD + 1] : 0.f;
+        const float L = wave_sum(w0 * l0) + wave_sum(w1 * l1);
+        if (tid < S) s_w[tid] = w0;
+        if (s1 < S) s_w[s1] = w1;
         if (tid == 0) s_inv = 1.0f / L;
     }
     __syncthreads();
     const int d = tid % HD, grp = tid / HD;
-    // Every split value this thread folds is loaded first (one memory round
-    // trip), then folded in split order.
-    constexpr int PER = kMaxSplits / GR;
-    float v[PER];
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        const int s = grp + GR * i;
-        v[i] = s < S ? p[(size_t)s * (HD + 2) + d] : 0.f;
-    }
+    // The split values this thread folds are loaded 16 at a time (one memory
+    // round trip per batch), then folded in split order.
+    constexpr int PER = kMaxSplits / GR, BATCH = PER < 16 ? PER : 16;
     float o = 0.f;
+    for (int i0 = 0; i0 < PER && grp + GR * i0 < S; i0 += BATCH) {
+        float v[BATCH];
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        const int s = grp + GR * i;
-        const float w = s < S ? s_w[s] : 0.f;
-        if (w != 0.f) o = fmaf(w, v[i], o);
+        for (int i = 0; i < BATCH; ++i) {
+            const int s = grp + GR * (i0 + i);
+            v[i] = s < S ? p[(size_t)s * (HD + 2) + d] : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < BATCH; ++i) {
+            const int s = grp + GR * (i0 + i);
+            const float w = s < S ? s_w[s] : 0.f;
+            if (w != 0.f) o = fmaf(w, v[i], o);
+        }
     }
     s_o[grp][d] = o;
     __syncthreads();
@@ -666,6 +676,16 @@ size_t attention_part_floats(size_t rows, int q_heads, int splits, int head_dim)
 }
 
 int attention_max_splits() { return kMaxSplits; }
+
+// Split-K of a decode-style launch: about two blocks per CU across the KV
+// heads and rows, at most one split per 64-position tile and kMaxSplits.
+int attention_decode_splits(size_t ctx, int kv_heads, size_t rows) {
+    const size_t target = 2 * (size_t)std::max(device_cus(), 1);
+    const size_t per = (size_t)std::max(kv_heads, 1) * std::max<size_t>(rows, 1);
+    size_t s = (target + per - 1) / per;
+    s = std::min({s, (ctx + TP - 1) / TP, (size_t)kMaxSplits});
+    return (int)std::max<size_t>(s, 1);
+}
 
 int attention_prefill_splits(size_t ctx) { return (int)std::max<size_t>(1, (ctx + kSpan - 1) / kSpan); }
 

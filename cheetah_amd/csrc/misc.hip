@@ -7,13 +7,23 @@ namespace {
 
 constexpr int kThreads = 256;
 
-// embedding_row_into (ops.rs:1083-1099): BF16 -> f32 widening.
-__global__ __launch_bounds__(kThreads) void embed_kernel(const uint16_t *table, int hidden, const uint32_t *tokens,
-                                                         float *out) {
-    const uint32_t tok = tokens[blockIdx.x];
+// embedding_row_into (ops.rs:1083-1099): BF16 -> f32 widening. blockIdx.y
+// is the row; each thread widens up to 8 consecutive elements of one block
+// of 8 * kThreads, with one 16-byte load when the row allows it.
+__global__ __launch_bounds__(kThreads) void embed_kernel(const uint16_t *__restrict__ table, int hidden,
+                                                         const uint32_t *__restrict__ tokens, float *__restrict__ out) {
+    const uint32_t tok = tokens[blockIdx.y];
     const uint16_t *src = table + (size_t)tok * hidden;
-    float *dst = out + (size_t)blockIdx.x * hidden;
-    for (int i = threadIdx.x; i < hidden; i += kThreads) dst[i] = bf16_f32(src[i]);
+    float *dst = out + (size_t)blockIdx.y * hidden;
+    const int i0 = (blockIdx.x * kThreads + threadIdx.x) * 8;
+    if (i0 >= hidden) return;
+    if (i0 + 8 <= hidden && hidden % 8 == 0 && ((uintptr_t)table & 15) == 0 && ((uintptr_t)out & 15) == 0) {
+        const u32x4 w = *(const u32x4 *)(src + i0);
+        *(f32x4 *)(dst + i0) = f32x4{bf16_lo(w[0]), bf16_hi(w[0]), bf16_lo(w[1]), bf16_hi(w[1])};
+        *(f32x4 *)(dst + i0 + 4) = f32x4{bf16_lo(w[2]), bf16_hi(w[2]), bf16_lo(w[3]), bf16_hi(w[3])};
+    } else {
+        for (int i = i0; i < min(i0 + 8, hidden); ++i) dst[i] = bf16_f32(src[i]);
+    }
 }
 
 // rmsnorm (ops.rs:646-652): x * (inv * gain), inv = 1 / sqrt(mean(x^2) + eps).
@@ -109,35 +119,42 @@ __device__ __forceinline__ float rope_elem(const float *src, int d, int half, in
     return d < half ? a * c - b * s : b * c + a * s;
 }
 
+// One thread per output element: blockIdx.y is the row, blockIdx.x a run of
+// kThreads elements over [q | k] (each k element also appends its v). A
+// thread issues its few loads at once, so a row costs one memory round trip
+// whatever its width.
 template <class KT>
-__global__ __launch_bounds__(kThreads) void rope_append_kernel(const float *qkv, float *qrot, int q_heads,
-                                                               int kv_heads, int head_dim, int rotary_dim,
-                                                               const float *cos_t, const float *sin_t,
-                                                               const int32_t *page_table, int page_size, KT *kc,
-                                                               KT *vc, long offset, const int32_t *pos_dev) {
-    const int row = blockIdx.x;
-    const long pos = (pos_dev ? (long)*pos_dev : offset) + row;
+__global__ __launch_bounds__(kThreads) void rope_append_kernel(const float *__restrict__ qkv, float *__restrict__ qrot,
+                                                               int q_heads, int kv_heads, int head_dim, int rotary_dim,
+                                                               const float *__restrict__ cos_t,
+                                                               const float *__restrict__ sin_t,
+                                                               const int32_t *__restrict__ page_table, int page_size,
+                                                               KT *__restrict__ kc, KT *__restrict__ vc, long offset,
+                                                               const int32_t *__restrict__ pos_dev) {
+    const int row = blockIdx.y;
+    const int t = blockIdx.x * kThreads + threadIdx.x;
     const int q_dim = q_heads * head_dim, kv_dim = kv_heads * head_dim;
+    if (t >= q_dim + kv_dim) return;
+    const long pos = (pos_dev ? (long)*pos_dev : offset) + row;
     const float *q = qkv + (size_t)row * (q_dim + 2 * kv_dim);
-    const float *k = q + q_dim;
-    const float *v = k + kv_dim;
-    float *qo = qrot + (size_t)row * q_dim;
     const int half = rotary_dim / 2;
     const float *cr = cos_t + (size_t)pos * half;
     const float *sr = sin_t + (size_t)pos * half;
-    for (int t = threadIdx.x; t < q_dim; t += kThreads) {
+    if (t < q_dim) {
         const int h = t / head_dim, d = t % head_dim;
-        qo[t] = rope_elem(q + h * head_dim, d, half, rotary_dim, cr, sr);
+        qrot[(size_t)row * q_dim + t] = rope_elem(q + h * head_dim, d, half, rotary_dim, cr, sr);
+        return;
     }
+    const int u = t - q_dim;
+    const float *k = q + q_dim;
+    const float *v = k + kv_dim;
+    const int h = u / head_dim, d = u % head_dim;
     const int page = page_table[pos / page_size];
     const int slot = (int)(pos % page_size);
-    for (int t = threadIdx.x; t < kv_dim; t += kThreads) {
-        const int h = t / head_dim, d = t % head_dim;
-        const float kv = rope_elem(k + h * head_dim, d, half, rotary_dim, cr, sr);
-        const size_t off = (((size_t)page * kv_heads + h) * page_size + slot) * head_dim + d;
-        store_kv(kc + off, kv);
-        store_kv(vc + off, v[t]);
-    }
+    const float kv = rope_elem(k + h * head_dim, d, half, rotary_dim, cr, sr);
+    const size_t off = (((size_t)page * kv_heads + h) * page_size + slot) * head_dim + d;
+    store_kv(kc + off, kv);
+    store_kv(vc + off, v[u]);
 }
 
 __global__ __launch_bounds__(kThreads) void gather_rows_kernel(const uint8_t *src, uint8_t *dst, const int32_t *map,
@@ -218,7 +235,9 @@ __global__ __launch_bounds__(kThreads) void argmax_final_kernel(const int *pkey,
 int launch_embed(const uint16_t *table, size_t hidden, const uint32_t *tokens, size_t rows, float *out,
                  hipStream_t s) {
     if (rows == 0) return 0;
-    hipLaunchKernelGGL(embed_kernel, dim3(rows), dim3(kThreads), 0, s, table, (int)hidden, tokens, out);
+    if (rows > 65535) return fail("HIP backend: embedding takes at most 65535 rows per launch.");
+    const dim3 grid((unsigned)((hidden + 8 * kThreads - 1) / (8 * kThreads)), (unsigned)rows);
+    hipLaunchKernelGGL(embed_kernel, grid, dim3(kThreads), 0, s, table, (int)hidden, tokens, out);
     CHIP_CHECK(hipGetLastError());
     return 0;
 }
@@ -260,12 +279,15 @@ int launch_rope_append(const float *qkv, float *qrot, size_t rows, int q_heads, 
     if (rows == 0) return 0;
     if (rotary_dim <= 0 || rotary_dim > g.head_dim || rotary_dim % 2)
         return fail("HIP backend: rotary_dim must be even and at most head_dim.");
+    const int width = q_heads * g.head_dim + g.kv_heads * g.head_dim;
+    const dim3 grid((width + kThreads - 1) / kThreads, (unsigned)rows);
+    if (rows > 65535) return fail("HIP backend: rope_append takes at most 65535 rows per launch.");
     if (g.kv_f32)
-        hipLaunchKernelGGL(rope_append_kernel<float>, dim3(rows), dim3(kThreads), 0, s, qkv, qrot, q_heads,
+        hipLaunchKernelGGL(rope_append_kernel<float>, grid, dim3(kThreads), 0, s, qkv, qrot, q_heads,
                            g.kv_heads, g.head_dim, rotary_dim, rope_cos, rope_sin, g.page_table, g.page_size,
                            (float *)kv.k, (float *)kv.v, (long)offset, pos_dev);
     else
-        hipLaunchKernelGGL(rope_append_kernel<uint16_t>, dim3(rows), dim3(kThreads), 0, s, qkv, qrot, q_heads,
+        hipLaunchKernelGGL(rope_append_kernel<uint16_t>, grid, dim3(kThreads), 0, s, qkv, qrot, q_heads,
                            g.kv_heads, g.head_dim, rotary_dim, rope_cos, rope_sin, g.page_table, g.page_size,
                            (uint16_t *)kv.k, (uint16_t *)kv.v, (long)offset, pos_dev);
     CHIP_CHECK(hipGetLastError());

@@ -813,10 +813,10 @@ int refresh_weights(cheetah_hip_model *m) {
     return 0;
 }
 
-// Attention splits of a decode step over `ctx` keys: ~128 positions each.
-int decode_splits(size_t ctx) {
-    const size_t s = (ctx + 127) / 128;
-    return (int)std::max<size_t>(1, std::min<size_t>(s, (size_t)attention_max_splits()));
+// Attention splits of a decode step over `ctx` keys (one captured graph per
+// split count).
+int decode_splits(const cheetah_hip_model *m, size_t ctx) {
+    return attention_decode_splits(ctx, (int)m->sh->cfg.kv_heads, 1);
 }
 
 // One decode step's kernels; token and position are read from step_dev.
@@ -897,7 +897,7 @@ bool graphs_enabled() {
 // One decode step at absolute position `pos` (the device step word must
 // already hold it): the captured graph for the step's split count.
 int launch_decode(cheetah_hip_model *m, size_t pos) {
-    const int splits = decode_splits(pos + 1);
+    const int splits = decode_splits(m, pos + 1);
     // Host-tier weights are fed by copies ordered with events on a second
     // stream: those steps run eagerly.
     if (!graphs_enabled() || m->sh->host_mats) return enqueue_decode(m, splits);
