@@ -211,6 +211,22 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(Args a) {
 }
 
 // ---------------------------------------------------------------------------
+// Q4 codes as BF16 pairs: nibble n of a dword (code c, n = c mod 16) gives
+// the BF16 0x4300 | (n ^ 8) = 128 + (c + 8) = 136 + c (exact), i.e.
+// (n & 0xF) ^ 0x4308: one shift and one AND-XOR (a single three-input
+// bit operation on gfx950) per pair; pair j holds nibbles j and j + 4.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ u32x4 q4_pairs(uint32_t w) {
+    u32x4 p;
+    p[0] = (w & 0x000F000Fu) ^ 0x43084308u;
+    p[1] = ((w >> 4) & 0x000F000Fu) ^ 0x43084308u;
+    p[2] = ((w >> 8) & 0x000F000Fu) ^ 0x43084308u;
+    p[3] = ((w >> 12) & 0x000F000Fu) ^ 0x43084308u;
+    return p;
+}
+
+
+// ---------------------------------------------------------------------------
 // Aligned-unit GEMV: every row is streamed as 16-byte units from its
 // 16-byte-aligned-down start, even when the reference layout only aligns rows
 // to 4 bytes (Q4 rows of 2052 / 7172 bytes, Q8 rows of K rounded up to 4).
@@ -224,6 +240,15 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(Args a) {
 // so each block stages x once and streams many row groups.
 // ---------------------------------------------------------------------------
 constexpr int kPad = 32;  // zero floats before and after x in LDS
+
+// Dynamic LDS of the aligned kernel: padded x and the norm gain as BF16.
+inline size_t aligned_lds(int K, bool norm) {
+    return (size_t)(K + 2 * kPad) * sizeof(float) + (norm ? (size_t)K * 2 + 16 : 0);
+}
+// Buffer descriptor word 3 for raw (untyped, unswizzled) buffer access on
+// gfx9-family chips, and the non-temporal cache policy bit of a buffer load.
+constexpr int kBufferDword3 = 0x00020000;
+constexpr int kBufferNT = 2;
 constexpr int kAThreads = 512;  // 8 waves share one x staging
 constexpr int kAWaves = kAThreads / 64;
 
@@ -242,7 +267,9 @@ __global__ __launch_bounds__(kAThreads) void gemv_aligned_kernel(Args a, int P) 
     __shared__ float kred[kAWaves][NM * R];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    // Wave-uniform, so the row pointers below live in scalar registers and
+    // make buffer descriptors without a per-lane loop.
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int sub = wave % KS, gib = wave / KS;
     const int klane = sub * 64 + lane;
     const int K = a.K;
@@ -251,6 +278,10 @@ __global__ __launch_bounds__(kAThreads) void gemv_aligned_kernel(Args a, int P) 
     const int groups = blocks_of_rows * P;
 
     const uint8_t *ap[NM][R];  // aligned-down row starts
+    // One buffer descriptor per row over its nfull whole units: a load past
+    // them returns zeros and moves no memory, so every batch load is issued
+    // unconditionally and the compiler can wait on exactly the older batch.
+    __amdgpu_buffer_rsrc_t rs[NM][R];
     int row_of[R];
     int shift = 0, nfull = 0;
     bool gvalid = false;
@@ -284,8 +315,15 @@ __global__ __launch_bounds__(kAThreads) void gemv_aligned_kernel(Args a, int P) 
             if constexpr (DUAL) ap[1][r] = a.w2 + (size_t)rr * a.stride - delta;
         }
     };
-    uint32_t cur[UNROLL][NM][R][D];
-    auto load_batch = [&](uint32_t (&buf)[UNROLL][NM][R][D], int u0) {
+    auto set_rsrc = [&]() {
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                rs[m][r] = __builtin_amdgcn_make_buffer_rsrc((void *)ap[m][r], (short)0, nfull * 16, kBufferDword3);
+    };
+    typedef uint32_t Batch[UNROLL][NM][R][D];
+    auto load_batch = [&](Batch &buf, int u0) {
 #pragma unroll
         for (int i = 0; i < UNROLL; ++i) {
             const int u = u0 + 64 * KS * i;
@@ -293,8 +331,12 @@ __global__ __launch_bounds__(kAThreads) void gemv_aligned_kernel(Args a, int P) 
             for (int m = 0; m < NM; ++m)
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
-                    if (u < nfull) load_raw<16>(ap[m][r] + (size_t)u * 16, buf[i][m][r]);
-                    else buf[i][m][r][0] = buf[i][m][r][1] = buf[i][m][r][2] = buf[i][m][r][3] = 0u;
+                    const u32x4 v = __builtin_bit_cast(
+                        u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs[m][r], u * 16, 0, kBufferNT));
+                    buf[i][m][r][0] = v[0];
+                    buf[i][m][r][1] = v[1];
+                    buf[i][m][r][2] = v[2];
+                    buf[i][m][r][3] = v[3];
                 }
         }
     };
@@ -302,9 +344,11 @@ __global__ __launch_bounds__(kAThreads) void gemv_aligned_kernel(Args a, int P) 
     int g = blockIdx.x * GPB + gib;
     const int gstride = gridDim.x * GPB;
     // The first row group's first batch is in flight while x is staged.
+    Batch A, B;
     if (g < groups) {
         set_group(g);
-        load_batch(cur, klane);
+        set_rsrc();
+        load_batch(A, klane);
     }
     for (int i = tid; i < kPad; i += kAThreads) {
         xs_all[i] = 0.f;
@@ -347,6 +391,56 @@ __global__ __launch_bounds__(kAThreads) void gemv_aligned_kernel(Args a, int P) 
             xs[i] = xs[i] * (inv * bf16_f32(dma_g ? gl[i] : a.gain[i]));
         __syncthreads();
     }
+    // acc += the batch's weights (units u0 + 64 KS i) times x.
+    auto mac_batch = [&](const Batch &cur, int u0, float (&acc)[NM][R]) {
+#pragma unroll
+        for (int i = 0; i < UNROLL; ++i) {
+            const int u = u0 + 64 * KS * i;
+            // One weight dword at a time: its E/4 x values (Q4 8, Q8 4,
+            // BF16 2) are read once and shared by every row. A unit past the
+            // row has zero weights (load_batch) and reads the last unit's x:
+            // LDS past x + padding holds whatever an earlier kernel left, and
+            // 0 * NaN is NaN.
+            const float *xu = xs + min(u, nfull - 1) * E - shift;
+#pragma unroll
+            for (int d = 0; d < D; ++d) {
+                constexpr int ED = E / 4;
+                float xv[ED];
+                if constexpr (ED >= 4) {
+#pragma unroll
+                    for (int q = 0; q < ED / 4; ++q) {
+                        const float4 t = ((const float4 *)(xu + d * ED))[q];
+                        xv[4 * q] = t.x;
+                        xv[4 * q + 1] = t.y;
+                        xv[4 * q + 2] = t.z;
+                        xv[4 * q + 3] = t.w;
+                    }
+                } else {
+                    const float2 t = *(const float2 *)(xu + d * ED);
+                    xv[0] = t.x;
+                    xv[1] = t.y;
+                }
+#pragma unroll
+                for (int m = 0; m < NM; ++m)
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        const uint32_t word = cur[i][m][r][d];
+                        if constexpr (FMT == FMT_Q4) {
+#pragma unroll
+                            for (int n = 0; n < 8; ++n)
+                                acc[m][r] = fmaf((float)(((int)(word << (28 - 4 * n))) >> 28), xv[n], acc[m][r]);
+                        } else if constexpr (FMT == FMT_Q8) {
+#pragma unroll
+                            for (int b = 0; b < 4; ++b)
+                                acc[m][r] = fmaf((float)(int)(int8_t)(word >> (8 * b)), xv[b], acc[m][r]);
+                        } else {
+                            acc[m][r] = fmaf(bf16_lo(word), xv[0], acc[m][r]);
+                            acc[m][r] = fmaf(bf16_hi(word), xv[1], acc[m][r]);
+                        }
+                    }
+            }
+        }
+    };
 
     // Every wave of the block runs the same number of iterations (the
     // cross-wave K reduction below synchronizes the block).
@@ -359,68 +453,23 @@ __global__ __launch_bounds__(kAThreads) void gemv_aligned_kernel(Args a, int P) 
 #pragma unroll
             for (int r = 0; r < R; ++r) acc[m][r] = 0.f;
         if (valid) {
-            for (int u0 = klane; u0 < nfull; u0 += STEP) {
-                uint32_t nxt[UNROLL][NM][R][D];
-                const bool more = u0 + STEP < nfull;
-                if (more) load_batch(nxt, u0 + STEP);
-#pragma unroll
-                for (int i = 0; i < UNROLL; ++i) {
-                    const int u = u0 + 64 * KS * i;
-                    // One weight dword at a time: its E/4 x values (Q4 8,
-                    // Q8 4, BF16 2) are read once and shared by every row.
-                    // A unit past the row has zero weights (load_batch) and
-                    // reads the last unit's x: LDS past x + padding holds
-                    // whatever an earlier kernel left, and 0 * NaN is NaN.
-                    const float *xu = xs + min(u, nfull - 1) * E - shift;
-#pragma unroll
-                    for (int d = 0; d < D; ++d) {
-                        constexpr int ED = E / 4;
-                        float xv[ED];
-                        if constexpr (ED >= 4) {
-#pragma unroll
-                            for (int q = 0; q < ED / 4; ++q) {
-                                const float4 t = ((const float4 *)(xu + d * ED))[q];
-                                xv[4 * q] = t.x;
-                                xv[4 * q + 1] = t.y;
-                                xv[4 * q + 2] = t.z;
-                                xv[4 * q + 3] = t.w;
-                            }
-                        } else {
-                            const float2 t = *(const float2 *)(xu + d * ED);
-                            xv[0] = t.x;
-                            xv[1] = t.y;
-                        }
-#pragma unroll
-                        for (int m = 0; m < NM; ++m)
-#pragma unroll
-                            for (int r = 0; r < R; ++r) {
-                                const uint32_t word = cur[i][m][r][d];
-                                if constexpr (FMT == FMT_Q4) {
-#pragma unroll
-                                    for (int n = 0; n < 8; ++n)
-                                        acc[m][r] = fmaf((float)(((int)(word << (28 - 4 * n))) >> 28), xv[n], acc[m][r]);
-                                } else if constexpr (FMT == FMT_Q8) {
-#pragma unroll
-                                    for (int b = 0; b < 4; ++b)
-                                        acc[m][r] = fmaf((float)(int)(int8_t)(word >> (8 * b)), xv[b], acc[m][r]);
-                                } else {
-                                    acc[m][r] = fmaf(bf16_lo(word), xv[0], acc[m][r]);
-                                    acc[m][r] = fmaf(bf16_hi(word), xv[1], acc[m][r]);
-                                }
-                            }
-                    }
-                }
-                if (more) {
-#pragma unroll
-                    for (int i = 0; i < UNROLL; ++i)
-#pragma unroll
-                        for (int m = 0; m < NM; ++m)
-#pragma unroll
-                            for (int r = 0; r < R; ++r)
-#pragma unroll
-                                for (int d = 0; d < D; ++d) cur[i][m][r][d] = nxt[i][m][r][d];
-                }
+            // Batches alternate between A and B, so no register copy (which
+            // would wait for the prefetch) separates a load from its use:
+            // batch j+1 streams in while batch j is multiplied. The batch
+            // count is wave-uniform; lanes past the row load zeros.
+            const int nb = (nfull - sub * 64 + STEP - 1) / STEP;
+            int j = 0;
+            // (The scheduling barriers keep the compiler from sinking a
+            // prefetch below the multiply-adds to save registers.)
+            for (; j + 2 <= nb; j += 2) {
+                load_batch(B, klane + (j + 1) * STEP);
+                __builtin_amdgcn_sched_barrier(0);
+                mac_batch(A, klane + j * STEP, acc);
+                load_batch(A, klane + (j + 2) * STEP);
+                __builtin_amdgcn_sched_barrier(0);
+                mac_batch(B, klane + (j + 1) * STEP, acc);
             }
+            if (j < nb) mac_batch(A, klane + j * STEP, acc);
             // Elements past the last whole unit (fewer than 16 bytes' worth).
             for (int e = max(nfull * E - shift, 0) + klane; e < K; e += 64 * KS) {
                 const float xv = xs[e];
@@ -441,7 +490,8 @@ __global__ __launch_bounds__(kAThreads) void gemv_aligned_kernel(Args a, int P) 
         // Prefetch the next group's first batch before the epilogue.
         if (g + gstride < groups) {
             set_group(g + gstride);
-            load_batch(cur, klane);
+            set_rsrc();
+            load_batch(A, klane);
         }
         if constexpr (KS > 1) {
             if (lane == 0) {
@@ -515,7 +565,7 @@ template <int FMT, int R, int KS, bool NORM, bool DUAL, int UNROLL>
 int launch_aligned(const Args &a, int P, hipStream_t s) {
     constexpr int GPB = kAWaves / KS;
     const int groups = (a.rows + R * P - 1) / (R * P) * P;
-    const size_t lds = (size_t)(a.K + 2 * kPad) * sizeof(float) + (NORM ? (size_t)a.K * 2 + 16 : 0);
+    const size_t lds = aligned_lds(a.K, NORM);
     auto kern = gemv_aligned_kernel<FMT, R, KS, NORM, DUAL, UNROLL>;
     const int cap = device_cus() * aligned_blocks_per_cu(kern, lds);
     const int blocks = std::max(1, std::min((groups + GPB - 1) / GPB, cap));
@@ -547,24 +597,31 @@ int pick_ks(const Args &a, int P, int ks, int n_units, hipStream_t s) {
 }
 
 // Rows per wave (R) and waves per row group (KS, splitting K), as measured
-// on MI355X: one row per wave streams BF16 / Q8 best; Q4 (twice the
-// elements per byte) gains from sharing each x read between 2-4 rows once
-// there are enough rows to keep every wave slot busy, except the dual
-// gate/up GEMV, which already reads two matrices per row: one row per wave
-// there (2 % faster than two on a 14336x4096 pair, four was 4 % slower). K is split only when
-// rows are too few for the wave slots, keeping >= 2 units per lane.
+// on MI355X (slots = 16 waves per CU): one row per wave streams BF16 / Q8
+// best. Q4 (twice the elements per byte) gains from sharing each x read
+// between rows once there are enough rows to keep the wave slots busy: two
+// rows per wave, four between 1.5 and 4 slots' worth of rows (not for the
+// dual gate/up GEMV, which already reads two matrices per row); measured
+// 5-12 % faster than one (dual 14336x4096: 20.1 vs 22.0 us). K is split when
+// the row groups are too few for the wave slots (Q4: below a quarter of
+// them, since its rows share x reads), keeping >= 2 units per lane.
 template <int FMT, bool NORM, bool DUAL>
 int pick_aligned(const Args &a, int P, hipStream_t s) {
     constexpr int E = Unit<FMT, 16>::E;
     const int n_units = (a.K + E - 1) / E;
     const long slots = (long)device_cus() * 16;
     int R = 1;
-    if constexpr (FMT == FMT_Q4 && !DUAL) R = a.rows >= 3 * slots ? 4 : (a.rows >= slots ? 2 : 1);
+    if constexpr (FMT == FMT_Q4) {
+        if (a.rows >= slots / 2) R = !DUAL && 2 * a.rows >= 3 * slots && a.rows < 4 * slots ? 4 : 2;
+    }
     const long groups = (a.rows + R - 1) / R;
+    const long busy = FMT == FMT_Q4 ? slots / 4 : slots;
     int ks = 1;
-    while (ks < 8 && groups * ks < slots && n_units >= 64 * 2 * ks * 2) ks *= 2;
-    if constexpr (FMT == FMT_Q4 && !DUAL) {
-        if (R == 4) return pick_ks<FMT, 4, NORM, DUAL>(a, P, ks, n_units, s);
+    while (ks < 8 && groups * ks < busy && n_units >= 64 * 2 * ks * 2) ks *= 2;
+    if constexpr (FMT == FMT_Q4) {
+        if (R == 4) {
+            if constexpr (!DUAL) return pick_ks<FMT, 4, NORM, DUAL>(a, P, ks, n_units, s);
+        }
         if (R == 2) return pick_ks<FMT, 2, NORM, DUAL>(a, P, ks, n_units, s);
     }
     return pick_ks<FMT, 1, NORM, DUAL>(a, P, ks, n_units, s);
@@ -636,10 +693,8 @@ int pick_mode(const Args &a, bool norm, bool dual, hipStream_t s) {
 // before their x group, so the B reads are shifted by whole groups, with
 // zero groups before and after x for the bytes outside the row.
 //
-// Persistent grid: a block stages x once and walks tiles blockIdx.x,
-// + gridDim.x, ...; its KS waves split each tile's k-steps, the next tile's
-// weights are loaded while the current one multiplies, and the KS partial
-// sums meet in LDS in wave order.
+// One tile per block: the block stages x, its KS waves split the tile's
+// k-steps, and their partial sums meet in LDS in wave order.
 // ---------------------------------------------------------------------------
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 constexpr int kQ4Front = 3;   // zero groups before x (delta / 4 <= 3)
@@ -656,16 +711,6 @@ bool q4_mfma_enabled() {
     return on;
 }
 
-__device__ __forceinline__ u32x4 q4_pairs(uint32_t w) {
-    w ^= 0x88888888u;
-    u32x4 p;
-    p[0] = (w & 0x000F000Fu) | 0x43004300u;
-    p[1] = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
-    p[2] = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
-    p[3] = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
-    return p;
-}
-
 struct Q4Geo {
     int P;           // rows between the rows of one tile
     int tiles;       // ceil(rows / (16 P)) * P
@@ -674,14 +719,21 @@ struct Q4Geo {
     int delta[4];    // misalignment of phase ph (tiles with tile % P == ph)
 };
 
-template <int KS, int SMAX, bool NORM, bool DUAL>
+// One 16-row tile per block; KS waves split its k-steps. Each wave streams
+// its steps through a ring of QR register sets, QR - 1 steps in flight ahead
+// of the one it multiplies, so load issue (which stalls while the memory
+// system is saturated), x staging and the MFMAs overlap instead of running
+// one after another.
+constexpr int QR = 4;
+
+template <int KS, bool NORM, bool DUAL>
 __global__ __launch_bounds__(64 * KS) void gemv_q4_mfma_kernel(Args a, Q4Geo geo, const uint8_t *wbase,
                                                               const uint8_t *wbase2) {
     constexpr int NT = 64 * KS;
     constexpr int NM = DUAL ? 2 : 1;
     constexpr int XG = 4;  // x groups a thread stages per round (loads first, then conversion)
     extern __shared__ u32x4 xq[];  // groups: [hi 8 x bf16][lo 8 x bf16], then per group sum(hi + lo)
-    __shared__ float red[2][KS][NM + 1][16][2];  // [.][.][NM] holds the x sums
+    __shared__ float red[KS][NM + 1][16][2];  // [.][NM] holds the x sums
     __shared__ float nred[KS];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int K = a.K;
@@ -693,40 +745,27 @@ __global__ __launch_bounds__(64 * KS) void gemv_q4_mfma_kernel(Args a, Q4Geo geo
     const __amdgpu_buffer_rsrc_t rs1 =
         __builtin_amdgcn_make_buffer_rsrc((void *)(DUAL ? wbase2 : wbase), (short)0, (int)geo.total, 0x00020000);
     const int P = geo.P;
+    const int tile = blockIdx.x;
+    const int ph = tile % P, dl = geo.delta[ph], sh = dl / 4;
+    // This wave's k-steps of the tile: [s0, s1).
+    const int nst = (geo.row_bytes + dl + 63) / 64;
+    const int per = (nst + KS - 1) / KS;
+    const int s0 = min(nst, wave * per), s1 = min(nst, s0 + per);
+    const int row = (tile / P) * 16 * P + ph + P * r;
+    const uint32_t base = geo.payload_off + (uint32_t)row * (uint32_t)a.stride - (uint32_t)dl;
 
-    // This wave's k-steps of a tile of phase ph: [s0, s1).
-    auto range = [&](int ph, int &s0, int &s1) {
-        const int nst = (geo.row_bytes + geo.delta[ph] + 63) / 64;
-        const int per = (nst + KS - 1) / KS;
-        s0 = min(nst, wave * per);
-        s1 = min(nst, s0 + per);
-    };
-    auto row_of = [&](int tile, int j) { return (tile / P) * 16 * P + tile % P + P * j; };
-
-    // Weight units of one tile into registers (rows past the matrix and
-    // units wholly past a row's codes read nothing: out-of-range offsets).
-    auto issue = [&](u32x4 (&wr)[NM][SMAX], int tile) {
-        const int ph = tile % P, dl = geo.delta[ph];
-        int s0, s1;
-        range(ph, s0, s1);
-        const int row = row_of(tile, r);
-        const uint32_t base = geo.payload_off + (uint32_t)row * (uint32_t)a.stride - (uint32_t)dl;
-#pragma unroll
-        for (int i = 0; i < SMAX; ++i) {
-            const int t = s0 + i;
-            const int lb = 64 * t + 16 * g - dl;  // first byte of the unit, from the row start
-            const bool on = row < a.rows && t < s1 && lb < geo.row_bytes;
-            const uint32_t off = on ? base + 64u * (uint32_t)t + 16u * (uint32_t)g : 0x80000000u;
-            wr[0][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs0, off, 0, 2));
-            if constexpr (DUAL)
-                wr[1][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs1, off, 0, 2));
-        }
+    // Step t's weight units (steps past the wave's range, rows past the
+    // matrix and units wholly past a row's codes read nothing). Issued for
+    // every ring slot on every path, so the compiler counts loads exactly.
+    auto issue = [&](u32x4 (&wr)[NM], int t) {
+        const int lb = 64 * t + 16 * g - dl;  // first byte of the unit, from the row start
+        const bool on = row < a.rows && t < s1 && lb < geo.row_bytes;
+        const uint32_t off = on ? base + 64u * (uint32_t)t + 16u * (uint32_t)g : 0x80000000u;
+        wr[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs0, off, 0, 2));
+        if constexpr (DUAL) wr[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs1, off, 0, 2));
     };
 
-    // x (normed when NORM) as BF16 halves in the nibble-pair order: each
-    // round loads XG groups per thread, then converts and stores them. The
-    // first round's x loads go out before this block's weights, so x arrives
-    // first and the conversion overlaps the weight stream.
+    // x loads first (they return first), then the first QR - 1 steps.
     const bool vec_x = ((uintptr_t)a.x & 15) == 0;
     float v[XG][8];
     auto load_x = [&](int q0) {
@@ -747,10 +786,11 @@ __global__ __launch_bounds__(64 * KS) void gemv_q4_mfma_kernel(Args a, Q4Geo geo
         }
     };
     load_x(0);
-    u32x4 wa[NM][SMAX], wb[NM][SMAX];
-    int tile = blockIdx.x;
-    if (tile < geo.tiles) issue(wa, tile);
+    u32x4 ring[QR][NM];
+#pragma unroll
+    for (int q = 0; q < QR - 1; ++q) issue(ring[q], s0 + q);
 
+    // x (normed when NORM) as BF16 halves in the nibble-pair order.
     float inv = 1.f;
     if constexpr (NORM) {
         float ss = 0.f;
@@ -794,161 +834,98 @@ __global__ __launch_bounds__(64 * KS) void gemv_q4_mfma_kernel(Args a, Q4Geo geo
     __syncthreads();
 
     // Columns 0 and 1 read x; the other lanes read the first (zero) group,
-    // one broadcast address, so every lane issues the same LDS reads and the
-    // compiler's waits stay exact.
-    auto bread = [&](int qi) { return n < 2 ? xq[2 * qi + n] : xq[0]; };
-    auto compute = [&](u32x4 (&wr)[NM][SMAX], int tl, int par) {
-        const int ph = tl % P, sh = geo.delta[ph] / 4;
-        int s0, s1;
-        range(ph, s0, s1);
-        f32x4 acc[NM][2];
+    // one broadcast address, so every lane issues the same LDS reads.
+    f32x4 acc[NM][2];
 #pragma unroll
-        for (int m = 0; m < NM; ++m) acc[m][0] = acc[m][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-        // Column-0 lanes also add up the group sums of their B groups: over
-        // the wave's four of them, the x sum the offset 136 multiplies.
-        float xs = 0.f;
-        const int qb = kQ4Front + 16 * s0 + 4 * g - sh;
-        u32x4 bcur[4], bnxt[4];
+    for (int m = 0; m < NM; ++m) acc[m][0] = acc[m][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // Column-0 lanes also add up the group sums of their B groups: over the
+    // wave's four of them, the x sum the offset 136 multiplies.
+    float xs = 0.f;
+    const int qb = kQ4Front + 4 * g - sh;
+    for (int t0 = s0; t0 < s1; t0 += QR) {
 #pragma unroll
-        for (int d = 0; d < 4; ++d) bcur[d] = bread(qb + d);
-#pragma unroll
-        for (int i = 0; i < SMAX; ++i) {
-            const int t = s0 + i;
+        for (int q = 0; q < QR; ++q) {
+            const int t = t0 + q;
+            // Step t + QR - 1 into the slot step t - 1 used.
+            issue(ring[(q + QR - 1) % QR], t + QR - 1);
             if (t < s1) {
-                if (i + 1 < SMAX) {
-#pragma unroll
-                    for (int d = 0; d < 4; ++d) bnxt[d] = bread(qb + 16 * (i + 1) + d);
-                }
+                const int qs = qb + 16 * t;
 #pragma unroll
                 for (int d = 0; d < 4; ++d) {
-                    const bf16x8_t b = __builtin_bit_cast(bf16x8_t, bcur[d]);
+                    const u32x4 bx = n < 2 ? xq[2 * (qs + d) + n] : xq[0];
+                    const bf16x8_t b = __builtin_bit_cast(bf16x8_t, bx);
 #pragma unroll
                     for (int m = 0; m < NM; ++m) {
-                        const bf16x8_t av = __builtin_bit_cast(bf16x8_t, q4_pairs(wr[m][i][d]));
+                        const bf16x8_t av = __builtin_bit_cast(bf16x8_t, q4_pairs(ring[q][m][d]));
                         acc[m][d & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b, acc[m][d & 1], 0, 0, 0);
                     }
-                    xs += gsum[qb + 16 * i + d];
-                }
-#pragma unroll
-                for (int d = 0; d < 4; ++d) bcur[d] = bnxt[d];
-            }
-        }
-        // Lane L holds rows 4 (L / 16) + j of column L % 16.
-        if (n < 2) {
-#pragma unroll
-            for (int m = 0; m < NM; ++m)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) red[par][wave][m][4 * g + j][n] = acc[m][0][j] + acc[m][1][j];
-            red[par][wave][NM][g][n] = n == 0 ? xs : 0.f;
-        }
-        __syncthreads();
-        if (tid < 16) {
-            const int row = row_of(tl, tid);
-            if (row < a.rows) {
-                float v[NM];
-#pragma unroll
-                for (int m = 0; m < NM; ++m) {
-                    double s = 0.0;
-#pragma unroll
-                    for (int w = 0; w < KS; ++w) {
-                        float sx = 0.f;
-#pragma unroll
-                        for (int q = 0; q < 4; ++q) sx += red[par][w][NM][q][0] + red[par][w][NM][q][1];
-                        s += ((double)red[par][w][m][tid][0] + (double)red[par][w][m][tid][1]) - 136.0 * (double)sx;
-                    }
-                    v[m] = (float)s;
-                }
-                float o = v[0];
-                if (a.sc) o = o * a.sc[row];
-                if constexpr (DUAL) {
-                    float u = v[1];
-                    if (a.sc2) u = u * a.sc2[row];
-                    // silu_multiply, ops.rs:743-747: g * (u / (1 + exp(-g))).
-                    a.y[row] = o * (u / (1.0f + expf(-o)));
-                } else {
-                    if (a.bias) o = o + a.bias[row];
-                    if (a.epi == EPI_RESIDUAL) a.residual[row] = a.residual[row] + o;
-                    else a.y[row] = o;
+                    xs += gsum[qs + d];
                 }
             }
         }
-    };
-
-    // Two tiles per iteration, register buffers alternating; red alternates
-    // too, so one barrier per tile separates its writes from the next reads.
-    for (; tile < geo.tiles; tile += 2 * gridDim.x) {
-        const int t2 = tile + gridDim.x;
-        if (t2 < geo.tiles) issue(wb, t2);
-        compute(wa, tile, 0);
-        if (t2 >= geo.tiles) break;
-        if (t2 + gridDim.x < geo.tiles) issue(wa, t2 + gridDim.x);
-        compute(wb, t2, 1);
+    }
+    // Lane L holds rows 4 (L / 16) + j of column L % 16.
+    if (n < 2) {
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) red[wave][m][4 * g + j][n] = acc[m][0][j] + acc[m][1][j];
+        red[wave][NM][g][n] = n == 0 ? xs : 0.f;
+    }
+    __syncthreads();
+    if (tid < 16) {
+        const int orow = (tile / P) * 16 * P + ph + P * tid;
+        if (orow < a.rows) {
+            float vv[NM];
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+                double sum = 0.0;
+#pragma unroll
+                for (int w = 0; w < KS; ++w) {
+                    float sx = 0.f;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) sx += red[w][NM][q][0] + red[w][NM][q][1];
+                    sum += ((double)red[w][m][tid][0] + (double)red[w][m][tid][1]) - 136.0 * (double)sx;
+                }
+                vv[m] = (float)sum;
+            }
+            float o = vv[0];
+            if (a.sc) o = o * a.sc[orow];
+            if constexpr (DUAL) {
+                float u = vv[1];
+                if (a.sc2) u = u * a.sc2[orow];
+                // silu_multiply, ops.rs:743-747: g * (u / (1 + exp(-g))).
+                a.y[orow] = o * (u / (1.0f + expf(-o)));
+            } else {
+                if (a.bias) o = o + a.bias[orow];
+                if (a.epi == EPI_RESIDUAL) a.residual[orow] = a.residual[orow] + o;
+                else a.y[orow] = o;
+            }
+        }
     }
 }
 
-template <int KS, int SMAX, bool NORM, bool DUAL>
+template <int KS, bool NORM, bool DUAL>
 int launch_q4_mfma_ks(const Args &a, const Q4Geo &geo, const uint8_t *wb, const uint8_t *wb2, hipStream_t s) {
     const int ngroups = (a.K + 7) / 8;
     const size_t lds = (size_t)(kQ4Front + ngroups + kQ4Back) * 36;
-    auto kern = gemv_q4_mfma_kernel<KS, SMAX, NORM, DUAL>;
-    static int regs = 0;
-    if (regs == 0) {
-        hipFuncAttributes attr{};
-        regs = hipFuncGetAttributes(&attr, (const void *)kern) == hipSuccess && attr.numRegs > 0 ? attr.numRegs : 256;
-    }
-    // Waves per SIMD the register file allows (512 per lane, granule 8), so
-    // blocks per CU; and what LDS allows.
-    const int waves_simd = std::min(8, 512 / ((regs + 7) / 8 * 8));
-    const int per_cu = std::max(1, std::min(waves_simd * 4 / KS, (int)(device_lds_per_cu() / (lds + 8192))));
-    const int blocks = std::max(1, std::min(geo.tiles, device_cus() * per_cu));
-    hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * KS), lds, s, a, geo, wb, wb2);
+    hipLaunchKernelGGL((gemv_q4_mfma_kernel<KS, NORM, DUAL>), dim3(geo.tiles), dim3(64 * KS), lds, s, a, geo, wb, wb2);
     CHIP_CHECK(hipGetLastError());
     return 0;
 }
 
-// Waves per tile (KS): the fewest that keep a wave's k-steps within 8
-// registers' worth (16 at eight waves), doubled while tiles x KS leave wave
-// slots idle and each wave keeps >= 4 k-steps. Returns 1 when the kernel
-// took the job, 0 when the shape does not fit it (more than 8 x 16 k-steps
-// per tile).
+// Waves per tile (KS): doubled while tiles x KS leave wave slots idle and
+// each wave keeps at least QR k-steps.
 template <bool NORM, bool DUAL>
-int try_q4_mfma(const Args &a, const Q4Geo &geo, const uint8_t *wb, const uint8_t *wb2, hipStream_t s, int *rc) {
+int launch_q4_mfma(const Args &a, const Q4Geo &geo, const uint8_t *wb, const uint8_t *wb2, hipStream_t s) {
     const int nst = (geo.row_bytes + 12 + 63) / 64;
     int ks = 1;
-    while (ks < 8 && (nst + ks - 1) / ks > 8) ks *= 2;
-    if ((nst + ks - 1) / ks > 16) return 0;
-    while (ks < 8 && (long)geo.tiles * ks < (long)device_cus() * 8 && nst >= 4 * ks) ks *= 2;
-    const int per = (nst + ks - 1) / ks;
-    auto go = [&](auto ksc, auto smc) {
-        *rc = launch_q4_mfma_ks<decltype(ksc)::value, decltype(smc)::value, NORM, DUAL>(a, geo, wb, wb2, s);
-        return 1;
-    };
-    using I1 = std::integral_constant<int, 1>;
-    using I2 = std::integral_constant<int, 2>;
-    using I4 = std::integral_constant<int, 4>;
-    using I8 = std::integral_constant<int, 8>;
-    using I16 = std::integral_constant<int, 16>;
-    if (per <= 4) {
-        switch (ks) {
-            case 8: return go(I8{}, I4{});
-            case 4: return go(I4{}, I4{});
-            case 2: return go(I2{}, I4{});
-            default: return go(I1{}, I4{});
-        }
-    }
-    if (per <= 8) {
-        switch (ks) {
-            case 8: return go(I8{}, I8{});
-            case 4: return go(I4{}, I8{});
-            case 2: return go(I2{}, I8{});
-            default: return go(I1{}, I8{});
-        }
-    }
+    while (ks < 8 && (long)geo.tiles * ks < (long)device_cus() * 16 && nst >= 2 * QR * ks) ks *= 2;
     switch (ks) {
-        case 8: return go(I8{}, I16{});
-        case 4: return go(I4{}, I16{});
-        case 2: return go(I2{}, I16{});
-        default: return go(I1{}, I16{});
+        case 8: return launch_q4_mfma_ks<8, NORM, DUAL>(a, geo, wb, wb2, s);
+        case 4: return launch_q4_mfma_ks<4, NORM, DUAL>(a, geo, wb, wb2, s);
+        case 2: return launch_q4_mfma_ks<2, NORM, DUAL>(a, geo, wb, wb2, s);
+        default: return launch_q4_mfma_ks<1, NORM, DUAL>(a, geo, wb, wb2, s);
     }
 }
 
@@ -994,12 +971,10 @@ int launch_gemv(const GemvJob &job, hipStream_t s) {
         geo.total = (uint32_t)w.bytes();
         for (int ph = 0; ph < 4; ++ph)
             geo.delta[ph] = (int)(((uintptr_t)a.w + (size_t)ph * a.stride) % 16);
-        int rc = 0;
-        const int took = norm ? (dual ? try_q4_mfma<true, true>(a, geo, w.base, job.w2.base, s, &rc)
-                                      : try_q4_mfma<true, false>(a, geo, w.base, nullptr, s, &rc))
-                              : (dual ? try_q4_mfma<false, true>(a, geo, w.base, job.w2.base, s, &rc)
-                                      : try_q4_mfma<false, false>(a, geo, w.base, nullptr, s, &rc));
-        if (took) return rc;
+        if (norm) return dual ? launch_q4_mfma<true, true>(a, geo, w.base, job.w2.base, s)
+                              : launch_q4_mfma<true, false>(a, geo, w.base, nullptr, s);
+        return dual ? launch_q4_mfma<false, true>(a, geo, w.base, job.w2.base, s)
+                    : launch_q4_mfma<false, false>(a, geo, w.base, nullptr, s);
     }
     // The aligned kernel needs 4-byte-aligned rows whose misalignment is a
     // multiple of 4 x floats (BF16: rows 16-byte aligned), gate and up
@@ -1009,8 +984,7 @@ int launch_gemv(const GemvJob &job, hipStream_t s) {
     // The aligned-down start of the first row must not precede the buffer.
     const bool aligned_ok = a.stride % bpe_mod == 0 && b0 % bpe_mod == 0 && (uintptr_t)w.base % 16 == 0 &&
                             (!dual || ((uintptr_t)job.w2.base % 16 == 0 && ((uintptr_t)a.w2 - b0) % 16 == 0)) &&
-                            (size_t)(a.K + 2 * kPad) * sizeof(float) + (norm ? (size_t)a.K * 2 + 16 : 0) + 256 <=
-                                device_max_lds();
+                            aligned_lds(a.K, norm) + 256 <= device_max_lds();
     if (aligned_ok) {
         const int sm = (int)(a.stride % 16);
         const int P = sm == 0 ? 1 : 16 / std::gcd(sm, 16);
