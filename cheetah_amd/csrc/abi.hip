@@ -295,7 +295,7 @@ static AttnJob attention_job(const float *q, const cheetah_hip_kv_view *kv, uint
     j.q_heads = (int)q_heads;
     j.rows = rows;
     j.offset = offset;
-    const size_t splits = (size_t)attention_decode_splits(offset + rows, (int)kv->kv_heads, rows);
+    const size_t splits = (size_t)attention_decode_splits(offset + rows, (int)kv->kv_heads, rows, false);
     j.splits = (int)splits;
     j.prefill = rows > 1;
     size_t need = attention_part_floats(rows, (int)q_heads, (int)splits, (int)kv->head_dim);

@@ -163,7 +163,7 @@ int launch_attention(const AttnJob &job, hipStream_t s);
 size_t attention_part_floats(size_t rows, int q_heads, int splits, int head_dim);
 // Split count of a decode-style launch (one row per query position) over ctx
 // keys: about two blocks per CU, at most one split per 64-position tile.
-int attention_decode_splits(size_t ctx, int kv_heads, size_t rows);
+int attention_decode_splits(size_t ctx, int kv_heads, size_t rows, bool kv_f32);
 int attention_max_splits();
 int attention_prefill_splits(size_t ctx);
 bool attention_prefill_on_mfma(const KvGeom &g, int q_heads);

@@ -816,7 +816,7 @@ int refresh_weights(cheetah_hip_model *m) {
 // Attention splits of a decode step over `ctx` keys (one captured graph per
 // split count).
 int decode_splits(const cheetah_hip_model *m, size_t ctx) {
-    return attention_decode_splits(ctx, (int)m->sh->cfg.kv_heads, 1);
+    return attention_decode_splits(ctx, (int)m->sh->cfg.kv_heads, 1, m->sh->kv_f32 != 0);
 }
 
 // One decode step's kernels; token and position are read from step_dev.
