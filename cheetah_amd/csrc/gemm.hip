@@ -21,6 +21,7 @@
 // same bits, so a token's outputs never depend on how many tokens share the
 // call (chunked prefill stays bit-exact however the prompt is cut).
 #include <algorithm>
+#include <cstdlib>
 
 #include "kernels.hpp"
 
@@ -300,7 +301,19 @@ __device__ __forceinline__ void epilogue_tile(const GArgs &a, const f32x16 (&tot
     }
 }
 
-// blockIdx: x = weight-row tile, y = token tile, z = chunk (split-K) or 0.
+// Output tile of this block. Blocks are numbered so that the token tiles of
+// one weight-row tile are consecutive, and (with the 8 XCDs taking block ids
+// round-robin) run on one XCD: each weight tile streams from HBM about once
+// and the block's neighbours find it in that XCD's L2, instead of every token
+// tile re-reading the whole matrix.
+__device__ __forceinline__ void tile_of(int nN, int nM, int &n0, int &m0, int BMt) {
+    const int total = nN * nM, bid = blockIdx.x;
+    const int lid = total % 8 == 0 ? (bid % 8) * (total / 8) + bid / 8 : bid;
+    m0 = (lid % nM) * BMt;
+    n0 = (lid / nM) * BN;
+}
+
+// blockIdx: x = output tile (tile_of), z = chunk (split-K) or 0.
 template <int FMT, bool DUAL, int MT, bool PRE>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GArgs a, int split) {
     constexpr int BM = 64 * MT;
@@ -309,7 +322,8 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GArgs a, int split) {
     __shared__ __attribute__((aligned(16))) uint16_t wsm[2][BN * LDK];
     __shared__ __attribute__((aligned(16))) uint16_t wsm2[DUAL ? 2 : 1][DUAL ? BN * LDK : 8];
 
-    const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+    int n0, m0;
+    tile_of((a.N + BN - 1) / BN, (a.M + BM - 1) / BM, n0, m0, BM);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = (wave >> 1) * 32 * MT, wn = (wave & 1) * 64;
     const int kbeg = split ? blockIdx.z * a.chunk : 0;
@@ -445,7 +459,8 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GArgs a, int split) 
     static_assert(NI % 4 == 0, "stage copies must split evenly over the waves");
     extern __shared__ __attribute__((aligned(16))) uint16_t ring[];
 
-    const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+    int n0, m0;
+    tile_of((a.N + BN - 1) / BN, (a.M + BM - 1) / BM, n0, m0, BM);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = (wave >> 1) * 32 * MT, wn = (wave & 1) * 64;
     const int kbeg = split ? blockIdx.z * a.chunk : 0;
@@ -572,6 +587,288 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GArgs a, int split) 
     }
 }
 
+// ---------------------------------------------------------------------------
+// Ring GEMM, every weight format (x pre-split, K % 32 == 0). Per 32-wide K
+// stage the block's x halves and its raw weight bytes (BF16 rows, Q8 codes,
+// Q4 nibbles) go global -> LDS by buffer loads that write LDS directly: a
+// lane's source offset is fixed for the whole launch and the stage's K
+// offset is a scalar, so issuing a stage costs no vector instructions. The
+// ring holds NS stages; stage s + NS - 2 is issued while stage s computes.
+// Q8/Q4 codes of stage s + 1 are converted to BF16 (exactly) once per block,
+// 16 per thread, into one of three converted tiles while stage s computes;
+// BF16 weights are read straight from the ring. One barrier per stage. The
+// MFMA sequence per output and the chunk folds are those of gemm_kernel and
+// gemm_dma_kernel, so the results are the same bits.
+// ---------------------------------------------------------------------------
+template <int FMT>
+constexpr int ring_w_row_bytes() { return FMT == FMT_BF16 ? 64 : FMT == FMT_Q8 ? 32 : 16; }
+
+template <int FMT, bool DUAL, int MT, int NS>
+constexpr size_t ring_lds_bytes() {
+    constexpr size_t slot = 2 * (64 * MT) * 64 + (DUAL ? 2 : 1) * BN * ring_w_row_bytes<FMT>();
+    return NS * slot + (FMT == FMT_BF16 ? 0 : 3 * (DUAL ? 2 : 1) * BN * 64);
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// size bytes per lane from buffer r at voffset + soffset into LDS at
+// lds + size * lane (lds wave-uniform).
+template <int SIZE>  // 16 or 4
+__device__ __forceinline__ void buf_to_lds(__amdgpu_buffer_rsrc_t r, void *lds, int voffset, int soffset) {
+    if constexpr (SIZE == 16) __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds, 16, voffset, soffset, 0, 0);
+    else __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds, 4, voffset, soffset, 0, 0);
+}
+
+template <int FMT, bool DUAL, int MT, int NS>
+__global__ __launch_bounds__(kThreads) void gemm_ring_kernel(GArgs a, int split) {
+    constexpr int BM = 64 * MT;
+    constexpr int XB = BM * 64;                      // bytes of one x half tile (BM rows x 32 BF16)
+    constexpr int WRB = ring_w_row_bytes<FMT>();     // raw weight bytes per row and stage
+    constexpr int WB = BN * WRB;                     // raw weight bytes per matrix and stage
+    constexpr int NWM = DUAL ? 2 : 1;
+    constexpr int SLOT = 2 * XB + NWM * WB;
+    constexpr bool CONV = FMT != FMT_BF16;
+    constexpr int WCB = BN * 64;                     // one converted BF16 weight tile
+    constexpr int GW = FMT == FMT_Q4 ? 4 : 16;       // weight copy granule (Q4 rows are 4-byte aligned)
+    constexpr int NIX = XB / 1024;                   // 1 KB copies per x half
+    constexpr int NIW = WB / (64 * GW);              // copies per weight matrix
+    constexpr int D = 2 * NIX / 4 + NWM * NIW / 4;   // copies per wave and stage
+    static_assert(NIX % 4 == 0 && NIW % 4 == 0, "copies must split evenly over the waves");
+    static_assert(NS >= 4, "the converted weights trail the ring by one stage");
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    uint8_t *ring = smem;
+    uint8_t *wcv = smem + NS * SLOT;  // CONV: [3][NWM] converted tiles
+
+    int n0, m0;
+    tile_of((a.N + BN - 1) / BN, (a.M + BM - 1) / BM, n0, m0, BM);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int wm = (wave >> 1) * 32 * MT, wn = (wave & 1) * 64;
+    const int kbeg = split ? blockIdx.z * a.chunk : 0;
+    const int kend = split ? min(a.K, kbeg + a.chunk) : a.K;
+    const int nst = (kend - kbeg) / BK;
+
+    const __amdgpu_buffer_rsrc_t rxh = __builtin_amdgcn_make_buffer_rsrc((void *)a.xh, (short)0, a.M * a.K * 2, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rxl = __builtin_amdgcn_make_buffer_rsrc((void *)a.xl, (short)0, a.M * a.K * 2, 0x00020000);
+    const int wbytes = (int)((size_t)a.N * a.stride);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void *)a.w, (short)0, wbytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rw2 =
+        __builtin_amdgcn_make_buffer_rsrc((void *)(DUAL ? a.w2 : a.w), (short)0, wbytes, 0x00020000);
+
+    // Per-lane source offsets of this wave's copies (fixed for the launch):
+    // x copy q covers rows 16q..16q+15, lane -> row 16q + lane/4 and 16-byte
+    // chunk swz(row, lane % 4) of the stage's 32 columns.
+    int xoff[NIX / 4], woff[NIW / 4];
+#pragma unroll
+    for (int i = 0; i < NIX / 4; ++i) {
+        const int q = wave + 4 * i, r = 16 * q + (lane >> 2);
+        const int m = min(m0 + r, a.M - 1);  // rows past M feed only unstored outputs
+        xoff[i] = (m * a.K + 8 * swz(r, lane & 3)) * 2;
+    }
+#pragma unroll
+    for (int i = 0; i < NIW / 4; ++i) {
+        const int q = wave + 4 * i;
+        int r, byte;
+        if constexpr (FMT == FMT_BF16) { r = 16 * q + (lane >> 2); byte = 16 * swz(r, lane & 3); }
+        else if constexpr (FMT == FMT_Q8) { r = 32 * q + (lane >> 1); byte = 16 * (lane & 1); }
+        else { r = 16 * q + (lane >> 2); byte = 4 * (lane & 3); }
+        const int n = min(n0 + r, a.N - 1);
+        woff[i] = n * (int)a.stride + byte;
+    }
+    // Stage st's copies into ring slot st % NS (stages past the range re-read
+    // the last one into a free slot, so every wave issues the same count).
+    auto issue = [&](int st) {
+        const int k0 = kbeg + min(st, nst - 1) * BK;
+        uint8_t *slot = ring + (st % NS) * SLOT;
+        const int kx = k0 * 2;
+        const int kw = FMT == FMT_BF16 ? k0 * 2 : FMT == FMT_Q8 ? k0 : k0 / 2;
+#pragma unroll
+        for (int i = 0; i < NIX / 4; ++i) {
+            const int q = wave + 4 * i;
+            buf_to_lds<16>(rxh, slot + 1024 * q, xoff[i], kx);
+            buf_to_lds<16>(rxl, slot + XB + 1024 * q, xoff[i], kx);
+        }
+#pragma unroll
+        for (int i = 0; i < NIW / 4; ++i) {
+            const int q = wave + 4 * i;
+            buf_to_lds<GW>(rw, slot + 2 * XB + 64 * GW * q, woff[i], kw);
+            if constexpr (DUAL)
+                buf_to_lds<GW>(rw2, slot + 2 * XB + WB + 64 * GW * q, woff[i], kw);
+        }
+    };
+    // Q8/Q4: stage st's codes -> BF16 tile(s) wcv[st % 3], thread t: row t/2,
+    // codes 16 (t % 2) .. + 15, written in the swizzled layout the MFMA reads.
+    // The raw codes are read by inline assembly: the compiler, which cannot
+    // tell these reads from the ring's in-flight copies, would otherwise wait
+    // for every copy (all NS stages) before them. The copies they need were
+    // awaited explicitly.
+    auto convert = [&](int st) {
+        const uint8_t *slot = ring + (st % NS) * SLOT + 2 * XB;
+        const int row = threadIdx.x >> 1, h = threadIdx.x & 1;
+        // (Each read waits for its data inside its own asm statement, so no
+        // use of the result can be scheduled ahead of the wait.)
+        u32x4 rv[NWM];
+#pragma unroll
+        for (int mi = 0; mi < NWM; ++mi) {
+            const uint32_t addr = (uint32_t)(uintptr_t)(slot + mi * WB + row * WRB + (FMT == FMT_Q8 ? 16 : 8) * h);
+            if constexpr (FMT == FMT_Q8) {
+                asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(rv[mi]) : "v"(addr) : "memory");
+            } else {
+                uint2 t;
+                asm volatile("ds_read_b64 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(t) : "v"(addr) : "memory");
+                rv[mi] = u32x4{t.x, t.y, 0u, 0u};
+            }
+        }
+#pragma unroll
+        for (int mi = 0; mi < NWM; ++mi) {
+            float f[16];
+            if constexpr (FMT == FMT_Q8) {
+                const u32x4 v = rv[mi];
+#pragma unroll
+                for (int q = 0; q < 16; ++q) f[q] = (float)(int)(int8_t)(v[q >> 2] >> (8 * (q & 3)));
+            } else {
+                const uint2 v = make_uint2(rv[mi][0], rv[mi][1]);
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    const uint32_t wd = q < 8 ? v.x : v.y;
+                    f[q] = (float)(((int)(wd << (28 - 4 * (q & 7)))) >> 28);
+                }
+            }
+            uint8_t *dst = wcv + ((st % 3) * NWM + mi) * WCB + row * 64;
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                bf16x8 b;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) b[e] = (__bf16)f[8 * c + e];
+                *(bf16x8 *)(dst + 16 * swz(row, 2 * h + c)) = b;
+            }
+        }
+    };
+
+    f32x16 acc[MT][2], acc2[DUAL ? MT : 1][2], tot[MT][2], tot2[DUAL ? MT : 1][2];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            tot[i][j] = f32x16{};
+            if constexpr (DUAL) tot2[i][j] = f32x16{};
+        }
+
+#pragma unroll
+    for (int st = 0; st < NS - 2; ++st) issue(st);
+    if constexpr (CONV) {
+        __builtin_amdgcn_s_waitcnt(vm_wait_imm(D * (NS - 3)));
+        __builtin_amdgcn_s_barrier();
+        convert(0);
+    }
+    const int cs = a.chunk / BK;  // stages per accumulation chunk
+    for (int c0 = 0; c0 < nst; c0 += cs) {
+        const int c1 = min(c0 + cs, nst);
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                acc[i][j] = f32x16{};
+                if constexpr (DUAL) acc2[i][j] = f32x16{};
+            }
+        for (int st = c0; st < c1; ++st) {
+            issue(st + NS - 2);
+            // This wave's copies of stage st (and, converting, st + 1) have
+            // landed once only the later stages' copies are pending; after
+            // the barrier every wave's have, and the tile converted in the
+            // previous iteration is visible.
+            __builtin_amdgcn_s_waitcnt(vm_wait_imm(D * (CONV ? NS - 3 : NS - 2)));
+            __builtin_amdgcn_s_waitcnt(vm_wait_imm(63) & ~(0xF << 8));  // lgkmcnt(0)
+            __builtin_amdgcn_s_barrier();
+            if constexpr (CONV) {
+                if (st + 1 < nst) convert(st + 1);
+            }
+            const uint8_t *xs = ring + (st % NS) * SLOT;
+            const uint8_t *wt = CONV ? wcv + (st % 3) * NWM * WCB : xs + 2 * XB;
+            const uint8_t *wt2 = wt + (CONV ? WCB : WB);
+#pragma unroll
+            for (int ks = 0; ks < BK; ks += 16) {
+                const int c = (ks >> 3) + (lane >> 5);
+                bf16x8 ah[MT], al[MT], bw[2], bw2[DUAL ? 2 : 1];
+#pragma unroll
+                for (int i = 0; i < MT; ++i) {
+                    const int r = wm + 32 * i + (lane & 31);
+                    ah[i] = *(const bf16x8 *)(xs + r * 64 + 16 * swz(r, c));
+                    al[i] = *(const bf16x8 *)(xs + XB + r * 64 + 16 * swz(r, c));
+                }
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int r = wn + 32 * j + (lane & 31);
+                    bw[j] = *(const bf16x8 *)(wt + r * 64 + 16 * swz(r, c));
+                    if constexpr (DUAL) bw2[j] = *(const bf16x8 *)(wt2 + r * 64 + 16 * swz(r, c));
+                }
+#pragma unroll
+                for (int i = 0; i < MT; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bw[j], acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bw[j], acc[i][j], 0, 0, 0);
+                        if constexpr (DUAL) {
+                            acc2[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bw2[j], acc2[i][j], 0, 0, 0);
+                            acc2[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bw2[j], acc2[i][j], 0, 0, 0);
+                        }
+                    }
+            }
+        }
+        // Chunk end: t += c.
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                tot[i][j] += acc[i][j];
+                if constexpr (DUAL) tot2[i][j] += acc2[i][j];
+            }
+    }
+    // Drain the copies of stages past the range before the block exits.
+    __builtin_amdgcn_s_waitcnt(vm_wait_imm(0));
+    if (!split) {
+        epilogue_tile<DUAL, MT>(a, tot, tot2, m0 + wm, n0 + wn, lane);
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int n = n0 + wn + 32 * j + (lane & 31);
+        if (n >= a.N) continue;
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int m = m0 + wm + 32 * i + 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
+                if (m >= a.M) continue;
+                const size_t o = ((size_t)blockIdx.z * a.M + m) * a.N + n;
+                a.ws[o] = tot[i][j][q];
+                if constexpr (DUAL) a.ws[(size_t)a.nchunks * a.M * a.N + o] = tot2[i][j][q];
+            }
+    }
+}
+
+template <int FMT, bool DUAL, int MT>
+int launch_ring(const GArgs &a, bool split, hipStream_t s) {
+    constexpr int NS = 6, BM = 64 * MT;
+    constexpr size_t lds = ring_lds_bytes<FMT, DUAL, MT, NS>();
+    static bool attr_set = false;
+    if (!attr_set) {
+        CHIP_CHECK(hipFuncSetAttribute((const void *)gemm_ring_kernel<FMT, DUAL, MT, NS>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        attr_set = true;
+    }
+    const dim3 grid((a.N + BN - 1) / BN * ((a.M + BM - 1) / BM), 1, split ? a.nchunks : 1);
+    hipLaunchKernelGGL((gemm_ring_kernel<FMT, DUAL, MT, NS>), grid, dim3(kThreads), lds, s, a, split ? 1 : 0);
+    CHIP_CHECK(hipGetLastError());
+    if (split && !a.defer) {
+        const size_t MN = (size_t)a.M * a.N;
+        hipLaunchKernelGGL((gemm_reduce_kernel<DUAL>), dim3((unsigned)((MN + kThreads - 1) / kThreads)),
+                           dim3(kThreads), 0, s, a);
+        CHIP_CHECK(hipGetLastError());
+    }
+    return 0;
+}
+
 template <bool DUAL, int MT>
 int launch_dma(const GArgs &a, bool split, hipStream_t s) {
     constexpr int NS = 4, BM = 64 * MT;
@@ -582,7 +879,7 @@ int launch_dma(const GArgs &a, bool split, hipStream_t s) {
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         attr_set = true;
     }
-    const dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM, split ? a.nchunks : 1);
+    const dim3 grid((a.N + BN - 1) / BN * ((a.M + BM - 1) / BM), 1, split ? a.nchunks : 1);
     hipLaunchKernelGGL((gemm_dma_kernel<DUAL, MT, NS>), grid, dim3(kThreads), lds, s, a, split ? 1 : 0);
     CHIP_CHECK(hipGetLastError());
     if (split && !a.defer) {
@@ -612,7 +909,7 @@ __global__ __launch_bounds__(kThreads) void gemm_reduce_kernel(GArgs a) {
 template <int FMT, bool DUAL, int MT>
 int launch_mt(const GArgs &a, bool split, hipStream_t s) {
     constexpr int BM = 64 * MT;
-    const dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM, split ? a.nchunks : 1);
+    const dim3 grid((a.N + BN - 1) / BN * ((a.M + BM - 1) / BM), 1, split ? a.nchunks : 1);
     if (a.xh) hipLaunchKernelGGL((gemm_kernel<FMT, DUAL, MT, true>), grid, dim3(kThreads), 0, s, a, split ? 1 : 0);
     else hipLaunchKernelGGL((gemm_kernel<FMT, DUAL, MT, false>), grid, dim3(kThreads), 0, s, a, split ? 1 : 0);
     CHIP_CHECK(hipGetLastError());
@@ -623,6 +920,16 @@ int launch_mt(const GArgs &a, bool split, hipStream_t s) {
         CHIP_CHECK(hipGetLastError());
     }
     return 0;
+}
+
+// The ring kernel is the default; CHEETAH_HIP_GEMM_RING=0 selects the
+// register-staged and BF16-only DMA kernels (the same bits).
+bool ring_enabled() {
+    static const bool on = [] {
+        const char *e = std::getenv("CHEETAH_HIP_GEMM_RING");
+        return !(e && e[0] == '0');
+    }();
+    return on;
 }
 
 template <int FMT>
@@ -636,6 +943,17 @@ int launch_fmt(const GArgs &a, bool dual, size_t ws_floats, hipStream_t s, bool 
     const bool split = a.nchunks > 1 && tiles64 < cus && a.ws &&
                        ws_floats >= gemm_workspace_floats(a.N, a.K, a.M, dual);
     split_out = split;
+    // Pre-split x with K a multiple of the stage and 32-bit buffer offsets:
+    // the ring kernel (weights copied 16 bytes at a time, Q4 4 at a time).
+    const int galign = FMT == FMT_Q4 ? 4 : 16;
+    const bool ring = ring_enabled() && a.xh && a.K % BK == 0 && a.stride % galign == 0 &&
+                      ((uintptr_t)a.w % galign) == 0 && (!dual || ((uintptr_t)a.w2 % galign) == 0) &&
+                      (size_t)a.M * a.K * 2 < (1ull << 31) && (size_t)a.N * a.stride < (1ull << 31);
+    if (ring) {
+        if (dual) return launch_ring<FMT, true, 1>(a, split, s);
+        if (!split && tiles128 >= cus) return launch_ring<FMT, false, 2>(a, false, s);
+        return launch_ring<FMT, false, 1>(a, split, s);
+    }
     // BF16 weights with pre-split x stream both operands straight into LDS.
     const bool dma = FMT == FMT_BF16 && a.xh && a.K % BK == 0 && a.stride % 16 == 0 &&
                      ((uintptr_t)a.w % 16) == 0 && (!dual || ((uintptr_t)a.w2 % 16) == 0);
