@@ -593,9 +593,10 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GArgs a, int split) 
 // Q4 nibbles) go global -> LDS by buffer loads that write LDS directly: a
 // lane's source offset is fixed for the whole launch and the stage's K
 // offset is a scalar, so issuing a stage costs no vector instructions. The
-// ring holds NS stages; stage s + NS - 2 is issued while stage s computes.
+// ring holds NS = 4 stages (6 measured no faster); stage s + NS - 2 is issued
+// while stage s computes.
 // Q8/Q4 codes of stage s + 1 are converted to BF16 (exactly) once per block,
-// 16 per thread, into one of three converted tiles while stage s computes;
+// 16 per thread, into one of three converted tiles after stage s's MFMAs;
 // BF16 weights are read straight from the ring. One barrier per stage. The
 // MFMA sequence per output and the chunk folds are those of gemm_kernel and
 // gemm_dma_kernel, so the results are the same bits.
@@ -780,9 +781,6 @@ __global__ __launch_bounds__(kThreads) void gemm_ring_kernel(GArgs a, int split)
             __builtin_amdgcn_s_waitcnt(vm_wait_imm(D * (CONV ? NS - 3 : NS - 2)));
             __builtin_amdgcn_s_waitcnt(vm_wait_imm(63) & ~(0xF << 8));  // lgkmcnt(0)
             __builtin_amdgcn_s_barrier();
-            if constexpr (CONV) {
-                if (st + 1 < nst) convert(st + 1);
-            }
             const uint8_t *xs = ring + (st % NS) * SLOT;
             const uint8_t *wt = CONV ? wcv + (st % 3) * NWM * WCB : xs + 2 * XB;
             const uint8_t *wt2 = wt + (CONV ? WCB : WB);
@@ -813,6 +811,11 @@ __global__ __launch_bounds__(kThreads) void gemm_ring_kernel(GArgs a, int split)
                             acc2[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bw2[j], acc2[i][j], 0, 0, 0);
                         }
                     }
+            }
+            // Stage st + 1's codes, converted while this stage's MFMAs drain
+            // (measured 2-7 % faster than converting before them).
+            if constexpr (CONV) {
+                if (st + 1 < nst) convert(st + 1);
             }
         }
         // Chunk end: t += c.
@@ -849,7 +852,7 @@ __global__ __launch_bounds__(kThreads) void gemm_ring_kernel(GArgs a, int split)
 
 template <int FMT, bool DUAL, int MT>
 int launch_ring(const GArgs &a, bool split, hipStream_t s) {
-    constexpr int NS = 6, BM = 64 * MT;
+    constexpr int NS = 4, BM = 64 * MT;
     constexpr size_t lds = ring_lds_bytes<FMT, DUAL, MT, NS>();
     static bool attr_set = false;
     if (!attr_set) {
