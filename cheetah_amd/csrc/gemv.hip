@@ -241,6 +241,19 @@ __device__ __forceinline__ u32x4 q4_pairs(uint32_t w) {
 // ---------------------------------------------------------------------------
 constexpr int kPad = 32;  // zero floats before and after x in LDS
 
+// Signed byte B of v as f32 in one instruction (the SDWA form the compiler
+// itself emits for int8 converts; spelled out because it does not find it
+// for bytes built from nibbles).
+template <int B>
+__device__ __forceinline__ float sbyte_f32(uint32_t v) {
+    float f;
+    if constexpr (B == 0) asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0" : "=v"(f) : "v"(v));
+    else if constexpr (B == 1) asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1" : "=v"(f) : "v"(v));
+    else if constexpr (B == 2) asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(f) : "v"(v));
+    else asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3" : "=v"(f) : "v"(v));
+    return f;
+}
+
 // Dynamic LDS of the aligned kernel: padded x and the norm gain as BF16.
 inline size_t aligned_lds(int K, bool norm) {
     return (size_t)(K + 2 * kPad) * sizeof(float) + (norm ? (size_t)K * 2 + 16 : 0);
@@ -426,9 +439,19 @@ __global__ __launch_bounds__(kAThreads) void gemv_aligned_kernel(Args a, int P) 
                     for (int r = 0; r < R; ++r) {
                         const uint32_t word = cur[i][m][r][d];
                         if constexpr (FMT == FMT_Q4) {
-#pragma unroll
-                            for (int n = 0; n < 8; ++n)
-                                acc[m][r] = fmaf((float)(((int)(word << (28 - 4 * n))) >> 28), xv[n], acc[m][r]);
+                            // Nibbles moved to the top of bytes read as int8
+                            // are 16 x the code; each byte converts in one
+                            // instruction. acc holds 16 x the sum, in the same
+                            // order, so scaling by 1/16 afterwards is exact.
+                            const uint32_t ev = (word << 4) & 0xF0F0F0F0u, od = word & 0xF0F0F0F0u;
+                            acc[m][r] = fmaf(sbyte_f32<0>(ev), xv[0], acc[m][r]);
+                            acc[m][r] = fmaf(sbyte_f32<0>(od), xv[1], acc[m][r]);
+                            acc[m][r] = fmaf(sbyte_f32<1>(ev), xv[2], acc[m][r]);
+                            acc[m][r] = fmaf(sbyte_f32<1>(od), xv[3], acc[m][r]);
+                            acc[m][r] = fmaf(sbyte_f32<2>(ev), xv[4], acc[m][r]);
+                            acc[m][r] = fmaf(sbyte_f32<2>(od), xv[5], acc[m][r]);
+                            acc[m][r] = fmaf(sbyte_f32<3>(ev), xv[6], acc[m][r]);
+                            acc[m][r] = fmaf(sbyte_f32<3>(od), xv[7], acc[m][r]);
                         } else if constexpr (FMT == FMT_Q8) {
 #pragma unroll
                             for (int b = 0; b < 4; ++b)
@@ -470,6 +493,12 @@ __global__ __launch_bounds__(kAThreads) void gemv_aligned_kernel(Args a, int P) 
                 mac_batch(B, klane + (j + 1) * STEP, acc);
             }
             if (j < nb) mac_batch(A, klane + j * STEP, acc);
+            if constexpr (FMT == FMT_Q4) {
+#pragma unroll
+                for (int m = 0; m < NM; ++m)
+#pragma unroll
+                    for (int r = 0; r < R; ++r) acc[m][r] *= 0.0625f;
+            }
             // Elements past the last whole unit (fewer than 16 bytes' worth).
             for (int e = max(nfull * E - shift, 0) + klane; e < K; e += 64 * KS) {
                 const float xv = xs[e];
