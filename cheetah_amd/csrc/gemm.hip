@@ -784,34 +784,40 @@ __global__ __launch_bounds__(kThreads) void gemm_ring_kernel(GArgs a, int split)
             const uint8_t *xs = ring + (st % NS) * SLOT;
             const uint8_t *wt = CONV ? wcv + (st % 3) * NWM * WCB : xs + 2 * XB;
             const uint8_t *wt2 = wt + (CONV ? WCB : WB);
+            // Every fragment of the stage is read before the first MFMA, so
+            // the LDS latency is paid once per stage, not once per k-step.
+            constexpr int KS = BK / 16;
+            bf16x8 ah[KS][MT], al[KS][MT], bw[KS][2], bw2[KS][DUAL ? 2 : 1];
 #pragma unroll
-            for (int ks = 0; ks < BK; ks += 16) {
-                const int c = (ks >> 3) + (lane >> 5);
-                bf16x8 ah[MT], al[MT], bw[2], bw2[DUAL ? 2 : 1];
+            for (int k = 0; k < KS; ++k) {
+                const int c = 2 * k + (lane >> 5);
 #pragma unroll
                 for (int i = 0; i < MT; ++i) {
                     const int r = wm + 32 * i + (lane & 31);
-                    ah[i] = *(const bf16x8 *)(xs + r * 64 + 16 * swz(r, c));
-                    al[i] = *(const bf16x8 *)(xs + XB + r * 64 + 16 * swz(r, c));
+                    ah[k][i] = *(const bf16x8 *)(xs + r * 64 + 16 * swz(r, c));
+                    al[k][i] = *(const bf16x8 *)(xs + XB + r * 64 + 16 * swz(r, c));
                 }
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     const int r = wn + 32 * j + (lane & 31);
-                    bw[j] = *(const bf16x8 *)(wt + r * 64 + 16 * swz(r, c));
-                    if constexpr (DUAL) bw2[j] = *(const bf16x8 *)(wt2 + r * 64 + 16 * swz(r, c));
+                    bw[k][j] = *(const bf16x8 *)(wt + r * 64 + 16 * swz(r, c));
+                    if constexpr (DUAL) bw2[k][j] = *(const bf16x8 *)(wt2 + r * 64 + 16 * swz(r, c));
                 }
+            }
+            __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
+#pragma unroll
+            for (int k = 0; k < KS; ++k)
 #pragma unroll
                 for (int i = 0; i < MT; ++i)
 #pragma unroll
                     for (int j = 0; j < 2; ++j) {
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bw[j], acc[i][j], 0, 0, 0);
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bw[j], acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[k][i], bw[k][j], acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[k][i], bw[k][j], acc[i][j], 0, 0, 0);
                         if constexpr (DUAL) {
-                            acc2[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bw2[j], acc2[i][j], 0, 0, 0);
-                            acc2[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bw2[j], acc2[i][j], 0, 0, 0);
+                            acc2[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[k][i], bw2[k][j], acc2[i][j], 0, 0, 0);
+                            acc2[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[k][i], bw2[k][j], acc2[i][j], 0, 0, 0);
                         }
                     }
-            }
             // Stage st + 1's codes, converted while this stage's MFMAs drain
             // (measured 2-7 % faster than converting before them).
             if constexpr (CONV) {
