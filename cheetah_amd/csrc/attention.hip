@@ -47,6 +47,11 @@ struct AttnArgs {
     const int32_t *pos_dev;
     float *part;
     float *out;
+    // Fused decode RoPE (attn_dec_mfma_kernel<.., ROPE>): raw QKV row and
+    // the cos/sin table; K/V are then also written (the new row).
+    const float *qkv;
+    const float *rope_cos, *rope_sin;
+    int rotary_dim;
 };
 
 // Eight consecutive K or V elements as loaded (converted to f32 at use), so
@@ -307,7 +312,7 @@ __device__ __forceinline__ void split_hilo(const float (&v)[8], bf16x8_t &hi, bf
     }
 }
 
-template <int HD, int G, bool DIRECT>
+template <int HD, int G, bool DIRECT, bool ROPE>
 __global__ __launch_bounds__(kThreads) void attn_dec_mfma_kernel(AttnArgs a) {
     constexpr int TW = 32;             // positions per wave tile
     constexpr int NS = HD / 32;        // K steps of the score product
@@ -336,6 +341,35 @@ __global__ __launch_bounds__(kThreads) void attn_dec_mfma_kernel(AttnArgs a) {
     if (start >= ctx) {  // empty split: contributes nothing to the merge
         if (threadIdx.x < G) part[threadIdx.x * part_head + HD] = -INFINITY;
         return;
+    }
+
+    // ROPE: the block whose range ends at the context holds position pos,
+    // whose K/V row is not in the cache yet. The wave whose tile holds it
+    // rotates k (rope_elem, as launch_rope_append), rounds K and V to BF16,
+    // appends them to the cache and keeps them in LDS to patch into its
+    // tile registers (bits equal to what the cache will hold).
+    __shared__ __attribute__((aligned(16))) uint16_t s_new[2][HD];
+    const int q_dim = a.q_heads * HD, kv_dim = a.kv_heads * HD, half = a.rotary_dim / 2;
+    const float *qkv_row = ROPE ? a.qkv + (size_t)row * (q_dim + 2 * kv_dim) : nullptr;
+    const float *cr = ROPE ? a.rope_cos + (size_t)pos * half : nullptr;
+    const float *sr = ROPE ? a.rope_sin + (size_t)pos * half : nullptr;
+    const int pos_tile = (int)((pos - start) / TW);  // tile index of pos in this block's range
+    const bool has_new = ROPE && end == ctx;
+    if constexpr (ROPE) {
+        if (has_new && wave == pos_tile % 4) {
+            const float *kr = qkv_row + q_dim + g * HD, *vr = qkv_row + q_dim + kv_dim + g * HD;
+            const int page = a.page_table[pos / a.page_size];
+            const size_t off = (((size_t)page * a.kv_heads + g) * a.page_size + pos % a.page_size) * HD;
+#pragma unroll
+            for (int d = lane; d < HD; d += 64) {
+                const uint16_t kb = f32_bf16_rne(rope_elem(kr, d, half, a.rotary_dim, cr, sr));
+                const uint16_t vb = f32_bf16_rne(vr[d]);
+                s_new[0][d] = kb;
+                s_new[1][d] = vb;
+                ((uint16_t *)a.k)[off + d] = kb;
+                ((uint16_t *)a.v)[off + d] = vb;
+            }
+        }
     }
 
     const float scale = 1.0f / sqrtf((float)HD);
@@ -383,7 +417,29 @@ __global__ __launch_bounds__(kThreads) void attn_dec_mfma_kernel(AttnArgs a) {
     uint8_t *sv = s_v[wave];
     // First half of a tile: the V tile into this wave's LDS copy and the
     // scores; after it the registers are free for the next tile's loads.
-    auto scores = [&](const Regs &R, f32x4 (&sc)[2]) {
+    auto scores = [&](int i, Regs &R, f32x4 (&sc)[2]) {
+        if constexpr (ROPE) {
+            // The tile holding pos gets the new K/V row (the cache row may
+            // not be written yet when the tile was loaded).
+            if (has_new && i * 4 + wave == pos_tile) {
+                const int rp = (int)(pos - (start + (long)TW * pos_tile));
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb) {
+                    const bool mine = 8 * (n >> 2) + 4 * mb + (n & 3) == rp;
+#pragma unroll
+                    for (int s = 0; s < NS; ++s) {
+                        const u32x4 nk = *(const u32x4 *)&s_new[0][32 * s + 8 * kg];
+                        R.k[mb][s] = mine ? nk : R.k[mb][s];
+                    }
+                }
+#pragma unroll
+                for (int i2 = 0; i2 < VI; ++i2) {
+                    const int f = 64 * i2 + lane;
+                    const u32x4 nv = *(const u32x4 *)&s_new[1][8 * (f % CH)];
+                    R.v[i2] = f / CH == rp ? nv : R.v[i2];
+                }
+            }
+        }
         // V tile into this wave's LDS copy (row f / CH, chunk f % CH).
 #pragma unroll
         for (int i2 = 0; i2 < VI; ++i2) {
@@ -459,13 +515,28 @@ __global__ __launch_bounds__(kThreads) void attn_dec_mfma_kernel(AttnArgs a) {
         // The group's queries (raw f32 now, converted after the first tile's
         // loads are issued, so the two round trips overlap).
         f32x4 qraw[NS][2];
+        // ROPE (rotary width = head_dim): the raw pairs and cos/sin of the
+        // lane's 8 dims (all below or all at/above half: multiples of 8).
+        f32x4 qpair[ROPE ? NS : 1][4], qcs[ROPE ? NS : 1][4];
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
             // Every lane loads (lanes past the group re-read head 0 and are
             // zeroed at conversion): no divergent load for the waits to trip on.
-            const float *qp = a.q + (size_t)row * a.q_stride + (size_t)(g * G + (n < G ? n : 0)) * HD + 32 * s + 8 * kg;
-            qraw[s][0] = *(const f32x4 *)qp;
-            qraw[s][1] = *(const f32x4 *)(qp + 4);
+            if constexpr (ROPE) {
+                const int d0 = 32 * s + 8 * kg;
+                const float *src = qkv_row + (size_t)(g * G + (n < G ? n : 0)) * HD;
+                const int i0 = d0 < half ? d0 : d0 - half;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) qpair[s][k] = *(const f32x4 *)(src + 2 * i0 + 4 * k);
+                qcs[s][0] = *(const f32x4 *)(cr + i0);
+                qcs[s][1] = *(const f32x4 *)(cr + i0 + 4);
+                qcs[s][2] = *(const f32x4 *)(sr + i0);
+                qcs[s][3] = *(const f32x4 *)(sr + i0 + 4);
+            } else {
+                const float *qp = a.q + (size_t)row * a.q_stride + (size_t)(g * G + (n < G ? n : 0)) * HD + 32 * s + 8 * kg;
+                qraw[s][0] = *(const f32x4 *)qp;
+                qraw[s][1] = *(const f32x4 *)(qp + 4);
+            }
         }
         const int pg0 = page_of(0);
         int pg_next = page_of(1);
@@ -476,16 +547,29 @@ __global__ __launch_bounds__(kThreads) void attn_dec_mfma_kernel(AttnArgs a) {
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
             float qv[8];
+            const int d0 = 32 * s + 8 * kg;
+            if constexpr (ROPE) {
+                // rope_elem's arithmetic: a*c - b*s below half, b*c + a*s above.
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                qv[e] = n < G ? qraw[s][0][e] : 0.f;
-                qv[4 + e] = n < G ? qraw[s][1][e] : 0.f;
+                for (int e = 0; e < 8; ++e) {
+                    const float pa = qpair[ROPE ? s : 0][(2 * e) >> 2][(2 * e) & 3];
+                    const float pb = qpair[ROPE ? s : 0][(2 * e + 1) >> 2][(2 * e + 1) & 3];
+                    const float c = qcs[ROPE ? s : 0][e >> 2][e & 3], sn = qcs[ROPE ? s : 0][2 + (e >> 2)][e & 3];
+                    const float r = d0 < half ? pa * c - pb * sn : pb * c + pa * sn;
+                    qv[e] = n < G ? r : 0.f;
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    qv[e] = n < G ? qraw[s][0][e] : 0.f;
+                    qv[4 + e] = n < G ? qraw[s][1][e] : 0.f;
+                }
             }
             split_hilo(qv, qh[s], ql[s]);
         }
         for (int i = 0; i < nt; ++i) {
             f32x4 sc[2];
-            scores(R, sc);
+            scores(i, R, sc);
             const int pg_after = page_of(i + 2);
             load_tile(i + 1, pg_next, R);
             pg_next = pg_after;
@@ -914,13 +998,17 @@ template <int HD, int G, class KT>
 int launch_hgk(const AttnJob &j, const AttnArgs &a, hipStream_t s) {
     const dim3 grid(j.splits, j.g.kv_heads, j.rows);
     const bool mfma = std::is_same<KT, uint16_t>::value && attn_mfma_enabled();
+    const bool rope = a.qkv != nullptr;
+    if (rope && !mfma) return fail("HIP backend: fused RoPE needs the matrix-core attention kernel.");
     if (j.splits == 1) {
-        if (mfma) hipLaunchKernelGGL((attn_dec_mfma_kernel<HD, G, true>), grid, dim3(kThreads), 0, s, a);
+        if (rope) hipLaunchKernelGGL((attn_dec_mfma_kernel<HD, G, true, true>), grid, dim3(kThreads), 0, s, a);
+        else if (mfma) hipLaunchKernelGGL((attn_dec_mfma_kernel<HD, G, true, false>), grid, dim3(kThreads), 0, s, a);
         else hipLaunchKernelGGL((attn_kernel<HD, G, KT, true>), grid, dim3(kThreads), 0, s, a);
         CHIP_CHECK(hipGetLastError());
         return 0;
     }
-    if (mfma) hipLaunchKernelGGL((attn_dec_mfma_kernel<HD, G, false>), grid, dim3(kThreads), 0, s, a);
+    if (rope) hipLaunchKernelGGL((attn_dec_mfma_kernel<HD, G, false, true>), grid, dim3(kThreads), 0, s, a);
+    else if (mfma) hipLaunchKernelGGL((attn_dec_mfma_kernel<HD, G, false, false>), grid, dim3(kThreads), 0, s, a);
     else hipLaunchKernelGGL((attn_kernel<HD, G, KT, false>), grid, dim3(kThreads), 0, s, a);
     CHIP_CHECK(hipGetLastError());
     hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3(j.q_heads, j.rows), dim3(kThreads), 0, s, a.part, j.splits,
@@ -974,6 +1062,11 @@ int attention_decode_splits(size_t ctx, int kv_heads, size_t rows, bool kv_f32) 
 
 int attention_prefill_splits(size_t ctx) { return (int)std::max<size_t>(1, (ctx + kSpan - 1) / kSpan); }
 
+bool attention_decode_fuses_rope(const KvGeom &g, int q_heads, int rotary_dim) {
+    return !g.kv_f32 && attn_mfma_enabled() && (g.head_dim == 64 || g.head_dim == 128) && g.kv_heads > 0 &&
+           q_heads % g.kv_heads == 0 && q_heads / g.kv_heads <= 8 && rotary_dim == g.head_dim;
+}
+
 bool attention_prefill_on_mfma(const KvGeom &g, int q_heads) {
     return !g.kv_f32 && (g.head_dim == 64 || g.head_dim == 128) && g.kv_heads > 0 && q_heads % g.kv_heads == 0 &&
            q_heads / g.kv_heads <= 8;
@@ -981,7 +1074,7 @@ bool attention_prefill_on_mfma(const KvGeom &g, int q_heads) {
 
 int launch_attention(const AttnJob &j, hipStream_t s) {
     if (j.rows == 0) return 0;
-    if (!j.q || !j.out || !j.k || !j.v || !j.g.page_table || (!j.prefill && j.splits > 1 && !j.part))
+    if ((!j.q && !j.qkv) || !j.out || !j.k || !j.v || !j.g.page_table || (!j.prefill && j.splits > 1 && !j.part))
         return fail("HIP backend: attention is missing a buffer.");
     if (j.g.kv_heads <= 0 || j.q_heads <= 0 || j.q_heads % j.g.kv_heads)
         return fail("HIP backend: q_heads must be a multiple of kv_heads.");
@@ -1002,6 +1095,15 @@ int launch_attention(const AttnJob &j, hipStream_t s) {
     a.pos_dev = j.pos_dev;
     a.part = j.part;
     a.out = j.out;
+    if (j.qkv) {
+        if (j.prefill || j.rows != 1 || !attention_decode_fuses_rope(j.g, j.q_heads, j.rotary_dim) || !j.rope_cos ||
+            !j.rope_sin)
+            return fail("HIP backend: fused RoPE attention takes one BF16 decode row with full-width rotary.");
+        a.qkv = j.qkv;
+        a.rope_cos = j.rope_cos;
+        a.rope_sin = j.rope_sin;
+        a.rotary_dim = j.rotary_dim;
+    }
     const int G = j.q_heads / j.g.kv_heads;
     if (j.prefill && attention_prefill_on_mfma(j.g, j.q_heads)) {
         if (j.pos_dev) return fail("HIP backend: prefill attention takes a host position.");

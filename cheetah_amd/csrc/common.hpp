@@ -73,6 +73,18 @@ __device__ __forceinline__ uint16_t f32_bf16_rne(float f) {
     return (uint16_t)(u >> 16);
 }
 
+// RoPE (rotate-half, rope_heads ops.rs:693-740): element d of one rotated
+// head whose pair-permuted projection is `src` (pair i at src[2i],
+// src[2i+1]): x1' = x1*cos - x2*sin, x2' = x2*cos + x1*sin, each product and
+// the sum rounded separately, with cos/sin rows cr/sr of the position.
+__device__ __forceinline__ float rope_elem(const float *src, int d, int half, int rotary_dim, const float *cr,
+                                           const float *sr) {
+    if (d >= rotary_dim) return src[d];
+    const int i = d < half ? d : d - half;
+    const float a = src[2 * i], b = src[2 * i + 1], c = cr[i], s = sr[i];
+    return d < half ? a * c - b * s : b * c + a * s;
+}
+
 // Cross-lane reductions with DPP row permutations (register-to-register,
 // no LDS round trip) inside each row of 16 lanes, then the four row results
 // read into a scalar. Steps, each exact once the previous one made its

@@ -158,11 +158,22 @@ struct AttnJob {
     // ignores `splits`; part must then hold part_floats >= the partials.
     bool prefill = false;
     size_t part_floats = 0;
+    // Decode (one row) from the raw QKV row [q | k | v] of launch_rope_append
+    // instead of q: the kernel rotates q itself and rotates and appends the
+    // position's K/V row (what launch_rope_append would write; q unused).
+    // Only where attention_decode_fuses_rope says so.
+    const float *qkv = nullptr;
+    const float *rope_cos = nullptr, *rope_sin = nullptr;
+    int rotary_dim = 0;
 };
 int launch_attention(const AttnJob &job, hipStream_t s);
+// BF16 K/V on the matrix cores, head_dim 64/128, <= 8 q heads per KV head,
+// rotary width = head_dim.
+bool attention_decode_fuses_rope(const KvGeom &g, int q_heads, int rotary_dim);
 size_t attention_part_floats(size_t rows, int q_heads, int splits, int head_dim);
 // Split count of a decode-style launch (one row per query position) over ctx
-// keys: about two blocks per CU, at most one split per 64-position tile.
+// keys: one or two blocks per CU (matrix-core or VALU kernel), at most one
+// split per 64-position tile.
 int attention_decode_splits(size_t ctx, int kv_heads, size_t rows, bool kv_f32);
 int attention_max_splits();
 int attention_prefill_splits(size_t ctx);

@@ -109,15 +109,6 @@ __global__ __launch_bounds__(kThreads) void residual_rmsnorm_rows_kernel(const f
 __device__ __forceinline__ void store_kv(uint16_t *p, float v) { *p = f32_bf16_rne(v); }
 __device__ __forceinline__ void store_kv(float *p, float v) { *p = v; }
 
-// Element d of one rotated head whose pair-permuted projection is `src`
-// (pair i at src[2i], src[2i+1]): x1' = x1*cos - x2*sin, x2' = x2*cos + x1*sin.
-__device__ __forceinline__ float rope_elem(const float *src, int d, int half, int rotary_dim, const float *cr,
-                                           const float *sr) {
-    if (d >= rotary_dim) return src[d];
-    const int i = d < half ? d : d - half;
-    const float a = src[2 * i], b = src[2 * i + 1], c = cr[i], s = sr[i];
-    return d < half ? a * c - b * s : b * c + a * s;
-}
 
 // One thread per output element: blockIdx.y is the row, blockIdx.x a run of
 // kThreads elements over [q | k] (each k element also appends its v). A

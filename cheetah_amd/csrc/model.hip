@@ -838,10 +838,21 @@ int enqueue_decode(cheetah_hip_model *m, int splits) {
         qkv.bias = L.qkv_bias;
         qkv.y = m->qkv;
         CHIP_TRY(launch_gemv(qkv, s));
-        CHIP_TRY(launch_rope_append(m->qkv, m->qrot, 1, (int)c.q_heads, geom(m), L.kv, sh.rope_cos, sh.rope_sin,
-                                    (int)c.rotary_dim, 0, pos, s));
+        // RoPE and the K/V append run inside the attention kernel where it
+        // can (one launch fewer per layer), else as their own kernel.
+        const bool fuse = attention_decode_fuses_rope(geom(m), (int)c.q_heads, (int)c.rotary_dim);
+        if (!fuse)
+            CHIP_TRY(launch_rope_append(m->qkv, m->qrot, 1, (int)c.q_heads, geom(m), L.kv, sh.rope_cos, sh.rope_sin,
+                                        (int)c.rotary_dim, 0, pos, s));
         AttnJob aj;
-        aj.q = m->qrot;
+        if (fuse) {
+            aj.qkv = m->qkv;
+            aj.rope_cos = sh.rope_cos;
+            aj.rope_sin = sh.rope_sin;
+            aj.rotary_dim = (int)c.rotary_dim;
+        } else {
+            aj.q = m->qrot;
+        }
         aj.q_stride = sh.q_dim();
         aj.out = m->attn;
         aj.k = L.kv.k;
