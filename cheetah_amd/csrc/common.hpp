@@ -73,6 +73,19 @@ __device__ __forceinline__ uint16_t f32_bf16_rne(float f) {
     return (uint16_t)(u >> 16);
 }
 
+// Signed byte B of v as f32 in one instruction (the SDWA form the compiler
+// itself emits for int8 converts; spelled out because it does not find it
+// for bytes built from nibbles).
+template <int B>
+__device__ __forceinline__ float sbyte_f32(uint32_t v) {
+    float f;
+    if constexpr (B == 0) asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0" : "=v"(f) : "v"(v));
+    else if constexpr (B == 1) asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1" : "=v"(f) : "v"(v));
+    else if constexpr (B == 2) asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(f) : "v"(v));
+    else asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3" : "=v"(f) : "v"(v));
+    return f;
+}
+
 // RoPE (rotate-half, rope_heads ops.rs:693-740): element d of one rotated
 // head whose pair-permuted projection is `src` (pair i at src[2i],
 // src[2i+1]): x1' = x1*cos - x2*sin, x2' = x2*cos + x1*sin, each product and

@@ -728,11 +728,21 @@ __global__ __launch_bounds__(kThreads) void gemm_ring_kernel(GArgs a, int split)
 #pragma unroll
                 for (int q = 0; q < 16; ++q) f[q] = (float)(int)(int8_t)(v[q >> 2] >> (8 * (q & 3)));
             } else {
-                const uint2 v = make_uint2(rv[mi][0], rv[mi][1]);
+                // 16 x code: each nibble moved to the top of a byte, read as
+                // int8 in one instruction (exact in BF16; the chunk sums are
+                // scaled back by 1/16, exactly).
 #pragma unroll
-                for (int q = 0; q < 16; ++q) {
-                    const uint32_t wd = q < 8 ? v.x : v.y;
-                    f[q] = (float)(((int)(wd << (28 - 4 * (q & 7)))) >> 28);
+                for (int h2 = 0; h2 < 2; ++h2) {
+                    const uint32_t wd = rv[mi][h2];
+                    const uint32_t ev = (wd << 4) & 0xF0F0F0F0u, od = wd & 0xF0F0F0F0u;
+                    f[8 * h2 + 0] = sbyte_f32<0>(ev);
+                    f[8 * h2 + 1] = sbyte_f32<0>(od);
+                    f[8 * h2 + 2] = sbyte_f32<1>(ev);
+                    f[8 * h2 + 3] = sbyte_f32<1>(od);
+                    f[8 * h2 + 4] = sbyte_f32<2>(ev);
+                    f[8 * h2 + 5] = sbyte_f32<2>(od);
+                    f[8 * h2 + 6] = sbyte_f32<3>(ev);
+                    f[8 * h2 + 7] = sbyte_f32<3>(od);
                 }
             }
             uint8_t *dst = wcv + ((st % 3) * NWM + mi) * WCB + row * 64;
@@ -824,13 +834,14 @@ __global__ __launch_bounds__(kThreads) void gemm_ring_kernel(GArgs a, int split)
                 if (st + 1 < nst) convert(st + 1);
             }
         }
-        // Chunk end: t += c.
+        // Chunk end: t += c (Q4: c = acc / 16, exactly).
+        constexpr float cs16 = FMT == FMT_Q4 ? 0.0625f : 1.0f;
 #pragma unroll
         for (int i = 0; i < MT; ++i)
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                tot[i][j] += acc[i][j];
-                if constexpr (DUAL) tot2[i][j] += acc2[i][j];
+                tot[i][j] += FMT == FMT_Q4 ? acc[i][j] * cs16 : acc[i][j];
+                if constexpr (DUAL) tot2[i][j] += FMT == FMT_Q4 ? acc2[i][j] * cs16 : acc2[i][j];
             }
     }
     // Drain the copies of stages past the range before the block exits.

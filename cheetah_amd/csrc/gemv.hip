@@ -241,18 +241,6 @@ __device__ __forceinline__ u32x4 q4_pairs(uint32_t w) {
 // ---------------------------------------------------------------------------
 constexpr int kPad = 32;  // zero floats before and after x in LDS
 
-// Signed byte B of v as f32 in one instruction (the SDWA form the compiler
-// itself emits for int8 converts; spelled out because it does not find it
-// for bytes built from nibbles).
-template <int B>
-__device__ __forceinline__ float sbyte_f32(uint32_t v) {
-    float f;
-    if constexpr (B == 0) asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0" : "=v"(f) : "v"(v));
-    else if constexpr (B == 1) asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1" : "=v"(f) : "v"(v));
-    else if constexpr (B == 2) asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(f) : "v"(v));
-    else asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3" : "=v"(f) : "v"(v));
-    return f;
-}
 
 // Dynamic LDS of the aligned kernel: padded x and the norm gain as BF16.
 inline size_t aligned_lds(int K, bool norm) {
