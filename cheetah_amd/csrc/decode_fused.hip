@@ -186,17 +186,120 @@ __device__ __forceinline__ void dma16(const void *g, const void *lds) {
 }
 __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// N device-coherent 16-byte loads p[i] -> r[i] and the wait for all of them in
+// one asm statement: no instruction sees r before its load has landed.
+template <int N>
+__device__ __forceinline__ void poll16(u32x4 (&r)[8], const uint64_t *const (&p)[8]) {
+    if constexpr (N == 1)
+        asm volatile("global_load_dwordx4 %0, %1, off sc1\n\ts_waitcnt vmcnt(0)"
+                     : "=&v"(r[0])
+                     : "v"(p[0])
+                     : "memory");
+    else if constexpr (N == 2)
+        asm volatile("global_load_dwordx4 %0, %2, off sc1\n\tglobal_load_dwordx4 %1, %3, off sc1\n\ts_waitcnt vmcnt(0)"
+                     : "=&v"(r[0]), "=&v"(r[1])
+                     : "v"(p[0]), "v"(p[1])
+                     : "memory");
+    else if constexpr (N == 3)
+        asm volatile("global_load_dwordx4 %0, %3, off sc1\n\tglobal_load_dwordx4 %1, %4, off sc1\n\tglobal_load_dwordx4 %2, %5, off sc1\n\ts_waitcnt vmcnt(0)"
+                     : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2])
+                     : "v"(p[0]), "v"(p[1]), "v"(p[2])
+                     : "memory");
+    else if constexpr (N == 4)
+        asm volatile("global_load_dwordx4 %0, %4, off sc1\n\tglobal_load_dwordx4 %1, %5, off sc1\n\tglobal_load_dwordx4 %2, %6, off sc1\n\tglobal_load_dwordx4 %3, %7, off sc1\n\ts_waitcnt vmcnt(0)"
+                     : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
+                     : "v"(p[0]), "v"(p[1]), "v"(p[2]), "v"(p[3])
+                     : "memory");
+    else if constexpr (N == 5)
+        asm volatile("global_load_dwordx4 %0, %5, off sc1\n\tglobal_load_dwordx4 %1, %6, off sc1\n\tglobal_load_dwordx4 %2, %7, off sc1\n\tglobal_load_dwordx4 %3, %8, off sc1\n\tglobal_load_dwordx4 %4, %9, off sc1\n\ts_waitcnt vmcnt(0)"
+                     : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4])
+                     : "v"(p[0]), "v"(p[1]), "v"(p[2]), "v"(p[3]), "v"(p[4])
+                     : "memory");
+    else if constexpr (N == 6)
+        asm volatile("global_load_dwordx4 %0, %6, off sc1\n\tglobal_load_dwordx4 %1, %7, off sc1\n\tglobal_load_dwordx4 %2, %8, off sc1\n\tglobal_load_dwordx4 %3, %9, off sc1\n\tglobal_load_dwordx4 %4, %10, off sc1\n\tglobal_load_dwordx4 %5, %11, off sc1\n\ts_waitcnt vmcnt(0)"
+                     : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5])
+                     : "v"(p[0]), "v"(p[1]), "v"(p[2]), "v"(p[3]), "v"(p[4]), "v"(p[5])
+                     : "memory");
+    else if constexpr (N == 7)
+        asm volatile("global_load_dwordx4 %0, %7, off sc1\n\tglobal_load_dwordx4 %1, %8, off sc1\n\tglobal_load_dwordx4 %2, %9, off sc1\n\tglobal_load_dwordx4 %3, %10, off sc1\n\tglobal_load_dwordx4 %4, %11, off sc1\n\tglobal_load_dwordx4 %5, %12, off sc1\n\tglobal_load_dwordx4 %6, %13, off sc1\n\ts_waitcnt vmcnt(0)"
+                     : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6])
+                     : "v"(p[0]), "v"(p[1]), "v"(p[2]), "v"(p[3]), "v"(p[4]), "v"(p[5]), "v"(p[6])
+                     : "memory");
+    else if constexpr (N == 8)
+        asm volatile("global_load_dwordx4 %0, %8, off sc1\n\tglobal_load_dwordx4 %1, %9, off sc1\n\tglobal_load_dwordx4 %2, %10, off sc1\n\tglobal_load_dwordx4 %3, %11, off sc1\n\tglobal_load_dwordx4 %4, %12, off sc1\n\tglobal_load_dwordx4 %5, %13, off sc1\n\tglobal_load_dwordx4 %6, %14, off sc1\n\tglobal_load_dwordx4 %7, %15, off sc1\n\ts_waitcnt vmcnt(0)"
+                     : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
+                     : "v"(p[0]), "v"(p[1]), "v"(p[2]), "v"(p[3]), "v"(p[4]), "v"(p[5]), "v"(p[6]), "v"(p[7])
+                     : "memory");
+}
+
+// Both words of a 16-byte unit (value, tag, value, tag) at word w of n carry
+// `tag` (words past n count as fresh).
+__device__ __forceinline__ bool unit_fresh(u32x4 v, int w, int n, unsigned tag) {
+    return (w >= n || v[1] == tag) && (w + 1 >= n || v[3] == tag);
+}
+
+// Register form of the gather for a wave that owns N <= 8 chunks: a round
+// loads every chunk of the wave into registers and waits for all of them
+// (one asm statement), then checks the tags there; once every word is fresh
+// the chunks are written to LDS. Re-loading fresh chunks costs traffic but no
+// time: a round takes one memory round trip either way, and without the LDS
+// round trip of the copy form a round is shorter.
+template <int N>
+__device__ void gather_regs(uint64_t *dst, const uint64_t *src, int n, unsigned tag, int *abort_flag, int wave,
+                            int lane) {
+    const uint64_t *p[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int w = (wave + kWaves * i) * kChunk + lane * 2;
+        p[i] = src + (i < N && w < n ? w : 0);
+    }
+    long spins = 0;
+    while (true) {
+        u32x4 r[8];
+        poll16<N>(r, p);
+        bool stale = false;
+#pragma unroll
+        for (int i = 0; i < N; ++i) stale |= !unit_fresh(r[i], (wave + kWaves * i) * kChunk + lane * 2, n, tag);
+        if (!__any(stale)) {
+#pragma unroll
+            for (int i = 0; i < N; ++i) {
+                const int w = (wave + kWaves * i) * kChunk + lane * 2;
+                if (w < n) *(u32x4 *)(dst + w) = r[i];
+            }
+            return;
+        }
+        if (++spins > kSpinLimit || ((spins & 15) == 0 && aborted(abort_flag))) {
+            raise_abort(abort_flag);
+            return;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
 // All waves: copies tagged words src[0, n) into LDS dst[0, n) and waits until
-// each carries `tag`. Wave w owns the 128-word chunks w, w + 8, ...: it loads
-// them with direct global->LDS copies and re-loads the stale ones until every
-// word of its chunks is fresh (its tag reads for eight chunks in flight at a
-// time); the caller's barrier then makes all of them visible to the block.
-// A wave's wait also covers the weight rows it has in flight. On timeout the
-// abort word is raised and the wave moves on with what it has.
+// each carries `tag`. Wave w owns the 128-word chunks w, w + 8, ...; up to
+// eight of them it polls in registers (gather_regs), more it loads with direct
+// global->LDS copies and re-loads the stale ones until every word of its
+// chunks is fresh (its tag reads for eight chunks in flight at a time). The
+// caller's barrier then makes all of them visible to the block. A wave's wait
+// also covers the weight rows it has in flight. On timeout the abort word is
+// raised and the wave moves on with what it has.
 __device__ void gather(uint64_t *dst, const uint64_t *src, int n, unsigned tag, int *abort_flag) {
     const int lane = lane_here(), wave = __builtin_amdgcn_readfirstlane(tid_here() >> 6);
     const int chunks = (n + kChunk - 1) / kChunk;
     const int mine = chunks > wave ? (chunks - 1 - wave) / kWaves + 1 : 0;  // at most 16
+    switch (mine) {
+        case 0: return;
+        case 1: return gather_regs<1>(dst, src, n, tag, abort_flag, wave, lane);
+        case 2: return gather_regs<2>(dst, src, n, tag, abort_flag, wave, lane);
+        case 3: return gather_regs<3>(dst, src, n, tag, abort_flag, wave, lane);
+        case 4: return gather_regs<4>(dst, src, n, tag, abort_flag, wave, lane);
+        case 5: return gather_regs<5>(dst, src, n, tag, abort_flag, wave, lane);
+        case 6: return gather_regs<6>(dst, src, n, tag, abort_flag, wave, lane);
+        case 7: return gather_regs<7>(dst, src, n, tag, abort_flag, wave, lane);
+        case 8: return gather_regs<8>(dst, src, n, tag, abort_flag, wave, lane);
+        default: break;
+    }
     const uint32_t *d32 = (const uint32_t *)dst;
     uint32_t pend = (1u << mine) - 1;
     long spins = 0;
