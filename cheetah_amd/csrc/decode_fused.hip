@@ -260,16 +260,18 @@ __device__ void gather_regs(uint64_t *dst, const uint64_t *src, int n, unsigned 
         bool stale = false;
 #pragma unroll
         for (int i = 0; i < N; ++i) stale |= !unit_fresh(r[i], (wave + kWaves * i) * kChunk + lane * 2, n, tag);
-        if (!__any(stale)) {
+        const bool done = !__any(stale);
+        const bool give_up = !done && (++spins > kSpinLimit || ((spins & 15) == 0 && aborted(abort_flag)));
+        if (done || give_up) {
+            // On a give-up the words are written too, stale or not: they are
+            // the source buffer's, so what readers take from them (a token's
+            // row index) stays one that buffer held.
 #pragma unroll
             for (int i = 0; i < N; ++i) {
                 const int w = (wave + kWaves * i) * kChunk + lane * 2;
                 if (w < n) *(u32x4 *)(dst + w) = r[i];
             }
-            return;
-        }
-        if (++spins > kSpinLimit || ((spins & 15) == 0 && aborted(abort_flag))) {
-            raise_abort(abort_flag);
+            if (give_up) raise_abort(abort_flag);
             return;
         }
         __builtin_amdgcn_s_sleep(1);
@@ -284,7 +286,7 @@ __device__ void gather_regs(uint64_t *dst, const uint64_t *src, int n, unsigned 
 // caller's barrier then makes all of them visible to the block. A wave's wait
 // also covers the weight rows it has in flight. On timeout the abort word is
 // raised and the wave moves on with what it has.
-__device__ void gather(uint64_t *dst, const uint64_t *src, int n, unsigned tag, int *abort_flag) {
+__device__ __attribute__((noinline)) void gather(uint64_t *dst, const uint64_t *src, int n, unsigned tag, int *abort_flag) {
     const int lane = lane_here(), wave = __builtin_amdgcn_readfirstlane(tid_here() >> 6);
     const int chunks = (n + kChunk - 1) / kChunk;
     const int mine = chunks > wave ? (chunks - 1 - wave) / kWaves + 1 : 0;  // at most 16
@@ -457,7 +459,7 @@ struct Shm {
 };
 
 // Reduces (key, idx) over the block; the result lands in every thread.
-__device__ void block_best(int &key, uint32_t &idx, Shm &sm) {
+__device__ __forceinline__ void block_best(int &key, uint32_t &idx, Shm &sm) {
     const int lane = lane_here(), wave = tid_here() >> 6;
     wave_best(key, idx);
     if (lane == 0) {
@@ -510,7 +512,7 @@ __host__ __device__ inline LdsLayout lds_layout(int H, int I, int nq, int hd, in
 // [start, lim) of KV head g into LDS (row p - start of each); completion is
 // awaited with wait_vm.
 template <int HD, class KT>
-__device__ void load_kv_lds(uint8_t *k_lds, uint8_t *v_lds, int l, int g, long start, long lim) {
+__device__ __forceinline__ void load_kv_lds(uint8_t *k_lds, uint8_t *v_lds, int l, int g, long start, long lim) {
     constexpr int ROW = HD * (int)sizeof(KT);
     const int lane = lane_here();
     for (long t0 = start; t0 < lim; t0 += TP) {
@@ -553,7 +555,7 @@ __device__ __forceinline__ void ld8(const KT *p, float (&f)[8]) {
 // part[j * (HD + 2) + ...] (compute waves store, so the poll wave has no
 // stores in flight when it polls next).
 template <int HD, int G, class KT>
-__device__ void attn_compute(const float *qs, const uint8_t *k_lds, const uint8_t *v_lds, int nv, AttnShm<HD, G> &sh,
+__device__ __forceinline__ void attn_compute(const float *qs, const uint8_t *k_lds, const uint8_t *v_lds, int nv, AttnShm<HD, G> &sh,
                              uint64_t *part, unsigned tag, uint64_t *tr) {
     constexpr int T = HD / 8, P = kThreads / T, ROW = HD * (int)sizeof(KT);
     const int tid = tid_here(), lane = tid & 63, wave = tid >> 6;
@@ -1155,7 +1157,9 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                 for (int i = lane; i < head_blocks; i += 64)
                     better(key, idx, (int)(uint32_t)tb[2 * i], (uint32_t)tb[2 * i + 1]);
                 wave_best(key, idx);
-                if (lane == 0) sm.token = (int)idx;
+                // A row index outside the vocabulary can only come from a
+                // poll that gave up; the token then keeps its last value.
+                if (lane == 0) sm.token = idx < (uint32_t)A()->V ? (int)idx : token;
             }
             bar();
             token = __builtin_amdgcn_readfirstlane(sm.token);
