@@ -877,7 +877,68 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
             const bool kv_early = hasB && (l > 0 || paced);
             if (spare && kv_early) load_kv_lds<HD, KT>(k_lds, v_lds, l, ig, kv_start, kv_lim);
 
-            // ---- A: QKV pairs + RoPE + K/V append.
+            // ---- A: QKV pairs + RoPE + K/V append. Everything a pair's
+            // epilogue reads besides its dot (row scale and bias, rotation
+            // factors, page, destinations) is loaded before the input poll:
+            // the chain of dependent scalar loads (layer table, pointer,
+            // value) would otherwise follow the dot on the critical path.
+            bool a_sc = false, a_bias = false, a_rope = false;
+            float a_s0 = 0.f, a_s1 = 0.f, a_b0 = 0.f, a_b1 = 0.f, a_c = 0.f, a_sn = 0.f;
+            int a_i0 = 0, a_i1 = 0, a_c0 = -1, a_c1 = -1;  // q/K/V word, cache element (bit 30: V)
+            if (myA()) {
+                const int r0 = 2 * pairA();
+                if (const float *sc = LY(l)->qkv_sc) {
+                    a_sc = true;
+                    a_s0 = ldc(sc, r0);
+                    a_s1 = ldc(sc, r0 + 1);
+                }
+                if (const float *bias = LY(l)->qkv_bias) {
+                    a_bias = true;
+                    a_b0 = ldc(bias, r0);
+                    a_b1 = ldc(bias, r0 + 1);
+                }
+                const int qd = A()->q_heads * HD, kvd = A()->kv_heads * HD, kvh = A()->kv_heads;
+                const int rot = A()->rotary, half = rot / 2;
+                const int page = ldc(A()->page_table, pos / TP), slot = (int)(pos % TP);
+                if (r0 < qd + kvd) {
+                    const bool is_q = r0 < qd;
+                    const int base = is_q ? r0 : r0 - qd;
+                    const int h = base / HD, d0 = base % HD;
+                    int o0 = d0, o1 = d0 + 1;
+                    if (d0 < rot) {
+                        const int i = d0 / 2;
+                        a_rope = true;
+                        a_c = ldc(A()->rope_cos, pos * half + i);
+                        a_sn = ldc(A()->rope_sin, pos * half + i);
+                        o0 = i;
+                        o1 = half + i;
+                    }
+                    if (is_q) {
+                        const int q0 = (h / G) * (G + 2) * HD + (h % G) * HD;
+                        a_i0 = q0 + o0;
+                        a_i1 = q0 + o1;
+                    } else {
+                        const int k0 = h * (G + 2) * HD + G * HD;
+                        a_i0 = k0 + o0;
+                        a_i1 = k0 + o1;
+                        const int e0 = ((page * kvh + h) * TP + slot) * HD;
+                        a_c0 = e0 + o0;
+                        a_c1 = e0 + o1;
+                    }
+                } else {
+                    const int base = r0 - qd - kvd;
+                    const int h = base / HD, d0 = base % HD;
+                    const int v0i = h * (G + 2) * HD + (G + 1) * HD;
+                    a_i0 = v0i + d0;
+                    a_i1 = v0i + d0 + 1;
+                    const int e0 = ((page * kvh + h) * TP + slot) * HD;
+                    a_c0 = (e0 + d0) | (1 << 30);
+                    a_c1 = (e0 + d0 + 1) | (1 << 30);
+                }
+                // The values are used here, so their loads complete now,
+                // while the block waits for its input anyway.
+                asm volatile("" : "+v"(a_s0), "+v"(a_s1), "+v"(a_b0), "+v"(a_b1), "+v"(a_c), "+v"(a_sn));
+            }
             if (hasA()) {
                 if (spare) dma_bytes(lds + A()->lds_gain, LY(l)->ln1, A()->H * 2);
                 if (l > 0) gather(tb, A()->hid1, A()->H, tA - 1, A()->abort_flag);
@@ -889,67 +950,31 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
             }
             mark(16 * l + 1);
             if (myA()) {
-                const int r0 = 2 * pairA();
                 float y[2];
                 dot_rows<FMT>(wA, xs, A()->H / U::E, y);
                 float v0 = y[0], v1 = y[1];
-                if (const float *sc = LY(l)->qkv_sc) {
-                    v0 = v0 * ldc(sc, r0);
-                    v1 = v1 * ldc(sc, r0 + 1);
+                if (a_sc) {
+                    v0 = v0 * a_s0;
+                    v1 = v1 * a_s1;
                 }
-                if (const float *bias = LY(l)->qkv_bias) {
-                    v0 = v0 + ldc(bias, r0);
-                    v1 = v1 + ldc(bias, r0 + 1);
+                if (a_bias) {
+                    v0 = v0 + a_b0;
+                    v1 = v1 + a_b1;
                 }
-                const int qd = A()->q_heads * HD, kvd = A()->kv_heads * HD, kvh = A()->kv_heads;
-                const int rot = A()->rotary, half = rot / 2;
-                const int page = ldc(A()->page_table, pos / TP), slot = (int)(pos % TP);
-                int i0, i1, c0 = -1, c1 = -1;  // q/K/V word, cache element
-                if (r0 < qd + kvd) {
-                    const bool is_q = r0 < qd;
-                    const int base = is_q ? r0 : r0 - qd;
-                    const int h = base / HD, d0 = base % HD;
-                    int o0 = d0, o1 = d0 + 1;
-                    if (d0 < rot) {
-                        const int i = d0 / 2;
-                        const float c = ldc(A()->rope_cos, pos * half + i), sn = ldc(A()->rope_sin, pos * half + i);
-                        const float x1 = v0 * c - v1 * sn, x2 = v1 * c + v0 * sn;
-                        v0 = x1;
-                        v1 = x2;
-                        o0 = i;
-                        o1 = half + i;
-                    }
-                    if (is_q) {
-                        const int q0 = (h / G) * (G + 2) * HD + (h % G) * HD;
-                        i0 = q0 + o0;
-                        i1 = q0 + o1;
-                    } else {
-                        const int k0 = h * (G + 2) * HD + G * HD;
-                        i0 = k0 + o0;
-                        i1 = k0 + o1;
-                        const int e0 = ((page * kvh + h) * TP + slot) * HD;
-                        c0 = e0 + o0;
-                        c1 = e0 + o1;
-                    }
-                } else {
-                    const int base = r0 - qd - kvd;
-                    const int h = base / HD, d0 = base % HD;
-                    const int v0i = h * (G + 2) * HD + (G + 1) * HD;
-                    i0 = v0i + d0;
-                    i1 = v0i + d0 + 1;
-                    const int e0 = ((page * kvh + h) * TP + slot) * HD;
-                    c0 = (e0 + d0) | (1 << 30);
-                    c1 = (e0 + d0 + 1) | (1 << 30);
+                if (a_rope) {
+                    const float x1 = v0 * a_c - v1 * a_sn, x2 = v1 * a_c + v0 * a_sn;
+                    v0 = x1;
+                    v1 = x2;
                 }
                 if (lane == 0) {
-                    if (c0 >= 0) {
-                        KT *cache = (KT *)((c0 >> 30) ? LY(l)->vc : LY(l)->kc);
-                        st_kv(cache + (c0 & ((1 << 30) - 1)), v0);
-                        st_kv(cache + (c1 & ((1 << 30) - 1)), v1);
+                    if (a_c0 >= 0) {
+                        KT *cache = (KT *)((a_c0 >> 30) ? LY(l)->vc : LY(l)->kc);
+                        st_kv(cache + (a_c0 & ((1 << 30) - 1)), v0);
+                        st_kv(cache + (a_c1 & ((1 << 30) - 1)), v1);
                     }
                     uint64_t *qkvn = A()->qkvn;
-                    stf(qkvn + i0, c0 >= 0 ? kv_round<KT>(v0) : v0, tA);
-                    stf(qkvn + i1, c1 >= 0 ? kv_round<KT>(v1) : v1, tA);
+                    stf(qkvn + a_i0, a_c0 >= 0 ? kv_round<KT>(v0) : v0, tA);
+                    stf(qkvn + a_i1, a_c1 >= 0 ? kv_round<KT>(v1) : v1, tA);
                 }
             }
             mark(16 * l + 2);
