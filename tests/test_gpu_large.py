@@ -140,17 +140,16 @@ def test_qwen2_7b_32k_f32_kv_matches_reference(hip):
 @pytest.mark.gpu
 @pytest.mark.timeout(900)
 def test_qwen2_7b_32k_bf16_kv_32_greedy_steps(hip):
-    """The BF16 cache against the oracle run with BF16 K/V; where the
-    reference-semantics golden exists, the departure from it is recorded and
-    must sit at a near-tie of the reference (top-2 margin below 0.05)."""
+    """The BF16 cache against the oracle run with BF16 K/V. Against the
+    reference-semantics (f32 KV) golden the device tokens depart at decode
+    step 10, where the reference's top-2 margin is 0.0133: the measured cost
+    of the BF16 cache at 32K context, pinned."""
     gold = _load("qwen2_7b_32k_greedy.json")
     info = _qwen2_7b(hip, "bf16", gold)
-    path = os.path.join(GOLDEN, "qwen2_7b_32k_f32kv_greedy.json")
-    if os.path.exists(path):
-        with open(path) as f:
-            ref = json.load(f)
-        first = _first_departure(info["tokens"][:32], ref["tokens"][:32])
-        if first is not None:
-            print(f"[large] bf16-KV tokens depart from the reference at step {first}, reference top-2 margin "
-                  f"{ref['top2_margins'][first]:.4f}", flush=True)
-            assert ref["top2_margins"][first] < 0.05
+    ref = _load("qwen2_7b_32k_f32kv_greedy.json")
+    assert info["turn1_token"] == ref["turn1_token"]
+    first = _first_departure(info["tokens"][:32], ref["tokens"][:32])
+    print(f"[large] bf16-KV tokens depart from the reference at step {first}, reference top-2 margin "
+          f"{ref['top2_margins'][first]:.4f}", flush=True)
+    assert first == 10
+    assert abs(ref["top2_margins"][first] - 0.0133) < 1e-3
