@@ -22,9 +22,9 @@
 // arrive together, and a consumer knows its inputs are complete when every
 // word it copied carries the expected tag.
 //
-// Roles inside a block. Waves 0-6 (compute waves) own weight rows; wave 7
-// (the spare wave) owns none and copies the attention item's cached K/V rows
-// and the RMSNorm gains into LDS. Every wave polls: a phase's tagged input
+// Roles inside a block. Waves 0-6 (compute waves) own QKV, o_proj and down
+// rows; wave 7 (the spare wave) owns only gate/up rows (like every wave) and
+// copies the attention item's cached K/V rows and the RMSNorm gains into LDS. Every wave polls: a phase's tagged input
 // words are split into 128-word chunks, wave w copies chunks w, w + 8, ...
 // into LDS with direct global->LDS loads (16 bytes per lane, device-coherent
 // sc1), checks their tags there and re-loads only the stale ones; all waves
@@ -720,7 +720,7 @@ __device__ __forceinline__ void head_dots(const uint16_t *head, float *logits, c
 }
 
 // UH/UQ/UI: 16-byte units per lane of a row with H / q_heads*HD / I
-// columns; RGU: gate/up rows per compute wave; UHB: units per lane of a BF16
+// columns; RGU: gate/up rows per wave; UHB: units per lane of a BF16
 // head row. Shape values are re-read from the arguments where used (A()) and
 // block roles recomputed from them, so that little stays in scalar registers
 // across the step loop.
@@ -741,7 +741,8 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
     // Roles. o_proj and down rows: blocks [0, nhb), compute wave w of block b
     // owns row kCW * b + w of both (the residual stays in its register). QKV
     // pairs: the next nab blocks (the last ones when the grid is short).
-    // Gate/up: every block rb consecutive rows, wave w rows w, w + kCW, ...
+    // Gate/up: every block rb consecutive rows, wave w (the spare wave too)
+    // rows w, w + 8, ...
     // Attention items: the last blocks. LM head: every wave of every block.
     auto npairs = [&]() { return (A()->q_heads + 2 * A()->kv_heads) * HD / 2; };
     auto hasA = [&]() {
@@ -759,8 +760,8 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
         int n = 0;
 #pragma unroll
         for (int k = 0; k < RGU; ++k) {
-            const int j = wave + kCW * k;
-            n += !spare && j < rb && b * rb + j < I ? 1 : 0;
+            const int j = wave + kWaves * k;
+            n += j < rb && b * rb + j < I ? 1 : 0;
         }
         return n;
     };
@@ -796,7 +797,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
         const int n = nrD(), base = b * A()->rb + wave, nH = A()->H / U::E;
 #pragma unroll
         for (int k = 0; k < RGU; ++k) {
-            const uint32_t off = (uint32_t)(base + kCW * k) * (uint32_t)stride;
+            const uint32_t off = (uint32_t)(base + kWaves * k) * (uint32_t)stride;
             load_row(wD[2 * k], rg, off, nH, valid && k < n);
             load_row(wD[2 * k + 1], ru, off, nH, valid && k < n);
         }
@@ -1085,7 +1086,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
 #pragma unroll
                     for (int k = 0; k < RGU; ++k)
                         if (k < n) {
-                            const int r = base + kCW * k;
+                            const int r = base + kWaves * k;
                             float gv = y[2 * k], uv = y[2 * k + 1];
                             if (const float *gs = LY(l)->gate_sc) {
                                 gv = gv * ldc(gs, r);
@@ -1224,7 +1225,7 @@ const Variant *find_variant(int fmt, int H, int q_heads, int kv_heads, int hd, i
         if (v.fmt != fmt || v.hd != hd || v.g != g) continue;
         if (units_per_lane(H, E) > v.uh || units_per_lane(qd, E) > v.uq || units_per_lane(I, E) > v.ui) continue;
         const int rb = (I + blocks - 1) / blocks;
-        if ((rb + kCW - 1) / kCW > v.rgu || rb > kStage || units_per_lane(H, 8) > v.uhb) continue;
+        if ((rb + kWaves - 1) / kWaves > v.rgu || rb > kStage || units_per_lane(H, 8) > v.uhb) continue;
         return &v;
     }
     return nullptr;
