@@ -497,6 +497,8 @@ __host__ __device__ inline LdsLayout lds_layout(int H, int I, int nq, int hd, in
     LdsLayout o{};
     int tbw = imax(imax(H, I), imax((G + 2) * hd, 2 * blocks));
     tbw = imax(tbw, max_splits * nq * (hd + 2));
+    const int rb = (I + blocks - 1) / blocks;
+    tbw = imax(tbw, (I + rb - 1) / rb * kCW);  // one o/down block's down partials
     o.tbw = round_up(tbw + 2, kChunk);
     const int xf = xpad(imax(imax(H, I), nq * hd)) + 10;
     o.xs = o.tbw * 8;
@@ -719,12 +721,13 @@ __device__ __forceinline__ void head_dots(const uint16_t *head, float *logits, c
     pin(hb[0]);
 }
 
-// UH/UQ/UI: 16-byte units per lane of a row with H / q_heads*HD / I
-// columns; RGU: gate/up rows per wave; UHB: units per lane of a BF16
+// UH/UQ: 16-byte units per lane of a row with H / q_heads*HD columns; UP:
+// 16-byte units of a down_cols row (one per thread); RGU: gate/up rows per
+// wave; UHB: units per lane of a BF16
 // head row. Shape values are re-read from the arguments where used (A()) and
 // block roles recomputed from them, so that little stays in scalar registers
 // across the step loop.
-template <int FMT, int HD, int G, class KT, int UH, int UQ, int UI, int RGU, int UHB, bool HS>
+template <int FMT, int HD, int G, class KT, int UH, int UQ, int UP, int RGU, int UHB, bool HS>
 __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
     using U = Unit<FMT, 16>;
     constexpr int ROW = HD * (int)sizeof(KT);
@@ -767,7 +770,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
     };
     auto hasHead = [&]() { return b * kWaves < A()->V; };
 
-    u32x4 wA[2][UH], wC[1][UQ], wD[2 * RGU][UH], wE[1][UI];
+    u32x4 wA[2][UH], wC[1][UQ], wD[2 * RGU][UH], wP[2][UP];
 
     // Weight rows of layer l. Every wave issues the same loads at the same
     // points (the spare wave's and those of rows a wave does not own read
@@ -802,10 +805,23 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
             load_row(wD[2 * k + 1], ru, off, nH, valid && k < n);
         }
     };
-    auto load_wE = [&](int l, bool valid) {
-        const size_t stride = A()->down_stride;
-        const Rsrc r = rsrc(LY(l)->down, (size_t)A()->H * stride);
-        load_row(wE[0], r, (uint32_t)rowH() * (uint32_t)stride, A()->I / U::E, valid && myH());
+    // This block's down_cols rows: output rows q and q + 512 of thread q,
+    // UP units each (units past the padded row read nothing).
+    auto load_wP = [&](int l, bool valid) {
+        const int H = A()->H;
+        const uint32_t row_bytes = (uint32_t)A()->rp * 2u;
+        const Rsrc r = rsrc(LY(l)->down_cols, (size_t)gridDim.x * H * row_bytes);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int row = tid_here() + kThreads * i;
+            const bool v = valid && hasD() && row < H;
+            const uint32_t base = ((uint32_t)b * (uint32_t)H + (uint32_t)row) * row_bytes;
+#pragma unroll
+            for (int u = 0; u < UP; ++u) {
+                const uint32_t off = v && (uint32_t)u * 16u < row_bytes ? base + (uint32_t)u * 16u : kNoRead;
+                wP[i][u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
+            }
+        }
     };
 
     // Layer 0's inputs need the token: the embedding row (spare wave of QKV
@@ -1014,7 +1030,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
             // would hold back the item's q poll.
             load_wC(l, true);
             load_wD(l, true);
-            load_wE(l, true);
+            load_wP(l, true);
             mark(16 * l + 7);
 
             // ---- C: partials merged in split order (weights exp(m_s - M),
@@ -1096,32 +1112,55 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                         }
                 }
             }
-            if (hasD()) {
-                bar();
-                const int cnt = min(A()->rb, A()->I - b * A()->rb);
-                if (wave == 0 && lane < cnt) stf(A()->act + b * A()->rb + lane, sm.out[lane], tD);
+            // The block's down partials: thread q's output rows r = q, q + 512
+            // sum down[r][b rb + j] * act_j over the block's gate/up rows j
+            // in order (padding columns are zero). Every block runs the
+            // multiply-adds, so every path consumes the loaded rows.
+            if (hasD()) bar();
+            {
+                const int cnt = hasD() ? min(A()->rb, A()->I - b * A()->rb) : 0;
+                float acc[2] = {0.f, 0.f};
+#pragma unroll
+                for (int u = 0; u < UP; ++u) {
+                    float av[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) av[e] = 8 * u + e < cnt ? sm.out[8 * u + e] : 0.f;
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) {
+                        const uint32_t raw[4] = {wP[i][u][0], wP[i][u][1], wP[i][u][2], wP[i][u][3]};
+                        U::decode(raw, [&](int e, float v) { acc[i] = fmaf(v, av[e], acc[i]); });
+                    }
+                }
+                // Rows up to 7 nhb (the last o/down block's group is whole;
+                // rows past H carry zeros).
+                if (cnt > 0) {
+                    const int rows = A()->nhb * kCW, nbd = A()->nbd;
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) {
+                        const int row = tid_here() + kThreads * i;
+                        if (row < rows) stf(A()->pdown + ((size_t)(row / kCW) * nbd + b) * kCW + row % kCW, acc[i], tD);
+                    }
+                }
             }
             load_wA(ln, more);
             mark(16 * l + 11);
 
-            // ---- E: down + residual.
-            const int nI_e = A()->I / U::E;
-            const float *down_sc = LY(l)->down_sc;
+            // ---- E: the down partials of this block's rows summed in block
+            // order (lane j adds blocks j, j + 64, ...; then the fixed wave
+            // tree), + residual. (BF16 weights only: no row scale.)
             uint64_t *hid1 = A()->hid1;
             if (hasH()) {
-                gather(tb, A()->act, A()->I, tD, A()->abort_flag);
-                bar();
-                block_stage<false>(xs, tb, A()->I, nullptr, 0.f);
+                const int nbd = A()->nbd;
+                gather(tb, A()->pdown + (size_t)b * nbd * kCW, nbd * kCW, tD, A()->abort_flag);
                 bar();
             }
             mark(16 * l + 12);
             if (myH()) {
-                const int r = rowH();
-                float y[1];
-                dot_rows<FMT>(wE, xs, nI_e, y);
+                const int nbd = A()->nbd;
+                float v = 0.f;
+                for (int j = lane; j < nbd; j += 64) v += val_of(tb[j * kCW + wave]);
+                v = wave_sum(v);
                 mark(16 * l + 15);
-                float v = y[0];
-                if (down_sc) v = v * ldc(down_sc, r);
                 h_own = h_own + v;
                 if (lane == 0) sm.out[wave] = h_own;
             }
@@ -1140,7 +1179,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
         pin(wA);
         pin(wC);
         pin(wD);
-        pin(wE);
+        pin(wP);
         const unsigned tH = tb0 + 5 * L;
         int key = INT_MIN;
         uint32_t idx = 0;
@@ -1161,7 +1200,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
         pin(wA);
         pin(wC);
         pin(wD);
-        pin(wE);
+        pin(wP);
         mark(16 * L + 1);
         uint64_t *am = A()->am + (size_t)(s & 1) * gridDim.x * 2;
         if (hasHead() && tid_here() == 0) {
@@ -1201,15 +1240,15 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
 }
 
 struct Variant {
-    int fmt, hd, g, uh, uq, ui, rgu, uhb;
+    int fmt, hd, g, uh, uq, up, rgu, uhb;
 };
 
 // Shapes with a built kernel: Qwen2-0.5B (hidden 896, 14/2 heads of 64,
 // intermediate 4864) and the two small test shapes.
 constexpr Variant kVariants[] = {
-    {FMT_BF16, 64, 7, 2, 2, 10, 3, 2},
+    {FMT_BF16, 64, 7, 2, 2, 3, 3, 2},
     {FMT_BF16, 64, 2, 1, 1, 1, 1, 1},
-    {FMT_BF16, 128, 4, 1, 2, 2, 1, 1},
+    {FMT_BF16, 128, 4, 1, 2, 1, 1, 1},
 };
 
 int units_per_lane(int cols, int elems_per_unit) { return (cols / elems_per_unit + 63) / 64; }
@@ -1223,7 +1262,10 @@ const Variant *find_variant(int fmt, int H, int q_heads, int kv_heads, int hd, i
     if ((qd + 2 * kvd) / 2 > W || H > W) return nullptr;
     for (const Variant &v : kVariants) {
         if (v.fmt != fmt || v.hd != hd || v.g != g) continue;
-        if (units_per_lane(H, E) > v.uh || units_per_lane(qd, E) > v.uq || units_per_lane(I, E) > v.ui) continue;
+        if (units_per_lane(H, E) > v.uh || units_per_lane(qd, E) > v.uq) continue;
+        // One thread per down_cols row pair: 7 ceil(H / 7) <= 2 * 512; UP
+        // units per row.
+        if ((H + kCW - 1) / kCW * kCW > 2 * kThreads || fused_gate_rows_padded(I, blocks) / 8 > v.up) continue;
         const int rb = (I + blocks - 1) / blocks;
         if ((rb + kWaves - 1) / kWaves > v.rgu || rb > kStage || units_per_lane(H, 8) > v.uhb) continue;
         return &v;
@@ -1239,9 +1281,9 @@ size_t static_lds_bytes(int hd, int g) {
     return sizeof(Shm) + att;
 }
 
-template <int FMT, int HD, int G, class KT, int UH, int UQ, int UI, int RGU, int UHB, bool HS>
+template <int FMT, int HD, int G, class KT, int UH, int UQ, int UP, int RGU, int UHB, bool HS>
 int launch_one(FusedArgs a, int nb, hipStream_t s) {
-    auto k = decode_flow_kernel<FMT, HD, G, KT, UH, UQ, UI, RGU, UHB, HS>;
+    auto k = decode_flow_kernel<FMT, HD, G, KT, UH, UQ, UP, RGU, UHB, HS>;
     const LdsLayout lay = lds_layout(a.H, a.I, a.q_heads, HD, G, (int)sizeof(KT), nb, a.max_splits);
     a.lds_xs = lay.xs;
     a.lds_kv = lay.kv;
@@ -1253,7 +1295,9 @@ int launch_one(FusedArgs a, int nb, hipStream_t s) {
     a.nhb = (a.H + kCW - 1) / kCW;
     a.nab = (npairs + kCW - 1) / kCW;
     a.a0 = a.nhb + a.nab <= nb ? a.nhb : nb - a.nab;
-    a.rb = (a.I + nb - 1) / nb;
+    a.rb = fused_gate_rows(a.I, nb);
+    a.rp = fused_gate_rows_padded(a.I, nb);
+    a.nbd = (a.I + a.rb - 1) / a.rb;
     a.head_blocks = std::min(nb, (a.V + kWaves - 1) / kWaves);
     const size_t lds = (size_t)lay.total;
     hipFuncAttributes attr{};
@@ -1276,9 +1320,9 @@ int launch_one(FusedArgs a, int nb, hipStream_t s) {
 
 template <class KT, bool HS>
 int launch_kt(const Variant &v, const FusedArgs &a, int nb, hipStream_t s) {
-    if (v.hd == 64 && v.g == 7) return launch_one<FMT_BF16, 64, 7, KT, 2, 2, 10, 3, 2, HS>(a, nb, s);
+    if (v.hd == 64 && v.g == 7) return launch_one<FMT_BF16, 64, 7, KT, 2, 2, 3, 3, 2, HS>(a, nb, s);
     if (v.hd == 64 && v.g == 2) return launch_one<FMT_BF16, 64, 2, KT, 1, 1, 1, 1, 1, HS>(a, nb, s);
-    if (v.hd == 128 && v.g == 4) return launch_one<FMT_BF16, 128, 4, KT, 1, 2, 2, 1, 1, HS>(a, nb, s);
+    if (v.hd == 128 && v.g == 4) return launch_one<FMT_BF16, 128, 4, KT, 1, 2, 1, 1, 1, HS>(a, nb, s);
     return fail("HIP backend: no persistent decode kernel for this shape.");
 }
 
@@ -1302,6 +1346,29 @@ int fused_positions_per_item(int head_dim, bool kv_f32) {
 bool fused_decode_supported(int fmt, int H, int q_heads, int kv_heads, int head_dim, int I, bool aligned16,
                             int blocks) {
     return aligned16 && blocks > 0 && find_variant(fmt, H, q_heads, kv_heads, head_dim, I, blocks) != nullptr;
+}
+
+// dst[b][r][j] = down[r][b rb + j] for j < rb and b rb + j < I, else 0;
+// one thread per element of dst.
+__global__ void down_columns_kernel(const uint16_t *down, size_t stride, int H, int I, int rb, int rp, int blocks,
+                                    uint16_t *dst) {
+    const size_t n = (size_t)blocks * H * rp;
+    for (size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x; t < n; t += (size_t)gridDim.x * blockDim.x) {
+        const int j = (int)(t % rp);
+        const size_t br = t / rp;
+        const int r = (int)(br % H), b = (int)(br / H);
+        const long col = (long)b * rb + j;
+        dst[t] = j < rb && col < I ? ((const uint16_t *)((const uint8_t *)down + (size_t)r * stride))[col] : (uint16_t)0;
+    }
+}
+
+int fused_down_columns(const uint16_t *down, size_t stride, int H, int I, int blocks, uint16_t *dst, hipStream_t s) {
+    const int rb = fused_gate_rows(I, blocks), rp = fused_gate_rows_padded(I, blocks);
+    const size_t n = (size_t)blocks * H * rp;
+    const int grid = (int)std::min<size_t>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(down_columns_kernel, dim3(grid), dim3(256), 0, s, down, stride, H, I, rb, rp, blocks, dst);
+    CHIP_CHECK(hipGetLastError());
+    return 0;
 }
 
 int fused_decode_blocks() {

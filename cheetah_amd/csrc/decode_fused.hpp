@@ -14,6 +14,9 @@ struct FusedLayer {
     const float *o_bias;    // f32 or null
     const uint16_t *ln1, *ln2;
     void *kc, *vc;
+    // down_proj columns of each block's gate/up rows, transposed and
+    // zero-padded: [blocks][H][rp] BF16 (fused_down_columns).
+    const uint16_t *down_cols;
 };
 
 // Cross-block values travel as 64-bit words: low half the f32 bits, high
@@ -36,7 +39,7 @@ struct FusedArgs {
     uint64_t *hid0, *hid1;      // [H] residual stream after o_proj / after down
     uint64_t *qkvn;             // [kv_heads][(G + 2) * hd]: a group's rotated q heads, then its new K and V rows
     uint64_t *part;             // [max_splits][q_heads][hd + 2] attention partials (output, max, sum)
-    uint64_t *act;              // [I] SwiGLU output
+    uint64_t *pdown;            // [nhb][nbd][7]: gate/up block j's down partial of output rows 7 i .. 7 i + 6
     uint64_t *am;               // [2][blocks][2] argmax partials (key, index) by step parity
     int *abort_flag;            // raised when a poll times out
     unsigned tag0;              // tag of step 0, phase 0 of this launch
@@ -50,6 +53,8 @@ struct FusedArgs {
     // per block, blocks owning LM-head rows).
     int lds_xs, lds_kv, lds_mw, lds_emb, lds_gain, lds_total;
     int nhb, a0, nab, rb, head_blocks;
+    int rp;   // rb rounded up to a multiple of 8 (a down_cols row)
+    int nbd;  // blocks that own gate/up rows
 };
 
 // Phases per decode step: 5 per layer (qkv, attention, o, gate/up, down) + head.
@@ -67,6 +72,15 @@ int fused_decode_blocks();
 // (capped by the grid and by `capacity` positions); 0 if none fits.
 int fused_max_splits(int H, int q_heads, int kv_heads, int head_dim, int I, bool kv_f32, int blocks,
                      size_t capacity);
+
+// Gate/up rows per block and their padded count on `blocks` blocks.
+inline int fused_gate_rows(int I, int blocks) { return (I + blocks - 1) / blocks; }
+inline int fused_gate_rows_padded(int I, int blocks) { return (fused_gate_rows(I, blocks) + 7) / 8 * 8; }
+
+// Writes dst[b][r][j] = down[r][b * rb + j] (BF16; 0 for j >= rb or a
+// column past I), rb = fused_gate_rows(I, blocks), for b < blocks, r < H,
+// j < fused_gate_rows_padded(I, blocks). down rows are `stride` bytes apart.
+int fused_down_columns(const uint16_t *down, size_t stride, int H, int I, int blocks, uint16_t *dst, hipStream_t s);
 
 // Fills in a.lds_* and launches (a is taken by value for that).
 int launch_decode_fused(FusedArgs a, int fmt, int head_dim, int group, bool kv_f32, hipStream_t s);

@@ -81,6 +81,9 @@ struct Layer {
     float *o_bias = nullptr;    // f32 [hidden] or null
     uint16_t *ln1 = nullptr, *ln2 = nullptr;
     KvLayer kv;
+    // The persistent decode kernel's copy of down_proj, columns regrouped
+    // per block (fused_down_columns); built once, while down is resident.
+    uint16_t *down_cols = nullptr;
     // Host tier: pinned copy of a matrix whose device buffer was released
     // (its WMat base is then null); indexed like mat(). Null when resident.
     uint8_t *host[kLayerMats] = {};
@@ -128,6 +131,7 @@ struct Shared {
     hipStream_t copy_stream = nullptr;
     int host_mats = 0;       // layer matrices on the host tier
     unsigned epoch = 0;      // bumped whenever a weight's device address changes
+    int down_cols_blocks = 0;  // grid size the layers' down_cols are built for (0: none)
     size_t slot_bytes = 0;   // one layer's matrices, as a feed slot holds them
 
     int q_dim() const { return (int)(cfg.q_heads * cfg.head_dim); }
@@ -206,6 +210,7 @@ struct cheetah_hip_model {
     // Persistent decode kernel state (decode_fused.hip).
     bool fused_ok = false;
     FusedLayer *fused_layers = nullptr;  // device [L]
+    int table_cols_blocks = 0;           // the table's down_cols were built for this grid (0: none yet)
     int fused_blocks = 0;
     int fused_max_splits = 0;
     uint64_t *tagged = nullptr;  // hid0 | hid1 | qkvn | part | act | am, tagged words
@@ -431,13 +436,15 @@ int finalize(cheetah_hip_model *m) {
 }
 
 // Sizes (words) of the tagged arrays in one allocation: hid0, hid1, qkvn,
-// part, act, am; each rounded to an even count plus 2 words, so every array
+// part, pdown, am; each rounded to an even count plus 2 words, so every array
 // starts 16-byte aligned and a 16-byte read at its last word stays inside.
 std::vector<size_t> fused_tagged_sizes(const cheetah_hip_model *m) {
     const auto &c = m->sh->cfg;
     const size_t hd = c.head_dim, G = c.q_heads / c.kv_heads;
+    const size_t rb = (size_t)fused_gate_rows((int)c.intermediate_size, m->fused_blocks);
+    const size_t nbd = (c.intermediate_size + rb - 1) / rb, nhb = (c.hidden_size + 6) / 7;
     const size_t raw[] = {c.hidden_size, c.hidden_size, c.kv_heads * (G + 2) * hd,
-                          (size_t)m->fused_max_splits * c.q_heads * (hd + 2), c.intermediate_size,
+                          (size_t)m->fused_max_splits * c.q_heads * (hd + 2), nhb * nbd * 7,
                           4 * (size_t)m->fused_blocks};
     std::vector<size_t> out;
     for (size_t n : raw) out.push_back((n + 1) / 2 * 2 + 2);
@@ -454,11 +461,13 @@ int upload_fused_layers(cheetah_hip_model *m) {
         const Layer &L = sh.layers[l];
         fl[l] = FusedLayer{L.qkv.payload(), L.o.payload(), L.gate.payload(), L.up.payload(), L.down.payload(),
                            L.qkv.scales(), L.o.scales(), L.gate.scales(), L.up.scales(), L.down.scales(),
-                           L.qkv_bias, L.o_bias, L.ln1, L.ln2, L.kv.k, L.kv.v};
+                           L.qkv_bias, L.o_bias, L.ln1, L.ln2, L.kv.k, L.kv.v, L.down_cols};
     }
     CHIP_CHECK(hipMemcpy(m->fused_layers, fl.data(), fl.size() * sizeof(FusedLayer), hipMemcpyHostToDevice));
     return 0;
 }
+
+int ensure_down_cols(cheetah_hip_model *m);
 
 // Persistent decode state of one instance: the per-layer pointer table and
 // the tagged hand-off words. Sets fused_ok when the model's shape and layout
@@ -497,6 +506,7 @@ int init_fused(cheetah_hip_model *m) {
     }
     CHIP_TRY(m->mem.alloc(&m->fused_layers, c.num_layers));
     CHIP_TRY(upload_fused_layers(m));
+    if (!sh.host_mats) CHIP_TRY(ensure_down_cols(m));
     m->tagged_words = 0;
     for (size_t n : fused_tagged_sizes(m)) m->tagged_words += n;
     CHIP_TRY(m->mem.alloc(&m->tagged, m->tagged_words));
@@ -530,9 +540,38 @@ bool fused_fits(const cheetah_hip_model *m, size_t offset, size_t steps) {
 // Runs `steps` decode steps in one persistent launch from the token and
 // position (`offset`, also in step_dev); leaves the last step's logits in m->logits, its
 // argmax in next_dev and every sampled id in hist_dev. Waits for the launch.
+// Builds every layer's down_cols for this instance's grid once per model
+// (the persistent kernel runs only while every matrix is resident), and
+// points this instance's layer table at them.
+int ensure_down_cols(cheetah_hip_model *m) {
+    Shared &sh = *m->sh;
+    if (m->table_cols_blocks == m->fused_blocks) return 0;
+    {
+        std::lock_guard<std::mutex> lock(sh.mu);
+        if (sh.down_cols_blocks != m->fused_blocks) {
+            const auto &c = sh.cfg;
+            const int H = (int)c.hidden_size, I = (int)c.intermediate_size, nb = m->fused_blocks;
+            const size_t elems = (size_t)nb * H * fused_gate_rows_padded(I, nb);
+            if (sh.down_cols_blocks != 0) return fail("HIP backend: persistent decode grid changed.");
+            for (Layer &L : sh.layers) {
+                if (!L.down.payload()) return fail("HIP backend: persistent decode needs every matrix resident.");
+                if (!L.down_cols) CHIP_TRY(sh.mem.alloc(&L.down_cols, elems));
+                CHIP_TRY(fused_down_columns((const uint16_t *)L.down.payload(), L.down.row_stride(), H, I, nb,
+                                            L.down_cols, m->stream));
+            }
+            CHIP_CHECK(hipStreamSynchronize(m->stream));
+            sh.down_cols_blocks = nb;
+        }
+    }
+    CHIP_TRY(upload_fused_layers(m));
+    m->table_cols_blocks = m->fused_blocks;
+    return 0;
+}
+
 int run_fused(cheetah_hip_model *m, size_t offset, size_t steps) {
     Shared &sh = *m->sh;
     const auto &c = sh.cfg;
+    CHIP_TRY(ensure_down_cols(m));
     const unsigned per_step = (unsigned)fused_phases_per_step((int)c.num_layers);
     if ((uint64_t)m->next_tag + (uint64_t)steps * per_step >= 0xFFFFFF00ull) {
         // Tags are about to wrap: start over from zeroed words.
@@ -565,7 +604,7 @@ int run_fused(cheetah_hip_model *m, size_t offset, size_t steps) {
     a.hist_cap = (long)sh.kv_capacity + 1;
     a.logits = m->logits;
     uint64_t *t = m->tagged;
-    uint64_t **dst[] = {&a.hid0, &a.hid1, &a.qkvn, &a.part, &a.act, &a.am};
+    uint64_t **dst[] = {&a.hid0, &a.hid1, &a.qkvn, &a.part, &a.pdown, &a.am};
     const std::vector<size_t> sizes = fused_tagged_sizes(m);
     for (size_t i = 0; i < sizes.size(); ++i) {
         *dst[i] = t;
