@@ -1111,12 +1111,19 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                             if (lane == 0) sm.out[r - b * A()->rb] = gv * (uv / (1.0f + expf(-gv)));
                         }
                 }
+                // Zeros after the block's outputs, up to the padded row.
+                {
+                    const int cnt = hasD() ? min(A()->rb, A()->I - b * A()->rb) : 0;
+                    if (tid_here() >= cnt && tid_here() < UP * 8) sm.out[tid_here()] = 0.f;
+                }
             }
             // The block's down partials: thread q's output rows r = q, q + 512
             // sum down[r][b rb + j] * act_j over the block's gate/up rows j
-            // in order (padding columns are zero). Every block runs the
-            // multiply-adds, so every path consumes the loaded rows.
+            // in order (padding columns and outputs are zero). Every block
+            // runs the multiply-adds, so every path consumes the loaded rows
+            // (pinned here: the compiler then waits for them once, up front).
             if (hasD()) bar();
+            pin(wP);
             {
                 const int cnt = hasD() ? min(A()->rb, A()->I - b * A()->rb) : 0;
                 float acc[2] = {0.f, 0.f};
@@ -1124,7 +1131,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                 for (int u = 0; u < UP; ++u) {
                     float av[8];
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) av[e] = 8 * u + e < cnt ? sm.out[8 * u + e] : 0.f;
+                    for (int e = 0; e < 8; ++e) av[e] = sm.out[8 * u + e];
 #pragma unroll
                     for (int i = 0; i < 2; ++i) {
                         const uint32_t raw[4] = {wP[i][u][0], wP[i][u][1], wP[i][u][2], wP[i][u][3]};
