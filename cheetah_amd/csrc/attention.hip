@@ -52,7 +52,23 @@ struct AttnArgs {
     const float *qkv;
     const float *rope_cos, *rope_sin;
     int rotary_dim;
+    // Chunked prefill: BF16 halves of out (null: not written).
+    uint16_t *out_hi, *out_lo;
 };
+
+// hi = bf16(v), lo = bf16(v - hi) (hardware round-to-nearest-even) of four
+// consecutive outputs at element i: the split the next GEMM takes as input.
+__device__ __forceinline__ void store_halves4(uint16_t *hi, uint16_t *lo, size_t i, f32x4 v) {
+    uint16_t h[4], l[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const __bf16 hb = (__bf16)v[q];
+        h[q] = __builtin_bit_cast(uint16_t, hb);
+        l[q] = __builtin_bit_cast(uint16_t, (__bf16)(v[q] - (float)hb));
+    }
+    *(uint2 *)(hi + i) = make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+    *(uint2 *)(lo + i) = make_uint2((uint32_t)l[0] | ((uint32_t)l[1] << 16), (uint32_t)l[2] | ((uint32_t)l[3] << 16));
+}
 
 // Eight consecutive K or V elements as loaded (converted to f32 at use), so
 // a whole tile can be in flight while the previous one computes.
@@ -899,14 +915,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     // O^T registers: lane's M row, dims 32 u + 8 (r / 4) + 4 half + r % 4.
     if (S == 1) {
         const float inv = 1.0f / l;
-        float *o = a.out + (size_t)row * (size_t)a.q_heads * HD + (size_t)head * HD;
+        const size_t ob = (size_t)row * (size_t)a.q_heads * HD + (size_t)head * HD;
+        float *o = a.out + ob;
 #pragma unroll
         for (int u = 0; u < UT; ++u)
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-                *(f32x4 *)(o + 32 * u + 8 * q + 4 * half) =
-                    f32x4{oacc[u][4 * q] * inv, oacc[u][4 * q + 1] * inv, oacc[u][4 * q + 2] * inv,
-                          oacc[u][4 * q + 3] * inv};
+            for (int q = 0; q < 4; ++q) {
+                const f32x4 v = f32x4{oacc[u][4 * q] * inv, oacc[u][4 * q + 1] * inv, oacc[u][4 * q + 2] * inv,
+                                      oacc[u][4 * q + 3] * inv};
+                *(f32x4 *)(o + 32 * u + 8 * q + 4 * half) = v;
+                if (a.out_hi) store_halves4(a.out_hi, a.out_lo, ob + 32 * u + 8 * q + 4 * half, v);
+            }
     } else {
 #pragma unroll
         for (int u = 0; u < UT; ++u)
@@ -928,7 +947,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 // kernel writes.
 template <int HD>
 __global__ __launch_bounds__(kThreads) void attn_merge2_kernel(const float *part, int S, int q_heads, int items,
-                                                              float *out) {
+                                                              float *out, uint16_t *out_hi, uint16_t *out_lo) {
     const int lane = threadIdx.x & 63;
     const int item = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
     if (item >= items) return;
@@ -950,7 +969,16 @@ __global__ __launch_bounds__(kThreads) void attn_merge2_kernel(const float *part
         }
     }
 #pragma unroll
-    for (int k = 0; k < DPL; ++k) out[(size_t)item * HD + lane + 64 * k] = o[k] * inv;
+    for (int k = 0; k < DPL; ++k) {
+        const size_t i = (size_t)item * HD + lane + 64 * k;
+        const float v = o[k] * inv;
+        out[i] = v;
+        if (out_hi) {
+            const __bf16 hb = (__bf16)v;
+            out_hi[i] = __builtin_bit_cast(uint16_t, hb);
+            out_lo[i] = __builtin_bit_cast(uint16_t, (__bf16)(v - (float)hb));
+        }
+    }
 }
 
 template <int HD, int G>
@@ -963,7 +991,7 @@ int launch_prefill_hg(const AttnJob &j, const AttnArgs &a, int S, hipStream_t s)
     if (S > 1) {
         const int items = (int)j.rows * j.q_heads;
         hipLaunchKernelGGL((attn_merge2_kernel<HD>), dim3((items + 3) / 4), dim3(kThreads), 0, s, a.part, S,
-                           j.q_heads, items, a.out);
+                           j.q_heads, items, a.out, a.out_hi, a.out_lo);
         CHIP_CHECK(hipGetLastError());
     }
     return 0;
@@ -1112,6 +1140,10 @@ int launch_attention(const AttnJob &j, hipStream_t s) {
         if (S > kMaxSplits) return fail("HIP backend: prefill context exceeds the attention split limit.");
         if (S > 1 && (!j.part || j.part_floats < attention_part_floats(j.rows, j.q_heads, S, j.g.head_dim)))
             return fail("HIP backend: prefill attention partial buffer too small.");
+        if (!j.out_hi != !j.out_lo || ((uintptr_t)j.out_hi % 8) || ((uintptr_t)j.out_lo % 8))
+            return fail("HIP backend: prefill attention halves need both 8-byte aligned buffers.");
+        a.out_hi = j.out_hi;
+        a.out_lo = j.out_lo;
         if (j.g.head_dim == 64) return launch_prefill_h<64>(j, a, G, S, s);
         return launch_prefill_h<128>(j, a, G, S, s);
     }

@@ -165,6 +165,10 @@ struct AttnJob {
     const float *qkv = nullptr;
     const float *rope_cos = nullptr, *rope_sin = nullptr;
     int rotary_dim = 0;
+    // Chunked prefill on the matrix cores (attention_prefill_on_mfma) also
+    // writes out's BF16 halves here when set: hi = bf16(v), lo = bf16(v - hi),
+    // the bits launch_split_bf16 would write. Other paths ignore them.
+    uint16_t *out_hi = nullptr, *out_lo = nullptr;
 };
 int launch_attention(const AttnJob &job, hipStream_t s);
 // BF16 K/V on the matrix cores, head_dim 64/128, <= 8 q heads per KV head,

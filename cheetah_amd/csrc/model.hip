@@ -1036,6 +1036,12 @@ int enqueue_chunk(cheetah_hip_model *m, const uint32_t *tokens_dev, size_t rows,
         aj.part = m->part;
         aj.part_floats = m->part_floats;
         aj.prefill = true;
+        // The matrix-core prefill writes the o_proj input halves itself.
+        const bool halves = attention_prefill_on_mfma(aj.g, aj.q_heads);
+        if (halves) {
+            aj.out_hi = m->xh;
+            aj.out_lo = m->xl;
+        }
         CHIP_TRY(launch_attention(aj, s));
         GemmJob o;
         o.w = L.o;
@@ -1046,7 +1052,7 @@ int enqueue_chunk(cheetah_hip_model *m, const uint32_t *tokens_dev, size_t rows,
         o.epi = EPI_RESIDUAL;
         o.ws = m->gemm_ws;
         o.ws_floats = m->gemm_ws_floats;
-        CHIP_TRY(launch_split_bf16(m->attn, rows * (size_t)(sh.q_dim()), m->xh, m->xl, s));
+        if (!halves) CHIP_TRY(launch_split_bf16(m->attn, rows * (size_t)(sh.q_dim()), m->xh, m->xl, s));
         o.xh = m->xh;
         o.xl = m->xl;
         int o_chunks = 0;
