@@ -249,7 +249,7 @@ constexpr int kPad = 32;  // zero floats before and after x in LDS
 // of 4 banks. Element e (>= -kPad, the zeros before x) is at
 // x_addr(e) = e + ((e >> 5) << 2); a 16-byte read of 4 elements never
 // straddles a gap. Measured: Q4 4096x14336 10.9 -> 9.5 us, 4096^2 6.0 -> 5.7;
-// with four rows per wave, the dual gate/up, or Q8/BF16 the extra address
+// with the dual gate/up or Q8/BF16 the extra address
 // arithmetic costs more than the conflicts (x stays unpadded: xl = 0).
 __host__ __device__ constexpr int x_shift_log2(int fmt, int rows, bool dual) {
     return fmt == FMT_Q4 && rows == 2 && !dual ? 5 : 0;
@@ -650,9 +650,8 @@ int pick_ks(const Args &a, int P, int ks, int n_units, hipStream_t s) {
 // on MI355X (slots = 16 waves per CU): one row per wave streams BF16 / Q8
 // best. Q4 (twice the elements per byte) gains from sharing each x read
 // between rows once there are enough rows to keep the wave slots busy: two
-// rows per wave, four between 1.5 and 4 slots' worth of rows (not for the
-// dual gate/up GEMV, which already reads two matrices per row); measured
-// 5-12 % faster than one (dual 14336x4096: 20.1 vs 22.0 us). K is split when
+// rows per wave, measured 5-12 % faster than one (dual 14336x4096: 20.1 vs
+// 22.0 us). K is split when
 // the row groups are too few for the wave slots (Q4: below a quarter of
 // them, since its rows share x reads), keeping >= 2 units per lane.
 template <int FMT, bool NORM, bool DUAL>
@@ -661,17 +660,16 @@ int pick_aligned(const Args &a, int P, hipStream_t s) {
     const int n_units = (a.K + E - 1) / E;
     const long slots = (long)device_cus() * 16;
     int R = 1;
+    // (Four Q4 rows per wave for 6144-row matrices left the grid under one
+    // block per CU: 2,474 vs 2,488 tok/s on a 4-layer Llama-3-8B Q4 decode.)
     if constexpr (FMT == FMT_Q4) {
-        if (a.rows >= slots / 2) R = !DUAL && 2 * a.rows >= 3 * slots && a.rows < 4 * slots ? 4 : 2;
+        if (a.rows >= slots / 2) R = 2;
     }
     const long groups = (a.rows + R - 1) / R;
     const long busy = FMT == FMT_Q4 ? slots / 4 : slots;
     int ks = 1;
     while (ks < 8 && groups * ks < busy && n_units >= 64 * 2 * ks * 2) ks *= 2;
     if constexpr (FMT == FMT_Q4) {
-        if (R == 4) {
-            if constexpr (!DUAL) return pick_ks<FMT, 4, NORM, DUAL>(a, P, ks, n_units, s);
-        }
         if (R == 2) return pick_ks<FMT, 2, NORM, DUAL>(a, P, ks, n_units, s);
     }
     return pick_ks<FMT, 1, NORM, DUAL>(a, P, ks, n_units, s);
