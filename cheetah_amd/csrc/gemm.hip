@@ -1074,7 +1074,7 @@ int launch_gemm(const GemmJob &job, hipStream_t s) {
     if (!job.yh != !job.yl) return fail("HIP backend: gemm output halves need both BF16 buffers or neither.");
     a.yh = dual ? job.yh : nullptr;
     a.yl = dual ? job.yl : nullptr;
-    a.defer = job.deferred && job.epi == EPI_RESIDUAL ? 1 : 0;
+    a.defer = job.deferred && !dual ? 1 : 0;
     if (job.deferred) *job.deferred = 0;
     a.epi = job.epi;
     a.chunk = gemm_chunk_depth(a.K);

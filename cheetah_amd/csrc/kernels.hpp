@@ -63,10 +63,10 @@ struct GemmJob {
     // EPI_SWIGLU only, optional: the output also as BF16 halves ([n][rows]
     // each, the bits launch_split_bf16 would give), for the next GEMM.
     uint16_t *yh = nullptr, *yl = nullptr;
-    // EPI_RESIDUAL only, optional: when the GEMM splits K, leave the chunk
-    // sums in ws ([*deferred][n][rows]) for the caller's reduction
-    // (launch_residual_rmsnorm_rows) and set *deferred to the chunk count;
-    // 0 when the GEMM applied its epilogue itself.
+    // EPI_RESIDUAL / EPI_STORE, optional: when the GEMM splits K, leave the
+    // chunk sums in ws ([*deferred][n][rows]) for the caller's reduction
+    // (launch_residual_rmsnorm_rows, launch_rope_append) and set *deferred to
+    // the chunk count; 0 when the GEMM applied its epilogue itself.
     int *deferred = nullptr;
 };
 int launch_gemm(const GemmJob &job, hipStream_t stream);
@@ -129,9 +129,13 @@ int qkv_perm_row(int stored_row, int q_heads, int kv_heads, int head_dim, int ro
 // qrot[rows][q_dim] in reference order, K and V rows are appended to the
 // paged cache. Positions are pos0 + i, where pos0 is read from *pos_dev when
 // pos_dev is set (decode graph) and is `offset` otherwise.
+// With nchunks > 0 the qkv values are a deferred split-K GEMM's: the chunk
+// sums ws[nchunks][rows][q_dim + 2*kv_dim] folded in order, times sc (if
+// set), plus bias (if set) - the GEMM epilogue's arithmetic; qkv is unused.
 int launch_rope_append(const float *qkv, float *qrot, size_t rows, int q_heads, const KvGeom &g, const KvLayer &kv,
                        const float *rope_cos, const float *rope_sin, int rotary_dim, size_t offset,
-                       const int32_t *pos_dev, hipStream_t s);
+                       const int32_t *pos_dev, hipStream_t s, const float *ws = nullptr, int nchunks = 0,
+                       const float *sc = nullptr, const float *bias = nullptr);
 
 // dst[r][:] = src[map[r]][:] for rows of row_bytes bytes (load-time layout).
 int launch_gather_rows(const uint8_t *src, uint8_t *dst, const int32_t *map, size_t rows, size_t row_bytes,

@@ -114,38 +114,59 @@ __device__ __forceinline__ void store_kv(float *p, float v) { *p = v; }
 // kThreads elements over [q | k] (each k element also appends its v). A
 // thread issues its few loads at once, so a row costs one memory round trip
 // whatever its width.
-template <class KT>
+template <class KT, bool SUM>
 __global__ __launch_bounds__(kThreads) void rope_append_kernel(const float *__restrict__ qkv, float *__restrict__ qrot,
                                                                int q_heads, int kv_heads, int head_dim, int rotary_dim,
                                                                const float *__restrict__ cos_t,
                                                                const float *__restrict__ sin_t,
                                                                const int32_t *__restrict__ page_table, int page_size,
                                                                KT *__restrict__ kc, KT *__restrict__ vc, long offset,
-                                                               const int32_t *__restrict__ pos_dev) {
-    const int row = blockIdx.y;
+                                                               const int32_t *__restrict__ pos_dev,
+                                                               const float *__restrict__ ws, int nchunks,
+                                                               const float *__restrict__ sc,
+                                                               const float *__restrict__ bias) {
+    const int row = blockIdx.y, rows = gridDim.y;
     const int t = blockIdx.x * kThreads + threadIdx.x;
-    const int q_dim = q_heads * head_dim, kv_dim = kv_heads * head_dim;
+    const int q_dim = q_heads * head_dim, kv_dim = kv_heads * head_dim, width = q_dim + 2 * kv_dim;
     if (t >= q_dim + kv_dim) return;
     const long pos = (pos_dev ? (long)*pos_dev : offset) + row;
-    const float *q = qkv + (size_t)row * (q_dim + 2 * kv_dim);
+    const float *q = qkv + (size_t)row * width;
+    // Element col of this row: stored, or (SUM) the deferred GEMM's chunk
+    // sums folded in order, then scale and bias (its epilogue, same bits).
+    auto val = [&](int col) -> float {
+        if constexpr (SUM) {
+            float v = 0.f;
+            for (int z = 0; z < nchunks; ++z) v += ws[((size_t)z * rows + row) * width + col];
+            if (sc) v = v * sc[col];
+            if (bias) v = v + bias[col];
+            return v;
+        } else {
+            return q[col];
+        }
+    };
     const int half = rotary_dim / 2;
     const float *cr = cos_t + (size_t)pos * half;
     const float *sr = sin_t + (size_t)pos * half;
+    // rope_elem's arithmetic on element d of the head starting at column base.
+    auto rot = [&](int base, int d) -> float {
+        if (d >= rotary_dim) return val(base + d);
+        const int i = d < half ? d : d - half;
+        const float a = val(base + 2 * i), b = val(base + 2 * i + 1), c = cr[i], s = sr[i];
+        return d < half ? a * c - b * s : b * c + a * s;
+    };
     if (t < q_dim) {
         const int h = t / head_dim, d = t % head_dim;
-        qrot[(size_t)row * q_dim + t] = rope_elem(q + h * head_dim, d, half, rotary_dim, cr, sr);
+        qrot[(size_t)row * q_dim + t] = rot(h * head_dim, d);
         return;
     }
     const int u = t - q_dim;
-    const float *k = q + q_dim;
-    const float *v = k + kv_dim;
     const int h = u / head_dim, d = u % head_dim;
     const int page = page_table[pos / page_size];
     const int slot = (int)(pos % page_size);
-    const float kv = rope_elem(k + h * head_dim, d, half, rotary_dim, cr, sr);
+    const float kv = rot(q_dim + h * head_dim, d);
     const size_t off = (((size_t)page * kv_heads + h) * page_size + slot) * head_dim + d;
     store_kv(kc + off, kv);
-    store_kv(vc + off, v[u]);
+    store_kv(vc + off, val(q_dim + kv_dim + u));
 }
 
 __global__ __launch_bounds__(kThreads) void gather_rows_kernel(const uint8_t *src, uint8_t *dst, const int32_t *map,
@@ -266,21 +287,27 @@ int qkv_perm_row(int stored, int q_heads, int kv_heads, int head_dim, int rotary
 
 int launch_rope_append(const float *qkv, float *qrot, size_t rows, int q_heads, const KvGeom &g, const KvLayer &kv,
                        const float *rope_cos, const float *rope_sin, int rotary_dim, size_t offset,
-                       const int32_t *pos_dev, hipStream_t s) {
+                       const int32_t *pos_dev, hipStream_t s, const float *ws, int nchunks, const float *sc,
+                       const float *bias) {
     if (rows == 0) return 0;
     if (rotary_dim <= 0 || rotary_dim > g.head_dim || rotary_dim % 2)
         return fail("HIP backend: rotary_dim must be even and at most head_dim.");
     const int width = q_heads * g.head_dim + g.kv_heads * g.head_dim;
     const dim3 grid((width + kThreads - 1) / kThreads, (unsigned)rows);
     if (rows > 65535) return fail("HIP backend: rope_append takes at most 65535 rows per launch.");
-    if (g.kv_f32)
-        hipLaunchKernelGGL(rope_append_kernel<float>, grid, dim3(kThreads), 0, s, qkv, qrot, q_heads,
-                           g.kv_heads, g.head_dim, rotary_dim, rope_cos, rope_sin, g.page_table, g.page_size,
-                           (float *)kv.k, (float *)kv.v, (long)offset, pos_dev);
-    else
-        hipLaunchKernelGGL(rope_append_kernel<uint16_t>, grid, dim3(kThreads), 0, s, qkv, qrot, q_heads,
-                           g.kv_heads, g.head_dim, rotary_dim, rope_cos, rope_sin, g.page_table, g.page_size,
-                           (uint16_t *)kv.k, (uint16_t *)kv.v, (long)offset, pos_dev);
+    if (nchunks > 0 && !ws) return fail("HIP backend: rope_append's deferred sums have no workspace.");
+#define CHIP_ROPE(KT, SUM)                                                                                      \
+    hipLaunchKernelGGL((rope_append_kernel<KT, SUM>), grid, dim3(kThreads), 0, s, qkv, qrot, q_heads, g.kv_heads, \
+                       g.head_dim, rotary_dim, rope_cos, rope_sin, g.page_table, g.page_size, (KT *)kv.k,         \
+                       (KT *)kv.v, (long)offset, pos_dev, ws, nchunks, sc, bias)
+    if (g.kv_f32) {
+        if (nchunks > 0) CHIP_ROPE(float, true);
+        else CHIP_ROPE(float, false);
+    } else {
+        if (nchunks > 0) CHIP_ROPE(uint16_t, true);
+        else CHIP_ROPE(uint16_t, false);
+    }
+#undef CHIP_ROPE
     CHIP_CHECK(hipGetLastError());
     return 0;
 }

@@ -1019,9 +1019,14 @@ int enqueue_chunk(cheetah_hip_model *m, const uint32_t *tokens_dev, size_t rows,
         qkv.ws_floats = m->gemm_ws_floats;
         qkv.xh = m->xh;
         qkv.xl = m->xl;
+        // A split-K QKV GEMM leaves its chunk sums; the RoPE kernel folds them
+        // (with the scale and bias) as it reads each element.
+        int qkv_chunks = 0;
+        qkv.deferred = &qkv_chunks;
         CHIP_TRY(launch_gemm(qkv, s));
         CHIP_TRY(launch_rope_append(m->qkv, m->qrot, rows, (int)c.q_heads, geom(m), L.kv, sh.rope_cos, sh.rope_sin,
-                                    (int)c.rotary_dim, pos, nullptr, s));
+                                    (int)c.rotary_dim, pos, nullptr, s, m->gemm_ws, qkv_chunks, L.qkv.scales(),
+                                    L.qkv_bias));
         AttnJob aj;
         aj.q = m->qrot;
         aj.q_stride = sh.q_dim();
