@@ -246,18 +246,20 @@ def test_persistent_decode_matches_graph_decode(hip, shape, kv, monkeypatch):
     assert rel_err(runs["1"][1], runs["0"][1]) < 1e-4
 
 
-def test_prefill_bits_independent_of_split_k(hip):
-    """A 2,048-row chunk gives the Qwen2-0.5B QKV and gate/up GEMMs enough
-    tiles to fold K in registers (gate/up on 128-token tiles); 128-row chunks
-    split K and fold the chunk sums in the RoPE kernel and the SwiGLU reduce.
-    Both follow the same chunk order, so the last row's logits are the same
-    bits (decoder.rs:1710-1728: a position's result does not depend on how
-    the prompt was cut)."""
-    shape = configs.QWEN2_0_5B
-    g = hip.HipForward(shape, weights(shape), kv_capacity=2048 + 64, max_chunk_rows=2048)
+@pytest.mark.parametrize("shape,quant,big", [(configs.QWEN2_0_5B, None, 2048),
+                                              (configs.LLAMA3_8B.replace(num_layers=2), "q4", 512)],
+                         ids=["qwen2-0.5b-bf16", "llama3-8b-2layer-q4"])
+def test_prefill_bits_independent_of_split_k(hip, shape, quant, big):
+    """A big chunk gives the QKV and gate/up GEMMs enough tiles to fold K in
+    registers (gate/up on 128-token tiles); 128-row chunks split K and fold
+    the chunk sums in the RoPE kernel and the SwiGLU reduce. Both follow the
+    same chunk order, so the last row's logits are the same bits
+    (decoder.rs:1710-1728: a position's result does not depend on how the
+    prompt was cut)."""
+    g = hip.HipForward(shape, weights(shape), quant=quant, kv_capacity=big + 64, max_chunk_rows=big)
     try:
-        toks = synth.make_tokens(shape.vocab_size, 2048, seed=6)
-        whole = g.forward(toks, 0, chunk_rows=2048)
+        toks = synth.make_tokens(shape.vocab_size, big, seed=6)
+        whole = g.forward(toks, 0, chunk_rows=big)
         g.clear_cache()
         chunked = g.forward(toks, 0, chunk_rows=128)
         assert np.array_equal(bits(whole), bits(chunked))
