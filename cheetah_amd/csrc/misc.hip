@@ -64,24 +64,47 @@ __global__ __launch_bounds__(kThreads) void residual_rmsnorm_rows_kernel(const f
     const int m = blockIdx.x;
     const size_t MN = (size_t)rows * n;
     float *h = hidden + (size_t)m * n;
+    // A thread's elements i = tid + kThreads k, EPT of them per pass: their
+    // residuals and eight chunk sums each are loaded together (one memory
+    // round trip per eight chunks, not per element), then each element folds
+    // its chunks in chunk order and the squares are summed in element order.
+    constexpr int EPT = 4, ZB = 8;
     float ss = 0.f;
-    for (int i = threadIdx.x; i < n; i += kThreads) {
-        const size_t e = (size_t)m * n + i;
-        // Eight chunk sums loaded at a time, folded in chunk order.
-        float v = 0.f;
-        for (int z0 = 0; z0 < nchunks; z0 += 8) {
-            float t[8];
+    for (int base = 0; base < n; base += EPT * kThreads) {
+        float v[EPT], hv[EPT];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) t[j] = z0 + j < nchunks ? ws[(size_t)(z0 + j) * MN + e] : 0.f;
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                if (z0 + j < nchunks) v += t[j];
+        for (int k = 0; k < EPT; ++k) {
+            const int i = base + (int)threadIdx.x + kThreads * k;
+            v[k] = 0.f;
+            hv[k] = i < n ? h[i] : 0.f;
         }
-        if (sc) v = v * sc[i];
-        if (bias) v = v + bias[i];
-        const float r = h[i] + v;
-        h[i] = r;
-        ss = fmaf(r, r, ss);
+        for (int z0 = 0; z0 < nchunks; z0 += ZB) {
+            float t[ZB][EPT];
+#pragma unroll
+            for (int j = 0; j < ZB; ++j)
+#pragma unroll
+                for (int k = 0; k < EPT; ++k) {
+                    const int i = base + (int)threadIdx.x + kThreads * k;
+                    t[j][k] = z0 + j < nchunks && i < n ? ws[(size_t)(z0 + j) * MN + (size_t)m * n + i] : 0.f;
+                }
+#pragma unroll
+            for (int j = 0; j < ZB; ++j)
+#pragma unroll
+                for (int k = 0; k < EPT; ++k)
+                    if (z0 + j < nchunks) v[k] += t[j][k];
+        }
+#pragma unroll
+        for (int k = 0; k < EPT; ++k) {
+            const int i = base + (int)threadIdx.x + kThreads * k;
+            if (i < n) {
+                float x = v[k];
+                if (sc) x = x * sc[i];
+                if (bias) x = x + bias[i];
+                const float r = hv[k] + x;
+                h[i] = r;
+                ss = fmaf(r, r, ss);
+            }
+        }
     }
     if (!gain) return;
     ss = wave_sum(ss);
