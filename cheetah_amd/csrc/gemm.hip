@@ -918,10 +918,22 @@ __global__ __launch_bounds__(kThreads) void gemm_reduce_kernel(GArgs a) {
     const size_t MN = (size_t)a.M * a.N;
     const size_t e = (size_t)blockIdx.x * kThreads + threadIdx.x;
     if (e >= MN) return;
+    // Eight chunk sums (of each matrix) loaded at a time, folded in order.
     float v = 0.f, u = 0.f;
-    for (int z = 0; z < a.nchunks; ++z) {
-        v += a.ws[(size_t)z * MN + e];
-        if constexpr (DUAL) u += a.ws[((size_t)a.nchunks + z) * MN + e];
+    for (int z0 = 0; z0 < a.nchunks; z0 += 8) {
+        float t[8], t2[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const bool in = z0 + j < a.nchunks;
+            t[j] = in ? a.ws[(size_t)(z0 + j) * MN + e] : 0.f;
+            if constexpr (DUAL) t2[j] = in ? a.ws[((size_t)a.nchunks + z0 + j) * MN + e] : 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (z0 + j < a.nchunks) {
+                v += t[j];
+                if constexpr (DUAL) u += t2[j];
+            }
     }
     epilogue<DUAL>(a, (int)(e / a.N), (int)(e % a.N), v, u);
 }

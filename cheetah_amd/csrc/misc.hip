@@ -32,8 +32,20 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_rows_kernel(const float *x, 
     __shared__ float red[kThreads / 64];
     const float *src = x + (size_t)blockIdx.x * n;
     float *dst = out + (size_t)blockIdx.x * n;
+    // Eight of the thread's elements loaded at a time; squares summed in
+    // element order.
     float ss = 0.f;
-    for (int i = threadIdx.x; i < n; i += kThreads) ss = fmaf(src[i], src[i], ss);
+    for (int base = threadIdx.x; base < n; base += 8 * kThreads) {
+        float t[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int i = base + kThreads * k;
+            t[k] = i < n ? src[i] : 0.f;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (base + kThreads * k < n) ss = fmaf(t[k], t[k], ss);
+    }
     ss = wave_sum(ss);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
     __syncthreads();
