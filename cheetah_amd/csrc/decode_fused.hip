@@ -147,16 +147,20 @@ __device__ __forceinline__ float ldc_bf16(const uint16_t *p, long i) {
 typedef const __attribute__((address_space(4))) FusedArgs CArgs;
 typedef const __attribute__((address_space(4))) FusedLayer CLayer;
 
-// The launch's arguments, read where used: through an opaque copy of the
-// kernarg pointer, so that fields are re-read (scalar-cache hits) instead of
-// each being held in a scalar register for the whole launch.
-__device__ __forceinline__ CArgs *A() {
-    auto p = (const __attribute__((address_space(4))) char *)__builtin_amdgcn_kernarg_segment_ptr();
+// The launch's arguments are read where used, through an opaque copy of the
+// pointer to them, so that fields are re-read (scalar-cache hits) instead of
+// each being held in a scalar register for the whole launch. The pointer is
+// taken once, in the kernel's own body (the kernarg-segment intrinsic means
+// something only there: in any other function the compiler lowers it to a
+// null pointer), and every helper that reads an argument receives it as a
+// parameter, so that an outlined helper still reads the right memory.
+__device__ __forceinline__ CArgs *opaque(CArgs *a) {
+    auto p = (const __attribute__((address_space(4))) char *)a;
     asm volatile("" : "+s"(p));
     return (CArgs *)p;
 }
 // Layer l's pointer table, read the same way.
-__device__ __forceinline__ CLayer *LY(int l) { return (CLayer *)A()->layers + l; }
+__device__ __forceinline__ CLayer *layer_of(CArgs *a, int l) { return (CLayer *)opaque(a)->layers + l; }
 
 // LDS barrier that waits on LDS (and scalar) traffic only: outstanding
 // vector memory loads stay in flight across it.
@@ -514,14 +518,15 @@ __host__ __device__ inline LdsLayout lds_layout(int H, int I, int nq, int hd, in
 // [start, lim) of KV head g into LDS (row p - start of each); completion is
 // awaited with wait_vm.
 template <int HD, class KT>
-__device__ __forceinline__ void load_kv_lds(uint8_t *k_lds, uint8_t *v_lds, int l, int g, long start, long lim) {
+__device__ __forceinline__ void load_kv_lds(CArgs *a, uint8_t *k_lds, uint8_t *v_lds, int l, int g, long start,
+                                            long lim) {
     constexpr int ROW = HD * (int)sizeof(KT);
     const int lane = lane_here();
     for (long t0 = start; t0 < lim; t0 += TP) {
-        const int page = ldc(A()->page_table, t0 / TP);
+        const int page = ldc(opaque(a)->page_table, t0 / TP);
         const int bytes = (int)(min((long)TP, lim - t0)) * ROW;
-        const size_t off = (((size_t)page * A()->kv_heads + g) * TP) * ROW;
-        const uint8_t *ks = (const uint8_t *)LY(l)->kc + off, *vs = (const uint8_t *)LY(l)->vc + off;
+        const size_t off = (((size_t)page * opaque(a)->kv_heads + g) * TP) * ROW;
+        const uint8_t *ks = (const uint8_t *)layer_of(a, l)->kc + off, *vs = (const uint8_t *)layer_of(a, l)->vc + off;
         uint8_t *kd = k_lds + (t0 - start) * ROW, *vd = v_lds + (t0 - start) * ROW;
         for (int c = 0; c < bytes; c += 1024) {
             const int byte = c + lane * 16;
@@ -731,6 +736,10 @@ template <int FMT, int HD, int G, class KT, int UH, int UQ, int UP, int RGU, int
 __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
     using U = Unit<FMT, 16>;
     constexpr int ROW = HD * (int)sizeof(KT);
+    // The only read of the kernarg-segment pointer (see opaque()).
+    CArgs *const kargs = (CArgs *)__builtin_amdgcn_kernarg_segment_ptr();
+    auto A = [kargs]() { return opaque(kargs); };
+    auto LY = [kargs](int l) { return layer_of(kargs, l); };
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ Shm sm;
     constexpr int GI = HS ? 1 : G;  // q heads per attention item
@@ -892,7 +901,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
             // The attention item's cached rows start loading at once (spare
             // wave: no weight rows in flight).
             const bool kv_early = hasB && (l > 0 || paced);
-            if (spare && kv_early) load_kv_lds<HD, KT>(k_lds, v_lds, l, ig, kv_start, kv_lim);
+            if (spare && kv_early) load_kv_lds<HD, KT>(kargs, k_lds, v_lds, l, ig, kv_start, kv_lim);
 
             // ---- A: QKV pairs + RoPE + K/V append. Everything a pair's
             // epilogue reads besides its dot (row scale and bias, rotation
@@ -1005,7 +1014,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                     // of this layer written); the spare wave owns no chunk of
                     // the gather, so it waits at a barrier first.
                     bar();
-                    if (spare) load_kv_lds<HD, KT>(k_lds, v_lds, l, ig, kv_start, kv_lim);
+                    if (spare) load_kv_lds<HD, KT>(kargs, k_lds, v_lds, l, ig, kv_start, kv_lim);
                 }
                 if (spare) wait_vm();
                 bar();
