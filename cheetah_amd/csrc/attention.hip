@@ -3,7 +3,9 @@
 // by 1/sqrt(head_dim), softmax, weighted value mix), as split-K flash
 // decoding:
 //
-//   attn_kernel: grid (splits, kv_heads, rows); block = 256 threads.
+//   attn_kernel (f32 K/V; BF16 K/V decode runs on the matrix cores,
+//   attn_dec_mfma_kernel below): grid (splits, kv_heads, rows); block = 256
+//   threads.
 //   Each block owns one KV head, one query row and one contiguous slice of
 //   that row's visible positions [0, pos]; it streams the slice in tiles of
 //   64 positions (one page-aligned 64 x head_dim tile of K, then of V),
@@ -1012,32 +1014,30 @@ int launch_prefill_h(const AttnJob &j, const AttnArgs &a, int G, int S, hipStrea
     return fail("HIP backend: attention supports 1..8 query heads per KV head.");
 }
 
-// Decode attention runs on the matrix cores for BF16 K/V unless
-// CHEETAH_HIP_ATTN_MFMA=0 (the VALU kernel, kept for f32 K/V).
-bool attn_mfma_enabled() {
-    static const bool on = [] {
-        const char *e = std::getenv("CHEETAH_HIP_ATTN_MFMA");
-        return !(e && e[0] == '0');
-    }();
-    return on;
-}
-
+// Decode attention: BF16 K/V on the matrix cores, f32 K/V on the vector
+// ALUs.
 template <int HD, int G, class KT>
 int launch_hgk(const AttnJob &j, const AttnArgs &a, hipStream_t s) {
     const dim3 grid(j.splits, j.g.kv_heads, j.rows);
-    const bool mfma = std::is_same<KT, uint16_t>::value && attn_mfma_enabled();
+    constexpr bool mfma = std::is_same<KT, uint16_t>::value;
     const bool rope = a.qkv != nullptr;
     if (rope && !mfma) return fail("HIP backend: fused RoPE needs the matrix-core attention kernel.");
     if (j.splits == 1) {
-        if (rope) hipLaunchKernelGGL((attn_dec_mfma_kernel<HD, G, true, true>), grid, dim3(kThreads), 0, s, a);
-        else if (mfma) hipLaunchKernelGGL((attn_dec_mfma_kernel<HD, G, true, false>), grid, dim3(kThreads), 0, s, a);
-        else hipLaunchKernelGGL((attn_kernel<HD, G, KT, true>), grid, dim3(kThreads), 0, s, a);
+        if constexpr (mfma) {
+            if (rope) hipLaunchKernelGGL((attn_dec_mfma_kernel<HD, G, true, true>), grid, dim3(kThreads), 0, s, a);
+            else hipLaunchKernelGGL((attn_dec_mfma_kernel<HD, G, true, false>), grid, dim3(kThreads), 0, s, a);
+        } else {
+            hipLaunchKernelGGL((attn_kernel<HD, G, KT, true>), grid, dim3(kThreads), 0, s, a);
+        }
         CHIP_CHECK(hipGetLastError());
         return 0;
     }
-    if (rope) hipLaunchKernelGGL((attn_dec_mfma_kernel<HD, G, false, true>), grid, dim3(kThreads), 0, s, a);
-    else if (mfma) hipLaunchKernelGGL((attn_dec_mfma_kernel<HD, G, false, false>), grid, dim3(kThreads), 0, s, a);
-    else hipLaunchKernelGGL((attn_kernel<HD, G, KT, false>), grid, dim3(kThreads), 0, s, a);
+    if constexpr (mfma) {
+        if (rope) hipLaunchKernelGGL((attn_dec_mfma_kernel<HD, G, false, true>), grid, dim3(kThreads), 0, s, a);
+        else hipLaunchKernelGGL((attn_dec_mfma_kernel<HD, G, false, false>), grid, dim3(kThreads), 0, s, a);
+    } else {
+        hipLaunchKernelGGL((attn_kernel<HD, G, KT, false>), grid, dim3(kThreads), 0, s, a);
+    }
     CHIP_CHECK(hipGetLastError());
     hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3(j.q_heads, j.rows), dim3(kThreads), 0, s, a.part, j.splits,
                        j.q_heads, a.out);
@@ -1080,7 +1080,7 @@ int attention_max_splits() { return kMaxSplits; }
 // time) and two for the VALU kernel (f32 K/V), at most one split per
 // 64-position tile and kMaxSplits.
 int attention_decode_splits(size_t ctx, int kv_heads, size_t rows, bool kv_f32) {
-    const size_t per_cu = !kv_f32 && attn_mfma_enabled() ? 1 : 2;
+    const size_t per_cu = kv_f32 ? 2 : 1;
     const size_t target = per_cu * (size_t)std::max(device_cus(), 1);
     const size_t per = (size_t)std::max(kv_heads, 1) * std::max<size_t>(rows, 1);
     size_t s = (target + per - 1) / per;
@@ -1091,7 +1091,7 @@ int attention_decode_splits(size_t ctx, int kv_heads, size_t rows, bool kv_f32) 
 int attention_prefill_splits(size_t ctx) { return (int)std::max<size_t>(1, (ctx + kSpan - 1) / kSpan); }
 
 bool attention_decode_fuses_rope(const KvGeom &g, int q_heads, int rotary_dim) {
-    return !g.kv_f32 && attn_mfma_enabled() && (g.head_dim == 64 || g.head_dim == 128) && g.kv_heads > 0 &&
+    return !g.kv_f32 && (g.head_dim == 64 || g.head_dim == 128) && g.kv_heads > 0 &&
            q_heads % g.kv_heads == 0 && q_heads / g.kv_heads <= 8 && rotary_dim == g.head_dim;
 }
 

@@ -432,15 +432,9 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GArgs a, int split) {
     }
 }
 
-// ---------------------------------------------------------------------------
-// BF16 weights with pre-split x: both operands reach LDS by direct
-// global->LDS copies (no registers), NS stages in flight in a ring, so the
-// MFMAs of one stage overlap the memory latency of the next NS - 1. Tiles
-// are unpadded 32-element (64-byte) rows; 16-byte chunk c of row r sits at
-// slot c ^ ((r / 4) % 4), which keeps the fragment reads of 16 consecutive
-// rows on distinct LDS banks. The MFMA order and the chunk folds are those of
-// gemm_kernel, so the results are the same bits.
-// ---------------------------------------------------------------------------
+// LDS tiles are unpadded 32-element (64-byte) rows; 16-byte chunk c of row r
+// sits at slot c ^ ((r / 4) % 4), which keeps the fragment reads of 16
+// consecutive rows on distinct LDS banks.
 __device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 2) & 3); }
 
 template <bool DUAL>
@@ -448,144 +442,6 @@ __global__ __launch_bounds__(kThreads) void gemm_reduce_kernel(GArgs a);
 
 // s_waitcnt immediate waiting until at most n vector-memory ops are pending.
 constexpr int vm_wait_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
-
-template <bool DUAL, int MT, int NS>
-__global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GArgs a, int split) {
-    constexpr int BM = 64 * MT;
-    constexpr int XT = BM * BK, WT = BN * BK;                 // elements per tile
-    constexpr int STAGE = 2 * XT + (DUAL ? 2 : 1) * WT;       // elements per ring stage
-    constexpr int NI = STAGE / 512;                           // 1 KB copy instructions per stage
-    constexpr int IPW = NI / 4;                               // per wave
-    static_assert(NI % 4 == 0, "stage copies must split evenly over the waves");
-    extern __shared__ __attribute__((aligned(16))) uint16_t ring[];
-
-    int n0, m0;
-    tile_of((a.N + BN - 1) / BN, (a.M + BM - 1) / BM, n0, m0, BM);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = (wave >> 1) * 32 * MT, wn = (wave & 1) * 64;
-    const int kbeg = split ? blockIdx.z * a.chunk : 0;
-    const int kend = split ? min(a.K, kbeg + a.chunk) : a.K;
-    const int nst = (kend - kbeg) / BK;  // K % BK == 0 on this path
-
-    // Stage s's copies: instruction q covers 16 rows of one tile.
-    auto issue = [&](int st) {
-        const int k0 = kbeg + st * BK;
-        uint16_t *base = ring + (st % NS) * STAGE;
-#pragma unroll
-        for (int i = 0; i < IPW; ++i) {
-            const int q = wave + 4 * i;
-            int tile, grp;
-            if (q < BM / 16) { tile = 0; grp = q; }
-            else if (q < BM / 8) { tile = 1; grp = q - BM / 16; }
-            else if (q < BM / 8 + BN / 16) { tile = 2; grp = q - BM / 8; }
-            else { tile = 3; grp = q - BM / 8 - BN / 16; }
-            const int r = 16 * grp + (lane >> 2), c = swz(r, lane & 3);
-            const void *src;
-            if (tile < 2) {
-                const int m = min(m0 + r, a.M - 1);  // rows past M feed only unstored outputs
-                src = (tile == 0 ? a.xh : a.xl) + (size_t)m * a.K + k0 + 8 * c;
-            } else {
-                const int n = min(n0 + r, a.N - 1);
-                src = (tile == 2 ? a.w : a.w2) + (size_t)n * a.stride + (size_t)(k0 + 8 * c) * 2;
-            }
-            uint16_t *dst = base + (tile == 0 ? 0 : tile == 1 ? XT : tile == 2 ? 2 * XT : 2 * XT + WT) + 16 * grp * BK;
-            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
-        }
-    };
-
-    f32x16 acc[MT][2], acc2[DUAL ? MT : 1][2], tot[MT][2], tot2[DUAL ? MT : 1][2];
-#pragma unroll
-    for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            acc[i][j] = f32x16{};
-            tot[i][j] = f32x16{};
-            if constexpr (DUAL) {
-                acc2[i][j] = f32x16{};
-                tot2[i][j] = f32x16{};
-            }
-        }
-
-#pragma unroll
-    for (int st = 0; st < NS - 1; ++st)
-        if (st < nst) issue(st);
-    for (int st = 0; st < nst; ++st) {
-        if (st + NS - 1 < nst) issue(st + NS - 1);
-        // Stage st is complete once only the later stages' copies are pending.
-        if (st + NS - 1 < nst) __builtin_amdgcn_s_waitcnt(vm_wait_imm(IPW * (NS - 1)));
-        else __builtin_amdgcn_s_waitcnt(vm_wait_imm(0));
-        // A bare barrier: each wave has just waited for its own copies of
-        // stage st, and LDS is coherent within the CU. (A fenced barrier
-        // would also drain the later stages' copies.)
-        __builtin_amdgcn_s_barrier();
-        const uint16_t *xh = ring + (st % NS) * STAGE, *xl = xh + XT, *wt = xh + 2 * XT, *wt2 = wt + WT;
-#pragma unroll
-        for (int ks = 0; ks < BK; ks += 16) {
-            const int c = (ks >> 3) + (lane >> 5);
-            bf16x8 ah[MT], al[MT], bw[2], bw2[DUAL ? 2 : 1];
-#pragma unroll
-            for (int i = 0; i < MT; ++i) {
-                const int r = wm + 32 * i + (lane & 31);
-                ah[i] = __builtin_bit_cast(bf16x8, *(const u32x4 *)(xh + r * BK + 8 * swz(r, c)));
-                al[i] = __builtin_bit_cast(bf16x8, *(const u32x4 *)(xl + r * BK + 8 * swz(r, c)));
-            }
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int r = wn + 32 * j + (lane & 31);
-                bw[j] = __builtin_bit_cast(bf16x8, *(const u32x4 *)(wt + r * BK + 8 * swz(r, c)));
-                if constexpr (DUAL) bw2[j] = __builtin_bit_cast(bf16x8, *(const u32x4 *)(wt2 + r * BK + 8 * swz(r, c)));
-            }
-#pragma unroll
-            for (int i = 0; i < MT; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bw[j], acc[i][j], 0, 0, 0);
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bw[j], acc[i][j], 0, 0, 0);
-                    if constexpr (DUAL) {
-                        acc2[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bw2[j], acc2[i][j], 0, 0, 0);
-                        acc2[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bw2[j], acc2[i][j], 0, 0, 0);
-                    }
-                }
-        }
-        const int k0 = kbeg + st * BK;
-        if (k0 + BK >= kend || ((k0 + BK) % a.chunk) == 0) {
-#pragma unroll
-            for (int i = 0; i < MT; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    tot[i][j] += acc[i][j];
-                    acc[i][j] = f32x16{};
-                    if constexpr (DUAL) {
-                        tot2[i][j] += acc2[i][j];
-                        acc2[i][j] = f32x16{};
-                    }
-                }
-        }
-        // The slot of stage st is refilled by the next iteration's copies; the
-        // fragments were already read into registers.
-        __builtin_amdgcn_s_waitcnt(vm_wait_imm(63) & ~(0xF << 8));  // lgkmcnt(0)
-        __builtin_amdgcn_s_barrier();
-    }
-    if (!split) {
-        epilogue_tile<DUAL, MT>(a, tot, tot2, m0 + wm, n0 + wn, lane);
-        return;
-    }
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int n = n0 + wn + 32 * j + (lane & 31);
-        if (n >= a.N) continue;
-#pragma unroll
-        for (int i = 0; i < MT; ++i)
-#pragma unroll
-            for (int q = 0; q < 16; ++q) {
-                const int m = m0 + wm + 32 * i + 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
-                if (m >= a.M) continue;
-                const size_t o = ((size_t)blockIdx.z * a.M + m) * a.N + n;
-                a.ws[o] = tot[i][j][q];
-                if constexpr (DUAL) a.ws[(size_t)a.nchunks * a.M * a.N + o] = tot2[i][j][q];
-            }
-    }
-}
 
 // ---------------------------------------------------------------------------
 // Ring GEMM, every weight format (x pre-split, K % 32 == 0). Per 32-wide K
@@ -598,8 +454,8 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GArgs a, int split) 
 // Q8/Q4 codes of stage s + 1 are converted to BF16 (exactly) once per block,
 // 16 per thread, into one of three converted tiles after stage s's MFMAs;
 // BF16 weights are read straight from the ring. One barrier per stage. The
-// MFMA sequence per output and the chunk folds are those of gemm_kernel and
-// gemm_dma_kernel, so the results are the same bits.
+// MFMA sequence per output and the chunk folds are those of gemm_kernel, so
+// the results are the same bits.
 // ---------------------------------------------------------------------------
 template <int FMT>
 constexpr int ring_w_row_bytes() { return FMT == FMT_BF16 ? 64 : FMT == FMT_Q8 ? 32 : 16; }
@@ -889,28 +745,6 @@ int launch_ring(const GArgs &a, bool split, hipStream_t s) {
     return 0;
 }
 
-template <bool DUAL, int MT>
-int launch_dma(const GArgs &a, bool split, hipStream_t s) {
-    constexpr int NS = 4, BM = 64 * MT;
-    constexpr size_t lds = (size_t)NS * (2 * BM * BK + (DUAL ? 2 : 1) * BN * BK) * sizeof(uint16_t);
-    static bool attr_set = false;
-    if (!attr_set) {
-        CHIP_CHECK(hipFuncSetAttribute((const void *)gemm_dma_kernel<DUAL, MT, NS>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        attr_set = true;
-    }
-    const dim3 grid((a.N + BN - 1) / BN * ((a.M + BM - 1) / BM), 1, split ? a.nchunks : 1);
-    hipLaunchKernelGGL((gemm_dma_kernel<DUAL, MT, NS>), grid, dim3(kThreads), lds, s, a, split ? 1 : 0);
-    CHIP_CHECK(hipGetLastError());
-    if (split && !a.defer) {
-        const size_t MN = (size_t)a.M * a.N;
-        hipLaunchKernelGGL((gemm_reduce_kernel<DUAL>), dim3((unsigned)((MN + kThreads - 1) / kThreads)),
-                           dim3(kThreads), 0, s, a);
-        CHIP_CHECK(hipGetLastError());
-    }
-    return 0;
-}
-
 // Folds the stored chunk sums in chunk order (t = 0; t += c_z) and applies
 // the epilogue: the same bits as the in-register fold.
 template <bool DUAL>
@@ -954,16 +788,6 @@ int launch_mt(const GArgs &a, bool split, hipStream_t s) {
     return 0;
 }
 
-// The ring kernel is the default; CHEETAH_HIP_GEMM_RING=0 selects the
-// register-staged and BF16-only DMA kernels (the same bits).
-bool ring_enabled() {
-    static const bool on = [] {
-        const char *e = std::getenv("CHEETAH_HIP_GEMM_RING");
-        return !(e && e[0] == '0');
-    }();
-    return on;
-}
-
 template <int FMT>
 int launch_fmt(const GArgs &a, bool dual, size_t ws_floats, hipStream_t s, bool &split_out) {
     const long n_tiles = (a.N + BN - 1) / BN;
@@ -978,7 +802,7 @@ int launch_fmt(const GArgs &a, bool dual, size_t ws_floats, hipStream_t s, bool 
     // Pre-split x with K a multiple of the stage and 32-bit buffer offsets:
     // the ring kernel (weights copied 16 bytes at a time, Q4 4 at a time).
     const int galign = FMT == FMT_Q4 ? 4 : 16;
-    const bool ring = ring_enabled() && a.xh && a.K % BK == 0 && a.stride % galign == 0 &&
+    const bool ring = a.xh && a.K % BK == 0 && a.stride % galign == 0 &&
                       ((uintptr_t)a.w % galign) == 0 && (!dual || ((uintptr_t)a.w2 % galign) == 0) &&
                       (size_t)a.M * a.K * 2 < (1ull << 31) && (size_t)a.N * a.stride < (1ull << 31);
     // The dual gate/up GEMM takes 128-token tiles when they still give every
@@ -989,18 +813,10 @@ int launch_fmt(const GArgs &a, bool dual, size_t ws_floats, hipStream_t s, bool 
     // 128-token tiles on the large shapes).
     if (ring && dual && !split && tiles128 >= cus) return launch_ring<FMT, true, 2>(a, split, s);
     if (ring) return dual ? launch_ring<FMT, true, 1>(a, split, s) : launch_ring<FMT, false, 1>(a, split, s);
-    // BF16 weights with pre-split x stream both operands straight into LDS.
-    const bool dma = FMT == FMT_BF16 && a.xh && a.K % BK == 0 && a.stride % 16 == 0 &&
-                     ((uintptr_t)a.w % 16) == 0 && (!dual || ((uintptr_t)a.w2 % 16) == 0);
-    if (dual) {
-        if (dma) return launch_dma<true, 1>(a, split, s);
-        return launch_mt<FMT, true, 1>(a, split, s);
-    }
-    if (!split && tiles128 >= cus) {
-        if (dma) return launch_dma<false, 2>(a, false, s);
-        return launch_mt<FMT, false, 2>(a, false, s);
-    }
-    if (dma) return launch_dma<false, 1>(a, split, s);
+    // Otherwise (K not a multiple of the stage, x not pre-split, or operands
+    // beyond the buffer loads' 32-bit offsets): the register-staged kernel.
+    if (dual) return launch_mt<FMT, true, 1>(a, split, s);
+    if (!split && tiles128 >= cus) return launch_mt<FMT, false, 2>(a, false, s);
     return launch_mt<FMT, false, 1>(a, split, s);
 }
 

@@ -714,269 +714,6 @@ int pick_mode(const Args &a, bool norm, bool dual, hipStream_t s) {
     return dual ? pick_shape<FMT, false, true>(a, s) : pick_shape<FMT, false, false>(a, s);
 }
 
-// ---------------------------------------------------------------------------
-// Q4 GEMV on the matrix cores. A vector ALU spends three operations per
-// 4-bit code (sign extend, convert, FMA); here each code costs one: a dword
-// of eight codes, XORed with 0x8 per nibble (u = c + 8 in 0..15), becomes
-// four BF16 pairs 0x4300 | u = 128 + u = 136 + c (exact) by one AND-OR per
-// pair, and v_mfma_f32_16x16x32_bf16 multiplies 16 rows x 32 codes by x.
-//
-// x rides in two columns of the MFMA's B operand: column 0 holds its BF16
-// high half, column 1 the low half (x - hi, rounded), so one MFMA carries x
-// to ~2^-17 relative; the other 14 columns are zero. Per row the result is
-// sum_k (136 + c_k) (hi_k + lo_k); subtracting 136 * sum_k (hi_k + lo_k)
-// (summed in f64, per wave's share of k) leaves sum_k c_k x_k, which the row
-// scale then multiplies, as gemv_q4 does (ops.rs:586-630).
-//
-// Lanes: lane L serves tile row L % 16 and k-group g = L / 16. In k-step t
-// (64 bytes of a row) it loads the 16 bytes at 64 t + 16 g; their dword d
-// is the A operand of one MFMA. Inside a dword the AND-OR pairs nibbles
-// (0,4), (1,5), (2,6), (3,7), so x is staged in LDS in that order: per 8
-// codes, 8 BF16 high halves then 8 low halves ("groups" of 32 bytes).
-//
-// Alignment: Q4 rows are only 4-byte aligned (2052 / 7172-byte rows). A
-// tile takes 16 rows P apart (P = 16 / gcd(stride mod 16, 16)), which share
-// their misalignment delta, and loads 16-byte units from each row's
-// 16-byte-aligned-down start; a unit's codes then sit delta / 4 groups
-// before their x group, so the B reads are shifted by whole groups, with
-// zero groups before and after x for the bytes outside the row.
-//
-// One tile per block: the block stages x, its KS waves split the tile's
-// k-steps, and their partial sums meet in LDS in wave order.
-// ---------------------------------------------------------------------------
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-constexpr int kQ4Front = 3;   // zero groups before x (delta / 4 <= 3)
-constexpr int kQ4Back = 32;   // zero groups after x (two k-steps: the prefetch reads one past a wave's last)
-
-// Off by default (CHEETAH_HIP_Q4_MFMA=1 turns it on): correct, but measured
-// slower than the vector-ALU kernel on MI355X (4096x4096 / 14336x4096:
-// 8.1 / 16.4 us against 6.5 / 13.3 us).
-bool q4_mfma_enabled() {
-    static const bool on = [] {
-        const char *e = getenv("CHEETAH_HIP_Q4_MFMA");
-        return e && e[0] == '1';
-    }();
-    return on;
-}
-
-struct Q4Geo {
-    int P;           // rows between the rows of one tile
-    int tiles;       // ceil(rows / (16 P)) * P
-    int row_bytes;   // ceil(K / 2): bytes of a row that hold codes
-    uint32_t payload_off, total;  // payload start and buffer bytes from the buffer base
-    int delta[4];    // misalignment of phase ph (tiles with tile % P == ph)
-};
-
-// One 16-row tile per block; KS waves split its k-steps. Each wave streams
-// its steps through a ring of QR register sets, QR - 1 steps in flight ahead
-// of the one it multiplies, so load issue (which stalls while the memory
-// system is saturated), x staging and the MFMAs overlap instead of running
-// one after another.
-constexpr int QR = 4;
-
-template <int KS, bool NORM, bool DUAL>
-__global__ __launch_bounds__(64 * KS) void gemv_q4_mfma_kernel(Args a, Q4Geo geo, const uint8_t *wbase,
-                                                              const uint8_t *wbase2) {
-    constexpr int NT = 64 * KS;
-    constexpr int NM = DUAL ? 2 : 1;
-    constexpr int XG = 4;  // x groups a thread stages per round (loads first, then conversion)
-    extern __shared__ u32x4 xq[];  // groups: [hi 8 x bf16][lo 8 x bf16], then per group sum(hi + lo)
-    __shared__ float red[KS][NM + 1][16][2];  // [.][NM] holds the x sums
-    __shared__ float nred[KS];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int K = a.K;
-    const int ngroups = (K + 7) / 8;
-    const int zeros = kQ4Front + ngroups + kQ4Back;
-    float *gsum = (float *)(xq + 2 * zeros);
-    const int r = lane & 15, g = lane >> 4, n = lane & 15;
-    const __amdgpu_buffer_rsrc_t rs0 = __builtin_amdgcn_make_buffer_rsrc((void *)wbase, (short)0, (int)geo.total, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rs1 =
-        __builtin_amdgcn_make_buffer_rsrc((void *)(DUAL ? wbase2 : wbase), (short)0, (int)geo.total, 0x00020000);
-    const int P = geo.P;
-    const int tile = blockIdx.x;
-    const int ph = tile % P, dl = geo.delta[ph], sh = dl / 4;
-    // This wave's k-steps of the tile: [s0, s1).
-    const int nst = (geo.row_bytes + dl + 63) / 64;
-    const int per = (nst + KS - 1) / KS;
-    const int s0 = min(nst, wave * per), s1 = min(nst, s0 + per);
-    const int row = (tile / P) * 16 * P + ph + P * r;
-    const uint32_t base = geo.payload_off + (uint32_t)row * (uint32_t)a.stride - (uint32_t)dl;
-
-    // Step t's weight units (steps past the wave's range, rows past the
-    // matrix and units wholly past a row's codes read nothing). Issued for
-    // every ring slot on every path, so the compiler counts loads exactly.
-    auto issue = [&](u32x4 (&wr)[NM], int t) {
-        const int lb = 64 * t + 16 * g - dl;  // first byte of the unit, from the row start
-        const bool on = row < a.rows && t < s1 && lb < geo.row_bytes;
-        const uint32_t off = on ? base + 64u * (uint32_t)t + 16u * (uint32_t)g : 0x80000000u;
-        wr[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs0, off, 0, 2));
-        if constexpr (DUAL) wr[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs1, off, 0, 2));
-    };
-
-    // x loads first (they return first), then the first QR - 1 steps.
-    const bool vec_x = ((uintptr_t)a.x & 15) == 0;
-    float v[XG][8];
-    auto load_x = [&](int q0) {
-#pragma unroll
-        for (int h = 0; h < XG; ++h) {
-            const int gq = q0 + tid + NT * h - kQ4Front;
-            if (gq >= 0 && 8 * gq + 8 <= K && vec_x) {
-                const f32x4 v0 = *(const f32x4 *)(a.x + 8 * gq), v1 = *(const f32x4 *)(a.x + 8 * gq + 4);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    v[h][e] = v0[e];
-                    v[h][4 + e] = v1[e];
-                }
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) v[h][e] = gq >= 0 && 8 * gq + e < K ? a.x[8 * gq + e] : 0.f;
-            }
-        }
-    };
-    load_x(0);
-    u32x4 ring[QR][NM];
-#pragma unroll
-    for (int q = 0; q < QR - 1; ++q) issue(ring[q], s0 + q);
-
-    // x (normed when NORM) as BF16 halves in the nibble-pair order.
-    float inv = 1.f;
-    if constexpr (NORM) {
-        float ss = 0.f;
-        for (int i = tid; i < K; i += NT) ss = fmaf(a.x[i], a.x[i], ss);
-        ss = wave_sum(ss);
-        if (lane == 0) nred[wave] = ss;
-        __syncthreads();
-        float total = 0.f;
-#pragma unroll
-        for (int w = 0; w < KS; ++w) total += nred[w];
-        inv = 1.0f / sqrtf(total / (float)K + a.eps);
-    }
-    for (int q0 = 0; q0 < zeros; q0 += NT * XG) {
-        if (q0 > 0) load_x(q0);
-#pragma unroll
-        for (int h = 0; h < XG; ++h) {
-            const int q = q0 + tid + NT * h;
-            if (q >= zeros) continue;
-            const int gq = q - kQ4Front;
-            uint32_t hi[4] = {0u, 0u, 0u, 0u}, lo[4] = {0u, 0u, 0u, 0u};
-            float gs = 0.f;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                constexpr int kPi[8] = {0, 4, 1, 5, 2, 6, 3, 7};
-                const int k = 8 * gq + kPi[e];
-                float xv = v[h][kPi[e]];
-                if constexpr (NORM) xv = k >= 0 && k < K ? xv * (inv * bf16_f32(a.gain[k])) : 0.f;
-                const __bf16 hb = (__bf16)xv;
-                const __bf16 lb = (__bf16)(xv - (float)hb);
-                const uint32_t hbits = __builtin_bit_cast(uint16_t, hb);
-                const uint32_t lbits = __builtin_bit_cast(uint16_t, lb);
-                hi[e >> 1] |= (e & 1) ? hbits << 16 : hbits;
-                lo[e >> 1] |= (e & 1) ? lbits << 16 : lbits;
-                gs += (float)hb + (float)lb;  // hi + lo is exact in f32
-            }
-            xq[2 * q] = u32x4{hi[0], hi[1], hi[2], hi[3]};
-            xq[2 * q + 1] = u32x4{lo[0], lo[1], lo[2], lo[3]};
-            gsum[q] = gs;
-        }
-    }
-    __syncthreads();
-
-    // Columns 0 and 1 read x; the other lanes read the first (zero) group,
-    // one broadcast address, so every lane issues the same LDS reads.
-    f32x4 acc[NM][2];
-#pragma unroll
-    for (int m = 0; m < NM; ++m) acc[m][0] = acc[m][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // Column-0 lanes also add up the group sums of their B groups: over the
-    // wave's four of them, the x sum the offset 136 multiplies.
-    float xs = 0.f;
-    const int qb = kQ4Front + 4 * g - sh;
-    for (int t0 = s0; t0 < s1; t0 += QR) {
-#pragma unroll
-        for (int q = 0; q < QR; ++q) {
-            const int t = t0 + q;
-            // Step t + QR - 1 into the slot step t - 1 used.
-            issue(ring[(q + QR - 1) % QR], t + QR - 1);
-            if (t < s1) {
-                const int qs = qb + 16 * t;
-#pragma unroll
-                for (int d = 0; d < 4; ++d) {
-                    const u32x4 bx = n < 2 ? xq[2 * (qs + d) + n] : xq[0];
-                    const bf16x8_t b = __builtin_bit_cast(bf16x8_t, bx);
-#pragma unroll
-                    for (int m = 0; m < NM; ++m) {
-                        const bf16x8_t av = __builtin_bit_cast(bf16x8_t, q4_pairs(ring[q][m][d]));
-                        acc[m][d & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b, acc[m][d & 1], 0, 0, 0);
-                    }
-                    xs += gsum[qs + d];
-                }
-            }
-        }
-    }
-    // Lane L holds rows 4 (L / 16) + j of column L % 16.
-    if (n < 2) {
-#pragma unroll
-        for (int m = 0; m < NM; ++m)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) red[wave][m][4 * g + j][n] = acc[m][0][j] + acc[m][1][j];
-        red[wave][NM][g][n] = n == 0 ? xs : 0.f;
-    }
-    __syncthreads();
-    if (tid < 16) {
-        const int orow = (tile / P) * 16 * P + ph + P * tid;
-        if (orow < a.rows) {
-            float vv[NM];
-#pragma unroll
-            for (int m = 0; m < NM; ++m) {
-                double sum = 0.0;
-#pragma unroll
-                for (int w = 0; w < KS; ++w) {
-                    float sx = 0.f;
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) sx += red[w][NM][q][0] + red[w][NM][q][1];
-                    sum += ((double)red[w][m][tid][0] + (double)red[w][m][tid][1]) - 136.0 * (double)sx;
-                }
-                vv[m] = (float)sum;
-            }
-            float o = vv[0];
-            if (a.sc) o = o * a.sc[orow];
-            if constexpr (DUAL) {
-                float u = vv[1];
-                if (a.sc2) u = u * a.sc2[orow];
-                // silu_multiply, ops.rs:743-747: g * (u / (1 + exp(-g))).
-                a.y[orow] = o * (u / (1.0f + expf(-o)));
-            } else {
-                if (a.bias) o = o + a.bias[orow];
-                if (a.epi == EPI_RESIDUAL) a.residual[orow] = a.residual[orow] + o;
-                else a.y[orow] = o;
-            }
-        }
-    }
-}
-
-template <int KS, bool NORM, bool DUAL>
-int launch_q4_mfma_ks(const Args &a, const Q4Geo &geo, const uint8_t *wb, const uint8_t *wb2, hipStream_t s) {
-    const int ngroups = (a.K + 7) / 8;
-    const size_t lds = (size_t)(kQ4Front + ngroups + kQ4Back) * 36;
-    hipLaunchKernelGGL((gemv_q4_mfma_kernel<KS, NORM, DUAL>), dim3(geo.tiles), dim3(64 * KS), lds, s, a, geo, wb, wb2);
-    CHIP_CHECK(hipGetLastError());
-    return 0;
-}
-
-// Waves per tile (KS): doubled while tiles x KS leave wave slots idle and
-// each wave keeps at least QR k-steps.
-template <bool NORM, bool DUAL>
-int launch_q4_mfma(const Args &a, const Q4Geo &geo, const uint8_t *wb, const uint8_t *wb2, hipStream_t s) {
-    const int nst = (geo.row_bytes + 12 + 63) / 64;
-    int ks = 1;
-    while (ks < 8 && (long)geo.tiles * ks < (long)device_cus() * 16 && nst >= 2 * QR * ks) ks *= 2;
-    switch (ks) {
-        case 8: return launch_q4_mfma_ks<8, NORM, DUAL>(a, geo, wb, wb2, s);
-        case 4: return launch_q4_mfma_ks<4, NORM, DUAL>(a, geo, wb, wb2, s);
-        case 2: return launch_q4_mfma_ks<2, NORM, DUAL>(a, geo, wb, wb2, s);
-        default: return launch_q4_mfma_ks<1, NORM, DUAL>(a, geo, wb, wb2, s);
-    }
-}
-
 }  // namespace
 
 int launch_gemv(const GemvJob &job, hipStream_t s) {
@@ -1005,25 +742,6 @@ int launch_gemv(const GemvJob &job, hipStream_t s) {
     a.residual = job.residual;
     a.epi = job.epi;
     const bool norm = job.norm_gain != nullptr;
-    // Q4 on the matrix cores: 4-byte strides, x staged whole in LDS, and
-    // byte offsets inside the 32-bit buffer range.
-    if (w.fmt == FMT_Q4 && q4_mfma_enabled() && a.stride % 4 == 0 && (uintptr_t)w.base % 16 == 0 &&
-        (!dual || (uintptr_t)job.w2.base % 16 == 0) && w.bytes() + 64 < (1ull << 31) &&
-        (size_t)(kQ4Front + (a.K + 7) / 8 + kQ4Back) * 36 + 8192 <= device_max_lds()) {
-        Q4Geo geo{};
-        const int sm = (int)(a.stride % 16);
-        geo.P = sm == 0 ? 1 : 16 / std::gcd(sm, 16);
-        geo.tiles = (a.rows + 16 * geo.P - 1) / (16 * geo.P) * geo.P;
-        geo.row_bytes = (a.K + 1) / 2;
-        geo.payload_off = (uint32_t)(w.rows * 4);
-        geo.total = (uint32_t)w.bytes();
-        for (int ph = 0; ph < 4; ++ph)
-            geo.delta[ph] = (int)(((uintptr_t)a.w + (size_t)ph * a.stride) % 16);
-        if (norm) return dual ? launch_q4_mfma<true, true>(a, geo, w.base, job.w2.base, s)
-                              : launch_q4_mfma<true, false>(a, geo, w.base, nullptr, s);
-        return dual ? launch_q4_mfma<false, true>(a, geo, w.base, job.w2.base, s)
-                    : launch_q4_mfma<false, false>(a, geo, w.base, nullptr, s);
-    }
     // The aligned kernel needs 4-byte-aligned rows whose misalignment is a
     // multiple of 4 x floats (BF16: rows 16-byte aligned), gate and up
     // misaligned alike, and x plus its padding in LDS.

@@ -213,7 +213,7 @@ struct cheetah_hip_model {
     int table_cols_blocks = 0;           // the table's down_cols were built for this grid (0: none yet)
     int fused_blocks = 0;
     int fused_max_splits = 0;
-    uint64_t *tagged = nullptr;  // hid0 | hid1 | qkvn | part | act | am, tagged words
+    uint64_t *tagged = nullptr;  // hid0 | hid1 | qkvn | part | pdown | am, tagged words
     size_t tagged_words = 0;
     int32_t *abort_dev = nullptr;
     unsigned next_tag = 1;          // tag of the next launch's first phase
@@ -537,9 +537,6 @@ bool fused_fits(const cheetah_hip_model *m, size_t offset, size_t steps) {
     return (ctx + per_item - 1) / per_item <= (size_t)m->fused_max_splits;
 }
 
-// Runs `steps` decode steps in one persistent launch from the token and
-// position (`offset`, also in step_dev); leaves the last step's logits in m->logits, its
-// argmax in next_dev and every sampled id in hist_dev. Waits for the launch.
 // Builds every layer's down_cols for this instance's grid once per model
 // (the persistent kernel runs only while every matrix is resident), and
 // points this instance's layer table at them.
@@ -568,6 +565,10 @@ int ensure_down_cols(cheetah_hip_model *m) {
     return 0;
 }
 
+// Runs `steps` decode steps in one persistent launch from the token and
+// position (`offset`, also in step_dev); leaves the last step's logits in
+// m->logits, its argmax in next_dev and every sampled id in hist_dev. Waits
+// for the launch.
 int run_fused(cheetah_hip_model *m, size_t offset, size_t steps) {
     Shared &sh = *m->sh;
     const auto &c = sh.cfg;
@@ -711,25 +712,37 @@ int init_instance(cheetah_hip_model *m) {
 
 // Makes positions [m->len, m->len + n) writable: maps new pages and copies a
 // shared page before its first write. Uploads the page table if it changed.
+// All or nothing: when the pool runs out part way, every page this call
+// copied or mapped is given back and the instance's page list is restored,
+// so the host list, the device table and the reference counts stay as they
+// were before the call (a later call maps the same positions afresh).
 int reserve_positions(cheetah_hip_model *m, size_t n) {
     Shared &sh = *m->sh;
     const size_t end = m->len + n;
     if (end > sh.kv_capacity)
         return fail("HIP backend: KV cache capacity of " + std::to_string(sh.kv_capacity) +
                     " positions exceeded (needs " + std::to_string(end) + ").");
-    bool changed = false;
-    // Shared pages this instance copied away from. Each keeps this instance's
-    // reference until the copies reading it have finished: released earlier,
-    // another holder could see itself as the only one and write the page in
-    // place while the copy still reads it.
-    std::vector<int> copied_from;
-    auto release_copied = [&]() {
-        if (copied_from.empty()) return hipSuccess;
+    // What this call changed: (logical page, page it replaced or -1 for a
+    // page appended, page it mapped). A replaced shared page keeps this
+    // instance's reference until the copies reading it have finished:
+    // released earlier, another holder could see itself as the only one and
+    // write the page in place while the copy still reads it.
+    struct Change {
+        size_t lp;
+        int old_page, new_page;
+    };
+    std::vector<Change> log;
+    auto roll_back = [&]() {
+        // The copies into the new pages finish before those pages return to
+        // the pool (a clone on another stream could be handed one at once).
         const hipError_t e = hipStreamSynchronize(m->stream);
-        if (e == hipSuccess)
-            for (int p : copied_from) sh.page_unref(p);
-        copied_from.clear();
-        return e;
+        for (auto it = log.rbegin(); it != log.rend(); ++it) {
+            if (it->old_page < 0) m->pages.pop_back();
+            else m->pages[it->lp] = it->old_page;
+            if (e == hipSuccess) sh.page_unref(it->new_page);
+        }
+        if (e != hipSuccess) return fail(std::string("HIP backend: ") + hipGetErrorString(e));
+        return fail("HIP backend: KV page pool exhausted.");
     };
     const size_t first = m->len / kPageSize, last = (end - 1) / kPageSize;
     for (size_t lp = first; lp <= last; ++lp) {
@@ -737,10 +750,7 @@ int reserve_positions(cheetah_hip_model *m, size_t n) {
             const int p = m->pages[lp];
             if (sh.page_refs(p) > 1) {  // copy on write
                 const int np = sh.page_alloc();
-                if (np < 0) {
-                    CHIP_CHECK(release_copied());
-                    return fail("HIP backend: KV page pool exhausted.");
-                }
+                if (np < 0) return roll_back();
                 for (auto &L : sh.layers) {
                     const size_t pb = sh.page_bytes();
                     uint8_t *k = (uint8_t *)L.kv.k, *v = (uint8_t *)L.kv.v;
@@ -749,27 +759,23 @@ int reserve_positions(cheetah_hip_model *m, size_t n) {
                     CHIP_CHECK(hipMemcpyAsync(v + (size_t)np * pb, v + (size_t)p * pb, pb, hipMemcpyDeviceToDevice,
                                               m->stream));
                 }
-                copied_from.push_back(p);
+                log.push_back({lp, p, np});
                 m->pages[lp] = np;
-                changed = true;
             }
         } else {
             const int np = sh.page_alloc();
-            if (np < 0) {
-                CHIP_CHECK(release_copied());
-                return fail("HIP backend: KV page pool exhausted.");
-            }
+            if (np < 0) return roll_back();
+            log.push_back({lp, -1, np});
             m->pages.push_back(np);
-            changed = true;
         }
     }
-    if (changed) {
-        for (size_t i = 0; i < m->pages.size(); ++i) m->page_host[i] = m->pages[i];
-        CHIP_CHECK(hipMemcpyAsync(m->page_dev, m->page_host.data(), m->pages.size() * sizeof(int32_t),
-                                  hipMemcpyHostToDevice, m->stream));
-        CHIP_CHECK(hipStreamSynchronize(m->stream));  // page_host is pageable
-    }
-    CHIP_CHECK(release_copied());
+    if (log.empty()) return 0;
+    for (size_t i = 0; i < m->pages.size(); ++i) m->page_host[i] = m->pages[i];
+    CHIP_CHECK(hipMemcpyAsync(m->page_dev, m->page_host.data(), m->pages.size() * sizeof(int32_t),
+                              hipMemcpyHostToDevice, m->stream));
+    CHIP_CHECK(hipStreamSynchronize(m->stream));  // page_host is pageable; the copies have finished
+    for (const Change &c : log)
+        if (c.old_page >= 0) sh.page_unref(c.old_page);
     return 0;
 }
 

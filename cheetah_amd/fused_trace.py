@@ -14,7 +14,7 @@ Stamp slots per layer l (16 l + k): 0 layer start, 1 A.in (QKV input normed
 and staged), 2 A.out (QKV rows stored), 3 B.in (attention item's q/K/V
 staged), 4 scores, 5 softmax, 6 weighted V + partials stored, 7 B.out
 (weight rows of C/D/E issued), 8 C.in (partials merged), 14 o_proj dot,
-9 C.out (hid0 stored), 10 D.in, 11 D.out (act stored, next QKV rows issued),
+9 C.out (hid0 stored), 10 D.in, 11 D.out (down partials stored, next QKV rows issued),
 12 E.in, 15 down dot, 13 E.out (hid1 stored). After the layers: 16 L head.in,
 16 L + 1 head.out, 16 L + 2 token known.
 """

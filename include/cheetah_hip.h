@@ -106,14 +106,18 @@ typedef struct cheetah_hip_kv_view {
 int cheetah_hip_attention(const float *q, const cheetah_hip_kv_view *kv, uint32_t q_heads, size_t rows,
                           size_t offset, float *out);
 /* cheetah_hip_attention that allocates nothing. No counterpart in the
- * reference: it is for callers that cannot allocate device memory (code
- * under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc). The split partials live in a fixed 48 MiB device array per GPU
- * instead of a buffer the library grows on demand; a call that needs more
- * (rows * q_heads * splits * (head_dim + 2) floats) is rejected with an
- * error before any device work. Same kernels and split choice, so the same
- * results as cheetah_hip_attention. Calls that overlap on one GPU share
- * that array and race. */
+ * reference: it is for callers that cannot allocate device memory (tight
+ * serving loops, harnesses that forbid hipMalloc). The split partials live
+ * in a fixed 48 MiB device array per GPU instead of a buffer the library
+ * grows on demand; a call that needs more (rows * q_heads * splits *
+ * (head_dim + 2) floats) is rejected with an error before any device work.
+ * Same kernels and split choice, so the same results as
+ * cheetah_hip_attention. Like every op-level entry point it launches on the
+ * library's own stream (created by cheetah_hip_init; cheetah_hip_synchronize
+ * waits for it), not on a stream of the caller's: it is not captured by a
+ * graph capture the caller runs on its own stream. Calls within a process
+ * are therefore ordered on that one stream and do not overlap on the
+ * device; the array keeps the last call's partials. */
 int cheetah_hip_attention_noalloc(const float *q, const cheetah_hip_kv_view *kv, uint32_t q_heads, size_t rows,
                                   size_t offset, float *out);
 
