@@ -4,13 +4,18 @@ The kernel (decode_fused.hip) depends on three properties the compiler could
 silently take away:
   * no scratch memory and no dynamic stack: a call frame or a spilled vector
     register would put private-memory traffic on every step's critical path;
-  * the only call is the out-of-line poll (`gather`); the other helpers are
-    inlined, so the compiler's waits for weight rows held in registers stay
-    exact;
+  * no calls: every helper (the polls included) is inlined, so the weight
+    registers held across them need no call-preserved registers and the
+    compiler's waits for weight rows held in registers stay exact;
   * the kernarg-segment intrinsic is read once, in the kernel's own body: the
     compiler lowers it to a null pointer in any function that is not a
     kernel, so a helper that called it and got outlined would read launch
-    arguments from address 0.
+    arguments from address 0;
+  * every global store of more than 64 data bits written as inline assembly
+    is followed at once by s_nop 1 or longer: such a store reads its data
+    registers after issue, a VALU write to them needs two wait states on
+    this chip, and the compiler cannot insert them for a store it does not
+    see (without them the store can write the registers' next values).
 
 The script compiles decode_fused.hip for the device with the compiler's
 resource-usage remarks, writes the device assembly next to the objects, and
@@ -25,7 +30,7 @@ import sys
 
 SRC = "decode_fused.hip"
 KERNEL = "decode_flow_kernel"
-ALLOWED_CALLEES = ("_ZN4chip12_GLOBAL__N_16gather",)
+ALLOWED_CALLEES = ()
 
 
 def fail(msg):
@@ -107,11 +112,28 @@ def main():
             for sym in re.findall(r"([\w.$]+)@(?:rel32|gotpcrel32)@lo", line):
                 if sym in names or "@gotpcrel" in line:
                     callees.add(sym)
-        bad = [c for c in callees if not c.startswith(ALLOWED_CALLEES)]
-        if bad:
-            fail(f"{k} calls {bad}: only the out-of-line poll may be a call")
+        bad = [c for c in callees if not (ALLOWED_CALLEES and c.startswith(ALLOWED_CALLEES))]
+        if bad or any("s_swappc" in line for line in funcs[k]):
+            fail(f"{k} calls {bad or 'a function'}: every helper must be inlined")
+        wide = check_wide_stores(funcs[k])
+        if wide:
+            fail(f"{k}: a store of more than 64 data bits is not followed by s_nop 1: {wide}")
     print(f"check_code_shape: {len(kernels)} {KERNEL} instances: no scratch, no dynamic stack, no vector "
-          f"spills, only the poll called")
+          f"spills, no calls, wide stores padded")
+
+
+def check_wide_stores(body):
+    """The first wide store (dwordx3/x4) whose next instruction is not an
+    s_nop of at least 2 wait states, or None."""
+    insts = [ln.split(";")[0].strip() for ln in body]
+    insts = [i for i in insts if i and not i.startswith(".") and not i.endswith(":")]
+    for n, ins in enumerate(insts):
+        if re.match(r"(global|buffer|flat)_store_dwordx[34]\b", ins):
+            nxt = insts[n + 1] if n + 1 < len(insts) else ""
+            m = re.match(r"s_nop\s+(\d+)", nxt)
+            if not m or int(m.group(1)) < 1:
+                return ins
+    return None
 
 
 if __name__ == "__main__":

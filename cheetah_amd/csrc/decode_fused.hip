@@ -2,65 +2,63 @@
 // block per CU) runs whole decode steps -- embedding, every layer, LM head,
 // greedy argmax -- with no device-wide barrier.
 //
-// Per layer five phases, per step one more:
-//   A  QKV rows (fused RMSNorm, bias, RoPE); K/V rows appended to the pages
-//   B  GQA attention: one item = (KV head, run of 128 positions, q head) when
-//      those items fit the grid, else (KV head, run) with all q heads of the
-//      group; two-pass softmax, (output, max, sum) partials per q head
-//   C  every o_proj block merges all partials in split order itself, then
-//      o_proj + residual
-//   D  gate/up (fused RMSNorm) + SwiGLU
-//   E  down + residual
-//   H  LM head (fused final RMSNorm) + per-block argmax partials; blocks that
-//      need the next token reduce all partials themselves (ties to the last
-//      index, engine.rs:2247-2253)
+// The grid is split into fixed roles (FusedGeom):
+//   items  one q head over one run of positions: its 64 q rows (fused
+//          RMSNorm, bias, RoPE), attention over the run's cached K/V rows
+//          (and the new position's, for the run that holds it), and the
+//          head's o_proj columns applied to the unnormalised output: an
+//          o_proj partial of every hidden row, with the run's max and sum
+//   KV     the new position's K and V rows (fused RMSNorm, bias, RoPE),
+//          appended to the pages and handed to the items that need them
+//   FFN    gate/up rows, SwiGLU and the matching down_proj columns (a down
+//          partial of every hidden row); the first of them also own 8
+//          residual rows each (one per wave, held in a register)
+// Per layer four hand-offs are on the critical path:
+//   residual -> items, KV          (the KV -> item hand-off overlaps the
+//                                   items' scores of their cached rows)
+//   item partials -> owners        owners merge the runs of every head in
+//                                  split order (weights exp(m_s - M) / sum)
+//                                  and add the residual
+//   residual -> FFN blocks
+//   down partials -> owners        summed in block order, + residual
+// and once per step the LM head (fused final RMSNorm) + per-block argmax
+// partials, which the blocks that need the next token reduce themselves
+// (ties to the last index, engine.rs:2247-2253).
 //
-// Phases are chained through the data. Every value one block hands to
-// another is a 64-bit word {f32 bits, tag}, where the tag names the phase
-// instance that produced it (launch base + step * (5L + 1) + 5 * layer +
-// phase). Aligned 8-byte stores are single-copy atomic, so value and tag
-// arrive together, and a consumer knows its inputs are complete when every
-// word it copied carries the expected tag.
+// Every value one block hands to another is a 64-bit word {f32 bits, tag},
+// where the tag names the phase instance that produced it (launch base +
+// step * (5L + 1) + 5 * layer + phase). Aligned 8-byte stores are
+// single-copy atomic, so value and tag arrive together, and a consumer knows
+// its inputs are complete when every word it copied carries the expected
+// tag.
 //
-// Roles inside a block. Waves 0-6 (compute waves) own QKV, o_proj and down
-// rows; wave 7 (the spare wave) owns only gate/up rows (like every wave) and
-// copies the attention item's cached K/V rows and the RMSNorm gains into LDS. Every wave polls: a phase's tagged input
-// words are split into 128-word chunks, wave w copies chunks w, w + 8, ...
-// into LDS with direct global->LDS loads (16 bytes per lane, device-coherent
-// sc1), checks their tags there and re-loads only the stale ones; all waves
-// then stage the f32 vector the dots read (RMSNorm fused where the phase has
-// one). The waves meet only at LDS barriers that wait on LDS traffic alone
-// (s_waitcnt lgkmcnt(0); s_barrier), never on vector memory.
-//
-// Weight streaming. Weight rows live in registers. A layer's o_proj, gate/up
-// and down rows are issued right after its attention phase (the o_proj/down
-// blocks idle while QKV and attention run), the next layer's QKV rows right
-// after gate/up, and layer 0's after the LM head. Issuing a phase's rows just
-// before its dot would stall the dot: a CU holds only so many outstanding
-// misses. The loads are buffer loads issued on every path, with rows a wave
-// does not own pointed past the buffer's range (those lanes read nothing and
-// return 0), so the compiler counts outstanding loads exactly and each use
-// waits only for its own rows. The LDS copies and the hand-off stores are
-// inline assembly for the same reason: the compiler would otherwise make
-// LDS reads and later loads wait for them.
+// Weight streaming. Every thread holds a pool of 16-byte weight units in
+// registers: an item's q rows and o_proj columns, a KV block's rows, an FFN
+// block's gate/up rows and down columns. All blocks refill the pool at one
+// point of each layer (after the items' work): items and KV blocks with the
+// next layer's rows, FFN blocks with this layer's, so every transfer
+// overlaps the hand-offs before its use. Every wave issues the same number
+// of loads there whatever its role (units it does not need point past the
+// buffer's range and read nothing), so no path through the loop has a
+// different load count and the compiler's waits stay exact. The LDS copies
+// and the hand-off stores are inline assembly so that the compiler does not
+// make LDS reads and later loads wait for them.
 //
 // Buffer reuse needs no barrier: a block polls a phase's inputs only in a
-// phase where it also produces outputs, and every buffer is rewritten only by
-// a phase that transitively depends on all of those outputs. Only blocks
-// that own LM-head rows (and so wait for the final hidden state) write
-// argmax partials; those alternate between two buffers by step parity.
+// phase where it also produces outputs, and every buffer is rewritten only
+// by a phase that transitively depends on all of those outputs. Argmax
+// partials alternate between two buffers by step parity.
 //
 // Every poll is bounded: on timeout a block raises the abort word, which all
 // polls watch, so every later poll gives up within a few rounds and the
-// launch runs to its end on stale values (no wave leaves early: an exit inside
-// the layer loop would add control-flow paths that make the compiler's waits
-// for weight rows conservative). The host sees the word, discards the steps
-// and resets the tagged words. The only data-dependent address, the token,
-// keeps its last good value when its poll gives up.
+// launch runs to its end on stale values. The host sees the word, discards
+// the steps and resets the tagged words. The only data-dependent address,
+// the token, keeps its last good value when its poll gives up.
 //
 // Math per phase is that of the multi-kernel path (gemv.hip, attention.hip,
 // misc.hip), i.e. the reference path of ops.rs / qwen2.rs; only f32
-// summation orders differ.
+// summation orders differ (o_proj is applied per head before the split
+// merge, which is linear).
 #include <cstdlib>
 
 #include "decode_fused.hpp"
@@ -71,15 +69,13 @@ namespace {
 
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
-constexpr int kCW = kWaves - 1;        // compute waves 0 .. kCW - 1
-constexpr int kSpareWave = kWaves - 1;  // owns no weight rows
+constexpr int kDmaWave = kWaves - 1;   // issues the block's copies into LDS
 constexpr int TP = 64;                 // positions per KV page
-constexpr int kItemPos = 2 * TP;       // positions per attention item, at most
-// Positions per item for a K/V row size: two pages, or one when a row is
-// wider than 256 bytes (one item's K and V rows stay within 64 KB of LDS).
-__host__ __device__ constexpr int item_positions(int row_bytes) { return row_bytes <= 256 ? 2 * TP : TP; }
+constexpr int kOwn = kWaves;           // residual rows per owner block, one per wave
+constexpr int kMaxSplits = 16;         // attention splits per q head, at most
+constexpr int kIpMax = 4 * TP;         // positions per attention item, at most
+constexpr int kKvLdsMax = 64 * 1024;   // LDS for one item's K and V rows, at most
 constexpr int kChunk = 128;            // tagged words per wave-wide 16-byte-per-lane load
-constexpr int kMaxChunks = 128;        // largest gather: 16384 words
 constexpr long kSpinLimit = 1L << 20;
 constexpr uint32_t kNoRead = 0x80000000u;  // buffer offset past every range
 
@@ -116,6 +112,16 @@ __device__ __forceinline__ void st_u16(void *p, uint32_t v) {
     asm volatile("global_store_short %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
 }
 __device__ __forceinline__ void stt(uint64_t *p, uint32_t bits, unsigned tag) { st_u64(p, ((uint64_t)tag << 32) | bits); }
+// Two tagged words {a, tag}, {b, tag} at p (16-byte aligned) in one store.
+// A vector memory store of more than 64 data bits reads its data registers
+// after issue; on this chip a VALU write to them needs two wait states
+// after the store, which the compiler inserts for its own stores but cannot
+// for one inside inline assembly (it reuses the registers at once). The
+// s_nop 1 provides them.
+__device__ __forceinline__ void stf2(uint64_t *p, float a, float b, unsigned tag) {
+    const u32x4 v = {__float_as_uint(a), tag, __float_as_uint(b), tag};
+    asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" ::"v"(p), "v"(v) : "memory");
+}
 __device__ __forceinline__ void stf(uint64_t *p, float v, unsigned tag) { stt(p, __float_as_uint(v), tag); }
 __device__ __forceinline__ float val_of(uint64_t w) { return __uint_as_float((uint32_t)w); }
 
@@ -190,49 +196,21 @@ __device__ __forceinline__ void dma16(const void *g, const void *lds) {
 }
 __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// N device-coherent 16-byte loads p[i] -> r[i] and the wait for all of them in
-// one asm statement: no instruction sees r before its load has landed.
+// N (1 or 2) device-coherent 16-byte loads p[i] -> r[i] and the wait for
+// all of them in one asm statement: no instruction sees r before its load
+// has landed.
 template <int N>
-__device__ __forceinline__ void poll16(u32x4 (&r)[8], const uint64_t *const (&p)[8]) {
+__device__ __forceinline__ void poll16(u32x4 (&r)[2], const uint64_t *const (&p)[2]) {
+    static_assert(N == 1 || N == 2, "one or two chunks per wave");
     if constexpr (N == 1)
         asm volatile("global_load_dwordx4 %0, %1, off sc1\n\ts_waitcnt vmcnt(0)"
                      : "=&v"(r[0])
                      : "v"(p[0])
                      : "memory");
-    else if constexpr (N == 2)
+    else
         asm volatile("global_load_dwordx4 %0, %2, off sc1\n\tglobal_load_dwordx4 %1, %3, off sc1\n\ts_waitcnt vmcnt(0)"
                      : "=&v"(r[0]), "=&v"(r[1])
                      : "v"(p[0]), "v"(p[1])
-                     : "memory");
-    else if constexpr (N == 3)
-        asm volatile("global_load_dwordx4 %0, %3, off sc1\n\tglobal_load_dwordx4 %1, %4, off sc1\n\tglobal_load_dwordx4 %2, %5, off sc1\n\ts_waitcnt vmcnt(0)"
-                     : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2])
-                     : "v"(p[0]), "v"(p[1]), "v"(p[2])
-                     : "memory");
-    else if constexpr (N == 4)
-        asm volatile("global_load_dwordx4 %0, %4, off sc1\n\tglobal_load_dwordx4 %1, %5, off sc1\n\tglobal_load_dwordx4 %2, %6, off sc1\n\tglobal_load_dwordx4 %3, %7, off sc1\n\ts_waitcnt vmcnt(0)"
-                     : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
-                     : "v"(p[0]), "v"(p[1]), "v"(p[2]), "v"(p[3])
-                     : "memory");
-    else if constexpr (N == 5)
-        asm volatile("global_load_dwordx4 %0, %5, off sc1\n\tglobal_load_dwordx4 %1, %6, off sc1\n\tglobal_load_dwordx4 %2, %7, off sc1\n\tglobal_load_dwordx4 %3, %8, off sc1\n\tglobal_load_dwordx4 %4, %9, off sc1\n\ts_waitcnt vmcnt(0)"
-                     : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4])
-                     : "v"(p[0]), "v"(p[1]), "v"(p[2]), "v"(p[3]), "v"(p[4])
-                     : "memory");
-    else if constexpr (N == 6)
-        asm volatile("global_load_dwordx4 %0, %6, off sc1\n\tglobal_load_dwordx4 %1, %7, off sc1\n\tglobal_load_dwordx4 %2, %8, off sc1\n\tglobal_load_dwordx4 %3, %9, off sc1\n\tglobal_load_dwordx4 %4, %10, off sc1\n\tglobal_load_dwordx4 %5, %11, off sc1\n\ts_waitcnt vmcnt(0)"
-                     : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5])
-                     : "v"(p[0]), "v"(p[1]), "v"(p[2]), "v"(p[3]), "v"(p[4]), "v"(p[5])
-                     : "memory");
-    else if constexpr (N == 7)
-        asm volatile("global_load_dwordx4 %0, %7, off sc1\n\tglobal_load_dwordx4 %1, %8, off sc1\n\tglobal_load_dwordx4 %2, %9, off sc1\n\tglobal_load_dwordx4 %3, %10, off sc1\n\tglobal_load_dwordx4 %4, %11, off sc1\n\tglobal_load_dwordx4 %5, %12, off sc1\n\tglobal_load_dwordx4 %6, %13, off sc1\n\ts_waitcnt vmcnt(0)"
-                     : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6])
-                     : "v"(p[0]), "v"(p[1]), "v"(p[2]), "v"(p[3]), "v"(p[4]), "v"(p[5]), "v"(p[6])
-                     : "memory");
-    else if constexpr (N == 8)
-        asm volatile("global_load_dwordx4 %0, %8, off sc1\n\tglobal_load_dwordx4 %1, %9, off sc1\n\tglobal_load_dwordx4 %2, %10, off sc1\n\tglobal_load_dwordx4 %3, %11, off sc1\n\tglobal_load_dwordx4 %4, %12, off sc1\n\tglobal_load_dwordx4 %5, %13, off sc1\n\tglobal_load_dwordx4 %6, %14, off sc1\n\tglobal_load_dwordx4 %7, %15, off sc1\n\ts_waitcnt vmcnt(0)"
-                     : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
-                     : "v"(p[0]), "v"(p[1]), "v"(p[2]), "v"(p[3]), "v"(p[4]), "v"(p[5]), "v"(p[6]), "v"(p[7])
                      : "memory");
 }
 
@@ -242,28 +220,40 @@ __device__ __forceinline__ bool unit_fresh(u32x4 v, int w, int n, unsigned tag) 
     return (w >= n || v[1] == tag) && (w + 1 >= n || v[3] == tag);
 }
 
-// Register form of the gather for a wave that owns N <= 8 chunks: a round
-// loads every chunk of the wave into registers and waits for all of them
-// (one asm statement), then checks the tags there; once every word is fresh
-// the chunks are written to LDS. Re-loading fresh chunks costs traffic but no
-// time: a round takes one memory round trip either way, and without the LDS
-// round trip of the copy form a round is shorter.
+// A gather's source: tagged words A[0, nA) in 128-word chunks [0, cA) of the
+// LDS copy, then B[0, nB) in the chunks after them.
+struct Ranges {
+    const uint64_t *a, *b;
+    int na, nb;
+};
+
+// Register form of the gather for a wave that owns N <= 2 chunks (w and
+// w + 8): a round loads every chunk of the wave into registers and waits
+// for all of them (one asm statement), then checks the tags there; once
+// every word is fresh the chunks are written to LDS. Re-loading fresh
+// chunks costs traffic but no time: a round takes one memory round trip
+// either way.
 template <int N>
-__device__ void gather_regs(uint64_t *dst, const uint64_t *src, int n, unsigned tag, int *abort_flag, int wave,
-                            int lane) {
-    const uint64_t *p[8];
+__device__ __forceinline__ void gather_regs(uint64_t *dst, Ranges g, unsigned tag, int *abort_flag, int wave, int lane) {
+    const int ca = (g.na + kChunk - 1) / kChunk;
+    const uint64_t *p[2];
+    int n[2];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int w = (wave + kWaves * i) * kChunk + lane * 2;
-        p[i] = src + (i < N && w < n ? w : 0);
+    for (int i = 0; i < 2; ++i) {
+        const int c = wave + kWaves * i;
+        const bool in_a = c < ca;
+        const int base = (in_a ? c : c - ca) * kChunk;
+        n[i] = (in_a ? g.na : g.nb) - base;  // valid words of the chunk
+        const uint64_t *src = in_a ? g.a : g.b;
+        p[i] = i < N && lane * 2 < n[i] ? src + base + lane * 2 : g.a;
     }
     long spins = 0;
     while (true) {
-        u32x4 r[8];
+        u32x4 r[2];
         poll16<N>(r, p);
         bool stale = false;
 #pragma unroll
-        for (int i = 0; i < N; ++i) stale |= !unit_fresh(r[i], (wave + kWaves * i) * kChunk + lane * 2, n, tag);
+        for (int i = 0; i < N; ++i) stale |= !unit_fresh(r[i], lane * 2, n[i], tag);
         const bool done = !__any(stale);
         const bool give_up = !done && (++spins > kSpinLimit || ((spins & 15) == 0 && aborted(abort_flag)));
         if (done || give_up) {
@@ -271,10 +261,8 @@ __device__ void gather_regs(uint64_t *dst, const uint64_t *src, int n, unsigned 
             // the source buffer's, so what readers take from them (a token's
             // row index) stays one that buffer held.
 #pragma unroll
-            for (int i = 0; i < N; ++i) {
-                const int w = (wave + kWaves * i) * kChunk + lane * 2;
-                if (w < n) *(u32x4 *)(dst + w) = r[i];
-            }
+            for (int i = 0; i < N; ++i)
+                if (lane * 2 < n[i]) *(u32x4 *)(dst + (wave + kWaves * i) * kChunk + lane * 2) = r[i];
             if (give_up) raise_abort(abort_flag);
             return;
         }
@@ -282,69 +270,27 @@ __device__ void gather_regs(uint64_t *dst, const uint64_t *src, int n, unsigned 
     }
 }
 
-// All waves: copies tagged words src[0, n) into LDS dst[0, n) and waits until
-// each carries `tag`. Wave w owns the 128-word chunks w, w + 8, ...; up to
-// eight of them it polls in registers (gather_regs), more it loads with direct
-// global->LDS copies and re-loads the stale ones until every word of its
-// chunks is fresh (its tag reads for eight chunks in flight at a time). The
-// caller's barrier then makes all of them visible to the block. A wave's wait
-// also covers the weight rows it has in flight. On timeout the abort word is
-// raised and the wave moves on with what it has.
-__device__ __attribute__((noinline)) void gather(uint64_t *dst, const uint64_t *src, int n, unsigned tag, int *abort_flag) {
+// All waves: copies tagged words into LDS (range A at dst[0, nA), range B
+// from the next 128-word boundary on) and waits until each carries `tag`.
+// Wave w owns the 128-word chunks w and w + 8 (at most 16 chunks) and polls
+// them in registers (gather_regs). The caller's barrier then makes all of
+// them visible to the block. A wave's wait also covers the weight rows it
+// has in flight. On timeout the abort word is raised and the wave moves on
+// with what it has. Inline (no call), so the weight registers held across
+// it need no call-preserved registers.
+constexpr int kMaxGather = 2 * kWaves * kChunk;
+__device__ __forceinline__ void gather(uint64_t *dst, Ranges g, unsigned tag, int *abort_flag) {
     const int lane = lane_here(), wave = __builtin_amdgcn_readfirstlane(tid_here() >> 6);
-    const int chunks = (n + kChunk - 1) / kChunk;
-    const int mine = chunks > wave ? (chunks - 1 - wave) / kWaves + 1 : 0;  // at most 16
-    switch (mine) {
-        case 0: return;
-        case 1: return gather_regs<1>(dst, src, n, tag, abort_flag, wave, lane);
-        case 2: return gather_regs<2>(dst, src, n, tag, abort_flag, wave, lane);
-        case 3: return gather_regs<3>(dst, src, n, tag, abort_flag, wave, lane);
-        case 4: return gather_regs<4>(dst, src, n, tag, abort_flag, wave, lane);
-        case 5: return gather_regs<5>(dst, src, n, tag, abort_flag, wave, lane);
-        case 6: return gather_regs<6>(dst, src, n, tag, abort_flag, wave, lane);
-        case 7: return gather_regs<7>(dst, src, n, tag, abort_flag, wave, lane);
-        case 8: return gather_regs<8>(dst, src, n, tag, abort_flag, wave, lane);
-        default: break;
-    }
-    const uint32_t *d32 = (const uint32_t *)dst;
-    uint32_t pend = (1u << mine) - 1;
-    long spins = 0;
-    while (pend) {
-        const uint32_t issued = pend;
-        for (uint32_t m = issued; m; m &= m - 1) {
-            const int c = wave + kWaves * __builtin_ctz(m), w = c * kChunk + lane * 2;
-            if (w < n) dma16(src + w, dst + c * kChunk);
-        }
-        wait_vm();
-        uint32_t still = 0;
-        for (int i0 = 0; i0 < mine; i0 += 8) {
-            uint32_t t0[8], t1[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int w = (wave + kWaves * min(i0 + j, mine - 1)) * kChunk + lane * 2;
-                t0[j] = d32[2 * w + 1];
-                t1[j] = d32[2 * w + 3];
-            }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int i = i0 + j, w = (wave + kWaves * i) * kChunk + lane * 2;
-                const bool stale = (w < n && t0[j] != tag) || (w + 1 < n && t1[j] != tag);
-                if (i < mine && ((issued >> i) & 1) && __any(stale)) still |= 1u << i;
-            }
-        }
-        pend = still;
-        if (pend) {
-            if (++spins > kSpinLimit || ((spins & 15) == 0 && aborted(abort_flag))) {
-                raise_abort(abort_flag);
-                return;
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
-    }
+    const int chunks = (g.na + kChunk - 1) / kChunk + (g.nb + kChunk - 1) / kChunk;
+    if (chunks > wave + kWaves) gather_regs<2>(dst, g, tag, abort_flag, wave, lane);
+    else if (chunks > wave) gather_regs<1>(dst, g, tag, abort_flag, wave, lane);
+}
+__device__ __forceinline__ void gather(uint64_t *dst, const uint64_t *src, int n, unsigned tag, int *abort_flag) {
+    gather(dst, Ranges{src, src, n, 0}, tag, abort_flag);
 }
 
-// Poll wave only: starts copying `bytes` (a multiple of 16) from global
-// memory into LDS; completion is awaited with wait_vm.
+// One wave: starts copying `bytes` (a multiple of 16) from global memory
+// into LDS; completion is awaited with wait_vm.
 __device__ __forceinline__ void dma_bytes(void *dst, const void *src, int bytes) {
     const int lane = lane_here();
     for (int c = 0; c < bytes; c += 1024) {
@@ -455,12 +401,37 @@ __device__ __forceinline__ void wave_best(int &key, uint32_t &idx) {
 
 constexpr int kStage = 64;  // outputs one block publishes per phase, at most
 
+constexpr int kWaveRows = 128;  // rows one wave stores at once (two per lane)
+
 struct Shm {
     int ikey[kWaves];
     uint32_t iidx[kWaves];
     int token;           // the step's sampled id
     float out[kStage];   // a phase's outputs of the block, stored as one run
+    float coef[kWaveRows];              // the owners' merge weight per item
+    float scr[kWaves][kWaveRows];       // a wave's row values on their way to the stores
 };
+
+// A wave's row values stored as tagged words, two rows per 16-byte store.
+// v[k] sits in the lanes with lane % LPR == 0 and belongs to the wave's row
+// (k 8 + wave) RPS + lane / LPR; the values pass through the wave's LDS
+// scratch so that lane j stores rows 2 j and 2 j + 1 (consecutive rows of
+// one owner's 8-word segment, dst(r) 16-byte aligned for even r). LDS
+// traffic of one wave is in order, so no barrier is needed.
+template <int NS, int RPS, int LPR, class D>
+__device__ __forceinline__ void store_rows(const float (&v)[NS], float *scr, int wave, int H, unsigned tag, D &&dst) {
+    static_assert(NS * RPS <= kWaveRows && RPS % 2 == 0, "rows per wave");
+    const int ln = lane_here();
+    if (ln % LPR == 0) {
+#pragma unroll
+        for (int k = 0; k < NS; ++k) scr[k * RPS + ln / LPR] = v[k];
+    }
+    const int j = 2 * ln;
+    if (j < NS * RPS) {
+        const int k = j / RPS, r = (k * kWaves + wave) * RPS + j % RPS;
+        if (r < H) stf2(dst(r), scr[j], scr[j + 1], tag);
+    }
+}
 
 // Reduces (key, idx) over the block; the result lands in every thread.
 __device__ __forceinline__ void block_best(int &key, uint32_t &idx, Shm &sm) {
@@ -477,200 +448,6 @@ __device__ __forceinline__ void block_best(int &key, uint32_t &idx, Shm &sm) {
     bar();
 }
 
-template <int HD, int G>
-struct AttnShm {
-    static constexpr int GP = (G + 3) / 4 * 4;
-    float p[kItemPos][GP];  // scores, then weights, of position x head
-    float red[kWaves][G][HD];
-    float m[G], l[G];
-};
-
-__host__ __device__ constexpr int round_up(int x, int m) { return (x + m - 1) / m * m; }
-__host__ __device__ constexpr int imax(int a, int b) { return a > b ? a : b; }
-
-// Dynamic LDS layout (byte offsets): tagged-word staging, the f32 vector the
-// compute waves read (also an attention item's q), one item's K and V rows,
-// the merge weights of every (split, q head) and 1 / sum per q head, the
-// next step's embedding row and a phase's RMSNorm gains (BF16).
-struct LdsLayout {
-    int tbw;  // staging words
-    int xs, kv, mw, emb, gain, total;
-};
-__host__ __device__ inline LdsLayout lds_layout(int H, int I, int nq, int hd, int G, int kv_bytes, int blocks,
-                                                int max_splits) {
-    LdsLayout o{};
-    int tbw = imax(imax(H, I), imax((G + 2) * hd, 2 * blocks));
-    tbw = imax(tbw, max_splits * nq * (hd + 2));
-    const int rb = (I + blocks - 1) / blocks;
-    tbw = imax(tbw, (I + rb - 1) / rb * kCW);  // one o/down block's down partials
-    o.tbw = round_up(tbw + 2, kChunk);
-    const int xf = xpad(imax(imax(H, I), nq * hd)) + 10;
-    o.xs = o.tbw * 8;
-    o.kv = o.xs + round_up(xf * 4, 16);
-    o.mw = o.kv + 2 * item_positions(hd * kv_bytes) * hd * kv_bytes;
-    o.emb = o.mw + round_up((max_splits + 1) * nq * 4, 16);
-    o.gain = o.emb + round_up(H * 2, 16);
-    o.total = o.gain + round_up(H * 2, 16);
-    return o;
-}
-
-// Poll wave only: starts the copies of the cached K and V rows of positions
-// [start, lim) of KV head g into LDS (row p - start of each); completion is
-// awaited with wait_vm.
-template <int HD, class KT>
-__device__ __forceinline__ void load_kv_lds(CArgs *a, uint8_t *k_lds, uint8_t *v_lds, int l, int g, long start,
-                                            long lim) {
-    constexpr int ROW = HD * (int)sizeof(KT);
-    const int lane = lane_here();
-    for (long t0 = start; t0 < lim; t0 += TP) {
-        const int page = ldc(opaque(a)->page_table, t0 / TP);
-        const int bytes = (int)(min((long)TP, lim - t0)) * ROW;
-        const size_t off = (((size_t)page * opaque(a)->kv_heads + g) * TP) * ROW;
-        const uint8_t *ks = (const uint8_t *)layer_of(a, l)->kc + off, *vs = (const uint8_t *)layer_of(a, l)->vc + off;
-        uint8_t *kd = k_lds + (t0 - start) * ROW, *vd = v_lds + (t0 - start) * ROW;
-        for (int c = 0; c < bytes; c += 1024) {
-            const int byte = c + lane * 16;
-            if (byte < bytes) {
-                dma16(ks + byte, kd + c);
-                dma16(vs + byte, vd + c);
-            }
-        }
-    }
-}
-
-template <class KT>
-__device__ __forceinline__ void ld8(const KT *p, float (&f)[8]) {
-    if constexpr (sizeof(KT) == 2) {
-        const u32x4 v = *(const u32x4 *)p;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            f[2 * i] = bf16_lo(v[i]);
-            f[2 * i + 1] = bf16_hi(v[i]);
-        }
-    } else {
-        const f32x4 a = *(const f32x4 *)p, b = *(const f32x4 *)(p + 4);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            f[i] = a[i];
-            f[4 + i] = b[i];
-        }
-    }
-}
-
-// One attention item, all waves: q (G heads, f32) in qs, nv K and V rows in
-// LDS; writes (unnormalised output, max, sum) per q head of the group to
-// part[j * (HD + 2) + ...] (compute waves store, so the poll wave has no
-// stores in flight when it polls next).
-template <int HD, int G, class KT>
-__device__ __forceinline__ void attn_compute(const float *qs, const uint8_t *k_lds, const uint8_t *v_lds, int nv, AttnShm<HD, G> &sh,
-                             uint64_t *part, unsigned tag, uint64_t *tr) {
-    constexpr int T = HD / 8, P = kThreads / T, ROW = HD * (int)sizeof(KT);
-    const int tid = tid_here(), lane = tid & 63, wave = tid >> 6;
-    const int d8 = tid % T, pg = tid / T;
-    auto mark = [&](int ev) {
-        if (tr && tid == 0) st_u64(tr + ev, wall_clock64());
-    };
-    const float scale = 1.0f / sqrtf((float)HD);
-    const int passes = (nv + P - 1) / P;
-    for (int ps = 0; ps < passes; ++ps) {
-        const int pi = ps * P + pg;
-        const bool valid = pi < nv;
-        float dot[G];
-#pragma unroll
-        for (int j = 0; j < G; ++j) dot[j] = 0.f;
-        if (valid) {
-            float kf[8];
-            ld8<KT>((const KT *)(k_lds + (size_t)pi * ROW) + d8 * 8, kf);
-#pragma unroll
-            for (int j = 0; j < G; ++j)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) dot[j] = fmaf(kf[e], qs[j * HD + d8 * 8 + e], dot[j]);
-        }
-#pragma unroll
-        for (int j = 0; j < G; ++j) {
-            const float s = group_sum<T>(dot[j]);
-            if (d8 == 0 && valid) sh.p[pi][j] = s * scale;
-        }
-    }
-    bar();
-    mark(1);
-    for (int j = wave; j < G; j += kWaves) {
-        float mx = -INFINITY;
-        for (int c = lane; c < nv; c += 64) mx = fmaxf(mx, sh.p[c][j]);
-        mx = wave_max(mx);
-        float sum = 0.f;
-        for (int c = lane; c < nv; c += 64) {
-            const float pv = expf(sh.p[c][j] - mx);
-            sh.p[c][j] = pv;
-            sum += pv;
-        }
-        sum = wave_sum(sum);
-        if (lane == 0) {
-            sh.m[j] = mx;
-            sh.l[j] = sum;
-        }
-    }
-    bar();
-    mark(2);
-    // Weighted V: lane owns DPL head dimensions, wave w positions w, w + 8,
-    // ...; the waves' sums are added in wave order.
-    constexpr int DPL = HD / 64;
-    constexpr int GP = AttnShm<HD, G>::GP;
-    float acc[G][DPL];
-#pragma unroll
-    for (int j = 0; j < G; ++j)
-#pragma unroll
-        for (int e = 0; e < DPL; ++e) acc[j][e] = 0.f;
-#pragma unroll 4
-    for (int pi = wave; pi < nv; pi += kWaves) {
-        const KT *vrow = (const KT *)(v_lds + (size_t)pi * ROW) + lane * DPL;
-        float vf[DPL];
-        if constexpr (sizeof(KT) == 2) {
-            if constexpr (DPL == 1) {
-                vf[0] = bf16_f32(*vrow);
-            } else {
-                const uint32_t w2 = *(const uint32_t *)vrow;
-                vf[0] = bf16_lo(w2);
-                vf[1] = bf16_hi(w2);
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < DPL; ++e) vf[e] = vrow[e];
-        }
-        float pj[GP];
-#pragma unroll
-        for (int j4 = 0; j4 < GP; j4 += 4) {
-            const f32x4 q4 = *(const f32x4 *)&sh.p[pi][j4];
-            pj[j4] = q4[0];
-            pj[j4 + 1] = q4[1];
-            pj[j4 + 2] = q4[2];
-            pj[j4 + 3] = q4[3];
-        }
-#pragma unroll
-        for (int j = 0; j < G; ++j)
-#pragma unroll
-            for (int e = 0; e < DPL; ++e) acc[j][e] = fmaf(pj[j], vf[e], acc[j][e]);
-    }
-#pragma unroll
-    for (int j = 0; j < G; ++j)
-#pragma unroll
-        for (int e = 0; e < DPL; ++e) sh.red[wave][j][lane * DPL + e] = acc[j][e];
-    bar();
-    mark(3);
-    if (tid < kCW * 64) {
-        for (int t = tid; t < G * HD; t += kCW * 64) {
-            const int j = t / HD, d = t % HD;
-            float o = sh.red[0][j][d];
-#pragma unroll
-            for (int w = 1; w < kWaves; ++w) o += sh.red[w][j][d];
-            stf(part + (size_t)j * (HD + 2) + d, o, tag);
-        }
-        if (tid < G) {
-            stf(part + (size_t)tid * (HD + 2) + HD, sh.m[tid], tag);
-            stf(part + (size_t)tid * (HD + 2) + HD + 1, sh.l[tid], tag);
-        }
-    }
-}
 
 // Keeps loaded rows in their registers across code that would otherwise
 // reuse them (the compiler then waits for their loads here).
@@ -726,595 +503,891 @@ __device__ __forceinline__ void head_dots(const uint16_t *head, float *logits, c
     pin(hb[0]);
 }
 
-// UH/UQ: 16-byte units per lane of a row with H / q_heads*HD columns; UP:
-// 16-byte units of a down_cols row (one per thread); RGU: gate/up rows per
-// wave; UHB: units per lane of a BF16
-// head row. Shape values are re-read from the arguments where used (A()) and
-// block roles recomputed from them, so that little stays in scalar registers
-// across the step loop.
-template <int FMT, int HD, int G, class KT, int UH, int UQ, int UP, int RGU, int UHB, bool HS>
-__global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
-    using U = Unit<FMT, 16>;
+
+__host__ __device__ constexpr int round_up(int x, int m) { return (x + m - 1) / m * m; }
+__host__ __device__ constexpr int imax(int a, int b) { return a > b ? a : b; }
+
+__device__ __forceinline__ u32x4 ld_unit(Rsrc r, uint32_t off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
+}
+
+// Wave-wide dot products of R rows held in pool slots OFF + i * N + k (unit
+// k of row i in lane k % 64 of slot k / 64's register) with xs; a unit's x
+// values are read once for all rows. Per row the summation order is fixed
+// (unit, then element); results land in every lane. Lanes past the row
+// (n_units) read a valid x at a clamped index while their weights are the
+// zeros of a load that read nothing.
+template <int R, int N, int OFF, int NP>
+__device__ __forceinline__ void dot_pool(const u32x4 (&W)[NP], const float *xs, int n_units, float (&out)[R]) {
+    static_assert(OFF + R * N <= NP, "pool slice out of range");
+    using U = Unit<FMT_BF16, 16>;
+    const int lane = lane_here();
+    float acc[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) acc[i] = 0.f;
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        const int u = min(lane + 64 * k, n_units - 1);
+        float xv[U::E];
+#pragma unroll
+        for (int e = 0; e < U::E; ++e) xv[e] = xs[xpad(u * U::E + e)];
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            const u32x4 w = W[OFF + i * N + k];
+            const uint32_t raw[4] = {w[0], w[1], w[2], w[3]};
+            U::decode(raw, [&](int e, float v) { acc[i] = fmaf(v, xv[e], acc[i]); });
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < R; ++i) out[i] = wave_sum(acc[i]);
+}
+
+template <int HD>
+struct ItemShm {
+    float p[kIpMax];       // scores, then weights, of the run's positions
+    float red[kWaves][HD];
+    float o[HD];           // the unnormalised output
+    float m, l;            // max score, sum of weights
+};
+
+// Dynamic LDS layout (byte offsets): tagged-word staging, the f32 vector
+// the dot products read, an item's q (with its biases and rotation factors),
+// its K and V rows, the embedding row, and two RMSNorm gain rows (BF16): g1
+// for the items' and KV blocks' input norm, g2 for the FFN norm and the
+// final norm.
+struct LdsLayout {
+    int tbw;  // staging words
+    int xs, q, kv, emb, g1, g2, total;
+};
+__host__ __device__ inline LdsLayout lds_layout(int H, int hd, int kv_bytes, int ip, int ni, int nbd, int blocks) {
+    LdsLayout o{};
+    int tbw = imax(imax(H, round_up(ni * kOwn, kChunk) + 2 * ni), imax(nbd * kOwn, imax(2 * hd, 2 * blocks)));
+    o.tbw = round_up(tbw + 2, kChunk);
+    o.xs = o.tbw * 8;
+    o.q = o.xs + round_up((xpad(H) + 10) * 4, 16);
+    o.kv = o.q + round_up(3 * hd * 4, 16);
+    o.emb = o.kv + round_up(2 * ip * hd * kv_bytes, 16);
+    o.g1 = o.emb + round_up(H * 2, 16);
+    o.g2 = o.g1 + round_up(H * 2, 16);
+    o.total = o.g2 + round_up(H * 2, 16);
+    return o;
+}
+
+// Starts the copies of the cached K and V rows of positions [start, lim) of
+// KV head g into LDS (row p - start of each), 1 KB pieces spread over the
+// waves; completion is awaited with wait_vm. start is page-aligned.
+template <int HD, class KT>
+__device__ __forceinline__ void load_kv_lds(CArgs *a, uint8_t *k_lds, uint8_t *v_lds, int l, int g, long start,
+                                            long lim) {
     constexpr int ROW = HD * (int)sizeof(KT);
+    const int lane = lane_here(), wave = __builtin_amdgcn_readfirstlane(tid_here() >> 6);
+    for (long t0 = start; t0 < lim; t0 += TP) {
+        const int page = ldc(opaque(a)->page_table, t0 / TP);
+        const int bytes = (int)(min((long)TP, lim - t0)) * ROW;
+        const size_t off = (((size_t)page * opaque(a)->kv_heads + g) * TP) * ROW;
+        const uint8_t *ks = (const uint8_t *)layer_of(a, l)->kc + off, *vs = (const uint8_t *)layer_of(a, l)->vc + off;
+        uint8_t *kd = k_lds + (t0 - start) * ROW, *vd = v_lds + (t0 - start) * ROW;
+        for (int c = wave * 1024; c < bytes; c += kWaves * 1024) {
+            const int byte = c + lane * 16;
+            if (byte < bytes) {
+                dma16(ks + byte, kd + c);
+                dma16(vs + byte, vd + c);
+            }
+        }
+    }
+}
+
+template <class KT>
+__device__ __forceinline__ void ld8(const KT *p, float (&f)[8]) {
+    if constexpr (sizeof(KT) == 2) {
+        const u32x4 v = *(const u32x4 *)p;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f[2 * i] = bf16_lo(v[i]);
+            f[2 * i + 1] = bf16_hi(v[i]);
+        }
+    } else {
+        const f32x4 a = *(const f32x4 *)p, b = *(const f32x4 *)(p + 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f[i] = a[i];
+            f[4 + i] = b[i];
+        }
+    }
+}
+
+// All threads: scores of K rows [p0, p1) (LDS) against q, scaled by
+// 1/sqrt(hd), into p[]; T = hd / 8 lanes per row, 8 dimensions each.
+template <int HD, class KT>
+__device__ __forceinline__ void item_scores(const float *qs, const uint8_t *k_lds, int p0, int p1, float *p) {
+    constexpr int T = HD / 8, P = kThreads / T, ROW = HD * (int)sizeof(KT);
+    const int tid = tid_here();
+    const int d8 = tid % T, pg = tid / T;
+    const float scale = 1.0f / sqrtf((float)HD);
+    for (int b0 = p0; b0 < p1; b0 += P) {
+        const int pi = b0 + pg;
+        const bool valid = pi < p1;
+        float dot = 0.f;
+        if (valid) {
+            float kf[8];
+            ld8<KT>((const KT *)(k_lds + (size_t)pi * ROW) + d8 * 8, kf);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) dot = fmaf(kf[e], qs[d8 * 8 + e], dot);
+        }
+        const float s = group_sum<T>(dot);
+        if (d8 == 0 && valid) p[pi] = s * scale;
+    }
+}
+
+// All threads: softmax of the nv scores (max, exp, sum) and the weighted V
+// rows: sh.o = sum_p w_p v_p (unnormalised), sh.m, sh.l. Lane owns hd / 64
+// dimensions, wave w positions w, w + 8, ...; the waves' sums are added in
+// wave order.
+template <int HD, class KT>
+__device__ __forceinline__ void item_softmax_pv(const uint8_t *v_lds, int nv, ItemShm<HD> &sh) {
+    constexpr int ROW = HD * (int)sizeof(KT), DPL = HD / 64;
+    const int tid = tid_here(), lane = tid & 63, wave = tid >> 6;
+    if (wave == 0) {
+        float mx = -INFINITY;
+        for (int c = lane; c < nv; c += 64) mx = fmaxf(mx, sh.p[c]);
+        mx = wave_max(mx);
+        float sum = 0.f;
+        for (int c = lane; c < nv; c += 64) {
+            const float pv = expf(sh.p[c] - mx);
+            sh.p[c] = pv;
+            sum += pv;
+        }
+        sum = wave_sum(sum);
+        if (lane == 0) {
+            sh.m = mx;
+            sh.l = sum;
+        }
+    }
+    bar();
+    float acc[DPL];
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) acc[e] = 0.f;
+#pragma unroll 4
+    for (int pi = wave; pi < nv; pi += kWaves) {
+        const KT *vrow = (const KT *)(v_lds + (size_t)pi * ROW) + lane * DPL;
+        float vf[DPL];
+        if constexpr (sizeof(KT) == 2) {
+            if constexpr (DPL == 1) {
+                vf[0] = bf16_f32(*vrow);
+            } else {
+                const uint32_t w2 = *(const uint32_t *)vrow;
+                vf[0] = bf16_lo(w2);
+                vf[1] = bf16_hi(w2);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < DPL; ++e) vf[e] = vrow[e];
+        }
+        const float pj = sh.p[pi];
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) acc[e] = fmaf(pj, vf[e], acc[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) sh.red[wave][lane * DPL + e] = acc[e];
+    bar();
+    if (tid < HD) {
+        float o = sh.red[0][tid];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) o += sh.red[w][tid];
+        sh.o[tid] = o;
+    }
+    bar();
+}
+
+// UH: 16-byte units per lane of a row with H columns; RO: rows of H per
+// thread (H <= 512 RO); RGU: gate (and up) rows per wave of an FFN block;
+// UP: 16-byte units of a down_cols row (lanes per row in the down
+// partials); UHB: units per lane of a BF16 head row; NWO: o_proj units per
+// lane of an item (64 / (hd / 8) rows per wave each). Shape values are
+// re-read from the arguments where used (A()) and block roles recomputed
+// from them, so that little stays in scalar registers across the step loop.
+//
+// Each role runs its own step and layer loops (one branch per role), with
+// the LM head and the token reduction shared: a loop carries only its
+// role's weight registers, and a CU's hot code is only its role's.
+template <int HD, int G, class KT, int UH, int RO, int RGU, int UP, int UHB, int NWO>
+__global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
+    using U = Unit<FMT_BF16, 16>;
+    constexpr int ROW = HD * (int)sizeof(KT);
+    constexpr int RQ = HD / kWaves;      // an item's q rows per wave
+    constexpr int UO = HD / U::E;        // units of one head's columns of an o_proj row (lanes per row)
+    constexpr int OW = 64 / UO;          // o_proj rows per wave and unit
+    constexpr int NQ = RQ * UH;          // an item's q-row units
+    constexpr int NI = NQ + NWO;         // an item's weight units
+    constexpr int NG = RGU * UH;         // an FFN block's gate (and up) units
+    constexpr int DW = 64 / UP;          // down rows per wave and unit (UP lanes per row)
+    constexpr int ND = (RO * kThreads + DW * kWaves - 1) / (DW * kWaves);  // down units: H <= 512 RO rows
+    constexpr int NF = 2 * NG + ND;      // an FFN block's weight units
+    constexpr int NK = 2 * UH;           // a KV block's weight units
+    static_assert(UP == 1 || UP == 2 || UP == 4 || UP == 8 || UP == 16, "lanes per down row");
+    static_assert(RQ % 2 == 0, "q rows come in rotation pairs");
+    static_assert(8 * UP <= kStage, "down columns beyond the staged outputs");
     // The only read of the kernarg-segment pointer (see opaque()).
     CArgs *const kargs = (CArgs *)__builtin_amdgcn_kernarg_segment_ptr();
     auto A = [kargs]() { return opaque(kargs); };
     auto LY = [kargs](int l) { return layer_of(kargs, l); };
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ Shm sm;
-    constexpr int GI = HS ? 1 : G;  // q heads per attention item
-    __shared__ AttnShm<HD, GI> ash;
-    const int lane = tid_here() & 63;
+    __shared__ ItemShm<HD> ish;
     const int wave = __builtin_amdgcn_readfirstlane(tid_here() >> 6);
-    const bool spare = wave == kSpareWave;
     const int b = blockIdx.x;
     uint64_t *tb = (uint64_t *)lds;
 
-    // Roles. o_proj and down rows: blocks [0, nhb), compute wave w of block b
-    // owns row kCW * b + w of both (the residual stays in its register). QKV
-    // pairs: the next nab blocks (the last ones when the grid is short).
-    // Gate/up: every block rb consecutive rows, wave w (the spare wave too)
-    // rows w, w + 8, ...
-    // Attention items: the last blocks. LM head: every wave of every block.
-    auto npairs = [&]() { return (A()->q_heads + 2 * A()->kv_heads) * HD / 2; };
-    auto hasA = [&]() {
-        const int s0 = A()->a0;
-        return b >= s0 && b < s0 + A()->nab;
-    };
-    auto pairA = [&]() { return (b - A()->a0) * kCW + wave; };
-    auto myA = [&]() { return !spare && hasA() && pairA() < npairs(); };
-    auto hasH = [&]() { return b < A()->nhb; };
-    auto rowH = [&]() { return b * kCW + wave; };
-    auto myH = [&]() { return !spare && hasH() && rowH() < A()->H; };
-    auto hasD = [&]() { return b * A()->rb < A()->I; };
-    auto nrD = [&]() {
-        const int rb = A()->rb, I = A()->I;
-        int n = 0;
-#pragma unroll
-        for (int k = 0; k < RGU; ++k) {
-            const int j = wave + kWaves * k;
-            n += j < rb && b * rb + j < I ? 1 : 0;
-        }
-        return n;
-    };
+    // Roles: items [0, ni) (item = split * q_heads + head), KV blocks
+    // [kv0, kv0 + nkv) (wave w of KV block k: rotation pair 8 k + w of the
+    // K/V rows), FFN blocks [f0, f0 + nf): block f owns gate/up rows
+    // [f rb, f rb + rb) (wave w rows w, w + 8, ...) and, for f < no, the
+    // residual rows 8 f + w. Blocks in none of these only join the LM head.
+    auto isItem = [&]() { return b < A()->ni; };
+    auto isKV = [&]() { return b >= A()->kv0 && b < A()->kv0 + A()->nkv; };
+    auto fIdx = [&]() { return b - A()->f0; };
+    auto isFFN = [&]() { return b >= A()->f0; };
+    auto isOwner = [&]() { return isFFN() && fIdx() < A()->no; };
+    auto hasRows = [&]() { return isFFN() && fIdx() < A()->nbd; };
     auto hasHead = [&]() { return b * kWaves < A()->V; };
+    auto itHead = [&]() { return b % A()->q_heads; };
+    auto itSplit = [&]() { return b / A()->q_heads; };
+    auto kvPair = [&]() { return (b - A()->kv0) * kWaves + wave; };
+    auto ownRow = [&]() { return fIdx() * kOwn + wave; };
 
-    u32x4 wA[2][UH], wC[1][UQ], wD[2 * RGU][UH], wP[2][UP];
-
-    // Weight rows of layer l. Every wave issues the same loads at the same
-    // points (the spare wave's and those of rows a wave does not own read
-    // nothing), so no path through the loop has a different load count and
-    // the compiler's waits stay exact. Issue points: right after B the
-    // o_proj, gate/up and down rows of the layer (the o_proj/down blocks are
-    // idle while QKV and attention run, and a CU sustains only so many
-    // outstanding misses, so issuing later would stall the wave for the
-    // transfer), after D the next layer's QKV rows.
-    auto load_wA = [&](int l, bool valid) {
-        const size_t stride = A()->qkv_stride;
-        const int rows = (A()->q_heads + 2 * A()->kv_heads) * HD;
-        const Rsrc r = rsrc(LY(l)->qkv, (size_t)rows * stride);
-        const bool v = valid && myA();
-        const uint32_t off = (uint32_t)(2 * pairA()) * (uint32_t)stride;
-        load_row(wA[0], r, off, A()->H / U::E, v);
-        load_row(wA[1], r, off + (uint32_t)stride, A()->H / U::E, v);
-    };
-    auto load_wC = [&](int l, bool valid) {
-        const size_t stride = A()->o_stride;
-        const Rsrc r = rsrc(LY(l)->o, (size_t)A()->H * stride);
-        load_row(wC[0], r, (uint32_t)rowH() * (uint32_t)stride, A()->q_heads * HD / U::E, valid && myH());
-    };
-    auto load_wD = [&](int l, bool valid) {
-        const size_t stride = A()->gu_stride, bytes = (size_t)A()->I * stride;
-        const Rsrc rg = rsrc(LY(l)->gate, bytes), ru = rsrc(LY(l)->up, bytes);
-        const int n = nrD(), base = b * A()->rb + wave, nH = A()->H / U::E;
-#pragma unroll
-        for (int k = 0; k < RGU; ++k) {
-            const uint32_t off = (uint32_t)(base + kWaves * k) * (uint32_t)stride;
-            load_row(wD[2 * k], rg, off, nH, valid && k < n);
-            load_row(wD[2 * k + 1], ru, off, nH, valid && k < n);
-        }
-    };
-    // This block's down_cols rows: output rows q and q + 512 of thread q,
-    // UP units each (units past the padded row read nothing).
-    auto load_wP = [&](int l, bool valid) {
-        const int H = A()->H;
-        const uint32_t row_bytes = (uint32_t)A()->rp * 2u;
-        const Rsrc r = rsrc(LY(l)->down_cols, (size_t)gridDim.x * H * row_bytes);
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int row = tid_here() + kThreads * i;
-            const bool v = valid && hasD() && row < H;
-            const uint32_t base = ((uint32_t)b * (uint32_t)H + (uint32_t)row) * row_bytes;
-#pragma unroll
-            for (int u = 0; u < UP; ++u) {
-                const uint32_t off = v && (uint32_t)u * 16u < row_bytes ? base + (uint32_t)u * 16u : kNoRead;
-                wP[i][u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
-            }
-        }
-    };
-
-    // Layer 0's inputs need the token: the embedding row (spare wave of QKV
-    // blocks, into LDS) and the residual element (compute waves of o/down
-    // blocks).
-    float h_own = 0.f, emb_r = 0.f;
-    auto fetch_embed = [&](int tok) {
-        if (spare && hasA()) dma_bytes(lds + A()->lds_emb, A()->embed + (size_t)tok * A()->H, A()->H * 2);
-        if (myH()) emb_r = ldc_bf16(A()->embed, (long)tok * A()->H + rowH());
+    // Optional per-phase timestamps of one step (thread 0 of each block).
+    auto mark = [&](int step, int ev) {
+        if (A()->trace && step == A()->trace_step && tid_here() == 0)
+            st_u64(A()->trace + (size_t)b * (16 * A()->L + 3) + ev, wall_clock64());
     };
     // A phase's normed input: every wave computes the scale itself (same
     // order, same value) and stages its share of xs.
-    auto stage_norm = [&](const void *src, bool bf16_src) {
-        const uint16_t *g = (const uint16_t *)(lds + A()->lds_gain);
+    auto stage_norm = [&](const void *src, bool bf16_src, int gain_off) {
+        const uint16_t *g = (const uint16_t *)(lds + gain_off);
         float *xs = (float *)(lds + A()->lds_xs);
         const int H = A()->H;
         if (bf16_src) block_stage<true>(xs, src, H, g, wave_norm_scale<true>(src, H, A()->eps));
         else block_stage<false>(xs, src, H, g, wave_norm_scale<false>(src, H, A()->eps));
     };
+    auto tag_base = [&](int s) { return A()->tag0 + (unsigned)(s * fused_phases_per_step(A()->L)); };
 
-    int token = __builtin_amdgcn_readfirstlane(__hip_atomic_load(A()->step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    long pos = __builtin_amdgcn_readfirstlane(__hip_atomic_load(A()->step + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    load_wA(0, true);
-    fetch_embed(token);
-
-    // A block is paced when it waited on the previous step's last layer (or
-    // this is the launch's first step): only then are the cached K/V rows of
-    // every earlier position written when it starts a step. Blocks with no
-    // role in the previous step may run ahead and must not prefetch them.
-    bool item_prev = false;
-    for (int s = 0; s < A()->steps; ++s, ++pos) {
+    // The LM head of step s (BF16, final norm fused) and this block's argmax
+    // partial (key, index), by step parity.
+    auto lm_head = [&](int s) {
         const int L = A()->L;
-        // Optional per-phase timestamps of one step (thread 0 of each block).
-        const bool traced = A()->trace && s == A()->trace_step;
-        auto mark = [&](int ev) {
-            if (traced && tid_here() == 0) st_u64(A()->trace + (size_t)b * (16 * A()->L + 3) + ev, wall_clock64());
-        };
-        const unsigned tb0 = A()->tag0 + (unsigned)(s * fused_phases_per_step(L));
-        // This block's attention item: KV head ig, positions [kv_start, kv_end).
-        const long ctx = pos + 1;
-        constexpr int IP = item_positions(ROW);
-        const int S = (int)((ctx + IP - 1) / IP);
-        // With HS every q head of a group is an item of its own:
-        // it = (ig * S + isplit) * G + ih; otherwise it = ig * S + isplit.
-        const int it = (int)gridDim.x - 1 - b;
-        const bool hasB = it < A()->kv_heads * S * (G / GI);
-        const int ih = HS ? it % G : 0;
-        int ig = 0, isplit = HS ? it / G : it;  // by subtraction (scalar)
-        while (hasB && isplit >= S) {
-            isplit -= S;
-            ++ig;
-        }
-        const bool paced = s == 0 || hasA() || hasH() || hasD() || hasHead() || item_prev;
-        item_prev = hasB;
-        const long kv_start = (long)isplit * IP;
-        const long kv_end = min(kv_start + IP, ctx);
-        const long kv_lim = min(kv_end, pos);  // cached rows; the new one comes tagged
-        const int nv = (int)(kv_end - kv_start);
-
-        for (int l = 0; l < L; ++l) {
-            const bool more = l + 1 < L;
-            const int ln = more ? l + 1 : l;
-            const unsigned tA = tb0 + 5 * l, tB = tA + 1, tC = tA + 2, tD = tA + 3, tE = tA + 4;
-            mark(16 * l);
-            uint8_t *k_lds = lds + A()->lds_kv, *v_lds = k_lds + IP * ROW;
-            float *xs = (float *)(lds + A()->lds_xs);
-
-            // The attention item's cached rows start loading at once (spare
-            // wave: no weight rows in flight).
-            const bool kv_early = hasB && (l > 0 || paced);
-            if (spare && kv_early) load_kv_lds<HD, KT>(kargs, k_lds, v_lds, l, ig, kv_start, kv_lim);
-
-            // ---- A: QKV pairs + RoPE + K/V append. Everything a pair's
-            // epilogue reads besides its dot (row scale and bias, rotation
-            // factors, page, destinations) is loaded before the input poll:
-            // the chain of dependent scalar loads (layer table, pointer,
-            // value) would otherwise follow the dot on the critical path.
-            bool a_sc = false, a_bias = false, a_rope = false;
-            float a_s0 = 0.f, a_s1 = 0.f, a_b0 = 0.f, a_b1 = 0.f, a_c = 0.f, a_sn = 0.f;
-            int a_i0 = 0, a_i1 = 0, a_c0 = -1, a_c1 = -1;  // q/K/V word, cache element (bit 30: V)
-            if (myA()) {
-                const int r0 = 2 * pairA();
-                if (const float *sc = LY(l)->qkv_sc) {
-                    a_sc = true;
-                    a_s0 = ldc(sc, r0);
-                    a_s1 = ldc(sc, r0 + 1);
-                }
-                if (const float *bias = LY(l)->qkv_bias) {
-                    a_bias = true;
-                    a_b0 = ldc(bias, r0);
-                    a_b1 = ldc(bias, r0 + 1);
-                }
-                const int qd = A()->q_heads * HD, kvd = A()->kv_heads * HD, kvh = A()->kv_heads;
-                const int rot = A()->rotary, half = rot / 2;
-                const int page = ldc(A()->page_table, pos / TP), slot = (int)(pos % TP);
-                if (r0 < qd + kvd) {
-                    const bool is_q = r0 < qd;
-                    const int base = is_q ? r0 : r0 - qd;
-                    const int h = base / HD, d0 = base % HD;
-                    int o0 = d0, o1 = d0 + 1;
-                    if (d0 < rot) {
-                        const int i = d0 / 2;
-                        a_rope = true;
-                        a_c = ldc(A()->rope_cos, pos * half + i);
-                        a_sn = ldc(A()->rope_sin, pos * half + i);
-                        o0 = i;
-                        o1 = half + i;
-                    }
-                    if (is_q) {
-                        const int q0 = (h / G) * (G + 2) * HD + (h % G) * HD;
-                        a_i0 = q0 + o0;
-                        a_i1 = q0 + o1;
-                    } else {
-                        const int k0 = h * (G + 2) * HD + G * HD;
-                        a_i0 = k0 + o0;
-                        a_i1 = k0 + o1;
-                        const int e0 = ((page * kvh + h) * TP + slot) * HD;
-                        a_c0 = e0 + o0;
-                        a_c1 = e0 + o1;
-                    }
-                } else {
-                    const int base = r0 - qd - kvd;
-                    const int h = base / HD, d0 = base % HD;
-                    const int v0i = h * (G + 2) * HD + (G + 1) * HD;
-                    a_i0 = v0i + d0;
-                    a_i1 = v0i + d0 + 1;
-                    const int e0 = ((page * kvh + h) * TP + slot) * HD;
-                    a_c0 = (e0 + d0) | (1 << 30);
-                    a_c1 = (e0 + d0 + 1) | (1 << 30);
-                }
-                // The values are used here, so their loads complete now,
-                // while the block waits for its input anyway.
-                asm volatile("" : "+v"(a_s0), "+v"(a_s1), "+v"(a_b0), "+v"(a_b1), "+v"(a_c), "+v"(a_sn));
-            }
-            if (hasA()) {
-                if (spare) dma_bytes(lds + A()->lds_gain, LY(l)->ln1, A()->H * 2);
-                if (l > 0) gather(tb, A()->hid1, A()->H, tA - 1, A()->abort_flag);
-                if (spare) wait_vm();
-                bar();
-                if (l == 0) stage_norm(lds + A()->lds_emb, true);
-                else stage_norm(tb, false);
-                bar();
-            }
-            mark(16 * l + 1);
-            if (myA()) {
-                float y[2];
-                dot_rows<FMT>(wA, xs, A()->H / U::E, y);
-                float v0 = y[0], v1 = y[1];
-                if (a_sc) {
-                    v0 = v0 * a_s0;
-                    v1 = v1 * a_s1;
-                }
-                if (a_bias) {
-                    v0 = v0 + a_b0;
-                    v1 = v1 + a_b1;
-                }
-                if (a_rope) {
-                    const float x1 = v0 * a_c - v1 * a_sn, x2 = v1 * a_c + v0 * a_sn;
-                    v0 = x1;
-                    v1 = x2;
-                }
-                if (lane == 0) {
-                    if (a_c0 >= 0) {
-                        KT *cache = (KT *)((a_c0 >> 30) ? LY(l)->vc : LY(l)->kc);
-                        st_kv(cache + (a_c0 & ((1 << 30) - 1)), v0);
-                        st_kv(cache + (a_c1 & ((1 << 30) - 1)), v1);
-                    }
-                    uint64_t *qkvn = A()->qkvn;
-                    stf(qkvn + a_i0, a_c0 >= 0 ? kv_round<KT>(v0) : v0, tA);
-                    stf(qkvn + a_i1, a_c1 >= 0 ? kv_round<KT>(v1) : v1, tA);
-                }
-            }
-            mark(16 * l + 2);
-
-            // ---- B: attention item.
-            if (hasB) {
-                gather(tb, A()->qkvn + (size_t)ig * (G + 2) * HD, (G + 2) * HD, tA, A()->abort_flag);
-                if (!kv_early) {
-                    // Not paced: the cached rows are read only once the
-                    // block holds q (whose tags prove every earlier position
-                    // of this layer written); the spare wave owns no chunk of
-                    // the gather, so it waits at a barrier first.
-                    bar();
-                    if (spare) load_kv_lds<HD, KT>(kargs, k_lds, v_lds, l, ig, kv_start, kv_lim);
-                }
-                if (spare) wait_vm();
-                bar();
-                // q (the item's heads) as f32; the new position's K and V rows
-                // as stored in the cache.
-                for (int i = tid_here(); i < GI * HD; i += kThreads) xs[i] = val_of(tb[ih * HD + i]);
-                if (kv_end == ctx)
-                    for (int i = tid_here(); i < 2 * HD; i += kThreads) {
-                        const float v = val_of(tb[G * HD + i]);
-                        KT *row = (KT *)((i < HD ? k_lds : v_lds) + (size_t)(nv - 1) * ROW);
-                        if constexpr (sizeof(KT) == 2) row[i % HD] = f32_bf16_rne(v);
-                        else row[i % HD] = v;
-                    }
-                bar();
-                mark(16 * l + 3);
-                uint64_t *tr = traced ? A()->trace + (size_t)b * (16 * A()->L + 3) + 16 * l + 3 : nullptr;
-                attn_compute<HD, GI, KT>(
-                    xs, k_lds, v_lds, nv, ash,
-                    A()->part + ((size_t)isplit * A()->q_heads + (size_t)ig * G + ih) * (HD + 2), tB, tr);
-            }
-            // Attention blocks issue these after their item: rows in flight
-            // would hold back the item's q poll.
-            load_wC(l, true);
-            load_wD(l, true);
-            load_wP(l, true);
-            mark(16 * l + 7);
-
-            // ---- C: partials merged in split order (weights exp(m_s - M),
-            // sum L = sum_s w_s l_s), o_proj + residual. Wave w merges q
-            // heads w, w + 8, ...: lane s holds split s's max and sum, lanes
-            // hold head dimensions for the weighted sum.
-            if (hasH()) {
-                const int Q = A()->q_heads;
-                gather(tb, A()->part, S * Q * (HD + 2), tB, A()->abort_flag);
-                bar();
-                for (int h = wave; h < Q; h += kWaves) {
-                    const uint64_t *ph = tb + (size_t)h * (HD + 2);
-                    const size_t stride = (size_t)Q * (HD + 2);
-                    const float ms = lane < S ? val_of(ph[lane * stride + HD]) : -INFINITY;
-                    const float M = wave_max(ms);
-                    const float ws = lane < S ? expf(ms - M) : 0.f;
-                    const float lsum = lane < S ? val_of(ph[lane * stride + HD + 1]) : 0.f;
-                    float Ls = 0.f;
-                    for (int s2 = 0; s2 < S; ++s2) Ls = fmaf(lane_read(ws, s2), lane_read(lsum, s2), Ls);
-                    const float linv = 1.0f / Ls;
-#pragma unroll
-                    for (int e = 0; e < HD / 64; ++e) {
-                        const int d = lane + 64 * e;
-                        float o = 0.f;
-                        for (int s2 = 0; s2 < S; ++s2) o = fmaf(lane_read(ws, s2), val_of(ph[s2 * stride + d]), o);
-                        xs[xpad(h * HD + d)] = o * linv;
-                    }
-                }
-                bar();
-            }
-            mark(16 * l + 8);
-            if (myH()) {
-                const int r = rowH();
-                float y[1];
-                dot_rows<FMT>(wC, xs, A()->q_heads * HD / U::E, y);
-                mark(16 * l + 14);
-                float v = y[0];
-                if (const float *sc = LY(l)->o_sc) v = v * ldc(sc, r);
-                if (const float *bias = LY(l)->o_bias) v = v + ldc(bias, r);
-                const float old = l == 0 ? emb_r : h_own;
-                h_own = old + v;
-                if (lane == 0) sm.out[wave] = h_own;
-            }
-            // The block's rows leave as one coalesced run (one writer per
-            // line instead of one per wave).
-            if (hasH()) {
-                bar();
-                const int cnt = min(kCW, A()->H - b * kCW);
-                if (wave == 0 && lane < cnt) stf(A()->hid0 + b * kCW + lane, sm.out[lane], tC);
-            }
-            mark(16 * l + 9);
-
-            // ---- D: gate/up + SwiGLU.
-            if (hasD()) {
-                if (spare) dma_bytes(lds + A()->lds_gain, LY(l)->ln2, A()->H * 2);
-                gather(tb, A()->hid0, A()->H, tC, A()->abort_flag);
-                if (spare) wait_vm();
-                bar();
-                stage_norm(tb, false);
-                bar();
-            }
-            mark(16 * l + 10);
-            {
-                const int n = nrD();
-                if (n > 0) {
-                    float y[2 * RGU];
-                    dot_rows<FMT>(wD, xs, A()->H / U::E, y);
-                    const int base = b * A()->rb + wave;
-#pragma unroll
-                    for (int k = 0; k < RGU; ++k)
-                        if (k < n) {
-                            const int r = base + kWaves * k;
-                            float gv = y[2 * k], uv = y[2 * k + 1];
-                            if (const float *gs = LY(l)->gate_sc) {
-                                gv = gv * ldc(gs, r);
-                                uv = uv * ldc(LY(l)->up_sc, r);
-                            }
-                            if (lane == 0) sm.out[r - b * A()->rb] = gv * (uv / (1.0f + expf(-gv)));
-                        }
-                }
-                // Zeros after the block's outputs, up to the padded row.
-                {
-                    const int cnt = hasD() ? min(A()->rb, A()->I - b * A()->rb) : 0;
-                    if (tid_here() >= cnt && tid_here() < UP * 8) sm.out[tid_here()] = 0.f;
-                }
-            }
-            // The block's down partials: thread q's output rows r = q, q + 512
-            // sum down[r][b rb + j] * act_j over the block's gate/up rows j
-            // in order (padding columns and outputs are zero). Every block
-            // runs the multiply-adds, so every path consumes the loaded rows
-            // (pinned here: the compiler then waits for them once, up front).
-            if (hasD()) bar();
-            pin(wP);
-            {
-                const int cnt = hasD() ? min(A()->rb, A()->I - b * A()->rb) : 0;
-                float acc[2] = {0.f, 0.f};
-#pragma unroll
-                for (int u = 0; u < UP; ++u) {
-                    float av[8];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) av[e] = sm.out[8 * u + e];
-#pragma unroll
-                    for (int i = 0; i < 2; ++i) {
-                        const uint32_t raw[4] = {wP[i][u][0], wP[i][u][1], wP[i][u][2], wP[i][u][3]};
-                        U::decode(raw, [&](int e, float v) { acc[i] = fmaf(v, av[e], acc[i]); });
-                    }
-                }
-                // Rows up to 7 nhb (the last o/down block's group is whole;
-                // rows past H carry zeros).
-                if (cnt > 0) {
-                    const int rows = A()->nhb * kCW, nbd = A()->nbd;
-#pragma unroll
-                    for (int i = 0; i < 2; ++i) {
-                        const int row = tid_here() + kThreads * i;
-                        if (row < rows) stf(A()->pdown + ((size_t)(row / kCW) * nbd + b) * kCW + row % kCW, acc[i], tD);
-                    }
-                }
-            }
-            load_wA(ln, more);
-            mark(16 * l + 11);
-
-            // ---- E: the down partials of this block's rows summed in block
-            // order (lane j adds blocks j, j + 64, ...; then the fixed wave
-            // tree), + residual. (BF16 weights only: no row scale.)
-            uint64_t *hid1 = A()->hid1;
-            if (hasH()) {
-                const int nbd = A()->nbd;
-                gather(tb, A()->pdown + (size_t)b * nbd * kCW, nbd * kCW, tD, A()->abort_flag);
-                bar();
-            }
-            mark(16 * l + 12);
-            if (myH()) {
-                const int nbd = A()->nbd;
-                float v = 0.f;
-                for (int j = lane; j < nbd; j += 64) v += val_of(tb[j * kCW + wave]);
-                v = wave_sum(v);
-                mark(16 * l + 15);
-                h_own = h_own + v;
-                if (lane == 0) sm.out[wave] = h_own;
-            }
-            if (hasH()) {
-                bar();
-                const int cnt = min(kCW, A()->H - b * kCW);
-                if (wave == 0 && lane < cnt) stf(hid1 + b * kCW + lane, sm.out[lane], tE);
-            }
-            mark(16 * l + 13);
-        }
-
-        // ---- LM head (BF16, final norm fused) + argmax partials. The weight
-        // registers hold the last layer's no-op prefetches; pinned across the
-        // head, its row buffers live elsewhere, and no path from a head load
-        // reaches a layer's use of a weight register.
-        pin(wA);
-        pin(wC);
-        pin(wD);
-        pin(wP);
-        const unsigned tH = tb0 + 5 * L;
+        const unsigned tH = tag_base(s) + 5 * L;
         int key = INT_MIN;
         uint32_t idx = 0;
         if (hasHead()) {
-            if (spare) dma_bytes(lds + A()->lds_gain, A()->final_norm, A()->H * 2);
+            if (wave == kDmaWave) dma_bytes(lds + A()->lds_g2, A()->final_norm, A()->H * 2);
             gather(tb, A()->hid1, A()->H, tH - 1, A()->abort_flag);
-            if (spare) wait_vm();
+            wait_vm();
             bar();
-            stage_norm(tb, false);
+            stage_norm(tb, false, A()->lds_g2);
             bar();
-            mark(16 * L);
-            const int W = (int)gridDim.x * kWaves, gw0 = b * kWaves + wave, V = A()->V;
-            const int head_rows = gw0 < V ? (V - 1 - gw0) / W + 1 : 0;
-            head_dots<UHB>(A()->head, A()->logits, (const float *)(lds + A()->lds_xs), A()->H, V, gw0, W, head_rows,
+            mark(s, 16 * L);
+            const int Wn = (int)gridDim.x * kWaves, gw0 = b * kWaves + wave, V = A()->V;
+            const int head_rows = gw0 < V ? (V - 1 - gw0) / Wn + 1 : 0;
+            head_dots<UHB>(A()->head, A()->logits, (const float *)(lds + A()->lds_xs), A()->H, V, gw0, Wn, head_rows,
                            key, idx);
         }
         block_best(key, idx, sm);
-        pin(wA);
-        pin(wC);
-        pin(wD);
-        pin(wP);
-        mark(16 * L + 1);
+        mark(s, 16 * L + 1);
         uint64_t *am = A()->am + (size_t)(s & 1) * gridDim.x * 2;
         if (hasHead() && tid_here() == 0) {
             stt(am + 2 * b, (uint32_t)key, tH);
             stt(am + 2 * b + 1, idx, tH);
         }
-        const bool next = s + 1 < A()->steps;
-        load_wA(0, next);
-        // Blocks that use the token (embedding row, residual) reduce the
-        // partials of every head block. A partial that never arrived (the
-        // poll gave up) still holds a valid row index.
-        if (hasA() || hasH()) {
-            const int head_blocks = A()->head_blocks;
-            gather(tb, am, 2 * head_blocks, tH, A()->abort_flag);
-            bar();
-            if (wave == 0) {
-                key = INT_MIN;
-                idx = 0;
-                for (int i = lane; i < head_blocks; i += 64)
-                    better(key, idx, (int)(uint32_t)tb[2 * i], (uint32_t)tb[2 * i + 1]);
-                wave_best(key, idx);
-                // A row index outside the vocabulary can only come from a
-                // poll that gave up; the token then keeps its last value.
-                if (lane == 0) sm.token = idx < (uint32_t)A()->V ? (int)idx : token;
-            }
-            bar();
-            token = __builtin_amdgcn_readfirstlane(sm.token);
-            if (b == 0 && tid_here() == 0) {
-                if (pos + 1 < A()->hist_cap) st_u32(A()->hist + pos + 1, (uint32_t)token);
-                st_u32(A()->step, (uint32_t)token);
-                st_u32(A()->step + 1, (uint32_t)(pos + 1));
-            }
-            if (next) fetch_embed(token);
+    };
+    // Blocks that use the token (embedding row, residual) reduce step s's
+    // argmax partials of every head block into the token at position
+    // pos + 1 (block 0 records it). A partial that never arrived (the poll
+    // gave up) still holds a valid row index; the token then keeps its last
+    // value.
+    auto reduce_token = [&](int s, long pos, int token) {
+        const int head_blocks = A()->head_blocks;
+        uint64_t *am = A()->am + (size_t)(s & 1) * gridDim.x * 2;
+        gather(tb, am, 2 * head_blocks, tag_base(s) + 5 * A()->L, A()->abort_flag);
+        bar();
+        if (wave == 0) {
+            int key = INT_MIN;
+            uint32_t idx = 0;
+            for (int i = lane_here(); i < head_blocks; i += 64)
+                better(key, idx, (int)(uint32_t)tb[2 * i], (uint32_t)tb[2 * i + 1]);
+            wave_best(key, idx);
+            if (lane_here() == 0) sm.token = idx < (uint32_t)A()->V ? (int)idx : token;
         }
-        mark(16 * L + 2);
+        bar();
+        token = __builtin_amdgcn_readfirstlane(sm.token);
+        if (b == 0 && tid_here() == 0) {
+            if (pos + 1 < A()->hist_cap) st_u32(A()->hist + pos + 1, (uint32_t)token);
+            st_u32(A()->step, (uint32_t)token);
+            st_u32(A()->step + 1, (uint32_t)(pos + 1));
+        }
+        mark(s, 16 * A()->L + 2);
+        return token;
+    };
+
+    int token = __builtin_amdgcn_readfirstlane(__hip_atomic_load(A()->step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    const long pos0 =
+        __builtin_amdgcn_readfirstlane(__hip_atomic_load(A()->step + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+
+    if (isItem()) {
+        // ---- Items: one q head over one run of positions. Per layer: the
+        // input (fused RMSNorm), the head's 64 q rows (bias, RoPE), scores
+        // of the run's cached K rows, the new position's K/V row from the
+        // KV blocks (the run that holds it), softmax, weighted V rows, and
+        // the head's o_proj columns applied to the unnormalised output.
+        u32x4 W[NI];
+        // Refill for layer l at position pos: q rows (unit k: row k / UH of
+        // the wave's RQ, lane units), o_proj units (row (k 8 + wave) OW +
+        // lane / UO, unit lane % UO of the head's columns), the input-norm
+        // gains and the run's cached K/V rows (when `act`).
+        auto refill = [&](int l, bool act, long pos) {
+            const int H = A()->H, nH = H / U::E, tid = tid_here(), lane = tid & 63;
+            const uint32_t qs = (uint32_t)A()->qkv_stride, os = (uint32_t)A()->o_stride;
+            const int qrows = (A()->q_heads + 2 * A()->kv_heads) * HD;
+            const Rsrc rq = rsrc(LY(l)->qkv, (size_t)qrows * qs), ro = rsrc(LY(l)->o, (size_t)H * os);
+            const int h = itHead();
+#pragma unroll
+            for (int k = 0; k < NI; ++k) {
+                uint32_t off = kNoRead;
+                if (k < NQ) {
+                    const int unit = lane + 64 * (k % UH), row = h * HD + wave * RQ + k / UH;
+                    if (act && unit < nH) off = (uint32_t)row * qs + (uint32_t)unit * 16u;
+                    W[k] = ld_unit(rq, off);
+                } else {
+                    const int r = ((k - NQ) * kWaves + wave) * OW + lane / UO, u = lane % UO;
+                    if (act && r < H) off = (uint32_t)r * os + (uint32_t)(h * HD + U::E * u) * 2u;
+                    W[k] = ld_unit(ro, off);
+                }
+            }
+            if (act) {
+                if (wave == kDmaWave) dma_bytes(lds + A()->lds_g1, LY(l)->ln1, H * 2);
+                const int ip = A()->ip;
+                const long start = (long)itSplit() * ip, lim = min(start + ip, pos);
+                uint8_t *k_lds = lds + A()->lds_kv;
+                load_kv_lds<HD, KT>(kargs, k_lds, k_lds + ip * ROW, l, itHead() / G, start, lim);
+            }
+        };
+        long pos = pos0;
+        for (int s = 0;; ++s) {
+            const bool run = s < A()->steps;
+            const int L = A()->L, ip = A()->ip;
+            const long ctx = pos + 1;
+            const int S = (int)((ctx + ip - 1) / ip);
+            // This block's run: q head ih, positions [kv_start, kv_end); rows
+            // below nc are cached, the new one comes tagged.
+            const bool active = run && itSplit() < S;
+            const int ih = itHead();
+            const long kv_start = (long)itSplit() * ip, kv_end = min(kv_start + ip, ctx);
+            const int nc = active ? (int)(min(kv_end, pos) - kv_start) : 0;
+            const bool has_new = active && kv_end == ctx;
+            const unsigned tb0 = tag_base(s);
+            refill(0, active, pos);
+            if (s > 0) token = reduce_token(s - 1, pos - 1, token);
+            if (!run) break;
+            if (wave == kDmaWave) dma_bytes(lds + A()->lds_emb, A()->embed + (size_t)token * A()->H, A()->H * 2);
+            for (int l = 0; l < L; ++l) {
+                const unsigned tK = tb0 + 5 * l, tP = tK + 1;
+                mark(s, 16 * l);
+                if (active) {
+                    float *xs = (float *)(lds + A()->lds_xs);
+                    float *qs = (float *)(lds + A()->lds_q);  // q[hd], bias[hd], cos[hd / 2], sin[hd / 2]
+                    uint8_t *k_lds = lds + A()->lds_kv, *v_lds = k_lds + ip * ROW;
+                    const int H = A()->H, nH = H / U::E, rot = A()->rotary, half = rot / 2;
+                    // q's biases (rows of head ih, pair-permuted like the
+                    // rows) and rotation factors, loaded before the poll.
+                    const float *qbias = LY(l)->qkv_bias;
+                    {
+                        const int tid = tid_here();
+                        if (tid < HD) {
+                            qs[HD + tid] = qbias ? qbias[ih * HD + tid] : 0.f;
+                        } else if (tid < HD + half) {
+                            const int i = tid - HD;
+                            qs[2 * HD + i] = A()->rope_cos[pos * half + i];
+                            qs[2 * HD + HD / 2 + i] = A()->rope_sin[pos * half + i];
+                        }
+                    }
+                    if (l > 0) gather(tb, A()->hid1, H, tK - 1, A()->abort_flag);
+                    wait_vm();  // the embedding row, the gains and the K/V rows
+                    bar();
+                    if (l == 0) stage_norm(lds + A()->lds_emb, true, A()->lds_g1);
+                    else stage_norm(tb, false, A()->lds_g1);
+                    bar();
+                    mark(s, 16 * l + 1);
+                    {
+                        float y[RQ];
+                        dot_pool<RQ, UH, 0>(W, xs, nH, y);
+                        // Lane j < RQ / 2 finishes rotation pair j of the
+                        // wave's rows (bias, RoPE).
+                        const int ln = lane_here();
+                        float v0 = y[0], v1 = y[1];
+#pragma unroll
+                        for (int j = 1; j < RQ / 2; ++j)
+                            if (ln == j) {
+                                v0 = y[2 * j];
+                                v1 = y[2 * j + 1];
+                            }
+                        if (ln < RQ / 2) {
+                            const int d0 = wave * RQ + 2 * ln;
+                            if (qbias) {
+                                v0 = v0 + qs[HD + d0];
+                                v1 = v1 + qs[HD + d0 + 1];
+                            }
+                            if (d0 < rot) {
+                                const int i = d0 / 2;
+                                const float c = qs[2 * HD + i], sn = qs[2 * HD + HD / 2 + i];
+                                qs[i] = v0 * c - v1 * sn;
+                                qs[half + i] = v1 * c + v0 * sn;
+                            } else {
+                                qs[d0] = v0;
+                                qs[d0 + 1] = v1;
+                            }
+                        }
+                    }
+                    bar();
+                    mark(s, 16 * l + 2);
+                    item_scores<HD, KT>(qs, k_lds, 0, nc, ish.p);
+                    mark(s, 16 * l + 3);
+                    if (has_new) {
+                        // The new position's K and V rows as stored in the cache.
+                        gather(tb, A()->kvw + (size_t)(ih / G) * 2 * HD, 2 * HD, tK, A()->abort_flag);
+                        bar();
+                        for (int i = tid_here(); i < 2 * HD; i += kThreads) {
+                            const float v = val_of(tb[i]);
+                            KT *rowp = (KT *)((i < HD ? k_lds : v_lds) + (size_t)nc * ROW);
+                            if constexpr (sizeof(KT) == 2) rowp[i % HD] = f32_bf16_rne(v);
+                            else rowp[i % HD] = v;
+                        }
+                        bar();
+                        item_scores<HD, KT>(qs, k_lds, nc, nc + 1, ish.p);
+                    }
+                    bar();
+                    mark(s, 16 * l + 4);
+                    item_softmax_pv<HD, KT>(v_lds, nc + (has_new ? 1 : 0), ish);
+                    mark(s, 16 * l + 5);
+                    // o_proj columns of head ih times the unnormalised output:
+                    // UO lanes per row, one unit each (elements in order),
+                    // summed over the row's lanes by a fixed tree; all rows
+                    // first, then the stores. Partial of owner r / 8, item b;
+                    // the run's max and sum once.
+                    {
+                        const int ln = lane_here();
+                        float ov[U::E], po[NWO];
+#pragma unroll
+                        for (int e = 0; e < U::E; ++e) ov[e] = ish.o[(ln % UO) * U::E + e];
+#pragma unroll
+                        for (int k = 0; k < NWO; ++k) {
+                            const u32x4 w = W[NQ + k];
+                            const uint32_t raw[4] = {w[0], w[1], w[2], w[3]};
+                            float acc = 0.f;
+                            U::decode(raw, [&](int e, float x) { acc = fmaf(x, ov[e], acc); });
+                            po[k] = group_sum<UO>(acc);
+                        }
+                        const int ni = A()->ni;
+                        uint64_t *part = A()->part;
+                        store_rows<NWO, OW, UO>(po, sm.scr[wave], wave, H, tP, [&](int r) {
+                            return part + ((size_t)(r / kOwn) * ni + b) * kOwn + r % kOwn;
+                        });
+                        if (tid_here() == 0) stf2(A()->ml + 2 * b, ish.m, ish.l, tP);
+                    }
+                    bar();
+                    mark(s, 16 * l + 6);
+                }
+                if (l + 1 < L) refill(l + 1, active, pos);
+            }
+            lm_head(s);
+            ++pos;
+        }
+    } else if (isKV()) {
+        // ---- KV blocks: the new position's K and V rows (fused RMSNorm,
+        // bias, RoPE), appended to the pages and handed to the items.
+        u32x4 W[NK];
+        auto refill = [&](int l, bool act) {
+            const int H = A()->H, nH = H / U::E, lane = lane_here();
+            const int qd = A()->q_heads * HD, kvd = A()->kv_heads * HD;
+            const uint32_t qs = (uint32_t)A()->qkv_stride;
+            const Rsrc rq = rsrc(LY(l)->qkv, (size_t)(qd + 2 * kvd) * qs);
+            const int p = kvPair();
+#pragma unroll
+            for (int k = 0; k < NK; ++k) {
+                const int unit = lane + 64 * (k % UH);
+                const bool v = act && p < kvd && unit < nH;
+                W[k] = ld_unit(rq, v ? (uint32_t)(qd + 2 * p + k / UH) * qs + (uint32_t)unit * 16u : kNoRead);
+            }
+            if (act && wave == kDmaWave) dma_bytes(lds + A()->lds_g1, LY(l)->ln1, H * 2);
+        };
+        long pos = pos0;
+        for (int s = 0;; ++s) {
+            const bool run = s < A()->steps;
+            const int L = A()->L;
+            const unsigned tb0 = tag_base(s);
+            refill(0, run);
+            if (s > 0) token = reduce_token(s - 1, pos - 1, token);
+            if (!run) break;
+            if (wave == kDmaWave) dma_bytes(lds + A()->lds_emb, A()->embed + (size_t)token * A()->H, A()->H * 2);
+            for (int l = 0; l < L; ++l) {
+                const unsigned tK = tb0 + 5 * l;
+                mark(s, 16 * l);
+                const int H = A()->H, nH = H / U::E, rot = A()->rotary, half = rot / 2;
+                const bool myKV = kvPair() < A()->kv_heads * HD;
+                // Everything the epilogue reads besides the dot (biases,
+                // rotation factors, page, destinations) is loaded before the
+                // input poll.
+                bool k_bias = false, k_rope = false;
+                float k_b0 = 0.f, k_b1 = 0.f, k_c = 0.f, k_sn = 0.f;
+                int k_i0 = 0, k_i1 = 0, k_c0 = 0, k_c1 = 0;  // K/V word, cache element (bit 30: V)
+                KT *cache = nullptr;
+                if (myKV) {
+                    const int qd = A()->q_heads * HD, kvd = A()->kv_heads * HD, kvh = A()->kv_heads;
+                    const int r0 = qd + 2 * kvPair();
+                    if (const float *bias = LY(l)->qkv_bias) {
+                        k_bias = true;
+                        k_b0 = ldc(bias, r0);
+                        k_b1 = ldc(bias, r0 + 1);
+                    }
+                    const int page = ldc(A()->page_table, pos / TP), slot = (int)(pos % TP);
+                    if (r0 < qd + kvd) {
+                        const int base = r0 - qd, hh = base / HD, d0 = base % HD;
+                        int o0 = d0, o1 = d0 + 1;
+                        if (d0 < rot) {
+                            const int i = d0 / 2;
+                            k_rope = true;
+                            k_c = ldc(A()->rope_cos, pos * half + i);
+                            k_sn = ldc(A()->rope_sin, pos * half + i);
+                            o0 = i;
+                            o1 = half + i;
+                        }
+                        k_i0 = hh * 2 * HD + o0;
+                        k_i1 = hh * 2 * HD + o1;
+                        const int e0 = ((page * kvh + hh) * TP + slot) * HD;
+                        k_c0 = e0 + o0;
+                        k_c1 = e0 + o1;
+                    } else {
+                        const int base = r0 - qd - kvd, hh = base / HD, d0 = base % HD;
+                        k_i0 = hh * 2 * HD + HD + d0;
+                        k_i1 = k_i0 + 1;
+                        const int e0 = ((page * kvh + hh) * TP + slot) * HD;
+                        k_c0 = (e0 + d0) | (1 << 30);
+                        k_c1 = (e0 + d0 + 1) | (1 << 30);
+                    }
+                    cache = (KT *)((k_c0 >> 30) ? LY(l)->vc : LY(l)->kc);
+                    asm volatile("" : "+v"(k_b0), "+v"(k_b1), "+v"(k_c), "+v"(k_sn));
+                }
+                if (l > 0) gather(tb, A()->hid1, H, tK - 1, A()->abort_flag);
+                wait_vm();  // the embedding row and the gains
+                bar();
+                if (l == 0) stage_norm(lds + A()->lds_emb, true, A()->lds_g1);
+                else stage_norm(tb, false, A()->lds_g1);
+                bar();
+                mark(s, 16 * l + 1);
+                {
+                    float y[2];
+                    dot_pool<2, UH, 0>(W, (const float *)(lds + A()->lds_xs), nH, y);
+                    float v0 = y[0], v1 = y[1];
+                    if (k_bias) {
+                        v0 = v0 + k_b0;
+                        v1 = v1 + k_b1;
+                    }
+                    if (k_rope) {
+                        const float x1 = v0 * k_c - v1 * k_sn, x2 = v1 * k_c + v0 * k_sn;
+                        v0 = x1;
+                        v1 = x2;
+                    }
+                    if (myKV && lane_here() == 0) {
+                        st_kv(cache + (k_c0 & ((1 << 30) - 1)), v0);
+                        st_kv(cache + (k_c1 & ((1 << 30) - 1)), v1);
+                        uint64_t *kvw = A()->kvw;
+                        stf(kvw + k_i0, kv_round<KT>(v0), tK);
+                        stf(kvw + k_i1, kv_round<KT>(v1), tK);
+                    }
+                }
+                mark(s, 16 * l + 6);
+                if (l + 1 < L) refill(l + 1, true);
+            }
+            lm_head(s);
+            ++pos;
+        }
+    } else {
+        // ---- FFN blocks (and blocks with no role, which only join the LM
+        // head). Per layer: owners merge every head's runs and add the
+        // residual; blocks with gate/up rows run gate/up (fused RMSNorm),
+        // SwiGLU and their down columns; owners sum the down partials and
+        // add the residual.
+        u32x4 W[NF];
+        // Refill for layer l: gate rows (unit k: row w + 8 (k / UH)), up rows,
+        // down_cols units (row (k 8 + wave) DW + lane / UP, unit lane % UP),
+        // and the gains of the FFN norm.
+        auto refill = [&](int l, bool act) {
+            const int H = A()->H, nH = H / U::E, lane = lane_here();
+            const uint32_t gs = (uint32_t)A()->gu_stride;
+            const int rb = A()->rb, rp = A()->rp, f = fIdx(), I = A()->I;
+            const Rsrc rg = rsrc(LY(l)->gate, (size_t)I * gs), ru = rsrc(LY(l)->up, (size_t)I * gs);
+            const Rsrc rd = rsrc(LY(l)->down_cols, (size_t)A()->nf * H * rp * 2);
+#pragma unroll
+            for (int k = 0; k < NF; ++k) {
+                uint32_t off = kNoRead;
+                if (k < 2 * NG) {
+                    const int jj = wave + kWaves * ((k % NG) / UH), unit = lane + 64 * (k % UH), row = f * rb + jj;
+                    if (act && jj < rb && row < I && unit < nH) off = (uint32_t)row * gs + (uint32_t)unit * 16u;
+                    W[k] = ld_unit(k < NG ? rg : ru, off);
+                } else {
+                    const int r = ((k - 2 * NG) * kWaves + wave) * DW + lane / UP, u = lane % UP;
+                    if (act && r < H && u * 16 < rp * 2)
+                        off = ((uint32_t)(f * H + r) * (uint32_t)rp) * 2u + (uint32_t)u * 16u;
+                    W[k] = ld_unit(rd, off);
+                }
+            }
+            if (act && wave == kDmaWave) dma_bytes(lds + A()->lds_g2, LY(l)->ln2, H * 2);
+        };
+        long pos = pos0;
+        float h_own = 0.f, emb_r = 0.f;
+        for (int s = 0;; ++s) {
+            const bool run = s < A()->steps;
+            const int L = A()->L, ip = A()->ip;
+            const int S = (int)((pos + ip) / ip);  // ceil((pos + 1) / ip)
+            const unsigned tb0 = tag_base(s);
+            if (s > 0 && isOwner()) token = reduce_token(s - 1, pos - 1, token);
+            if (!run) break;
+            if (isOwner() && ownRow() < A()->H) emb_r = ldc_bf16(A()->embed, (long)token * A()->H + ownRow());
+            for (int l = 0; l < L; ++l) {
+                const unsigned tK = tb0 + 5 * l, tP = tK + 1, tC = tK + 2, tD = tK + 3, tE = tK + 4;
+                const int H = A()->H, nH = H / U::E;
+                mark(s, 16 * l);
+                refill(l, hasRows());
+                mark(s, 16 * l + 7);
+
+                // ---- Owners: every head's runs merged in split order (lane
+                // h: weights exp(m_s - M), sum L = sum_s w_s l_s), + residual.
+                if (isOwner()) {
+                    const int Q = A()->q_heads, ni = A()->ni, r = ownRow();
+                    // The o_proj bias of the row, loaded before the poll.
+                    const float *ob = LY(l)->o_bias;
+                    const bool has_ob = ob != nullptr && r < H;
+                    float obv = has_ob ? ldc(ob, r) : 0.f;
+                    asm volatile("" : "+v"(obv));
+                    const int na = S * Q * kOwn;
+                    gather(tb, Ranges{A()->part + (size_t)fIdx() * ni * kOwn, A()->ml, na, 2 * S * Q}, tP,
+                           A()->abort_flag);
+                    bar();
+                    mark(s, 16 * l + 8);
+                    // The merge weights once per block (wave 0, lane h):
+                    // w_s = exp(m_s - M) over the head's runs, L = sum_s w_s
+                    // l_s in split order, weight of run s w_s / L.
+                    const int ln = lane_here();
+                    if (wave == 0 && ln < Q) {
+                        const uint64_t *ml = tb + round_up(na, kChunk);
+                        float ms[kMaxSplits], ls[kMaxSplits];
+#pragma unroll
+                        for (int sp = 0; sp < kMaxSplits; ++sp) {
+                            const int it = min(sp, S - 1) * Q + ln;
+                            ms[sp] = sp < S ? val_of(ml[2 * it]) : -INFINITY;
+                            ls[sp] = val_of(ml[2 * it + 1]);
+                        }
+                        float mx = -INFINITY;
+#pragma unroll
+                        for (int sp = 0; sp < kMaxSplits; ++sp) mx = fmaxf(mx, ms[sp]);
+                        float ws[kMaxSplits], Ls = 0.f;
+#pragma unroll
+                        for (int sp = 0; sp < kMaxSplits; ++sp) {
+                            ws[sp] = sp < S ? expf(ms[sp] - mx) : 0.f;
+                            if (sp < S) Ls = fmaf(ws[sp], ls[sp], Ls);
+                        }
+                        const float linv = 1.0f / Ls;
+#pragma unroll
+                        for (int sp = 0; sp < kMaxSplits; ++sp)
+                            if (sp < S) sm.coef[sp * Q + ln] = ws[sp] * linv;
+                    }
+                    bar();
+                    // The row's o_proj value: every run's partial times its
+                    // weight, lane i taking runs i and i + 64, then the fixed
+                    // wave tree.
+                    float contrib = 0.f;
+                    for (int it = ln; it < S * Q; it += 64) contrib = fmaf(sm.coef[it], val_of(tb[it * kOwn + wave]), contrib);
+                    const float o = wave_sum(contrib);
+                    if (r < H) {
+                        float v = o;
+                        if (has_ob) v = v + obv;
+                        h_own = (l == 0 ? emb_r : h_own) + v;
+                        if (lane_here() == 0) sm.out[wave] = h_own;
+                    }
+                    bar();
+                    const int cnt = min(kOwn, H - fIdx() * kOwn);
+                    if (wave == 0 && lane_here() < cnt)
+                        stf(A()->hid0 + fIdx() * kOwn + lane_here(), sm.out[lane_here()], tC);
+                    mark(s, 16 * l + 9);
+                }
+
+                // ---- Gate/up (fused RMSNorm), SwiGLU, down partials of every
+                // hidden row.
+                if (hasRows()) {
+                    float *xs = (float *)(lds + A()->lds_xs);
+                    gather(tb, A()->hid0, H, tC, A()->abort_flag);
+                    wait_vm();  // the gains
+                    bar();
+                    stage_norm(tb, false, A()->lds_g2);
+                    bar();
+                    mark(s, 16 * l + 10);
+                    const int rb = A()->rb, f = fIdx(), I = A()->I;
+                    {
+                        float yg[RGU], yu[RGU];
+                        dot_pool<RGU, UH, 0>(W, xs, nH, yg);
+                        dot_pool<RGU, UH, NG>(W, xs, nH, yu);
+#pragma unroll
+                        for (int j = 0; j < RGU; ++j) {
+                            const int jj = wave + kWaves * j, row = f * rb + jj;
+                            if (jj < rb && row < I && lane_here() == 0) {
+                                const float gv = yg[j], uv = yu[j];
+                                sm.out[jj] = gv * (uv / (1.0f + expf(-gv)));
+                            }
+                        }
+                        // Zeros after the block's outputs, up to the padded row.
+                        const int cnt = min(rb, I - f * rb);
+                        if (tid_here() >= cnt && tid_here() < 8 * UP) sm.out[tid_here()] = 0.f;
+                    }
+                    bar();
+                    mark(s, 16 * l + 11);
+                    // Down partials: UP lanes per row, one unit of the block's
+                    // columns each (elements in order), summed over the row's
+                    // lanes by a fixed tree.
+                    const int nbd = A()->nbd, ln = lane_here();
+                    float av[U::E];
+#pragma unroll
+                    for (int e = 0; e < U::E; ++e) av[e] = sm.out[(ln % UP) * U::E + e];
+                    float pd[ND];
+#pragma unroll
+                    for (int k = 0; k < ND; ++k) {
+                        const u32x4 w = W[2 * NG + k];
+                        const uint32_t raw[4] = {w[0], w[1], w[2], w[3]};
+                        float acc = 0.f;
+                        U::decode(raw, [&](int e, float x) { acc = fmaf(x, av[e], acc); });
+                        pd[k] = group_sum<UP>(acc);
+                    }
+                    uint64_t *pdown = A()->pdown;
+                    store_rows<ND, DW, UP>(pd, sm.scr[wave], wave, H, tD, [&](int r) {
+                        return pdown + ((size_t)(r / kOwn) * nbd + f) * kOwn + r % kOwn;
+                    });
+                    mark(s, 16 * l + 12);
+                }
+
+                // ---- Owners: the down partials of their rows summed in block
+                // order (lane j adds blocks j, j + 64, ...; then the fixed
+                // wave tree), + residual.
+                if (isOwner()) {
+                    const int nbd = A()->nbd;
+                    gather(tb, A()->pdown + (size_t)fIdx() * nbd * kOwn, nbd * kOwn, tD, A()->abort_flag);
+                    bar();
+                    mark(s, 16 * l + 13);
+                    float v = 0.f;
+                    for (int j = lane_here(); j < nbd; j += 64) v += val_of(tb[j * kOwn + wave]);
+                    v = wave_sum(v);
+                    if (ownRow() < H) {
+                        h_own = h_own + v;
+                        if (lane_here() == 0) sm.out[wave] = h_own;
+                    }
+                    bar();
+                    const int cnt = min(kOwn, H - fIdx() * kOwn);
+                    if (wave == 0 && lane_here() < cnt)
+                        stf(A()->hid1 + fIdx() * kOwn + lane_here(), sm.out[lane_here()], tE);
+                    mark(s, 16 * l + 14);
+                }
+            }
+            lm_head(s);
+            ++pos;
+        }
     }
+    // Loads still in flight (refills that read nothing) retire before the
+    // waves end.
+    wait_vm();
 }
 
 struct Variant {
-    int fmt, hd, g, uh, uq, up, rgu, uhb;
+    int hd, g, uh, ro, rgu, up, uhb, nwo;
 };
 
 // Shapes with a built kernel: Qwen2-0.5B (hidden 896, 14/2 heads of 64,
 // intermediate 4864) and the two small test shapes.
 constexpr Variant kVariants[] = {
-    {FMT_BF16, 64, 7, 2, 2, 3, 3, 2},
-    {FMT_BF16, 64, 2, 1, 1, 1, 1, 1},
-    {FMT_BF16, 128, 4, 1, 2, 1, 1, 1},
+    {64, 7, 2, 2, 4, 4, 2, 14},
+    {64, 2, 1, 1, 1, 1, 1, 2},
+    {128, 4, 1, 1, 1, 1, 1, 8},
 };
 
 int units_per_lane(int cols, int elems_per_unit) { return (cols / elems_per_unit + 63) / 64; }
 
-const Variant *find_variant(int fmt, int H, int q_heads, int kv_heads, int hd, int I, int blocks) {
-    if (kv_heads <= 0 || q_heads % kv_heads) return nullptr;
-    const int g = q_heads / kv_heads, E = fmt == FMT_Q8 ? 16 : 8, W = blocks * kCW;
-    const int qd = q_heads * hd, kvd = kv_heads * hd;
-    if (H % 8 || qd % E || H % E || I % E) return nullptr;
-    if (H > kMaxChunks * kChunk || I > kMaxChunks * kChunk) return nullptr;  // one gather each
-    if ((qd + 2 * kvd) / 2 > W || H > W) return nullptr;
+FusedGeom geometry(int H, int q_heads, int kv_heads, int hd, int I, bool kv_f32, int blocks) {
+    FusedGeom g{};
+    g.nf = blocks * 5 / 8;
+    g.f0 = blocks - g.nf;
+    g.nkv = (kv_heads * hd + kWaves - 1) / kWaves;  // one rotation pair of K/V rows per wave
+    g.kv0 = g.f0 - g.nkv;
+    g.s_cap = q_heads > 0 ? std::min(kMaxSplits, g.kv0 / q_heads) : 0;
+    const int row = hd * (kv_f32 ? 4 : 2);
+    g.ip_max = 0;
+    for (int ip = TP; ip <= kIpMax && 2 * ip * row <= kKvLdsMax; ip *= 2) g.ip_max = ip;
+    g.no = H / kOwn;
+    g.rb = g.nf > 0 ? fused_gate_rows(I, g.nf) : 0;
+    g.rp = g.nf > 0 ? fused_gate_rows_padded(I, g.nf) : 0;
+    g.nbd = g.rb > 0 ? (I + g.rb - 1) / g.rb : 0;
+    g.ni_max = q_heads * g.s_cap;
+    return g;
+}
+
+size_t static_lds_bytes(int hd) {
+    return sizeof(Shm) + (hd == 64 ? sizeof(ItemShm<64>) : sizeof(ItemShm<128>));
+}
+
+const Variant *find_variant(int fmt, int H, int q_heads, int kv_heads, int hd, int I, bool kv_f32, int blocks) {
+    if (fmt != FMT_BF16 || kv_heads <= 0 || q_heads % kv_heads || blocks < 64) return nullptr;
+    const int g = q_heads / kv_heads, qd = q_heads * hd;
+    if (H % 8 || qd % 8 || I % 8 || H > 1024 || q_heads > 64) return nullptr;
+    const FusedGeom geo = geometry(H, q_heads, kv_heads, hd, I, kv_f32, blocks);
+    if (geo.s_cap < 1 || geo.ip_max < TP || geo.no > geo.nf || geo.rb > kStage || geo.kv0 < q_heads ||
+        geo.ni_max > kWaveRows)
+        return nullptr;
+    const LdsLayout lay = lds_layout(H, hd, kv_f32 ? 4 : 2, geo.ip_max, geo.ni_max, geo.nbd, blocks);
+    if (lay.tbw > kMaxGather || (size_t)lay.total + static_lds_bytes(hd) > device_max_lds()) return nullptr;
     for (const Variant &v : kVariants) {
-        if (v.fmt != fmt || v.hd != hd || v.g != g) continue;
-        if (units_per_lane(H, E) > v.uh || units_per_lane(qd, E) > v.uq) continue;
-        // One thread per down_cols row pair: 7 ceil(H / 7) <= 2 * 512; UP
-        // units per row.
-        if ((H + kCW - 1) / kCW * kCW > 2 * kThreads || fused_gate_rows_padded(I, blocks) / 8 > v.up) continue;
-        const int rb = (I + blocks - 1) / blocks;
-        if ((rb + kWaves - 1) / kWaves > v.rgu || rb > kStage || units_per_lane(H, 8) > v.uhb) continue;
+        if (v.hd != hd || v.g != g) continue;
+        if (units_per_lane(H, 8) > v.uh || (H + kThreads - 1) / kThreads > v.ro) continue;
+        if ((geo.rb + kWaves - 1) / kWaves > v.rgu || geo.rp / 8 > v.up || units_per_lane(H, 8) > v.uhb) continue;
+        // o_proj units: one per o_proj row of 64 / (hd / 8) rows per wave
+        if ((H + kWaves * 64 / (hd / 8) - 1) / (kWaves * 64 / (hd / 8)) > v.nwo) continue;
         return &v;
     }
     return nullptr;
 }
 
-size_t static_lds_bytes(int hd, int g) {
-    size_t att = 0;
-    if (hd == 64 && g == 7) att = sizeof(AttnShm<64, 7>);
-    else if (hd == 64 && g == 2) att = sizeof(AttnShm<64, 2>);
-    else if (hd == 128 && g == 4) att = sizeof(AttnShm<128, 4>);
-    return sizeof(Shm) + att;
-}
-
-template <int FMT, int HD, int G, class KT, int UH, int UQ, int UP, int RGU, int UHB, bool HS>
+template <int HD, int G, class KT, int UH, int RO, int RGU, int UP, int UHB, int NWO>
 int launch_one(FusedArgs a, int nb, hipStream_t s) {
-    auto k = decode_flow_kernel<FMT, HD, G, KT, UH, UQ, UP, RGU, UHB, HS>;
-    const LdsLayout lay = lds_layout(a.H, a.I, a.q_heads, HD, G, (int)sizeof(KT), nb, a.max_splits);
-    a.lds_xs = lay.xs;
-    a.lds_kv = lay.kv;
-    a.lds_mw = lay.mw;
-    a.lds_emb = lay.emb;
-    a.lds_gain = lay.gain;
-    a.lds_total = lay.total;
-    const int npairs = (a.q_heads + 2 * a.kv_heads) * HD / 2;
-    a.nhb = (a.H + kCW - 1) / kCW;
-    a.nab = (npairs + kCW - 1) / kCW;
-    a.a0 = a.nhb + a.nab <= nb ? a.nhb : nb - a.nab;
-    a.rb = fused_gate_rows(a.I, nb);
-    a.rp = fused_gate_rows_padded(a.I, nb);
-    a.nbd = (a.I + a.rb - 1) / a.rb;
+    auto k = decode_flow_kernel<HD, G, KT, UH, RO, RGU, UP, UHB, NWO>;
+    const FusedGeom geo = geometry(a.H, a.q_heads, a.kv_heads, HD, a.I, sizeof(KT) == 4, nb);
+    // Positions per item: the shortest run that lets the launch's longest
+    // context fit the item blocks.
+    int ip = TP;
+    while (ip < geo.ip_max && (a.ctx_end + ip - 1) / ip > geo.s_cap) ip *= 2;
+    a.splits = (int)((a.ctx_end + ip - 1) / ip);
+    if (a.splits > geo.s_cap) return fail("HIP backend: context too long for the persistent decode kernel.");
+    a.ip = ip;
+    a.ni = a.q_heads * a.splits;
+    a.kv0 = geo.kv0;
+    a.nkv = geo.nkv;
+    a.f0 = geo.f0;
+    a.nf = geo.nf;
+    a.no = geo.no;
+    a.nbd = geo.nbd;
+    a.rb = geo.rb;
+    a.rp = geo.rp;
     a.head_blocks = std::min(nb, (a.V + kWaves - 1) / kWaves);
+    const LdsLayout lay = lds_layout(a.H, HD, (int)sizeof(KT), ip, a.ni, a.nbd, nb);
+    a.lds_xs = lay.xs;
+    a.lds_q = lay.q;
+    a.lds_kv = lay.kv;
+    a.lds_emb = lay.emb;
+    a.lds_g1 = lay.g1;
+    a.lds_g2 = lay.g2;
+    a.lds_total = lay.total;
     const size_t lds = (size_t)lay.total;
     hipFuncAttributes attr{};
     CHIP_CHECK(hipFuncGetAttributes(&attr, (const void *)k));
@@ -1334,41 +1407,31 @@ int launch_one(FusedArgs a, int nb, hipStream_t s) {
     return 0;
 }
 
-template <class KT, bool HS>
+template <class KT>
 int launch_kt(const Variant &v, const FusedArgs &a, int nb, hipStream_t s) {
-    if (v.hd == 64 && v.g == 7) return launch_one<FMT_BF16, 64, 7, KT, 2, 2, 3, 3, 2, HS>(a, nb, s);
-    if (v.hd == 64 && v.g == 2) return launch_one<FMT_BF16, 64, 2, KT, 1, 1, 1, 1, 1, HS>(a, nb, s);
-    if (v.hd == 128 && v.g == 4) return launch_one<FMT_BF16, 128, 4, KT, 1, 2, 1, 1, 1, HS>(a, nb, s);
+    if (v.hd == 64 && v.g == 7) return launch_one<64, 7, KT, 2, 2, 4, 4, 2, 14>(a, nb, s);
+    if (v.hd == 64 && v.g == 2) return launch_one<64, 2, KT, 1, 1, 1, 1, 1, 2>(a, nb, s);
+    if (v.hd == 128 && v.g == 4) return launch_one<128, 4, KT, 1, 1, 1, 1, 1, 8>(a, nb, s);
     return fail("HIP backend: no persistent decode kernel for this shape.");
-}
-
-// Attention items one per (KV head, split, q head) when they all fit the
-// grid at the launch's longest context (CHEETAH_HIP_FUSED_HEAD_SPLIT=0: one
-// per (KV head, split), all q heads of the group).
-bool head_split(const FusedArgs &a, int group, int head_dim, bool kv_f32, int nb) {
-    const char *e = getenv("CHEETAH_HIP_FUSED_HEAD_SPLIT");
-    if (e && e[0] == '0') return false;
-    const long ip = item_positions(head_dim * (kv_f32 ? 4 : 2));
-    const long S = (a.ctx_end + ip - 1) / ip;
-    return group > 1 && (long)a.kv_heads * S * group <= (long)nb;
 }
 
 }  // namespace
 
-int fused_positions_per_item(int head_dim, bool kv_f32) {
-    return item_positions(head_dim * (kv_f32 ? 4 : 2));
-}
-
 bool fused_decode_supported(int fmt, int H, int q_heads, int kv_heads, int head_dim, int I, bool aligned16,
                             int blocks) {
-    return aligned16 && blocks > 0 && find_variant(fmt, H, q_heads, kv_heads, head_dim, I, blocks) != nullptr;
+    // Either KV precision: the LDS check is made for the wider one.
+    return aligned16 && blocks > 0 && find_variant(fmt, H, q_heads, kv_heads, head_dim, I, true, blocks) != nullptr;
+}
+
+FusedGeom fused_geometry(int H, int q_heads, int kv_heads, int head_dim, int I, bool kv_f32, int blocks) {
+    return geometry(H, q_heads, kv_heads, head_dim, I, kv_f32, blocks);
 }
 
 // dst[b][r][j] = down[r][b rb + j] for j < rb and b rb + j < I, else 0;
 // one thread per element of dst.
-__global__ void down_columns_kernel(const uint16_t *down, size_t stride, int H, int I, int rb, int rp, int blocks,
+__global__ void down_columns_kernel(const uint16_t *down, size_t stride, int H, int I, int rb, int rp, int nf,
                                     uint16_t *dst) {
-    const size_t n = (size_t)blocks * H * rp;
+    const size_t n = (size_t)nf * H * rp;
     for (size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x; t < n; t += (size_t)gridDim.x * blockDim.x) {
         const int j = (int)(t % rp);
         const size_t br = t / rp;
@@ -1378,11 +1441,11 @@ __global__ void down_columns_kernel(const uint16_t *down, size_t stride, int H, 
     }
 }
 
-int fused_down_columns(const uint16_t *down, size_t stride, int H, int I, int blocks, uint16_t *dst, hipStream_t s) {
-    const int rb = fused_gate_rows(I, blocks), rp = fused_gate_rows_padded(I, blocks);
-    const size_t n = (size_t)blocks * H * rp;
+int fused_down_columns(const uint16_t *down, size_t stride, int H, int I, int nf, uint16_t *dst, hipStream_t s) {
+    const int rb = fused_gate_rows(I, nf), rp = fused_gate_rows_padded(I, nf);
+    const size_t n = (size_t)nf * H * rp;
     const int grid = (int)std::min<size_t>((n + 255) / 256, 4096);
-    hipLaunchKernelGGL(down_columns_kernel, dim3(grid), dim3(256), 0, s, down, stride, H, I, rb, rp, blocks, dst);
+    hipLaunchKernelGGL(down_columns_kernel, dim3(grid), dim3(256), 0, s, down, stride, H, I, rb, rp, nf, dst);
     CHIP_CHECK(hipGetLastError());
     return 0;
 }
@@ -1394,31 +1457,13 @@ int fused_decode_blocks() {
     return cus;
 }
 
-int fused_max_splits(int H, int q_heads, int kv_heads, int head_dim, int I, bool kv_f32, int blocks,
-                     size_t capacity) {
-    // The most splits whose partials every o_proj block can hold in LDS next
-    // to everything else (capped by the grid and by `capacity` positions).
-    const int kvb = kv_f32 ? 4 : 2, G = q_heads / kv_heads;
-    const size_t budget = device_max_lds(), fixed = static_lds_bytes(head_dim, G);
-    const size_t per_item = (size_t)item_positions(head_dim * kvb);
-    const size_t need = (capacity + per_item - 1) / per_item;
-    // At most 64: the merge holds one split per lane.
-    int ms = (int)std::min({(size_t)(blocks / kv_heads), std::max<size_t>(need, 1), (size_t)64});
-    for (; ms >= 1; --ms) {
-        const LdsLayout lay = lds_layout(H, I, q_heads, head_dim, G, kvb, blocks, ms);
-        if (fixed + (size_t)lay.total <= budget && lay.tbw <= kMaxChunks * kChunk) return ms;
-    }
-    return 0;  // not even one split fits: no persistent kernel for this shape
-}
-
 int launch_decode_fused(FusedArgs a, int fmt, int head_dim, int group, bool kv_f32, hipStream_t s) {
     const int nb = fused_decode_blocks();
     if (nb <= 0) return fail("HIP backend: cannot size the persistent decode grid.");
-    const Variant *v = find_variant(fmt, a.H, a.q_heads, a.kv_heads, head_dim, a.I, nb);
+    const Variant *v = find_variant(fmt, a.H, a.q_heads, a.kv_heads, head_dim, a.I, kv_f32, nb);
     if (!v || v->g != group) return fail("HIP backend: no persistent decode kernel for this shape.");
-    const bool hs = head_split(a, group, head_dim, kv_f32, nb);
-    if (kv_f32) return hs ? launch_kt<float, true>(*v, a, nb, s) : launch_kt<float, false>(*v, a, nb, s);
-    return hs ? launch_kt<uint16_t, true>(*v, a, nb, s) : launch_kt<uint16_t, false>(*v, a, nb, s);
+    if (kv_f32) return launch_kt<float>(*v, a, nb, s);
+    return launch_kt<uint16_t>(*v, a, nb, s);
 }
 
 }  // namespace chip

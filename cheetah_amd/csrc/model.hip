@@ -82,7 +82,8 @@ struct Layer {
     uint16_t *ln1 = nullptr, *ln2 = nullptr;
     KvLayer kv;
     // The persistent decode kernel's copy of down_proj, columns regrouped
-    // per block (fused_down_columns); built once, while down is resident.
+    // per FFN block of the grid (fused_down_columns); built while down is
+    // resident, freed when down is evicted to the host tier.
     uint16_t *down_cols = nullptr;
     // Host tier: pinned copy of a matrix whose device buffer was released
     // (its WMat base is then null); indexed like mat(). Null when resident.
@@ -131,7 +132,10 @@ struct Shared {
     hipStream_t copy_stream = nullptr;
     int host_mats = 0;       // layer matrices on the host tier
     unsigned epoch = 0;      // bumped whenever a weight's device address changes
-    int down_cols_blocks = 0;  // grid size the layers' down_cols are built for (0: none)
+    // The layers' down_cols: built for down_cols_nf FFN blocks, generation
+    // down_cols_gen (0: none; an eviction of a down_proj frees them).
+    int down_cols_nf = 0;
+    unsigned down_cols_gen = 0, down_cols_builds = 0;
     size_t slot_bytes = 0;   // one layer's matrices, as a feed slot holds them
 
     int q_dim() const { return (int)(cfg.q_heads * cfg.head_dim); }
@@ -210,10 +214,10 @@ struct cheetah_hip_model {
     // Persistent decode kernel state (decode_fused.hip).
     bool fused_ok = false;
     FusedLayer *fused_layers = nullptr;  // device [L]
-    int table_cols_blocks = 0;           // the table's down_cols were built for this grid (0: none yet)
+    unsigned table_cols_gen = 0;         // generation of the down_cols the table points at (0: none yet)
     int fused_blocks = 0;
-    int fused_max_splits = 0;
-    uint64_t *tagged = nullptr;  // hid0 | hid1 | qkvn | part | pdown | am, tagged words
+    FusedGeom fused_geo{};               // role geometry on fused_blocks blocks
+    uint64_t *tagged = nullptr;  // hid0 | hid1 | kvw | part | ml | pdown | am, tagged words
     size_t tagged_words = 0;
     int32_t *abort_dev = nullptr;
     unsigned next_tag = 1;          // tag of the next launch's first phase
@@ -435,16 +439,14 @@ int finalize(cheetah_hip_model *m) {
     return 0;
 }
 
-// Sizes (words) of the tagged arrays in one allocation: hid0, hid1, qkvn,
-// part, pdown, am; each rounded to an even count plus 2 words, so every array
+// Sizes (words) of the tagged arrays in one allocation: hid0, hid1, kvw,
+// part, ml, pdown, am; each rounded to an even count plus 2 words, so every array
 // starts 16-byte aligned and a 16-byte read at its last word stays inside.
 std::vector<size_t> fused_tagged_sizes(const cheetah_hip_model *m) {
     const auto &c = m->sh->cfg;
-    const size_t hd = c.head_dim, G = c.q_heads / c.kv_heads;
-    const size_t rb = (size_t)fused_gate_rows((int)c.intermediate_size, m->fused_blocks);
-    const size_t nbd = (c.intermediate_size + rb - 1) / rb, nhb = (c.hidden_size + 6) / 7;
-    const size_t raw[] = {c.hidden_size, c.hidden_size, c.kv_heads * (G + 2) * hd,
-                          (size_t)m->fused_max_splits * c.q_heads * (hd + 2), nhb * nbd * 7,
+    const FusedGeom &g = m->fused_geo;
+    const size_t raw[] = {c.hidden_size, c.hidden_size, c.kv_heads * 2 * c.head_dim,
+                          (size_t)g.no * g.ni_max * 8, 2 * (size_t)g.ni_max, (size_t)g.no * g.nbd * 8,
                           4 * (size_t)m->fused_blocks};
     std::vector<size_t> out;
     for (size_t n : raw) out.push_back((n + 1) / 2 * 2 + 2);
@@ -497,13 +499,8 @@ int init_fused(cheetah_hip_model *m) {
                                                        (int)c.kv_heads, (int)c.head_dim, (int)c.intermediate_size,
                                                        al, m->fused_blocks);
     if (!m->fused_ok) return 0;
-    m->fused_max_splits = fused_max_splits((int)c.hidden_size, (int)c.q_heads, (int)c.kv_heads, (int)c.head_dim,
-                                           (int)c.intermediate_size, sh.kv_f32 != 0, m->fused_blocks,
-                                           sh.kv_capacity);
-    if (m->fused_max_splits == 0) {
-        m->fused_ok = false;
-        return 0;
-    }
+    m->fused_geo = fused_geometry((int)c.hidden_size, (int)c.q_heads, (int)c.kv_heads, (int)c.head_dim,
+                                  (int)c.intermediate_size, sh.kv_f32 != 0, m->fused_blocks);
     CHIP_TRY(m->mem.alloc(&m->fused_layers, c.num_layers));
     CHIP_TRY(upload_fused_layers(m));
     if (!sh.host_mats) CHIP_TRY(ensure_down_cols(m));
@@ -526,43 +523,42 @@ bool fused_enabled(const cheetah_hip_model *m) {
 }
 
 // Whether one persistent launch can run decode steps at positions
-// [offset, offset + steps): the attention items of the longest context must
-// fit the grid.
+// [offset, offset + steps): the attention runs of the longest context must
+// fit the item blocks.
 bool fused_fits(const cheetah_hip_model *m, size_t offset, size_t steps) {
     // The persistent kernel reads every layer from HBM in place.
     if (!fused_enabled(m) || m->sh->host_mats) return false;
-    const Shared &sh = *m->sh;
-    const size_t per_item = (size_t)fused_positions_per_item((int)sh.cfg.head_dim, sh.kv_f32 != 0);
-    const size_t ctx = offset + steps;
-    return (ctx + per_item - 1) / per_item <= (size_t)m->fused_max_splits;
+    return (long)(offset + steps) <= fused_max_context(m->fused_geo);
 }
 
-// Builds every layer's down_cols for this instance's grid once per model
-// (the persistent kernel runs only while every matrix is resident), and
-// points this instance's layer table at them.
+// Builds every layer's down_cols for the FFN blocks of this instance's grid
+// once per model (the persistent kernel runs only while every matrix is
+// resident; an eviction of a down_proj frees them and they are rebuilt
+// here), and points this instance's layer table at them.
 int ensure_down_cols(cheetah_hip_model *m) {
     Shared &sh = *m->sh;
-    if (m->table_cols_blocks == m->fused_blocks) return 0;
     {
         std::lock_guard<std::mutex> lock(sh.mu);
-        if (sh.down_cols_blocks != m->fused_blocks) {
+        const int nf = m->fused_geo.nf;
+        if (sh.down_cols_gen != 0 && sh.down_cols_nf != nf) return fail("HIP backend: persistent decode grid changed.");
+        if (sh.down_cols_gen == 0) {
             const auto &c = sh.cfg;
-            const int H = (int)c.hidden_size, I = (int)c.intermediate_size, nb = m->fused_blocks;
-            const size_t elems = (size_t)nb * H * fused_gate_rows_padded(I, nb);
-            if (sh.down_cols_blocks != 0) return fail("HIP backend: persistent decode grid changed.");
+            const int H = (int)c.hidden_size, I = (int)c.intermediate_size;
+            const size_t elems = (size_t)nf * H * fused_gate_rows_padded(I, nf);
             for (Layer &L : sh.layers) {
                 if (!L.down.payload()) return fail("HIP backend: persistent decode needs every matrix resident.");
                 if (!L.down_cols) CHIP_TRY(sh.mem.alloc(&L.down_cols, elems));
-                CHIP_TRY(fused_down_columns((const uint16_t *)L.down.payload(), L.down.row_stride(), H, I, nb,
+                CHIP_TRY(fused_down_columns((const uint16_t *)L.down.payload(), L.down.row_stride(), H, I, nf,
                                             L.down_cols, m->stream));
             }
             CHIP_CHECK(hipStreamSynchronize(m->stream));
-            sh.down_cols_blocks = nb;
+            sh.down_cols_nf = nf;
+            sh.down_cols_gen = ++sh.down_cols_builds;
         }
+        if (m->table_cols_gen == sh.down_cols_gen) return 0;
+        m->table_cols_gen = sh.down_cols_gen;
     }
-    CHIP_TRY(upload_fused_layers(m));
-    m->table_cols_blocks = m->fused_blocks;
-    return 0;
+    return upload_fused_layers(m);
 }
 
 // Runs `steps` decode steps in one persistent launch from the token and
@@ -605,7 +601,7 @@ int run_fused(cheetah_hip_model *m, size_t offset, size_t steps) {
     a.hist_cap = (long)sh.kv_capacity + 1;
     a.logits = m->logits;
     uint64_t *t = m->tagged;
-    uint64_t **dst[] = {&a.hid0, &a.hid1, &a.qkvn, &a.part, &a.pdown, &a.am};
+    uint64_t **dst[] = {&a.hid0, &a.hid1, &a.kvw, &a.part, &a.ml, &a.pdown, &a.am};
     const std::vector<size_t> sizes = fused_tagged_sizes(m);
     for (size_t i = 0; i < sizes.size(); ++i) {
         *dst[i] = t;
@@ -615,7 +611,6 @@ int run_fused(cheetah_hip_model *m, size_t offset, size_t steps) {
     a.tag0 = m->next_tag;
     a.steps = (int)steps;
     a.ctx_end = (long)(offset + steps);
-    a.max_splits = m->fused_max_splits;
     // CHEETAH_HIP_FUSED_TRACE=<file>: per-phase timestamps of the launch's
     // last step, one line per block (wall clock ticks).
     const char *trace_path = getenv("CHEETAH_HIP_FUSED_TRACE");
@@ -1421,6 +1416,14 @@ int cheetah_hip_evict_unit(cheetah_hip_model *m, const char *unit_id) {
     sh.mem.release((void *)w.base);
     w.base = nullptr;
     L.host[i] = h;
+    if (i == kLayerMats - 1 && L.down_cols) {
+        // The persistent kernel's copy of this down_proj goes too (it is
+        // rebuilt from the resident matrices once every unit is back).
+        std::lock_guard<std::mutex> lock(sh.mu);
+        sh.mem.release(L.down_cols);
+        L.down_cols = nullptr;
+        sh.down_cols_gen = 0;
+    }
     ++sh.host_mats;
     ++sh.epoch;
     return 1;

@@ -10,13 +10,15 @@ its producers finished and when its consumers were released, as a markdown
 report: the critical path of a layer split into hand-offs (last producer
 store -> consumers' inputs staged) and phase compute.
 
-Stamp slots per layer l (16 l + k): 0 layer start, 1 A.in (QKV input normed
-and staged), 2 A.out (QKV rows stored), 3 B.in (attention item's q/K/V
-staged), 4 scores, 5 softmax, 6 weighted V + partials stored, 7 B.out
-(weight rows of C/D/E issued), 8 C.in (partials merged), 14 o_proj dot,
-9 C.out (hid0 stored), 10 D.in, 11 D.out (down partials stored, next QKV rows issued),
-12 E.in, 15 down dot, 13 E.out (hid1 stored). After the layers: 16 L head.in,
-16 L + 1 head.out, 16 L + 2 token known.
+Stamp slots per layer l (16 l + k): 0 layer start, 1 P1.in (items' and KV
+blocks' input normed and staged), 2 q.out (an item's q rotated), 3 scores of
+the cached rows, 4 new row (the new K/V row polled and scored), 5 softmax +
+weighted V, 6 P1.out (items: o_proj partials stored; KV blocks: K/V stored),
+7 refill issued, 8 C.in (owners: item partials gathered), 9 C.out (hid0
+stored), 10 D.in (FFN blocks: input normed), 11 gate/up + SwiGLU, 12 D.out
+(down partials stored), 13 E.in (owners: down partials gathered), 14 E.out
+(hid1 stored). After the layers: 16 L head.in, 16 L + 1 head.out, 16 L + 2
+token known.
 """
 import argparse
 import os
@@ -26,36 +28,51 @@ import numpy as np
 
 from . import configs, hip, synth
 
-KCW = 7      # compute waves per block (rows per block of o_proj/down, QKV pairs)
 KWAVES = 8
+KV_LDS_MAX = 64 * 1024
+IP_MAX = 256
+MAX_SPLITS = 16
 
 
-def block_roles(shape, blocks: int, context: int, kv_bf16: bool = True):
-    """Block index sets per role, as the launcher assigns them
-    (decode_fused.hip launch_one / head_split)."""
+def block_roles(shape, blocks: int, context: int, ctx_end: int = 0, kv_bf16: bool = True):
+    """Block index sets per role at a step of context `context` in a launch
+    whose last step reaches `ctx_end`, as the launcher assigns them
+    (decode_fused.hip geometry / launch_one)."""
     H, I, hd = shape.hidden_size, shape.intermediate_size, shape.head_dim
     qh, kvh = shape.q_heads, shape.kv_heads
-    g = qh // kvh
-    npairs = (qh + 2 * kvh) * hd // 2
-    nhb = (H + KCW - 1) // KCW
-    nab = (npairs + KCW - 1) // KCW
-    a0 = nhb if nhb + nab <= blocks else blocks - nab
+    ctx_end = ctx_end or context
+    nf = blocks * 5 // 8
+    f0 = blocks - nf
+    nkv = (kvh * hd + KWAVES - 1) // KWAVES
+    kv0 = f0 - nkv
+    s_cap = min(MAX_SPLITS, kv0 // qh)
     row = hd * (2 if kv_bf16 else 4)
-    ip = 128 if row <= 256 else 64
+    ip_max, ip = 0, 64
+    while ip <= IP_MAX and 2 * ip * row <= KV_LDS_MAX:
+        ip_max, ip = ip, ip * 2
+    ip = 64
+    while ip < ip_max and (ctx_end + ip - 1) // ip > s_cap:
+        ip *= 2
     S = (context + ip - 1) // ip
-    hs = g > 1 and kvh * S * g <= blocks
-    items = kvh * S * (g if hs else 1)
-    b_items = set(range(blocks - items, blocks))
-    a_set = set(range(a0, a0 + nab))
+    rb = (I + nf - 1) // nf
+    nbd = (I + rb - 1) // rb
+    no = H // 8
+    items = list(range(qh * S))
     return {
-        "H": sorted(range(nhb)),
-        "A": sorted(a_set - b_items),
-        "AB": sorted(a_set & b_items),
-        "B": sorted(b_items - a_set),
+        "items": items,
+        "last": [b for b in items if b // qh == S - 1],
+        "kv": list(range(kv0, kv0 + nkv)),
+        "p1": items + list(range(kv0, kv0 + nkv)),
+        "ffn": list(range(f0, f0 + nbd)),
+        "owners": list(range(f0, f0 + no)),
         "all": list(range(blocks)),
-        "Aall": sorted(a_set),
-        "Ball": sorted(b_items),
+        "ip": ip,
     }
+
+
+SEGMENTS = ("q dot", "cached scores", "new K/V row wait (last runs)", "softmax + weighted V", "o_proj partials",
+            "hand-off items -> owners", "merge + residual", "hand-off owners -> FFN (+ norm)", "gate/up + SwiGLU",
+            "down partials", "hand-off FFN -> owners", "sum + residual", "hand-off owners -> items (+ norm)")
 
 
 def report(t: np.ndarray, roles: dict, layers: int) -> str:
@@ -68,35 +85,35 @@ def report(t: np.ndarray, roles: dict, layers: int) -> str:
     def mx(rg, slot):
         return float(np.nanmax(us[roles[rg], slot]))
 
-    segs = {k: [] for k in ("A dot + store", "hand-off A->B", "attention item", "hand-off B->C (+ merge)",
-                             "o_proj dot + store", "hand-off C->D", "gate/up dot + store", "hand-off D->E",
-                             "down dot + store", "hand-off E->A(next)")}
+    segs = {k: [] for k in SEGMENTS}
+    kv_dot = []
     for l in range(1, layers - 1):
         b, n = 16 * l, 16 * (l + 1)
-        segs["A dot + store"].append(mx("Aall", b + 2) - med("Aall", b + 1))
-        segs["hand-off A->B"].append(med("Ball", b + 3) - mx("Aall", b + 2))
-        segs["attention item"].append(mx("Ball", b + 6) - med("Ball", b + 3))
-        segs["hand-off B->C (+ merge)"].append(med("H", b + 8) - mx("Ball", b + 6))
-        segs["o_proj dot + store"].append(mx("H", b + 9) - med("H", b + 8))
-        segs["hand-off C->D"].append(med("all", b + 10) - mx("H", b + 9))
-        segs["gate/up dot + store"].append(mx("all", b + 11) - med("all", b + 10))
-        segs["hand-off D->E"].append(med("H", b + 12) - mx("all", b + 11))
-        segs["down dot + store"].append(mx("H", b + 13) - med("H", b + 12))
-        segs["hand-off E->A(next)"].append(med("Aall", n + 1) - mx("H", b + 13))
-    span = [med("Aall", 16 * (l + 1) + 1) - med("Aall", 16 * l + 1) for l in range(1, layers - 1)]
-    lines = [f"Layers 1..{layers - 2}: mean span {np.mean(span):.2f} us per layer (median A.in to the next layer's "
-             f"A.in); head.in -> token {mx('all', 16 * layers + 2) - med('all', 16 * layers):.1f} us.", "",
+        # Consecutive points of the layer's critical path: the segments tile
+        # the span from the items' input to the next layer's.
+        pts = [med("items", b + 1), mx("items", b + 2), mx("items", b + 3), mx("last", b + 4), mx("items", b + 5),
+               mx("items", b + 6), med("owners", b + 8), mx("owners", b + 9), med("ffn", b + 10),
+               mx("ffn", b + 11), mx("ffn", b + 12), med("owners", b + 13), mx("owners", b + 14),
+               med("items", n + 1)]
+        for name, a, z in zip(SEGMENTS, pts, pts[1:]):
+            segs[name].append(z - a)
+        kv_dot.append(mx("kv", b + 6) - med("kv", b + 1))
+    span = [med("items", 16 * (l + 1) + 1) - med("items", 16 * l + 1) for l in range(1, layers - 1)]
+    lines = [f"Layers 1..{layers - 2}: mean span {np.mean(span):.2f} us per layer (median item input to the next "
+             f"layer's); head.in -> token {mx('all', 16 * layers + 2) - med('all', 16 * layers):.1f} us; KV blocks' "
+             f"dot + K/V store (beside the path) {np.mean(kv_dot):.2f} us.", "",
              "| segment (critical path of a layer) | mean us | min | max |", "|---|---:|---:|---:|"]
     for k, v in segs.items():
         lines.append(f"| {k} | {np.mean(v):.2f} | {np.min(v):.2f} | {np.max(v):.2f} |")
     lines.append(f"| sum | {sum(np.mean(v) for v in segs.values()):.2f} | | |")
-    lines += ["", "Per-role stamps of layer 12, us from the median A.in (median / max over the role's blocks):", ""]
-    names = {0: "start", 1: "A.in", 2: "A.out", 3: "B.in", 4: "score", 5: "softmax", 6: "PV", 7: "B.out", 8: "C.in",
-             14: "C.dot", 9: "C.out", 10: "D.in", 11: "D.out", 12: "E.in", 15: "E.dot", 13: "E.out"}
+    lines += ["", "Per-role stamps of layer 12, us from the median item input (median / max over the role's "
+              "blocks):", ""]
+    names = {0: "start", 1: "P1.in", 2: "q", 3: "scores", 4: "new row", 5: "PV", 6: "P1.out", 7: "refill",
+             8: "C.in", 9: "C.out", 10: "D.in", 11: "gate/up", 12: "D.out", 13: "E.in", 14: "E.out"}
     l = min(12, layers - 2)
-    ref = med("Aall", 16 * l + 1)
+    ref = med("items", 16 * l + 1)
     lines += ["| role (blocks) | " + " | ".join(names.values()) + " |", "|---|" + "---:|" * len(names)]
-    for rn in ("H", "A", "AB", "B"):
+    for rn in ("items", "last", "kv", "owners", "ffn"):
         rg = roles[rn]
         if not rg:
             continue
@@ -130,9 +147,11 @@ def main():
     finally:
         del os.environ["CHEETAH_HIP_FUSED_TRACE"]
     t = np.loadtxt(path, dtype=np.float64)
-    roles = block_roles(shape, t.shape[0], args.context + args.steps)
+    # The traced step is the launch's last: its context is context + steps.
+    ctx = args.context + args.steps
+    roles = block_roles(shape, t.shape[0], ctx, ctx)
     print(f"# Persistent decode phase timeline: Qwen2-0.5B shape, BF16 KV, context {args.context}, step "
-          f"{args.steps} of {args.steps}, {t.shape[0]} blocks\n")
+          f"{args.steps} of {args.steps}, {t.shape[0]} blocks, {roles['ip']} positions per item\n")
     print(report(t, roles, shape.num_layers))
 
 

@@ -7,24 +7,30 @@ from cheetah_amd import configs, fused_trace
 
 
 def test_block_roles_partition_the_grid():
-    roles = fused_trace.block_roles(configs.QWEN2_0_5B, 256, 544)
-    # 896 rows of o_proj/down over 7 rows per block; 1,152 QKV rows in pairs
-    # over 7 pairs per block; 2 KV heads x 5 splits x 7 q heads items.
-    assert roles["H"] == list(range(128))
-    assert len(roles["Aall"]) == 83 and len(roles["Ball"]) == 70
-    assert set(roles["A"]) | set(roles["AB"]) == set(roles["Aall"])
-    assert set(roles["B"]) | set(roles["AB"]) == set(roles["Ball"])
-    assert not set(roles["A"]) & set(roles["B"])
-    assert max(roles["Ball"]) == 255
+    roles = fused_trace.block_roles(configs.QWEN2_0_5B, 256, 544, 640)
+    # 160 FFN blocks (5/8 of the grid): 31 gate/up rows each, 157 with rows,
+    # 112 owners of 8 residual rows; 128 K/V rotation pairs over 16 KV
+    # blocks; the items below them: 14 q heads x 5 runs of 128 positions
+    # (640 positions fit 5 runs of 128 in the 80 item blocks).
+    assert roles["ip"] == 128
+    assert roles["items"] == list(range(70))
+    assert roles["last"] == list(range(56, 70))
+    assert roles["kv"] == list(range(80, 96))
+    assert roles["owners"] == list(range(96, 208))
+    assert roles["ffn"] == list(range(96, 253))
+    # Shorter launches take shorter runs: 320 positions in 5 runs of 64
+    # (the 80 item blocks hold 5 runs of each of the 14 q heads).
+    short = fused_trace.block_roles(configs.QWEN2_0_5B, 256, 200, 320)
+    assert short["ip"] == 64 and short["items"] == list(range(14 * 4))
 
 
 def test_report_recovers_known_segments():
     shape = configs.QWEN2_0_5B
     L, nb = shape.num_layers, 256
-    roles = fused_trace.block_roles(shape, nb, 544)
+    roles = fused_trace.block_roles(shape, nb, 544, 640)
     # Stamps in 100 MHz ticks: layer l starts at 2,000 l ticks (20 us per
-    # layer); within a layer each slot k fires at 100 k ticks (1 us apart),
-    # the same in every block.
+    # layer); within a layer slot k fires at 100 k ticks (1 us apart), the
+    # same in every block.
     t = np.zeros((nb, 16 * L + 3))
     for l in range(L):
         for k in range(16):
@@ -32,17 +38,17 @@ def test_report_recovers_known_segments():
     t[:, 16 * L:] = 1 + 2000 * L + np.array([0, 100, 200])
     out = fused_trace.report(t, roles, L)
     assert "mean span 20.00 us per layer" in out
-    # A dot + store: A.out (slot 2) - A.in (slot 1) = 1 us; the hand-off
-    # A -> B: B.in (3) - A.out (2) = 1 us; B -> C: C.in (8) - PV (6) = 2 us.
     rows = {}
     for line in out.splitlines():
         cells = [c.strip() for c in line.split("|")]
         if len(cells) == 6 and cells[1] and cells[2] not in ("", "mean us", "---:"):
             rows[cells[1]] = float(cells[2])
-    assert rows["A dot + store"] == 1.0
-    assert rows["hand-off A->B"] == 1.0
-    assert rows["hand-off B->C (+ merge)"] == 2.0
-    # E -> next A: the next layer's A.in (20 us + slot 1) - E.out (slot 13).
-    assert rows["hand-off E->A(next)"] == 8.0
+    # q dot: slot 2 - slot 1; items -> owners: C.in (8) - P1.out (6).
+    assert rows["q dot"] == 1.0
+    assert rows["hand-off items -> owners"] == 2.0
+    assert rows["merge + residual"] == 1.0
+    # owners -> next layer's items: the next layer's P1.in (20 us + slot 1)
+    # - E.out (slot 14).
+    assert rows["hand-off owners -> items (+ norm)"] == 7.0
     # The segments tile the layer: their sum is the span.
     assert rows["sum"] == 20.0
