@@ -1,6 +1,6 @@
 """Build guard for the persistent decode kernel's code shape.
 
-The kernel (decode_fused.hip) depends on three properties the compiler could
+The kernel (decode_fused.hip) depends on properties the compiler could
 silently take away:
   * no scratch memory and no dynamic stack: a call frame or a spilled vector
     register would put private-memory traffic on every step's critical path;
@@ -15,7 +15,11 @@ silently take away:
     is followed at once by s_nop 1 or longer: such a store reads its data
     registers after issue, a VALU write to them needs two wait states on
     this chip, and the compiler cannot insert them for a store it does not
-    see (without them the store can write the registers' next values).
+    see (without them the store can write the registers' next values);
+  * every matrix-core instruction runs with the whole wave enabled: its
+    operands come from all 64 lanes, so one placed inside a lane-divergent
+    branch (after an s_and_saveexec before the branch's exec restore)
+    would combine operands that only some lanes loaded.
 
 The script compiles decode_fused.hip for the device with the compiler's
 resource-usage remarks, writes the device assembly next to the objects, and
@@ -118,8 +122,25 @@ def main():
         wide = check_wide_stores(funcs[k])
         if wide:
             fail(f"{k}: a store of more than 64 data bits is not followed by s_nop 1: {wide}")
+        masked = check_mfma_exec(funcs[k])
+        if masked:
+            fail(f"{k}: a matrix-core instruction inside a lane-divergent branch: {masked}")
     print(f"check_code_shape: {len(kernels)} {KERNEL} instances: no scratch, no dynamic stack, no vector "
-          f"spills, no calls, wide stores padded")
+          f"spills, no calls, wide stores padded, matrix-core products on whole waves")
+
+
+def check_mfma_exec(body):
+    """The first v_mfma whose closest preceding exec change in the code
+    layout narrows exec (s_and_saveexec) rather than restoring it, or None."""
+    last = ""
+    for ln in body:
+        ins = ln.split(";")[0].strip()
+        if re.match(r"s_and_saveexec_b64|s_or_b64 exec, exec|s_andn2_b64 exec|s_mov_b64 exec|s_xor_b64 exec|"
+                    r"s_and_b64 exec", ins):
+            last = ins
+        elif ins.startswith("v_mfma") and last.startswith("s_and_saveexec"):
+            return ins
+    return None
 
 
 def check_wide_stores(body):

@@ -401,37 +401,14 @@ __device__ __forceinline__ void wave_best(int &key, uint32_t &idx) {
 
 constexpr int kStage = 64;  // outputs one block publishes per phase, at most
 
-constexpr int kWaveRows = 128;  // rows one wave stores at once (two per lane)
-
 struct Shm {
     int ikey[kWaves];
     uint32_t iidx[kWaves];
-    int token;           // the step's sampled id
-    float out[kStage];   // a phase's outputs of the block, stored as one run
-    float coef[kWaveRows];              // the owners' merge weight per item
-    float scr[kWaves][kWaveRows];       // a wave's row values on their way to the stores
+    int token;                 // the step's sampled id
+    float out[kStage];         // a phase's outputs of the block, stored as one run
+    float red[kWaves][16];     // each wave's tile outputs (matrix-core phases split over K)
+    alignas(16) uint16_t dp[4][32];  // an FFN block's SwiGLU outputs, split (put_split)
 };
-
-// A wave's row values stored as tagged words, two rows per 16-byte store.
-// v[k] sits in the lanes with lane % LPR == 0 and belongs to the wave's row
-// (k 8 + wave) RPS + lane / LPR; the values pass through the wave's LDS
-// scratch so that lane j stores rows 2 j and 2 j + 1 (consecutive rows of
-// one owner's 8-word segment, dst(r) 16-byte aligned for even r). LDS
-// traffic of one wave is in order, so no barrier is needed.
-template <int NS, int RPS, int LPR, class D>
-__device__ __forceinline__ void store_rows(const float (&v)[NS], float *scr, int wave, int H, unsigned tag, D &&dst) {
-    static_assert(NS * RPS <= kWaveRows && RPS % 2 == 0, "rows per wave");
-    const int ln = lane_here();
-    if (ln % LPR == 0) {
-#pragma unroll
-        for (int k = 0; k < NS; ++k) scr[k * RPS + ln / LPR] = v[k];
-    }
-    const int j = 2 * ln;
-    if (j < NS * RPS) {
-        const int k = j / RPS, r = (k * kWaves + wave) * RPS + j % RPS;
-        if (r < H) stf2(dst(r), scr[j], scr[j + 1], tag);
-    }
-}
 
 // Reduces (key, idx) over the block; the result lands in every thread.
 __device__ __forceinline__ void block_best(int &key, uint32_t &idx, Shm &sm) {
@@ -542,29 +519,132 @@ __device__ __forceinline__ void dot_pool(const u32x4 (&W)[NP], const float *xs, 
     for (int i = 0; i < R; ++i) out[i] = wave_sum(acc[i]);
 }
 
+// ---- Matrix-core matrix-vector products.
+//
+// y = W x for 16 rows of W at a time with v_mfma_f32_16x16x32_bf16: the B
+// operand of K-step ks is the 16 rows' BF16 elements [32 ks, 32 ks + 32),
+// lane l holding 8 consecutive elements (one 16-byte weight unit, elements
+// 32 ks + 8 (l / 16) ...) of row l % 16; the A operand's rows 0..2 hold x
+// split into three BF16 parts (x_split), rows 3..15 zeros. Each part times
+// a BF16 weight is exact in f32 and the three parts carry all 24
+// significant bits of x, so the tile's output rows 0..2 add up to the f32
+// dot product (lanes 0..15 hold rows 0..3 of output column l: c[0..3]).
+// The VALU form needs an unpack and an FMA per element; a wave64 VALU
+// instruction occupies its SIMD for 4 cycles, which made the decode's
+// matrix-vector phases instruction-bound.
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+
+// hi = x with its low 16 bits cleared, mid = the same of x - hi, lo =
+// x - hi - mid rounded to nearest even: x - hi and x - hi - mid are exact.
+__device__ __forceinline__ void x_split(float x, uint16_t &hi, uint16_t &mid, uint16_t &lo) {
+    hi = (uint16_t)(__float_as_uint(x) >> 16);
+    const float r1 = x - bf16_f32(hi);
+    mid = (uint16_t)(__float_as_uint(r1) >> 16);
+    lo = f32_bf16_rne(r1 - bf16_f32(mid));
+}
+
+// The split of element i of a K-padded vector in LDS: xb[p kp + i] holds
+// part p (p < 3) and xb[3 kp + i] a zero, the rows the A operand reads.
+__device__ __forceinline__ void put_split(uint16_t *xb, int kp, int i, float x) {
+    uint16_t hi, mid, lo;
+    x_split(x, hi, mid, lo);
+    xb[i] = hi;
+    xb[kp + i] = mid;
+    xb[2 * kp + i] = lo;
+    xb[3 * kp + i] = 0;
+}
+
+// This lane's offset (elements) into a split vector for K-step 0: row
+// min(lane % 16, 3), elements 8 (lane / 16) ...
+__device__ __forceinline__ int a_offset(int kp) {
+    const int l = lane_here();
+    return min(l & 15, 3) * kp + 8 * (l >> 4);
+}
+__device__ __forceinline__ u32x4 a_frag(const uint16_t *xb, int aoff, int ks) {
+    return *(const u32x4 *)(xb + aoff + 32 * ks);
+}
+__device__ __forceinline__ f32x4 mfma_bf16(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                   0, 0);
+}
+// The dot product of the tile's row `lane` (lanes 0..15).
+__device__ __forceinline__ float tile_dot(f32x4 c) { return (c[0] + c[1]) + c[2]; }
+
+// One tile over N consecutive K-steps: pool slots OFF + k against the
+// split vector at xa + 32 k (xa: this lane's A offset, a_offset, plus the
+// first K-step's). All A operands are read first (their LDS latency once),
+// and the K-steps alternate between two accumulators (two MFMA chains).
+// Call with all 64 lanes active: every lane's operands enter the product
+// (inside a lane-divergent branch the reads would skip lanes).
+template <int N, int OFF, int NP>
+__device__ __forceinline__ float kdot(const uint16_t *xa, const u32x4 (&W)[NP]) {
+    static_assert(OFF + N <= NP, "pool slice out of range");
+    u32x4 af[N];
+#pragma unroll
+    for (int k = 0; k < N; ++k) af[k] = *(const u32x4 *)(xa + 32 * k);
+    // Every read issued before the first product waits for one.
+#pragma unroll
+    for (int k = 0; k < N; ++k) asm volatile("" : "+v"(af[k]));
+    f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        if (k & 1) c1 = mfma_bf16(af[k], W[OFF + k], c1);
+        else c0 = mfma_bf16(af[k], W[OFF + k], c0);
+    }
+    return tile_dot(c0) + tile_dot(c1);
+}
+
+// The tile's 16 row values (lanes 0..15) stored two rows per 16-byte
+// store: lane 2 j stores rows 2 j and 2 j + 1 at dst(2 j) (rows r < n).
+template <class D>
+__device__ __forceinline__ void store_tile(float y, int r0, int n, unsigned tag, D &&dst) {
+    const float nb = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, y), 0xB1, 0xF, 0xF,
+                                                                         true));  // quad_perm [1,0,3,2]
+    const int l = lane_here(), r = r0 + l;
+    if (l < 16 && (l & 1) == 0 && r < n) stf2(dst(r), y, nb, tag);
+}
+
+// All waves: the split (put_split) of x[i] * (inv * g[i]) for i < n into
+// the K-padded xb (kp elements per part), zeros for n <= i < kp.
+template <bool BF16_SRC>
+__device__ __forceinline__ void block_stage_split(uint16_t *xb, int kp, const void *src, int n, const uint16_t *g,
+                                                  float inv) {
+    for (int i = tid_here(); i < kp; i += kThreads) {
+        float v = 0.f;
+        if (i < n) {
+            if constexpr (BF16_SRC) v = bf16_f32(((const uint16_t *)src)[i]);
+            else v = val_of(((const uint64_t *)src)[i]);
+            v = v * (inv * bf16_f32(g[i]));
+        }
+        put_split(xb, kp, i, v);
+    }
+}
+
 template <int HD>
 struct ItemShm {
     float p[kIpMax];       // scores, then weights, of the run's positions
     float red[kWaves][HD];
-    float o[HD];           // the unnormalised output
+    alignas(16) uint16_t op[4][HD];  // the unnormalised output, split (put_split)
     float m, l;            // max score, sum of weights
 };
 
 // Dynamic LDS layout (byte offsets): tagged-word staging, the f32 vector
-// the dot products read, an item's q (with its biases and rotation factors),
-// its K and V rows, the embedding row, and two RMSNorm gain rows (BF16): g1
-// for the items' and KV blocks' input norm, g2 for the FFN norm and the
-// final norm.
+// the VALU dot products read, its split for the matrix-core products (4
+// rows of H padded to 32), an item's q (with its biases and rotation
+// factors), its K and V rows, the embedding row, and two RMSNorm gain rows
+// (BF16): g1 for the items' and KV blocks' input norm, g2 for the FFN norm
+// and the final norm.
 struct LdsLayout {
     int tbw;  // staging words
-    int xs, q, kv, emb, g1, g2, total;
+    int xs, xb, q, kv, emb, g1, g2, total;
 };
 __host__ __device__ inline LdsLayout lds_layout(int H, int hd, int kv_bytes, int ip, int ni, int nbd, int blocks) {
     LdsLayout o{};
     int tbw = imax(imax(H, round_up(ni * kOwn, kChunk) + 2 * ni), imax(nbd * kOwn, imax(2 * hd, 2 * blocks)));
     o.tbw = round_up(tbw + 2, kChunk);
     o.xs = o.tbw * 8;
-    o.q = o.xs + round_up((xpad(H) + 10) * 4, 16);
+    o.xb = o.xs + round_up((xpad(H) + 10) * 4, 16);
+    o.q = o.xb + 4 * round_up(H, 32) * 2;
     o.kv = o.q + round_up(3 * hd * 4, 16);
     o.emb = o.kv + round_up(2 * ip * hd * kv_bytes, 16);
     o.g1 = o.emb + round_up(H * 2, 16);
@@ -640,7 +720,7 @@ __device__ __forceinline__ void item_scores(const float *qs, const uint8_t *k_ld
 }
 
 // All threads: softmax of the nv scores (max, exp, sum) and the weighted V
-// rows: sh.o = sum_p w_p v_p (unnormalised), sh.m, sh.l. Lane owns hd / 64
+// rows: o = sum_p w_p v_p (unnormalised, split into sh.op), sh.m, sh.l. Lane owns hd / 64
 // dimensions, wave w positions w, w + 8, ...; the waves' sums are added in
 // wave order.
 template <int HD, class KT>
@@ -694,39 +774,51 @@ __device__ __forceinline__ void item_softmax_pv(const uint8_t *v_lds, int nv, It
         float o = sh.red[0][tid];
 #pragma unroll
         for (int w = 1; w < kWaves; ++w) o += sh.red[w][tid];
-        sh.o[tid] = o;
+        put_split(&sh.op[0][0], HD, tid, o);
     }
     bar();
 }
 
-// UH: 16-byte units per lane of a row with H columns; RO: rows of H per
-// thread (H <= 512 RO); RGU: gate (and up) rows per wave of an FFN block;
-// UP: 16-byte units of a down_cols row (lanes per row in the down
-// partials); UHB: units per lane of a BF16 head row; NWO: o_proj units per
-// lane of an item (64 / (hd / 8) rows per wave each). Shape values are
-// re-read from the arguments where used (A()) and block roles recomputed
-// from them, so that little stays in scalar registers across the step loop.
+// UH: 16-byte units per lane of a row with H columns (the KV blocks' and
+// the LM head's VALU dot products); KS: K-steps of 32 columns of a row with
+// H columns (H <= 32 KS); OTW: 16-row tiles of H rows per wave (H <= 128
+// OTW); GT: 16-row tiles of an FFN block's gate (and up) rows. Shape values
+// are re-read from the arguments where used (A()) and block roles
+// recomputed from them, so that little stays in scalar registers across the
+// step loop.
+//
+// Matrix-core work per wave (one 16-byte weight unit per lane and MFMA):
+//   items' q: the head's HD / 16 tiles, each split over K between
+//     8 / (HD / 16) waves (QK K-steps each), combined in LDS;
+//   items' o_proj: tiles wave, wave + 8, ... of the H rows, HD / 32 K-steps;
+//   FFN gate/up: 2 GT tiles, each split over K between 8 / (2 GT) waves;
+//   FFN down: tiles wave, wave + 8, ... of the H rows, one K-step (the
+//     block's gate/up rows padded to 32).
 //
 // Each role runs its own step and layer loops (one branch per role), with
 // the LM head and the token reduction shared: a loop carries only its
 // role's weight registers, and a CU's hot code is only its role's.
-template <int HD, int G, class KT, int UH, int RO, int RGU, int UP, int UHB, int NWO>
+template <int HD, int G, class KT, int UH, int KS, int OTW, int GT>
 __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
     using U = Unit<FMT_BF16, 16>;
     constexpr int ROW = HD * (int)sizeof(KT);
-    constexpr int RQ = HD / kWaves;      // an item's q rows per wave
-    constexpr int UO = HD / U::E;        // units of one head's columns of an o_proj row (lanes per row)
-    constexpr int OW = 64 / UO;          // o_proj rows per wave and unit
-    constexpr int NQ = RQ * UH;          // an item's q-row units
-    constexpr int NI = NQ + NWO;         // an item's weight units
-    constexpr int NG = RGU * UH;         // an FFN block's gate (and up) units
-    constexpr int DW = 64 / UP;          // down rows per wave and unit (UP lanes per row)
-    constexpr int ND = (RO * kThreads + DW * kWaves - 1) / (DW * kWaves);  // down units: H <= 512 RO rows
-    constexpr int NF = 2 * NG + ND;      // an FFN block's weight units
-    constexpr int NK = 2 * UH;           // a KV block's weight units
-    static_assert(UP == 1 || UP == 2 || UP == 4 || UP == 8 || UP == 16, "lanes per down row");
-    static_assert(RQ % 2 == 0, "q rows come in rotation pairs");
-    static_assert(8 * UP <= kStage, "down columns beyond the staged outputs");
+    constexpr int KP = 32 * KS;           // padded K of a row with H columns
+    constexpr int QT = HD / 16;           // q tiles of a head
+    constexpr int QWP = kWaves / QT;      // waves per q tile
+    constexpr int QK = (KS + QWP - 1) / QWP;  // K-steps per wave of a q tile
+    constexpr int OK = HD / 32;           // K-steps of an o_proj row's head columns
+    constexpr int NQ = QK;                // an item's q units
+    constexpr int NWO = OTW * OK;         // an item's o_proj units
+    constexpr int NI = NQ + NWO;          // an item's weight units
+    constexpr int GT2 = 2 * GT;           // gate and up tiles of an FFN block
+    constexpr int GWP = kWaves / GT2;     // waves per gate/up tile
+    constexpr int GK = (KS + GWP - 1) / GWP;  // K-steps per wave of a gate/up tile
+    constexpr int NG = GK;                // an FFN block's gate/up units
+    constexpr int ND = OTW;               // an FFN block's down units
+    constexpr int NF = NG + ND;           // an FFN block's weight units
+    constexpr int NK = 2 * UH;            // a KV block's weight units
+    static_assert(HD % 32 == 0 && kWaves % QT == 0 && QK * QWP == KS, "q tiles over the waves");
+    static_assert(kWaves % GT2 == 0 && GK * GWP == KS, "gate/up tiles over the waves");
     // The only read of the kernarg-segment pointer (see opaque()).
     CArgs *const kargs = (CArgs *)__builtin_amdgcn_kernarg_segment_ptr();
     auto A = [kargs]() { return opaque(kargs); };
@@ -769,6 +861,14 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
         if (bf16_src) block_stage<true>(xs, src, H, g, wave_norm_scale<true>(src, H, A()->eps));
         else block_stage<false>(xs, src, H, g, wave_norm_scale<false>(src, H, A()->eps));
     };
+    // The same normed input split for the matrix-core products (xb).
+    auto stage_split = [&](const void *src, bool bf16_src, int gain_off) {
+        const uint16_t *g = (const uint16_t *)(lds + gain_off);
+        uint16_t *xb = (uint16_t *)(lds + A()->lds_xb);
+        const int H = A()->H;
+        if (bf16_src) block_stage_split<true>(xb, KP, src, H, g, wave_norm_scale<true>(src, H, A()->eps));
+        else block_stage_split<false>(xb, KP, src, H, g, wave_norm_scale<false>(src, H, A()->eps));
+    };
     auto tag_base = [&](int s) { return A()->tag0 + (unsigned)(s * fused_phases_per_step(A()->L)); };
 
     // The LM head of step s (BF16, final norm fused) and this block's argmax
@@ -788,7 +888,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
             mark(s, 16 * L);
             const int Wn = (int)gridDim.x * kWaves, gw0 = b * kWaves + wave, V = A()->V;
             const int head_rows = gw0 < V ? (V - 1 - gw0) / Wn + 1 : 0;
-            head_dots<UHB>(A()->head, A()->logits, (const float *)(lds + A()->lds_xs), A()->H, V, gw0, Wn, head_rows,
+            head_dots<UH>(A()->head, A()->logits, (const float *)(lds + A()->lds_xs), A()->H, V, gw0, Wn, head_rows,
                            key, idx);
         }
         block_best(key, idx, sm);
@@ -839,12 +939,15 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
         // KV blocks (the run that holds it), softmax, weighted V rows, and
         // the head's o_proj columns applied to the unnormalised output.
         u32x4 W[NI];
-        // Refill for layer l at position pos: q rows (unit k: row k / UH of
-        // the wave's RQ, lane units), o_proj units (row (k 8 + wave) OW +
-        // lane / UO, unit lane % UO of the head's columns), the input-norm
-        // gains and the run's cached K/V rows (when `act`).
+        // Refill for layer l at position pos: q units (k < NQ: K-step
+        // ks = (wave / QT) QK + k of the head's tile wave % QT, row
+        // 16 (wave % QT) + lane % 16, unit 4 ks + lane / 16), o_proj units
+        // (k = NQ + m OK + j: tile wave + 8 m of the H rows, row 16 t +
+        // lane % 16, K-step j of the head's columns, elements
+        // h HD + 32 j + 8 (lane / 16) ...), the input-norm gains and the
+        // run's cached K/V rows (when `act`).
         auto refill = [&](int l, bool act, long pos) {
-            const int H = A()->H, nH = H / U::E, tid = tid_here(), lane = tid & 63;
+            const int H = A()->H, nH = H / U::E, lane = lane_here(), i16 = lane & 15, g4 = lane >> 4;
             const uint32_t qs = (uint32_t)A()->qkv_stride, os = (uint32_t)A()->o_stride;
             const int qrows = (A()->q_heads + 2 * A()->kv_heads) * HD;
             const Rsrc rq = rsrc(LY(l)->qkv, (size_t)qrows * qs), ro = rsrc(LY(l)->o, (size_t)H * os);
@@ -853,12 +956,12 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
             for (int k = 0; k < NI; ++k) {
                 uint32_t off = kNoRead;
                 if (k < NQ) {
-                    const int unit = lane + 64 * (k % UH), row = h * HD + wave * RQ + k / UH;
-                    if (act && unit < nH) off = (uint32_t)row * qs + (uint32_t)unit * 16u;
+                    const int ks = (wave / QT) * QK + k, unit = 4 * ks + g4, row = h * HD + (wave % QT) * 16 + i16;
+                    if (act && ks < KS && unit < nH) off = (uint32_t)row * qs + (uint32_t)unit * 16u;
                     W[k] = ld_unit(rq, off);
                 } else {
-                    const int r = ((k - NQ) * kWaves + wave) * OW + lane / UO, u = lane % UO;
-                    if (act && r < H) off = (uint32_t)r * os + (uint32_t)(h * HD + U::E * u) * 2u;
+                    const int m = (k - NQ) / OK, j = (k - NQ) % OK, r = (wave + kWaves * m) * 16 + i16;
+                    if (act && r < H) off = (uint32_t)r * os + (uint32_t)(h * HD + 32 * j + 8 * g4) * 2u;
                     W[k] = ld_unit(ro, off);
                 }
             }
@@ -892,10 +995,9 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                 const unsigned tK = tb0 + 5 * l, tP = tK + 1;
                 mark(s, 16 * l);
                 if (active) {
-                    float *xs = (float *)(lds + A()->lds_xs);
                     float *qs = (float *)(lds + A()->lds_q);  // q[hd], bias[hd], cos[hd / 2], sin[hd / 2]
                     uint8_t *k_lds = lds + A()->lds_kv, *v_lds = k_lds + ip * ROW;
-                    const int H = A()->H, nH = H / U::E, rot = A()->rotary, half = rot / 2;
+                    const int H = A()->H, rot = A()->rotary, half = rot / 2;
                     // q's biases (rows of head ih, pair-permuted like the
                     // rows) and rotation factors, loaded before the poll.
                     const float *qbias = LY(l)->qkv_bias;
@@ -912,25 +1014,31 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                     if (l > 0) gather(tb, A()->hid1, H, tK - 1, A()->abort_flag);
                     wait_vm();  // the embedding row, the gains and the K/V rows
                     bar();
-                    if (l == 0) stage_norm(lds + A()->lds_emb, true, A()->lds_g1);
-                    else stage_norm(tb, false, A()->lds_g1);
+                    if (l == 0) stage_split(lds + A()->lds_emb, true, A()->lds_g1);
+                    else stage_split(tb, false, A()->lds_g1);
                     bar();
                     mark(s, 16 * l + 1);
                     {
-                        float y[RQ];
-                        dot_pool<RQ, UH, 0>(W, xs, nH, y);
-                        // Lane j < RQ / 2 finishes rotation pair j of the
-                        // wave's rows (bias, RoPE).
-                        const int ln = lane_here();
-                        float v0 = y[0], v1 = y[1];
+                        // The head's q rows on the matrix cores: tile
+                        // wave % QT over K-steps [(wave / QT) QK, + QK),
+                        // the K parts added in wave order through LDS.
+                        const uint16_t *xq =
+                            (const uint16_t *)(lds + A()->lds_xb) + a_offset(KP) + 32 * (wave / QT) * QK;
+                        // All 64 lanes: the products read every lane's operands.
+                        const float y = kdot<NQ, 0>(xq, W);
+                        if (lane_here() < 16) sm.red[wave][lane_here()] = y;
+                        bar();
+                        // Thread j < HD / 2 finishes rotation pair j (rows
+                        // 2 j and 2 j + 1: bias, RoPE).
+                        const int tid = tid_here();
+                        if (tid < HD / 2) {
+                            const int d0 = 2 * tid, t = d0 / 16, c0 = d0 % 16;
+                            float v0 = sm.red[t][c0], v1 = sm.red[t][c0 + 1];
 #pragma unroll
-                        for (int j = 1; j < RQ / 2; ++j)
-                            if (ln == j) {
-                                v0 = y[2 * j];
-                                v1 = y[2 * j + 1];
+                            for (int kp = 1; kp < QWP; ++kp) {
+                                v0 += sm.red[t + QT * kp][c0];
+                                v1 += sm.red[t + QT * kp][c0 + 1];
                             }
-                        if (ln < RQ / 2) {
-                            const int d0 = wave * RQ + 2 * ln;
                             if (qbias) {
                                 v0 = v0 + qs[HD + d0];
                                 v1 = v1 + qs[HD + d0 + 1];
@@ -967,29 +1075,30 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                     mark(s, 16 * l + 4);
                     item_softmax_pv<HD, KT>(v_lds, nc + (has_new ? 1 : 0), ish);
                     mark(s, 16 * l + 5);
-                    // o_proj columns of head ih times the unnormalised output:
-                    // UO lanes per row, one unit each (elements in order),
-                    // summed over the row's lanes by a fixed tree; all rows
-                    // first, then the stores. Partial of owner r / 8, item b;
-                    // the run's max and sum once.
+                    // o_proj columns of head ih times the unnormalised output
+                    // on the matrix cores: tiles wave + 8 m of the H rows
+                    // over the head's OK K-steps, each row stored as owner
+                    // r / 8's partial of item b (two rows per store); the
+                    // run's max and sum once.
                     {
-                        const int ln = lane_here();
-                        float ov[U::E], po[NWO];
+                        const int aoff = a_offset(HD);
+                        u32x4 oa[OK];
 #pragma unroll
-                        for (int e = 0; e < U::E; ++e) ov[e] = ish.o[(ln % UO) * U::E + e];
-#pragma unroll
-                        for (int k = 0; k < NWO; ++k) {
-                            const u32x4 w = W[NQ + k];
-                            const uint32_t raw[4] = {w[0], w[1], w[2], w[3]};
-                            float acc = 0.f;
-                            U::decode(raw, [&](int e, float x) { acc = fmaf(x, ov[e], acc); });
-                            po[k] = group_sum<UO>(acc);
-                        }
+                        for (int j = 0; j < OK; ++j) oa[j] = a_frag(&ish.op[0][0], aoff, j);
                         const int ni = A()->ni;
                         uint64_t *part = A()->part;
-                        store_rows<NWO, OW, UO>(po, sm.scr[wave], wave, H, tP, [&](int r) {
-                            return part + ((size_t)(r / kOwn) * ni + b) * kOwn + r % kOwn;
-                        });
+                        f32x4 acc[OTW];
+#pragma unroll
+                        for (int m = 0; m < OTW; ++m) {
+                            acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                            for (int j = 0; j < OK; ++j) acc[m] = mfma_bf16(oa[j], W[NQ + m * OK + j], acc[m]);
+                        }
+#pragma unroll
+                        for (int m = 0; m < OTW; ++m)
+                            store_tile(tile_dot(acc[m]), (wave + kWaves * m) * 16, H, tP, [&](int r) {
+                                return part + ((size_t)(r / kOwn) * ni + b) * kOwn + r % kOwn;
+                            });
                         if (tid_here() == 0) stf2(A()->ml + 2 * b, ish.m, ish.l, tP);
                     }
                     bar();
@@ -1116,26 +1225,29 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
         // SwiGLU and their down columns; owners sum the down partials and
         // add the residual.
         u32x4 W[NF];
-        // Refill for layer l: gate rows (unit k: row w + 8 (k / UH)), up rows,
-        // down_cols units (row (k 8 + wave) DW + lane / UP, unit lane % UP),
-        // and the gains of the FFN norm.
+        // Refill for layer l: gate/up units (k < NG: tile T = wave % GT2,
+        // gate tiles first, then up; K-step ks = (wave / GT2) GK + k; row
+        // f rb + 16 (T % GT) + lane % 16, unit 4 ks + lane / 16), down units
+        // (k = NG + m: tile wave + 8 m of the H rows, row 16 t + lane % 16
+        // of the block's down_cols, unit lane / 16) and the gains of the FFN
+        // norm.
         auto refill = [&](int l, bool act) {
-            const int H = A()->H, nH = H / U::E, lane = lane_here();
+            const int H = A()->H, nH = H / U::E, lane = lane_here(), i16 = lane & 15, g4 = lane >> 4;
             const uint32_t gs = (uint32_t)A()->gu_stride;
             const int rb = A()->rb, rp = A()->rp, f = fIdx(), I = A()->I;
             const Rsrc rg = rsrc(LY(l)->gate, (size_t)I * gs), ru = rsrc(LY(l)->up, (size_t)I * gs);
             const Rsrc rd = rsrc(LY(l)->down_cols, (size_t)A()->nf * H * rp * 2);
+            const int T = wave % GT2, jj = (T % GT) * 16 + i16, row = f * rb + jj;
 #pragma unroll
             for (int k = 0; k < NF; ++k) {
                 uint32_t off = kNoRead;
-                if (k < 2 * NG) {
-                    const int jj = wave + kWaves * ((k % NG) / UH), unit = lane + 64 * (k % UH), row = f * rb + jj;
-                    if (act && jj < rb && row < I && unit < nH) off = (uint32_t)row * gs + (uint32_t)unit * 16u;
-                    W[k] = ld_unit(k < NG ? rg : ru, off);
+                if (k < NG) {
+                    const int ks = (wave / GT2) * GK + k, unit = 4 * ks + g4;
+                    if (act && jj < rb && row < I && ks < KS && unit < nH) off = (uint32_t)row * gs + (uint32_t)unit * 16u;
+                    W[k] = ld_unit(T < GT ? rg : ru, off);
                 } else {
-                    const int r = ((k - 2 * NG) * kWaves + wave) * DW + lane / UP, u = lane % UP;
-                    if (act && r < H && u * 16 < rp * 2)
-                        off = ((uint32_t)(f * H + r) * (uint32_t)rp) * 2u + (uint32_t)u * 16u;
+                    const int r = (wave + kWaves * (k - NG)) * 16 + i16;
+                    if (act && r < H && g4 * 8 < rp) off = ((uint32_t)(f * H + r) * (uint32_t)rp) * 2u + (uint32_t)g4 * 16u;
                     W[k] = ld_unit(rd, off);
                 }
             }
@@ -1172,39 +1284,35 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                            A()->abort_flag);
                     bar();
                     mark(s, 16 * l + 8);
-                    // The merge weights once per block (wave 0, lane h):
-                    // w_s = exp(m_s - M) over the head's runs, L = sum_s w_s
-                    // l_s in split order, weight of run s w_s / L.
+                    float contrib = 0.f;
                     const int ln = lane_here();
-                    if (wave == 0 && ln < Q) {
+                    if (ln < Q) {
+                        // Every split's max, sum and partial of this row
+                        // (splits past S weigh nothing), then the fold in
+                        // split order.
                         const uint64_t *ml = tb + round_up(na, kChunk);
-                        float ms[kMaxSplits], ls[kMaxSplits];
+                        float ms[kMaxSplits], ls[kMaxSplits], ps[kMaxSplits];
 #pragma unroll
                         for (int sp = 0; sp < kMaxSplits; ++sp) {
                             const int it = min(sp, S - 1) * Q + ln;
                             ms[sp] = sp < S ? val_of(ml[2 * it]) : -INFINITY;
                             ls[sp] = val_of(ml[2 * it + 1]);
+                            ps[sp] = val_of(tb[it * kOwn + wave]);
                         }
                         float mx = -INFINITY;
 #pragma unroll
                         for (int sp = 0; sp < kMaxSplits; ++sp) mx = fmaxf(mx, ms[sp]);
-                        float ws[kMaxSplits], Ls = 0.f;
+                        float Ls = 0.f, acc = 0.f;
 #pragma unroll
                         for (int sp = 0; sp < kMaxSplits; ++sp) {
-                            ws[sp] = sp < S ? expf(ms[sp] - mx) : 0.f;
-                            if (sp < S) Ls = fmaf(ws[sp], ls[sp], Ls);
+                            if (sp < S) {
+                                const float w = expf(ms[sp] - mx);
+                                Ls = fmaf(w, ls[sp], Ls);
+                                acc = fmaf(w, ps[sp], acc);
+                            }
                         }
-                        const float linv = 1.0f / Ls;
-#pragma unroll
-                        for (int sp = 0; sp < kMaxSplits; ++sp)
-                            if (sp < S) sm.coef[sp * Q + ln] = ws[sp] * linv;
+                        contrib = acc * (1.0f / Ls);
                     }
-                    bar();
-                    // The row's o_proj value: every run's partial times its
-                    // weight, lane i taking runs i and i + 64, then the fixed
-                    // wave tree.
-                    float contrib = 0.f;
-                    for (int it = ln; it < S * Q; it += 64) contrib = fmaf(sm.coef[it], val_of(tb[it * kOwn + wave]), contrib);
                     const float o = wave_sum(contrib);
                     if (r < H) {
                         float v = o;
@@ -1222,52 +1330,58 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                 // ---- Gate/up (fused RMSNorm), SwiGLU, down partials of every
                 // hidden row.
                 if (hasRows()) {
-                    float *xs = (float *)(lds + A()->lds_xs);
                     gather(tb, A()->hid0, H, tC, A()->abort_flag);
                     wait_vm();  // the gains
                     bar();
-                    stage_norm(tb, false, A()->lds_g2);
+                    stage_split(tb, false, A()->lds_g2);
                     bar();
                     mark(s, 16 * l + 10);
                     const int rb = A()->rb, f = fIdx(), I = A()->I;
                     {
-                        float yg[RGU], yu[RGU];
-                        dot_pool<RGU, UH, 0>(W, xs, nH, yg);
-                        dot_pool<RGU, UH, NG>(W, xs, nH, yu);
+                        // Gate and up rows on the matrix cores: tile
+                        // wave % GT2 over K-steps [(wave / GT2) GK, + GK),
+                        // the K parts added in wave order through LDS.
+                        const uint16_t *xg =
+                            (const uint16_t *)(lds + A()->lds_xb) + a_offset(KP) + 32 * (wave / GT2) * GK;
+                        const float y = kdot<NG, 0>(xg, W);  // all 64 lanes
+                        if (lane_here() < 16) sm.red[wave][lane_here()] = y;
+                        bar();
+                        // Thread j < 32: SwiGLU of the block's row j (zero
+                        // past its rows), split for the down product.
+                        const int tid = tid_here();
+                        if (tid < 32) {
+                            float v = 0.f;
+                            if (tid < rb && f * rb + tid < I) {
+                                const int t = tid / 16, c = tid % 16;
+                                float gv = sm.red[t][c], uv = sm.red[GT + t][c];
 #pragma unroll
-                        for (int j = 0; j < RGU; ++j) {
-                            const int jj = wave + kWaves * j, row = f * rb + jj;
-                            if (jj < rb && row < I && lane_here() == 0) {
-                                const float gv = yg[j], uv = yu[j];
-                                sm.out[jj] = gv * (uv / (1.0f + expf(-gv)));
+                                for (int kp = 1; kp < GWP; ++kp) {
+                                    gv += sm.red[t + GT2 * kp][c];
+                                    uv += sm.red[GT + t + GT2 * kp][c];
+                                }
+                                v = gv * (uv / (1.0f + expf(-gv)));
                             }
+                            put_split(&sm.dp[0][0], 32, tid, v);
                         }
-                        // Zeros after the block's outputs, up to the padded row.
-                        const int cnt = min(rb, I - f * rb);
-                        if (tid_here() >= cnt && tid_here() < 8 * UP) sm.out[tid_here()] = 0.f;
                     }
                     bar();
                     mark(s, 16 * l + 11);
-                    // Down partials: UP lanes per row, one unit of the block's
-                    // columns each (elements in order), summed over the row's
-                    // lanes by a fixed tree.
-                    const int nbd = A()->nbd, ln = lane_here();
-                    float av[U::E];
+                    // Down partials on the matrix cores: tiles wave + 8 m of
+                    // the H rows, one K-step over the block's 32 columns;
+                    // each row stored as owner r / 8's partial of block f
+                    // (two rows per store).
+                    {
+                        const u32x4 da = a_frag(&sm.dp[0][0], a_offset(32), 0);
+                        const int nbd = A()->nbd;
+                        uint64_t *pdown = A()->pdown;
+                        f32x4 acc[ND];
 #pragma unroll
-                    for (int e = 0; e < U::E; ++e) av[e] = sm.out[(ln % UP) * U::E + e];
-                    float pd[ND];
+                        for (int m = 0; m < ND; ++m) acc[m] = mfma_bf16(da, W[NG + m], f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-                    for (int k = 0; k < ND; ++k) {
-                        const u32x4 w = W[2 * NG + k];
-                        const uint32_t raw[4] = {w[0], w[1], w[2], w[3]};
-                        float acc = 0.f;
-                        U::decode(raw, [&](int e, float x) { acc = fmaf(x, av[e], acc); });
-                        pd[k] = group_sum<UP>(acc);
+                        for (int m = 0; m < ND; ++m)
+                            store_tile(tile_dot(acc[m]), (wave + kWaves * m) * 16, H, tD,
+                                       [&](int r) { return pdown + ((size_t)(r / kOwn) * nbd + f) * kOwn + r % kOwn; });
                     }
-                    uint64_t *pdown = A()->pdown;
-                    store_rows<ND, DW, UP>(pd, sm.scr[wave], wave, H, tD, [&](int r) {
-                        return pdown + ((size_t)(r / kOwn) * nbd + f) * kOwn + r % kOwn;
-                    });
                     mark(s, 16 * l + 12);
                 }
 
@@ -1303,15 +1417,15 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
 }
 
 struct Variant {
-    int hd, g, uh, ro, rgu, up, uhb, nwo;
+    int hd, g, uh, ks, otw, gt;
 };
 
 // Shapes with a built kernel: Qwen2-0.5B (hidden 896, 14/2 heads of 64,
 // intermediate 4864) and the two small test shapes.
 constexpr Variant kVariants[] = {
-    {64, 7, 2, 2, 4, 4, 2, 14},
-    {64, 2, 1, 1, 1, 1, 1, 2},
-    {128, 4, 1, 1, 1, 1, 1, 8},
+    {64, 7, 2, 28, 7, 2},
+    {64, 2, 1, 4, 1, 1},
+    {128, 4, 1, 8, 2, 1},
 };
 
 int units_per_lane(int cols, int elems_per_unit) { return (cols / elems_per_unit + 63) / 64; }
@@ -1343,25 +1457,24 @@ const Variant *find_variant(int fmt, int H, int q_heads, int kv_heads, int hd, i
     const int g = q_heads / kv_heads, qd = q_heads * hd;
     if (H % 8 || qd % 8 || I % 8 || H > 1024 || q_heads > 64) return nullptr;
     const FusedGeom geo = geometry(H, q_heads, kv_heads, hd, I, kv_f32, blocks);
-    if (geo.s_cap < 1 || geo.ip_max < TP || geo.no > geo.nf || geo.rb > kStage || geo.kv0 < q_heads ||
-        geo.ni_max > kWaveRows)
-        return nullptr;
+    // The down product takes a block's gate/up rows as one K-step of 32.
+    if (geo.s_cap < 1 || geo.ip_max < TP || geo.no > geo.nf || geo.rp > 32 || geo.kv0 < q_heads) return nullptr;
     const LdsLayout lay = lds_layout(H, hd, kv_f32 ? 4 : 2, geo.ip_max, geo.ni_max, geo.nbd, blocks);
     if (lay.tbw > kMaxGather || (size_t)lay.total + static_lds_bytes(hd) > device_max_lds()) return nullptr;
     for (const Variant &v : kVariants) {
         if (v.hd != hd || v.g != g) continue;
-        if (units_per_lane(H, 8) > v.uh || (H + kThreads - 1) / kThreads > v.ro) continue;
-        if ((geo.rb + kWaves - 1) / kWaves > v.rgu || geo.rp / 8 > v.up || units_per_lane(H, 8) > v.uhb) continue;
-        // o_proj units: one per o_proj row of 64 / (hd / 8) rows per wave
-        if ((H + kWaves * 64 / (hd / 8) - 1) / (kWaves * 64 / (hd / 8)) > v.nwo) continue;
+        // The split input holds exactly KS K-steps (the LDS layout pads H
+        // to 32); H rows in OTW tiles per wave; gate rows in GT tiles.
+        if (units_per_lane(H, 8) > v.uh || (H + 31) / 32 != v.ks) continue;
+        if ((H + 16 * kWaves - 1) / (16 * kWaves) > v.otw || (geo.rb + 15) / 16 > v.gt) continue;
         return &v;
     }
     return nullptr;
 }
 
-template <int HD, int G, class KT, int UH, int RO, int RGU, int UP, int UHB, int NWO>
+template <int HD, int G, class KT, int UH, int KS, int OTW, int GT>
 int launch_one(FusedArgs a, int nb, hipStream_t s) {
-    auto k = decode_flow_kernel<HD, G, KT, UH, RO, RGU, UP, UHB, NWO>;
+    auto k = decode_flow_kernel<HD, G, KT, UH, KS, OTW, GT>;
     const FusedGeom geo = geometry(a.H, a.q_heads, a.kv_heads, HD, a.I, sizeof(KT) == 4, nb);
     // Positions per item: the shortest run that lets the launch's longest
     // context fit the item blocks.
@@ -1382,6 +1495,7 @@ int launch_one(FusedArgs a, int nb, hipStream_t s) {
     a.head_blocks = std::min(nb, (a.V + kWaves - 1) / kWaves);
     const LdsLayout lay = lds_layout(a.H, HD, (int)sizeof(KT), ip, a.ni, a.nbd, nb);
     a.lds_xs = lay.xs;
+    a.lds_xb = lay.xb;
     a.lds_q = lay.q;
     a.lds_kv = lay.kv;
     a.lds_emb = lay.emb;
@@ -1409,9 +1523,9 @@ int launch_one(FusedArgs a, int nb, hipStream_t s) {
 
 template <class KT>
 int launch_kt(const Variant &v, const FusedArgs &a, int nb, hipStream_t s) {
-    if (v.hd == 64 && v.g == 7) return launch_one<64, 7, KT, 2, 2, 4, 4, 2, 14>(a, nb, s);
-    if (v.hd == 64 && v.g == 2) return launch_one<64, 2, KT, 1, 1, 1, 1, 1, 2>(a, nb, s);
-    if (v.hd == 128 && v.g == 4) return launch_one<128, 4, KT, 1, 1, 1, 1, 1, 8>(a, nb, s);
+    if (v.hd == 64 && v.g == 7) return launch_one<64, 7, KT, 2, 28, 7, 2>(a, nb, s);
+    if (v.hd == 64 && v.g == 2) return launch_one<64, 2, KT, 1, 4, 1, 1>(a, nb, s);
+    if (v.hd == 128 && v.g == 4) return launch_one<128, 4, KT, 1, 8, 2, 1>(a, nb, s);
     return fail("HIP backend: no persistent decode kernel for this shape.");
 }
 

@@ -70,7 +70,7 @@ struct FusedArgs {
     // offsets).
     int ni, ip, splits;         // item blocks (q_heads * splits), positions per item
     int kv0, nkv, f0, nf, no, nbd, rb, rp, head_blocks;
-    int lds_xs, lds_q, lds_kv, lds_emb, lds_g1, lds_g2, lds_total;
+    int lds_xs, lds_xb, lds_q, lds_kv, lds_emb, lds_g1, lds_g2, lds_total;
 };
 
 // Phases per decode step: 5 per layer (new K/V, item partials, attention
