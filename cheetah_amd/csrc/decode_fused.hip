@@ -76,6 +76,13 @@ constexpr int kMaxSplits = 16;         // attention splits per q head, at most
 constexpr int kIpMax = 4 * TP;         // positions per attention item, at most
 constexpr int kKvLdsMax = 64 * 1024;   // LDS for one item's K and V rows, at most
 constexpr int kChunk = 128;            // tagged words per wave-wide 16-byte-per-lane load
+constexpr int kXcds = 8;               // the dispatcher places block b on XCD b % 8 (each XCD has its own L2)
+
+// Blocks per attention split: q heads rounded up to the XCD count, so that
+// item (split s, head h) at block s * heads_padded + h runs on XCD h % 8
+// for every s: the splits of one head, which read the same q rows and
+// o_proj columns, share one L2.
+__host__ __device__ constexpr int heads_padded(int q_heads) { return (q_heads + kXcds - 1) / kXcds * kXcds; }
 constexpr long kSpinLimit = 1L << 20;
 constexpr uint32_t kNoRead = 0x80000000u;  // buffer offset past every range
 
@@ -85,6 +92,13 @@ constexpr uint32_t kNoRead = 0x80000000u;  // buffer offset past every range
 // the unpadded 32-byte stride, lanes 8 apart share banks and seven waves
 // reading one vector serialise on the conflicts).
 __host__ __device__ constexpr int xpad(int i) { return (i >> 3) * 10 + (i & 7); }
+
+// Row stride (elements) of a split vector of k (a multiple of 8) elements
+// per part: 16 bytes past the row, so that the four rows start four LDS
+// banks apart. The A operand's lanes 0..15 read rows 0, 1, 2, 3, 3, ...
+// at the same column; at a stride of a multiple of 128 bytes every row
+// would start on the same bank and each read would serialise four ways.
+__host__ __device__ constexpr int split_stride(int k) { return k + 8; }
 
 // threadIdx.x through an opaque copy: address arithmetic stays next to its
 // use inside the step loop instead of being hoisted out of it and held in
@@ -289,6 +303,28 @@ __device__ __forceinline__ void gather(uint64_t *dst, const uint64_t *src, int n
     gather(dst, Ranges{src, src, n, 0}, tag, abort_flag);
 }
 
+// One wave: polls words [base, base + 128) of src (n words in all) into
+// registers until every one of them carries `tag` (lane l holds words
+// base + 2 l and base + 2 l + 1 as value, tag, value, tag; lanes past n
+// hold src[0], counted as fresh). Bounded like gather_regs: on timeout it
+// raises the abort word and returns what it loaded.
+__device__ __forceinline__ u32x4 poll_chunk(const uint64_t *src, int base, int n, unsigned tag, int *abort_flag) {
+    const int lane = lane_here(), cnt = n - base;
+    const uint64_t *p[2] = {lane * 2 < cnt ? src + base + lane * 2 : src, src};
+    long spins = 0;
+    while (true) {
+        u32x4 r[2];
+        poll16<1>(r, p);
+        const bool done = !__any(!unit_fresh(r[0], lane * 2, cnt, tag));
+        const bool give_up = !done && (++spins > kSpinLimit || ((spins & 15) == 0 && aborted(abort_flag)));
+        if (done || give_up) {
+            if (give_up) raise_abort(abort_flag);
+            return r[0];
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
 // One wave: starts copying `bytes` (a multiple of 16) from global memory
 // into LDS; completion is awaited with wait_vm.
 __device__ __forceinline__ void dma_bytes(void *dst, const void *src, int bytes) {
@@ -407,7 +443,8 @@ struct Shm {
     int token;                 // the step's sampled id
     float out[kStage];         // a phase's outputs of the block, stored as one run
     float red[kWaves][16];     // each wave's tile outputs (matrix-core phases split over K)
-    alignas(16) uint16_t dp[4][32];  // an FFN block's SwiGLU outputs, split (put_split)
+    float ss[kWaves];          // each wave's sum of squares of its chunk (polled RMSNorm input)
+    alignas(16) uint16_t dp[4][split_stride(32)];  // an FFN block's SwiGLU outputs, split (put_split)
 };
 
 // Reduces (key, idx) over the block; the result lands in every thread.
@@ -543,22 +580,23 @@ __device__ __forceinline__ void x_split(float x, uint16_t &hi, uint16_t &mid, ui
     lo = f32_bf16_rne(r1 - bf16_f32(mid));
 }
 
-// The split of element i of a K-padded vector in LDS: xb[p kp + i] holds
-// part p (p < 3) and xb[3 kp + i] a zero, the rows the A operand reads.
-__device__ __forceinline__ void put_split(uint16_t *xb, int kp, int i, float x) {
+// The split of element i of a K-padded vector in LDS (row stride st,
+// split_stride): xb[p st + i] holds part p (p < 3) and xb[3 st + i] a zero,
+// the rows the A operand reads.
+__device__ __forceinline__ void put_split(uint16_t *xb, int st, int i, float x) {
     uint16_t hi, mid, lo;
     x_split(x, hi, mid, lo);
     xb[i] = hi;
-    xb[kp + i] = mid;
-    xb[2 * kp + i] = lo;
-    xb[3 * kp + i] = 0;
+    xb[st + i] = mid;
+    xb[2 * st + i] = lo;
+    xb[3 * st + i] = 0;
 }
 
-// This lane's offset (elements) into a split vector for K-step 0: row
-// min(lane % 16, 3), elements 8 (lane / 16) ...
-__device__ __forceinline__ int a_offset(int kp) {
+// This lane's offset (elements) into a split vector (row stride st) for
+// K-step 0: row min(lane % 16, 3), elements 8 (lane / 16) ...
+__device__ __forceinline__ int a_offset(int st) {
     const int l = lane_here();
-    return min(l & 15, 3) * kp + 8 * (l >> 4);
+    return min(l & 15, 3) * st + 8 * (l >> 4);
 }
 __device__ __forceinline__ u32x4 a_frag(const uint16_t *xb, int aoff, int ks) {
     return *(const u32x4 *)(xb + aoff + 32 * ks);
@@ -605,10 +643,12 @@ __device__ __forceinline__ void store_tile(float y, int r0, int n, unsigned tag,
 }
 
 // All waves: the split (put_split) of x[i] * (inv * g[i]) for i < n into
-// the K-padded xb (kp elements per part), zeros for n <= i < kp.
+// the K-padded xb (kp elements per part, row stride split_stride(kp)),
+// zeros for n <= i < kp.
 template <bool BF16_SRC>
 __device__ __forceinline__ void block_stage_split(uint16_t *xb, int kp, const void *src, int n, const uint16_t *g,
                                                   float inv) {
+    const int st = split_stride(kp);
     for (int i = tid_here(); i < kp; i += kThreads) {
         float v = 0.f;
         if (i < n) {
@@ -616,7 +656,7 @@ __device__ __forceinline__ void block_stage_split(uint16_t *xb, int kp, const vo
             else v = val_of(((const uint64_t *)src)[i]);
             v = v * (inv * bf16_f32(g[i]));
         }
-        put_split(xb, kp, i, v);
+        put_split(xb, st, i, v);
     }
 }
 
@@ -624,7 +664,7 @@ template <int HD>
 struct ItemShm {
     float p[kIpMax];       // scores, then weights, of the run's positions
     float red[kWaves][HD];
-    alignas(16) uint16_t op[4][HD];  // the unnormalised output, split (put_split)
+    alignas(16) uint16_t op[4][split_stride(HD)];  // the unnormalised output, split (put_split)
     float m, l;            // max score, sum of weights
 };
 
@@ -644,7 +684,7 @@ __host__ __device__ inline LdsLayout lds_layout(int H, int hd, int kv_bytes, int
     o.tbw = round_up(tbw + 2, kChunk);
     o.xs = o.tbw * 8;
     o.xb = o.xs + round_up((xpad(H) + 10) * 4, 16);
-    o.q = o.xb + 4 * round_up(H, 32) * 2;
+    o.q = o.xb + 4 * split_stride(round_up(H, 32)) * 2;
     o.kv = o.q + round_up(3 * hd * 4, 16);
     o.emb = o.kv + round_up(2 * ip * hd * kv_bytes, 16);
     o.g1 = o.emb + round_up(H * 2, 16);
@@ -774,7 +814,7 @@ __device__ __forceinline__ void item_softmax_pv(const uint8_t *v_lds, int nv, It
         float o = sh.red[0][tid];
 #pragma unroll
         for (int w = 1; w < kWaves; ++w) o += sh.red[w][tid];
-        put_split(&sh.op[0][0], HD, tid, o);
+        put_split(&sh.op[0][0], split_stride(HD), tid, o);
     }
     bar();
 }
@@ -830,20 +870,25 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
     const int b = blockIdx.x;
     uint64_t *tb = (uint64_t *)lds;
 
-    // Roles: items [0, ni) (item = split * q_heads + head), KV blocks
+    // Roles: items (split s, head h) at block s * heads_padded + h for
+    // s < splits (item index s * q_heads + h), KV blocks
     // [kv0, kv0 + nkv) (wave w of KV block k: rotation pair 8 k + w of the
     // K/V rows), FFN blocks [f0, f0 + nf): block f owns gate/up rows
     // [f rb, f rb + rb) (wave w rows w, w + 8, ...) and, for f < no, the
     // residual rows 8 f + w. Blocks in none of these only join the LM head.
-    auto isItem = [&]() { return b < A()->ni; };
+    auto isItem = [&]() {
+        const int qp = heads_padded(A()->q_heads);
+        return b < A()->splits * qp && b % qp < A()->q_heads;
+    };
     auto isKV = [&]() { return b >= A()->kv0 && b < A()->kv0 + A()->nkv; };
     auto fIdx = [&]() { return b - A()->f0; };
     auto isFFN = [&]() { return b >= A()->f0; };
     auto isOwner = [&]() { return isFFN() && fIdx() < A()->no; };
     auto hasRows = [&]() { return isFFN() && fIdx() < A()->nbd; };
     auto hasHead = [&]() { return b * kWaves < A()->V; };
-    auto itHead = [&]() { return b % A()->q_heads; };
-    auto itSplit = [&]() { return b / A()->q_heads; };
+    auto itHead = [&]() { return b % heads_padded(A()->q_heads); };
+    auto itSplit = [&]() { return b / heads_padded(A()->q_heads); };
+    auto itIdx = [&]() { return itSplit() * A()->q_heads + itHead(); };
     auto kvPair = [&]() { return (b - A()->kv0) * kWaves + wave; };
     auto ownRow = [&]() { return fIdx() * kOwn + wave; };
 
@@ -868,6 +913,45 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
         const int H = A()->H;
         if (bf16_src) block_stage_split<true>(xb, KP, src, H, g, wave_norm_scale<true>(src, H, A()->eps));
         else block_stage_split<false>(xb, KP, src, H, g, wave_norm_scale<false>(src, H, A()->eps));
+    };
+    // A normed input straight from the tagged words src (H <= 1024): wave w
+    // polls chunk w (words [128 w, 128 w + 128)) into registers and adds up
+    // the squares of its values; after the barrier every thread folds the
+    // eight wave sums in wave order into the RMSNorm scale (ops.rs:646-652)
+    // and each lane splits its own two values (times the gains) into xb,
+    // two elements per LDS store. The words never pass through LDS, and the
+    // scale costs one DPP reduction per wave instead of a strided pass over
+    // the whole vector. Also waits for the wave's loads and copies in flight
+    // (wait_vm) before the barrier. The caller's barrier publishes xb.
+    auto stage_split_polled = [&](const uint64_t *src, unsigned tag, int gain_off) {
+        const int H = A()->H, lane = lane_here(), base = wave * kChunk, i0 = base + 2 * lane;
+        float v0 = 0.f, v1 = 0.f, ss = 0.f;
+        if (base < H) {
+            const u32x4 r = poll_chunk(src, base, H, tag, A()->abort_flag);
+            v0 = i0 < H ? __uint_as_float(r[0]) : 0.f;
+            v1 = i0 + 1 < H ? __uint_as_float(r[2]) : 0.f;
+            ss = wave_sum(fmaf(v1, v1, v0 * v0));
+        }
+        if (lane == 0) sm.ss[wave] = ss;
+        wait_vm();
+        bar();
+        float tot = sm.ss[0];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) tot += sm.ss[w];
+        const float inv = 1.0f / sqrtf(tot / (float)H + A()->eps);
+        // Elements [H, KP) are zeros: they lie in the chunk that holds H - 1.
+        if (base < H && i0 < KP) {
+            const uint16_t *g = (const uint16_t *)(lds + gain_off);
+            const uint32_t gw = i0 < H ? *(const uint32_t *)(g + i0) : 0u;
+            uint16_t a[3], c[3];
+            x_split(v0 * (inv * bf16_lo(gw)), a[0], a[1], a[2]);
+            x_split(v1 * (inv * bf16_hi(gw)), c[0], c[1], c[2]);
+            uint32_t *xb = (uint32_t *)(lds + A()->lds_xb);
+            constexpr int st = split_stride(KP) / 2;  // row stride in 32-bit words
+#pragma unroll
+            for (int p = 0; p < 3; ++p) xb[p * st + i0 / 2] = (uint32_t)a[p] | ((uint32_t)c[p] << 16);
+            xb[3 * st + i0 / 2] = 0u;
+        }
     };
     auto tag_base = [&](int s) { return A()->tag0 + (unsigned)(s * fused_phases_per_step(A()->L)); };
 
@@ -1011,11 +1095,14 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                             qs[2 * HD + HD / 2 + i] = A()->rope_sin[pos * half + i];
                         }
                     }
-                    if (l > 0) gather(tb, A()->hid1, H, tK - 1, A()->abort_flag);
-                    wait_vm();  // the embedding row, the gains and the K/V rows
-                    bar();
-                    if (l == 0) stage_split(lds + A()->lds_emb, true, A()->lds_g1);
-                    else stage_split(tb, false, A()->lds_g1);
+                    // (wait_vm: the embedding row, the gains and the K/V rows)
+                    if (l > 0) {
+                        stage_split_polled(A()->hid1, tK - 1, A()->lds_g1);
+                    } else {
+                        wait_vm();
+                        bar();
+                        stage_split(lds + A()->lds_emb, true, A()->lds_g1);
+                    }
                     bar();
                     mark(s, 16 * l + 1);
                     {
@@ -1023,7 +1110,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                         // wave % QT over K-steps [(wave / QT) QK, + QK),
                         // the K parts added in wave order through LDS.
                         const uint16_t *xq =
-                            (const uint16_t *)(lds + A()->lds_xb) + a_offset(KP) + 32 * (wave / QT) * QK;
+                            (const uint16_t *)(lds + A()->lds_xb) + a_offset(split_stride(KP)) + 32 * (wave / QT) * QK;
                         // All 64 lanes: the products read every lane's operands.
                         const float y = kdot<NQ, 0>(xq, W);
                         if (lane_here() < 16) sm.red[wave][lane_here()] = y;
@@ -1081,12 +1168,12 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                     // r / 8's partial of item b (two rows per store); the
                     // run's max and sum once.
                     {
-                        const int aoff = a_offset(HD);
+                        const int aoff = a_offset(split_stride(HD));
                         u32x4 oa[OK];
 #pragma unroll
                         for (int j = 0; j < OK; ++j) oa[j] = a_frag(&ish.op[0][0], aoff, j);
-                        const int ni = A()->ni;
-                        uint64_t *part = A()->part;
+                        const int ni = A()->ni, it = __builtin_amdgcn_readfirstlane(itIdx());
+                        uint64_t *part = A()->part + (size_t)it * kOwn;
                         f32x4 acc[OTW];
 #pragma unroll
                         for (int m = 0; m < OTW; ++m) {
@@ -1097,9 +1184,9 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
 #pragma unroll
                         for (int m = 0; m < OTW; ++m)
                             store_tile(tile_dot(acc[m]), (wave + kWaves * m) * 16, H, tP, [&](int r) {
-                                return part + ((size_t)(r / kOwn) * ni + b) * kOwn + r % kOwn;
+                                return part + (size_t)(r / kOwn) * ni * kOwn + r % kOwn;
                             });
-                        if (tid_here() == 0) stf2(A()->ml + 2 * b, ish.m, ish.l, tP);
+                        if (tid_here() == 0) stf2(A()->ml + 2 * it, ish.m, ish.l, tP);
                     }
                     bar();
                     mark(s, 16 * l + 6);
@@ -1322,7 +1409,10 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                     }
                     bar();
                     const int cnt = min(kOwn, H - fIdx() * kOwn);
-                    if (wave == 0 && lane_here() < cnt)
+                    // Stored by the wave that polls no chunk of the gather
+                    // that follows: a poll's wait also waits for the
+                    // acknowledgement of its own wave's stores.
+                    if (wave == kDmaWave && lane_here() < cnt)
                         stf(A()->hid0 + fIdx() * kOwn + lane_here(), sm.out[lane_here()], tC);
                     mark(s, 16 * l + 9);
                 }
@@ -1330,10 +1420,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                 // ---- Gate/up (fused RMSNorm), SwiGLU, down partials of every
                 // hidden row.
                 if (hasRows()) {
-                    gather(tb, A()->hid0, H, tC, A()->abort_flag);
-                    wait_vm();  // the gains
-                    bar();
-                    stage_split(tb, false, A()->lds_g2);
+                    stage_split_polled(A()->hid0, tC, A()->lds_g2);  // (wait_vm: the gains)
                     bar();
                     mark(s, 16 * l + 10);
                     const int rb = A()->rb, f = fIdx(), I = A()->I;
@@ -1342,7 +1429,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                         // wave % GT2 over K-steps [(wave / GT2) GK, + GK),
                         // the K parts added in wave order through LDS.
                         const uint16_t *xg =
-                            (const uint16_t *)(lds + A()->lds_xb) + a_offset(KP) + 32 * (wave / GT2) * GK;
+                            (const uint16_t *)(lds + A()->lds_xb) + a_offset(split_stride(KP)) + 32 * (wave / GT2) * GK;
                         const float y = kdot<NG, 0>(xg, W);  // all 64 lanes
                         if (lane_here() < 16) sm.red[wave][lane_here()] = y;
                         bar();
@@ -1361,7 +1448,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                                 }
                                 v = gv * (uv / (1.0f + expf(-gv)));
                             }
-                            put_split(&sm.dp[0][0], 32, tid, v);
+                            put_split(&sm.dp[0][0], split_stride(32), tid, v);
                         }
                     }
                     bar();
@@ -1371,7 +1458,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                     // each row stored as owner r / 8's partial of block f
                     // (two rows per store).
                     {
-                        const u32x4 da = a_frag(&sm.dp[0][0], a_offset(32), 0);
+                        const u32x4 da = a_frag(&sm.dp[0][0], a_offset(split_stride(32)), 0);
                         const int nbd = A()->nbd;
                         uint64_t *pdown = A()->pdown;
                         f32x4 acc[ND];
@@ -1402,7 +1489,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                     }
                     bar();
                     const int cnt = min(kOwn, H - fIdx() * kOwn);
-                    if (wave == 0 && lane_here() < cnt)
+                    if (wave == kDmaWave && lane_here() < cnt)
                         stf(A()->hid1 + fIdx() * kOwn + lane_here(), sm.out[lane_here()], tE);
                     mark(s, 16 * l + 14);
                 }
@@ -1436,7 +1523,7 @@ FusedGeom geometry(int H, int q_heads, int kv_heads, int hd, int I, bool kv_f32,
     g.f0 = blocks - g.nf;
     g.nkv = (kv_heads * hd + kWaves - 1) / kWaves;  // one rotation pair of K/V rows per wave
     g.kv0 = g.f0 - g.nkv;
-    g.s_cap = q_heads > 0 ? std::min(kMaxSplits, g.kv0 / q_heads) : 0;
+    g.s_cap = q_heads > 0 ? std::min(kMaxSplits, g.kv0 / heads_padded(q_heads)) : 0;
     const int row = hd * (kv_f32 ? 4 : 2);
     g.ip_max = 0;
     for (int ip = TP; ip <= kIpMax && 2 * ip * row <= kKvLdsMax; ip *= 2) g.ip_max = ip;
@@ -1458,7 +1545,7 @@ const Variant *find_variant(int fmt, int H, int q_heads, int kv_heads, int hd, i
     if (H % 8 || qd % 8 || I % 8 || H > 1024 || q_heads > 64) return nullptr;
     const FusedGeom geo = geometry(H, q_heads, kv_heads, hd, I, kv_f32, blocks);
     // The down product takes a block's gate/up rows as one K-step of 32.
-    if (geo.s_cap < 1 || geo.ip_max < TP || geo.no > geo.nf || geo.rp > 32 || geo.kv0 < q_heads) return nullptr;
+    if (geo.s_cap < 1 || geo.ip_max < TP || geo.no > geo.nf || geo.rp > 32 || geo.kv0 < heads_padded(q_heads)) return nullptr;
     const LdsLayout lay = lds_layout(H, hd, kv_f32 ? 4 : 2, geo.ip_max, geo.ni_max, geo.nbd, blocks);
     if (lay.tbw > kMaxGather || (size_t)lay.total + static_lds_bytes(hd) > device_max_lds()) return nullptr;
     for (const Variant &v : kVariants) {

@@ -20,8 +20,9 @@ struct FusedLayer {
 };
 
 // How the grid divides into roles for one model shape (fused_geometry).
-//   items:  blocks [0, q_heads * splits): one q head over one run of `ip`
-//           positions each (split-major: item = split * q_heads + head)
+//   items:  one q head over one run of `ip` positions each: item (split s,
+//           head h) at block s * qp + h, qp = q_heads rounded up to 8 (the
+//           XCD count), item index s * q_heads + h
 //   KV:     blocks [kv0, kv0 + nkv): the new position's K/V rows, one
 //           rotation pair per wave
 //   FFN:    blocks [f0, f0 + nf): gate/up rows, SwiGLU, down columns; the
@@ -68,7 +69,7 @@ struct FusedArgs {
     // Filled in by launch_decode_fused: roles (FusedGeom), the launch's
     // split count and positions per item, and the dynamic LDS layout (byte
     // offsets).
-    int ni, ip, splits;         // item blocks (q_heads * splits), positions per item
+    int ni, ip, splits;         // items (q_heads * splits), positions per item
     int kv0, nkv, f0, nf, no, nbd, rb, rp, head_blocks;
     int lds_xs, lds_xb, lds_q, lds_kv, lds_emb, lds_g1, lds_g2, lds_total;
 };

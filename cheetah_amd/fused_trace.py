@@ -45,7 +45,8 @@ def block_roles(shape, blocks: int, context: int, ctx_end: int = 0, kv_bf16: boo
     f0 = blocks - nf
     nkv = (kvh * hd + KWAVES - 1) // KWAVES
     kv0 = f0 - nkv
-    s_cap = min(MAX_SPLITS, kv0 // qh)
+    qp = (qh + 7) // 8 * 8  # item (split s, head h) at block s * qp + h
+    s_cap = min(MAX_SPLITS, kv0 // qp)
     row = hd * (2 if kv_bf16 else 4)
     ip_max, ip = 0, 64
     while ip <= IP_MAX and 2 * ip * row <= KV_LDS_MAX:
@@ -57,10 +58,10 @@ def block_roles(shape, blocks: int, context: int, ctx_end: int = 0, kv_bf16: boo
     rb = (I + nf - 1) // nf
     nbd = (I + rb - 1) // rb
     no = H // 8
-    items = list(range(qh * S))
+    items = [sp * qp + h for sp in range(S) for h in range(qh)]
     return {
         "items": items,
-        "last": [b for b in items if b // qh == S - 1],
+        "last": [b for b in items if b // qp == S - 1],
         "kv": list(range(kv0, kv0 + nkv)),
         "p1": items + list(range(kv0, kv0 + nkv)),
         "ffn": list(range(f0, f0 + nbd)),

@@ -11,17 +11,19 @@ def test_block_roles_partition_the_grid():
     # 160 FFN blocks (5/8 of the grid): 31 gate/up rows each, 157 with rows,
     # 112 owners of 8 residual rows; 128 K/V rotation pairs over 16 KV
     # blocks; the items below them: 14 q heads x 5 runs of 128 positions
-    # (640 positions fit 5 runs of 128 in the 80 item blocks).
+    # (640 positions fit 5 runs of 128 in the 80 item blocks), run s of head
+    # h at block 16 s + h, so that every run of a head is on XCD h % 8.
     assert roles["ip"] == 128
-    assert roles["items"] == list(range(70))
-    assert roles["last"] == list(range(56, 70))
+    assert roles["items"] == [16 * s + h for s in range(5) for h in range(14)]
+    assert all(b % 8 == (b % 16) % 8 for b in roles["items"])
+    assert roles["last"] == list(range(64, 78))
     assert roles["kv"] == list(range(80, 96))
     assert roles["owners"] == list(range(96, 208))
     assert roles["ffn"] == list(range(96, 253))
     # Shorter launches take shorter runs: 320 positions in 5 runs of 64
     # (the 80 item blocks hold 5 runs of each of the 14 q heads).
     short = fused_trace.block_roles(configs.QWEN2_0_5B, 256, 200, 320)
-    assert short["ip"] == 64 and short["items"] == list(range(14 * 4))
+    assert short["ip"] == 64 and short["items"] == [16 * s + h for s in range(4) for h in range(14)]
 
 
 def test_report_recovers_known_segments():
