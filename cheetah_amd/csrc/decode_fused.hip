@@ -642,24 +642,6 @@ __device__ __forceinline__ void store_tile(float y, int r0, int n, unsigned tag,
     if (l < 16 && (l & 1) == 0 && r < n) stf2(dst(r), y, nb, tag);
 }
 
-// All waves: the split (put_split) of x[i] * (inv * g[i]) for i < n into
-// the K-padded xb (kp elements per part, row stride split_stride(kp)),
-// zeros for n <= i < kp.
-template <bool BF16_SRC>
-__device__ __forceinline__ void block_stage_split(uint16_t *xb, int kp, const void *src, int n, const uint16_t *g,
-                                                  float inv) {
-    const int st = split_stride(kp);
-    for (int i = tid_here(); i < kp; i += kThreads) {
-        float v = 0.f;
-        if (i < n) {
-            if constexpr (BF16_SRC) v = bf16_f32(((const uint16_t *)src)[i]);
-            else v = val_of(((const uint64_t *)src)[i]);
-            v = v * (inv * bf16_f32(g[i]));
-        }
-        put_split(xb, st, i, v);
-    }
-}
-
 template <int HD>
 struct ItemShm {
     float p[kIpMax];       // scores, then weights, of the run's positions
@@ -906,52 +888,59 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
         if (bf16_src) block_stage<true>(xs, src, H, g, wave_norm_scale<true>(src, H, A()->eps));
         else block_stage<false>(xs, src, H, g, wave_norm_scale<false>(src, H, A()->eps));
     };
-    // The same normed input split for the matrix-core products (xb).
-    auto stage_split = [&](const void *src, bool bf16_src, int gain_off) {
-        const uint16_t *g = (const uint16_t *)(lds + gain_off);
-        uint16_t *xb = (uint16_t *)(lds + A()->lds_xb);
-        const int H = A()->H;
-        if (bf16_src) block_stage_split<true>(xb, KP, src, H, g, wave_norm_scale<true>(src, H, A()->eps));
-        else block_stage_split<false>(xb, KP, src, H, g, wave_norm_scale<false>(src, H, A()->eps));
-    };
-    // A normed input straight from the tagged words src (H <= 1024): wave w
-    // polls chunk w (words [128 w, 128 w + 128)) into registers and adds up
-    // the squares of its values; after the barrier every thread folds the
-    // eight wave sums in wave order into the RMSNorm scale (ops.rs:646-652)
-    // and each lane splits its own two values (times the gains) into xb,
-    // two elements per LDS store. The words never pass through LDS, and the
-    // scale costs one DPP reduction per wave instead of a strided pass over
-    // the whole vector. Also waits for the wave's loads and copies in flight
-    // (wait_vm) before the barrier. The caller's barrier publishes xb.
-    auto stage_split_polled = [&](const uint64_t *src, unsigned tag, int gain_off) {
+    // A normed input for the matrix-core products, in two halves: before
+    // the barrier, wave w takes elements [128 w, 128 w + 128) of the input
+    // (lane l: 128 w + 2 l and + 1, values v0 and v1, gains gw as two BF16
+    // halves), writes the split of x * g into xb (two elements per LDS
+    // store; zeros past H up to KP) and its sum of squares into sm.ss[w];
+    // after it, norm_scale() folds the eight sums in wave order into the
+    // RMSNorm scale (ops.rs:646-652), which multiplies the dot products of
+    // x * g (the same value as the dot product of the normed x up to one
+    // rounding). No wave waits for another between its input and its
+    // share of xb, and the block passes one barrier on the way to the
+    // products.
+    auto stage_gx = [&](float v0, float v1, uint32_t gw) {
         const int H = A()->H, lane = lane_here(), base = wave * kChunk, i0 = base + 2 * lane;
-        float v0 = 0.f, v1 = 0.f, ss = 0.f;
+        float ss = 0.f;
+        if (base < H) {
+            ss = wave_sum(fmaf(v1, v1, v0 * v0));
+            // Elements [H, KP) are zeros: they lie in the chunk that holds H - 1.
+            if (i0 < KP) {
+                uint16_t a[3], c[3];
+                x_split(v0 * bf16_lo(gw), a[0], a[1], a[2]);
+                x_split(v1 * bf16_hi(gw), c[0], c[1], c[2]);
+                uint32_t *xb = (uint32_t *)(lds + A()->lds_xb);
+                constexpr int st = split_stride(KP) / 2;  // row stride in 32-bit words
+#pragma unroll
+                for (int p = 0; p < 3; ++p) xb[p * st + i0 / 2] = (uint32_t)a[p] | ((uint32_t)c[p] << 16);
+                xb[3 * st + i0 / 2] = 0u;
+            }
+        }
+        if (lane == 0) sm.ss[wave] = ss;
+    };
+    auto norm_scale = [&]() {
+        float tot = sm.ss[0];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) tot += sm.ss[w];
+        return 1.0f / sqrtf(tot / (float)A()->H + A()->eps);
+    };
+    // This wave's input values from the tagged words src (chunk `wave`,
+    // polled into registers; zeros past H).
+    auto poll_x = [&](const uint64_t *src, unsigned tag, float &v0, float &v1) {
+        const int H = A()->H, base = wave * kChunk, i0 = base + 2 * lane_here();
+        v0 = v1 = 0.f;
         if (base < H) {
             const u32x4 r = poll_chunk(src, base, H, tag, A()->abort_flag);
             v0 = i0 < H ? __uint_as_float(r[0]) : 0.f;
             v1 = i0 + 1 < H ? __uint_as_float(r[2]) : 0.f;
-            ss = wave_sum(fmaf(v1, v1, v0 * v0));
         }
-        if (lane == 0) sm.ss[wave] = ss;
-        wait_vm();
-        bar();
-        float tot = sm.ss[0];
-#pragma unroll
-        for (int w = 1; w < kWaves; ++w) tot += sm.ss[w];
-        const float inv = 1.0f / sqrtf(tot / (float)H + A()->eps);
-        // Elements [H, KP) are zeros: they lie in the chunk that holds H - 1.
-        if (base < H && i0 < KP) {
-            const uint16_t *g = (const uint16_t *)(lds + gain_off);
-            const uint32_t gw = i0 < H ? *(const uint32_t *)(g + i0) : 0u;
-            uint16_t a[3], c[3];
-            x_split(v0 * (inv * bf16_lo(gw)), a[0], a[1], a[2]);
-            x_split(v1 * (inv * bf16_hi(gw)), c[0], c[1], c[2]);
-            uint32_t *xb = (uint32_t *)(lds + A()->lds_xb);
-            constexpr int st = split_stride(KP) / 2;  // row stride in 32-bit words
-#pragma unroll
-            for (int p = 0; p < 3; ++p) xb[p * st + i0 / 2] = (uint32_t)a[p] | ((uint32_t)c[p] << 16);
-            xb[3 * st + i0 / 2] = 0u;
-        }
+    };
+    // The gains of this lane's two input elements (a BF16 pair), loaded with
+    // the layer's weights.
+    auto load_gains = [&](const uint16_t *g, bool act) {
+        const int H = A()->H, i0 = wave * kChunk + 2 * lane_here();
+        const uint32_t off = act && i0 < H ? (uint32_t)i0 * 2u : kNoRead;
+        return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rsrc(g, (size_t)H * 2), off, 0, 2);
     };
     auto tag_base = [&](int s) { return A()->tag0 + (unsigned)(s * fused_phases_per_step(A()->L)); };
 
@@ -1023,6 +1012,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
         // KV blocks (the run that holds it), softmax, weighted V rows, and
         // the head's o_proj columns applied to the unnormalised output.
         u32x4 W[NI];
+        uint32_t gw1 = 0;  // input-norm gains of this lane's two elements
         // Refill for layer l at position pos: q units (k < NQ: K-step
         // ks = (wave / QT) QK + k of the head's tile wave % QT, row
         // 16 (wave % QT) + lane % 16, unit 4 ks + lane / 16), o_proj units
@@ -1036,6 +1026,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
             const int qrows = (A()->q_heads + 2 * A()->kv_heads) * HD;
             const Rsrc rq = rsrc(LY(l)->qkv, (size_t)qrows * qs), ro = rsrc(LY(l)->o, (size_t)H * os);
             const int h = itHead();
+            gw1 = load_gains(LY(l)->ln1, act);
 #pragma unroll
             for (int k = 0; k < NI; ++k) {
                 uint32_t off = kNoRead;
@@ -1050,7 +1041,6 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                 }
             }
             if (act) {
-                if (wave == kDmaWave) dma_bytes(lds + A()->lds_g1, LY(l)->ln1, H * 2);
                 const int ip = A()->ip;
                 const long start = (long)itSplit() * ip, lim = min(start + ip, pos);
                 uint8_t *k_lds = lds + A()->lds_kv;
@@ -1095,14 +1085,20 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                             qs[2 * HD + HD / 2 + i] = A()->rope_sin[pos * half + i];
                         }
                     }
-                    // (wait_vm: the embedding row, the gains and the K/V rows)
+                    // (wait_vm: the embedding row and the K/V rows)
+                    float x0, x1;
                     if (l > 0) {
-                        stage_split_polled(A()->hid1, tK - 1, A()->lds_g1);
+                        poll_x(A()->hid1, tK - 1, x0, x1);
                     } else {
                         wait_vm();
                         bar();
-                        stage_split(lds + A()->lds_emb, true, A()->lds_g1);
+                        const int i0 = wave * kChunk + 2 * lane_here();
+                        const uint16_t *e = (const uint16_t *)(lds + A()->lds_emb);
+                        x0 = i0 < H ? bf16_f32(e[i0]) : 0.f;
+                        x1 = i0 + 1 < H ? bf16_f32(e[i0 + 1]) : 0.f;
                     }
+                    stage_gx(x0, x1, gw1);
+                    wait_vm();
                     bar();
                     mark(s, 16 * l + 1);
                     {
@@ -1116,7 +1112,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                         if (lane_here() < 16) sm.red[wave][lane_here()] = y;
                         bar();
                         // Thread j < HD / 2 finishes rotation pair j (rows
-                        // 2 j and 2 j + 1: bias, RoPE).
+                        // 2 j and 2 j + 1: norm scale, bias, RoPE).
                         const int tid = tid_here();
                         if (tid < HD / 2) {
                             const int d0 = 2 * tid, t = d0 / 16, c0 = d0 % 16;
@@ -1126,6 +1122,9 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                                 v0 += sm.red[t + QT * kp][c0];
                                 v1 += sm.red[t + QT * kp][c0 + 1];
                             }
+                            const float inv = norm_scale();
+                            v0 = inv * v0;
+                            v1 = inv * v1;
                             if (qbias) {
                                 v0 = v0 + qs[HD + d0];
                                 v1 = v1 + qs[HD + d0 + 1];
@@ -1312,6 +1311,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
         // SwiGLU and their down columns; owners sum the down partials and
         // add the residual.
         u32x4 W[NF];
+        uint32_t gw2 = 0;  // FFN-norm gains of this lane's two elements
         // Refill for layer l: gate/up units (k < NG: tile T = wave % GT2,
         // gate tiles first, then up; K-step ks = (wave / GT2) GK + k; row
         // f rb + 16 (T % GT) + lane % 16, unit 4 ks + lane / 16), down units
@@ -1325,6 +1325,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
             const Rsrc rg = rsrc(LY(l)->gate, (size_t)I * gs), ru = rsrc(LY(l)->up, (size_t)I * gs);
             const Rsrc rd = rsrc(LY(l)->down_cols, (size_t)A()->nf * H * rp * 2);
             const int T = wave % GT2, jj = (T % GT) * 16 + i16, row = f * rb + jj;
+            gw2 = load_gains(LY(l)->ln2, act);
 #pragma unroll
             for (int k = 0; k < NF; ++k) {
                 uint32_t off = kNoRead;
@@ -1338,7 +1339,6 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                     W[k] = ld_unit(rd, off);
                 }
             }
-            if (act && wave == kDmaWave) dma_bytes(lds + A()->lds_g2, LY(l)->ln2, H * 2);
         };
         long pos = pos0;
         float h_own = 0.f, emb_r = 0.f;
@@ -1352,7 +1352,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
             if (isOwner() && ownRow() < A()->H) emb_r = ldc_bf16(A()->embed, (long)token * A()->H + ownRow());
             for (int l = 0; l < L; ++l) {
                 const unsigned tK = tb0 + 5 * l, tP = tK + 1, tC = tK + 2, tD = tK + 3, tE = tK + 4;
-                const int H = A()->H, nH = H / U::E;
+                const int H = A()->H;
                 mark(s, 16 * l);
                 refill(l, hasRows());
                 mark(s, 16 * l + 7);
@@ -1420,7 +1420,10 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                 // ---- Gate/up (fused RMSNorm), SwiGLU, down partials of every
                 // hidden row.
                 if (hasRows()) {
-                    stage_split_polled(A()->hid0, tC, A()->lds_g2);  // (wait_vm: the gains)
+                    float x0, x1;
+                    poll_x(A()->hid0, tC, x0, x1);
+                    stage_gx(x0, x1, gw2);
+                    wait_vm();
                     bar();
                     mark(s, 16 * l + 10);
                     const int rb = A()->rb, f = fIdx(), I = A()->I;
@@ -1446,6 +1449,9 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                                     gv += sm.red[t + GT2 * kp][c];
                                     uv += sm.red[GT + t + GT2 * kp][c];
                                 }
+                                const float inv = norm_scale();
+                                gv = inv * gv;
+                                uv = inv * uv;
                                 v = gv * (uv / (1.0f + expf(-gv)));
                             }
                             put_split(&sm.dp[0][0], split_stride(32), tid, v);
