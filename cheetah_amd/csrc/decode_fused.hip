@@ -644,8 +644,11 @@ __device__ __forceinline__ void store_tile(float y, int r0, int n, unsigned tag,
 
 template <int HD>
 struct ItemShm {
-    float p[kIpMax];       // scores, then weights, of the run's positions
-    float red[kWaves][HD];
+    // Per-wave attention partials (item_flash), the new position's last:
+    // weighted V rows relative to the partial's own max, that max, and the
+    // sum of the weights.
+    float red[kWaves + 1][HD];
+    float mw[kWaves + 1], lw[kWaves + 1];
     alignas(16) uint16_t op[4][split_stride(HD)];  // the unnormalised output, split (put_split)
     float m, l;            // max score, sum of weights
 };
@@ -699,106 +702,168 @@ __device__ __forceinline__ void load_kv_lds(CArgs *a, uint8_t *k_lds, uint8_t *v
     }
 }
 
-template <class KT>
-__device__ __forceinline__ void ld8(const KT *p, float (&f)[8]) {
-    if constexpr (sizeof(KT) == 2) {
-        const u32x4 v = *(const u32x4 *)p;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            f[2 * i] = bf16_lo(v[i]);
-            f[2 * i + 1] = bf16_hi(v[i]);
-        }
-    } else {
-        const f32x4 a = *(const f32x4 *)p, b = *(const f32x4 *)(p + 4);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            f[i] = a[i];
-            f[4 + i] = b[i];
-        }
-    }
-}
-
-// All threads: scores of K rows [p0, p1) (LDS) against q, scaled by
-// 1/sqrt(hd), into p[]; T = hd / 8 lanes per row, 8 dimensions each.
+// ---- An item's attention, flash style: no wave waits for another until
+// the partials merge.
+//
+// item_flash: wave w takes the cached positions [w cw, min(w cw + cw, nc)),
+// cw = ceil(nc / 8) <= 32: scores with eight lanes per position (lane i
+// reads bytes 128 r + 16 i of the K row, so the eight lanes of a position
+// cover 128 contiguous bytes per read, conflict-free), its own max m_w,
+// weights exp(s - m_w) and their sum l_w, then the weighted V rows (lane:
+// HD / 64 dimensions; a position's weight read from the lane that scored
+// it) into sh.red[w], sh.mw[w], sh.lw[w]. A wave without positions leaves
+// m_w = -inf, l_w = 0 and zeros.
 template <int HD, class KT>
-__device__ __forceinline__ void item_scores(const float *qs, const uint8_t *k_lds, int p0, int p1, float *p) {
-    constexpr int T = HD / 8, P = kThreads / T, ROW = HD * (int)sizeof(KT);
-    const int tid = tid_here();
-    const int d8 = tid % T, pg = tid / T;
+__device__ __forceinline__ void item_flash(const float *qs, const uint8_t *k_lds, const uint8_t *v_lds, int nc,
+                                           ItemShm<HD> &sh) {
+    constexpr int ROW = HD * (int)sizeof(KT);
+    constexpr int NR = ROW / 128;              // 16-byte reads per lane and row
+    constexpr int EPR = 16 / (int)sizeof(KT);  // elements per read
+    constexpr int DV = HD / 64;                // V dimensions per lane
+    constexpr int NPASS = kIpMax / kWaves / 8;  // passes of 8 positions, at most
+    static_assert(NR >= 1 && NPASS <= 4, "row and run shape");
+    const int lane = lane_here(), li = lane & 7, pj = lane >> 3;
+    const int wave = __builtin_amdgcn_readfirstlane(tid_here() >> 6);
+    const int cw = (nc + kWaves - 1) / kWaves;
+    const int p0 = wave * cw, cnt = max(0, min(cw, nc - p0));
     const float scale = 1.0f / sqrtf((float)HD);
-    for (int b0 = p0; b0 < p1; b0 += P) {
-        const int pi = b0 + pg;
-        const bool valid = pi < p1;
-        float dot = 0.f;
-        if (valid) {
-            float kf[8];
-            ld8<KT>((const KT *)(k_lds + (size_t)pi * ROW) + d8 * 8, kf);
+    // This lane's elements of q: (128 r + 16 li) / sizeof(KT) + e.
+    float qv[NR][EPR];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) dot = fmaf(kf[e], qs[d8 * 8 + e], dot);
+    for (int r = 0; r < NR; ++r)
+#pragma unroll
+        for (int e = 0; e < EPR; ++e) qv[r][e] = qs[(128 * r + 16 * li) / (int)sizeof(KT) + e];
+    float sc[NPASS];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int ps = 0; ps < NPASS; ++ps) {
+        sc[ps] = -INFINITY;
+        if (8 * ps < cnt) {
+            const int j = 8 * ps + pj;
+            const uint8_t *krow = k_lds + (size_t)(p0 + min(j, cnt - 1)) * ROW + 16 * li;
+            float dot = 0.f;
+#pragma unroll
+            for (int r = 0; r < NR; ++r) {
+                const u32x4 w = *(const u32x4 *)(krow + 128 * r);
+                if constexpr (sizeof(KT) == 2) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        dot = fmaf(bf16_lo(w[e]), qv[r][2 * e], dot);
+                        dot = fmaf(bf16_hi(w[e]), qv[r][2 * e + 1], dot);
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) dot = fmaf(__uint_as_float(w[e]), qv[r][e], dot);
+                }
+            }
+            dot = group_sum<8>(dot);
+            if (j < cnt) sc[ps] = dot * scale;
+            mx = fmaxf(mx, sc[ps]);
         }
-        const float s = group_sum<T>(dot);
-        if (d8 == 0 && valid) p[pi] = s * scale;
+    }
+    mx = wave_max(mx);
+    float ew[NPASS], ls = 0.f;
+#pragma unroll
+    for (int ps = 0; ps < NPASS; ++ps) {
+        ew[ps] = sc[ps] == -INFINITY ? 0.f : expf(sc[ps] - mx);
+        if (li == 0) ls += ew[ps];
+    }
+    ls = wave_sum(ls);
+    float acc[DV];
+#pragma unroll
+    for (int e = 0; e < DV; ++e) acc[e] = 0.f;
+#pragma unroll
+    for (int ps = 0; ps < NPASS; ++ps) {
+        if (8 * ps < cnt) {
+            float vf[8][DV];
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) {
+                const KT *vrow = (const KT *)(v_lds + (size_t)(p0 + min(8 * ps + jj, cnt - 1)) * ROW) + lane * DV;
+                if constexpr (sizeof(KT) == 2) {
+                    if constexpr (DV == 1) {
+                        vf[jj][0] = bf16_f32(*vrow);
+                    } else {
+                        const uint32_t w2 = *(const uint32_t *)vrow;
+                        vf[jj][0] = bf16_lo(w2);
+                        vf[jj][1] = bf16_hi(w2);
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < DV; ++e) vf[jj][e] = vrow[e];
+                }
+            }
+            // Positions past the run weigh zero (their lanes hold ew = 0).
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) {
+                const float w = lane_read(ew[ps], 8 * jj);
+#pragma unroll
+                for (int e = 0; e < DV; ++e) acc[e] = fmaf(w, vf[jj][e], acc[e]);
+            }
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < DV; ++e) sh.red[wave][lane * DV + e] = acc[e];
+    if (lane == 0) {
+        sh.mw[wave] = mx;
+        sh.lw[wave] = ls;
     }
 }
 
-// All threads: softmax of the nv scores (max, exp, sum) and the weighted V
-// rows: o = sum_p w_p v_p (unnormalised, split into sh.op), sh.m, sh.l. Lane owns hd / 64
-// dimensions, wave w positions w, w + 8, ...; the waves' sums are added in
-// wave order.
-template <int HD, class KT>
-__device__ __forceinline__ void item_softmax_pv(const uint8_t *v_lds, int nv, ItemShm<HD> &sh) {
-    constexpr int ROW = HD * (int)sizeof(KT), DPL = HD / 64;
-    const int tid = tid_here(), lane = tid & 63, wave = tid >> 6;
+// The new position's partial (sh.red/mw/lw[8]) from its K and V rows as
+// stored in the cache (tagged words kv: K then V, HD each): wave 0 polls K
+// and scores it against q, wave 1 polls V. Bounded like every poll.
+template <int HD>
+__device__ __forceinline__ void item_new_row(const float *qs, const uint64_t *kv, unsigned tag, int *abort_flag,
+                                             ItemShm<HD> &sh) {
+    static_assert(HD <= 2 * 64, "a row of the new position in one chunk");
+    const int lane = lane_here(), wave = __builtin_amdgcn_readfirstlane(tid_here() >> 6), d = 2 * lane;
     if (wave == 0) {
-        float mx = -INFINITY;
-        for (int c = lane; c < nv; c += 64) mx = fmaxf(mx, sh.p[c]);
-        mx = wave_max(mx);
-        float sum = 0.f;
-        for (int c = lane; c < nv; c += 64) {
-            const float pv = expf(sh.p[c] - mx);
-            sh.p[c] = pv;
-            sum += pv;
-        }
-        sum = wave_sum(sum);
+        const u32x4 r = poll_chunk(kv, 0, HD, tag, abort_flag);
+        float dot = 0.f;
+        if (d < HD) dot = fmaf(__uint_as_float(r[2]), qs[d + 1], __uint_as_float(r[0]) * qs[d]);
+        dot = wave_sum(dot);
         if (lane == 0) {
-            sh.m = mx;
-            sh.l = sum;
+            sh.mw[kWaves] = dot * (1.0f / sqrtf((float)HD));
+            sh.lw[kWaves] = 1.f;
+        }
+    } else if (wave == 1) {
+        const u32x4 r = poll_chunk(kv + HD, 0, HD, tag, abort_flag);
+        if (d < HD) {
+            sh.red[kWaves][d] = __uint_as_float(r[0]);
+            sh.red[kWaves][d + 1] = __uint_as_float(r[2]);
         }
     }
-    bar();
-    float acc[DPL];
-#pragma unroll
-    for (int e = 0; e < DPL; ++e) acc[e] = 0.f;
-#pragma unroll 4
-    for (int pi = wave; pi < nv; pi += kWaves) {
-        const KT *vrow = (const KT *)(v_lds + (size_t)pi * ROW) + lane * DPL;
-        float vf[DPL];
-        if constexpr (sizeof(KT) == 2) {
-            if constexpr (DPL == 1) {
-                vf[0] = bf16_f32(*vrow);
-            } else {
-                const uint32_t w2 = *(const uint32_t *)vrow;
-                vf[0] = bf16_lo(w2);
-                vf[1] = bf16_hi(w2);
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < DPL; ++e) vf[e] = vrow[e];
-        }
-        const float pj = sh.p[pi];
-#pragma unroll
-        for (int e = 0; e < DPL; ++e) acc[e] = fmaf(pj, vf[e], acc[e]);
-    }
-#pragma unroll
-    for (int e = 0; e < DPL; ++e) sh.red[wave][lane * DPL + e] = acc[e];
-    bar();
+}
+
+// Threads d < HD, after a barrier: the partials (the waves', then the new
+// position's when there is one) rescaled to their common max and added in
+// that order: the unnormalised output split into sh.op, sh.m, sh.l. Lane w
+// of each wave computes partial w's factor exp(m_w - M) (one exponential
+// per lane), the others read it from there.
+template <int HD>
+__device__ __forceinline__ void item_merge(bool has_new, ItemShm<HD> &sh) {
+    constexpr int NP = kWaves + 1;
+    const int tid = tid_here(), lane = tid & 63;
     if (tid < HD) {
-        float o = sh.red[0][tid];
+        const int np = kWaves + (has_new ? 1 : 0);
+        const int li = min(lane, NP - 1);
+        const float mw = lane < np ? sh.mw[li] : -INFINITY;
+        const float M = wave_max(mw);
+        const float f = mw == -INFINITY ? 0.f : expf(mw - M);
+        const float l = wave_sum(lane < np ? f * sh.lw[li] : 0.f);
+        // (The new position's slot holds nothing to read when there is none.)
+        float rv[NP];
 #pragma unroll
-        for (int w = 1; w < kWaves; ++w) o += sh.red[w][tid];
+        for (int w = 0; w < NP; ++w) rv[w] = w < np ? sh.red[w][tid] : 0.f;
+        float o = 0.f;
+#pragma unroll
+        for (int w = 0; w < NP; ++w) o = fmaf(lane_read(f, w), rv[w], o);
         put_split(&sh.op[0][0], split_stride(HD), tid, o);
+        if (tid == 0) {
+            sh.m = M;
+            sh.l = l;
+        }
     }
-    bar();
 }
 
 // UH: 16-byte units per lane of a row with H columns (the KV blocks' and
@@ -1142,24 +1207,16 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                     }
                     bar();
                     mark(s, 16 * l + 2);
-                    item_scores<HD, KT>(qs, k_lds, 0, nc, ish.p);
+                    // Attention: the waves' partials over the cached rows,
+                    // the new position's (its K and V rows as stored in the
+                    // cache, from the KV blocks), then one merge.
+                    item_flash<HD, KT>(qs, k_lds, v_lds, nc, ish);
                     mark(s, 16 * l + 3);
-                    if (has_new) {
-                        // The new position's K and V rows as stored in the cache.
-                        gather(tb, A()->kvw + (size_t)(ih / G) * 2 * HD, 2 * HD, tK, A()->abort_flag);
-                        bar();
-                        for (int i = tid_here(); i < 2 * HD; i += kThreads) {
-                            const float v = val_of(tb[i]);
-                            KT *rowp = (KT *)((i < HD ? k_lds : v_lds) + (size_t)nc * ROW);
-                            if constexpr (sizeof(KT) == 2) rowp[i % HD] = f32_bf16_rne(v);
-                            else rowp[i % HD] = v;
-                        }
-                        bar();
-                        item_scores<HD, KT>(qs, k_lds, nc, nc + 1, ish.p);
-                    }
-                    bar();
+                    if (has_new) item_new_row<HD>(qs, A()->kvw + (size_t)(ih / G) * 2 * HD, tK, A()->abort_flag, ish);
                     mark(s, 16 * l + 4);
-                    item_softmax_pv<HD, KT>(v_lds, nc + (has_new ? 1 : 0), ish);
+                    bar();
+                    item_merge<HD>(has_new, ish);
+                    bar();
                     mark(s, 16 * l + 5);
                     // o_proj columns of head ih times the unnormalised output
                     // on the matrix cores: tiles wave + 8 m of the H rows

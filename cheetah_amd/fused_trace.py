@@ -11,9 +11,9 @@ report: the critical path of a layer split into hand-offs (last producer
 store -> consumers' inputs staged) and phase compute.
 
 Stamp slots per layer l (16 l + k): 0 layer start, 1 P1.in (items' and KV
-blocks' input normed and staged), 2 q.out (an item's q rotated), 3 scores of
-the cached rows, 4 new row (the new K/V row polled and scored), 5 softmax +
-weighted V, 6 P1.out (items: o_proj partials stored; KV blocks: K/V stored),
+blocks' input normed and staged), 2 q.out (an item's q rotated), 3 the
+waves' attention partials over the cached rows, 4 new row (the new K/V row
+polled and scored), 5 partials merged, 6 P1.out (items: o_proj partials stored; KV blocks: K/V stored),
 7 refill issued, 8 C.in (owners: item partials gathered), 9 C.out (hid0
 stored), 10 D.in (FFN blocks: input normed), 11 gate/up + SwiGLU, 12 D.out
 (down partials stored), 13 E.in (owners: down partials gathered), 14 E.out
@@ -71,7 +71,7 @@ def block_roles(shape, blocks: int, context: int, ctx_end: int = 0, kv_bf16: boo
     }
 
 
-SEGMENTS = ("q dot", "cached scores", "new K/V row wait (last runs)", "softmax + weighted V", "o_proj partials",
+SEGMENTS = ("q dot", "cached rows (per-wave partials)", "new K/V row (last runs)", "merge of the partials", "o_proj partials",
             "hand-off items -> owners", "merge + residual", "hand-off owners -> FFN (+ norm)", "gate/up + SwiGLU",
             "down partials", "hand-off FFN -> owners", "sum + residual", "hand-off owners -> items (+ norm)")
 
