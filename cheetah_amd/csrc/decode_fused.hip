@@ -442,7 +442,7 @@ struct Shm {
     uint32_t iidx[kWaves];
     int token;                 // the step's sampled id
     float out[kStage];         // a phase's outputs of the block, stored as one run
-    float red[kWaves][16];     // each wave's tile outputs (matrix-core phases split over K)
+    float red[kWaves][128];    // each wave's tile outputs over its input chunk (up to 8 tiles of 16)
     float ss[kWaves];          // each wave's sum of squares of its chunk (polled RMSNorm input)
     alignas(16) uint16_t dp[4][split_stride(32)];  // an FFN block's SwiGLU outputs, split (put_split)
 };
@@ -875,10 +875,11 @@ __device__ __forceinline__ void item_merge(bool has_new, ItemShm<HD> &sh) {
 // step loop.
 //
 // Matrix-core work per wave (one 16-byte weight unit per lane and MFMA):
-//   items' q: the head's HD / 16 tiles, each split over K between
-//     8 / (HD / 16) waves (QK K-steps each), combined in LDS;
+//   items' q and FFN gate/up: every tile (HD / 16 q tiles; GT gate and GT
+//     up tiles) over the four K-steps of the wave's own input chunk (wave w
+//     polls elements [128 w, 128 w + 128)), so a wave multiplies as soon as
+//     its chunk is in, with no barrier before; the chunks' sums meet in LDS;
 //   items' o_proj: tiles wave, wave + 8, ... of the H rows, HD / 32 K-steps;
-//   FFN gate/up: 2 GT tiles, each split over K between 8 / (2 GT) waves;
 //   FFN down: tiles wave, wave + 8, ... of the H rows, one K-step (the
 //     block's gate/up rows padded to 32).
 //
@@ -891,21 +892,17 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
     constexpr int ROW = HD * (int)sizeof(KT);
     constexpr int KP = 32 * KS;           // padded K of a row with H columns
     constexpr int QT = HD / 16;           // q tiles of a head
-    constexpr int QWP = kWaves / QT;      // waves per q tile
-    constexpr int QK = (KS + QWP - 1) / QWP;  // K-steps per wave of a q tile
+    constexpr int CK = kChunk / 32;       // K-steps of one wave's input chunk
     constexpr int OK = HD / 32;           // K-steps of an o_proj row's head columns
-    constexpr int NQ = QK;                // an item's q units
+    constexpr int NQ = QT * CK;           // an item's q units
     constexpr int NWO = OTW * OK;         // an item's o_proj units
     constexpr int NI = NQ + NWO;          // an item's weight units
     constexpr int GT2 = 2 * GT;           // gate and up tiles of an FFN block
-    constexpr int GWP = kWaves / GT2;     // waves per gate/up tile
-    constexpr int GK = (KS + GWP - 1) / GWP;  // K-steps per wave of a gate/up tile
-    constexpr int NG = GK;                // an FFN block's gate/up units
+    constexpr int NG = GT2 * CK;          // an FFN block's gate/up units
     constexpr int ND = OTW;               // an FFN block's down units
     constexpr int NF = NG + ND;           // an FFN block's weight units
     constexpr int NK = 2 * UH;            // a KV block's weight units
-    static_assert(HD % 32 == 0 && kWaves % QT == 0 && QK * QWP == KS, "q tiles over the waves");
-    static_assert(kWaves % GT2 == 0 && GK * GWP == KS, "gate/up tiles over the waves");
+    static_assert(HD % 32 == 0 && QT * 16 <= 128 && GT2 * 16 <= 128 && KS <= kWaves * CK, "tiles and chunks");
     // The only read of the kernarg-segment pointer (see opaque()).
     CArgs *const kargs = (CArgs *)__builtin_amdgcn_kernarg_segment_ptr();
     auto A = [kargs]() { return opaque(kargs); };
@@ -989,6 +986,30 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
         for (int w = 1; w < kWaves; ++w) tot += sm.ss[w];
         return 1.0f / sqrtf(tot / (float)A()->H + A()->eps);
     };
+    // This wave's products of NT tiles (pool slots OFF + t CK + k) over the
+    // K-steps of its own input chunk (staged in xb by stage_gx, read back by
+    // the same wave: no barrier), tile t's 16 outputs into sm.red[wave][16 t
+    // + lane]. Every lane takes part (the products read all 64 lanes).
+    auto chunk_products = [&](auto nt_c, auto off_c, const u32x4 *W) {
+        constexpr int NT = decltype(nt_c)::value, OFF = decltype(off_c)::value;
+        const uint16_t *xa = (const uint16_t *)(lds + A()->lds_xb) + a_offset(split_stride(KP)) + 32 * CK * wave;
+        u32x4 af[CK];
+#pragma unroll
+        for (int k = 0; k < CK; ++k) {
+            af[k] = u32x4{0u, 0u, 0u, 0u};
+            if (CK * wave + k < KS) af[k] = *(const u32x4 *)(xa + 32 * k);
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            f32x4 c = {0.f, 0.f, 0.f, 0.f};
+            // K-steps past KS hold zeros on both sides (no read, no load).
+#pragma unroll
+            for (int k = 0; k < CK; ++k) c = mfma_bf16(af[k], W[OFF + t * CK + k], c);
+            if (lane_here() < 16) sm.red[wave][16 * t + lane_here()] = tile_dot(c);
+        }
+    };
+    // Input chunks of H: the waves whose sums sm.red holds.
+    auto n_chunks = [&]() { return (A()->H + kChunk - 1) / kChunk; };
     // This wave's input values from the tagged words src (chunk `wave`,
     // polled into registers; zeros past H).
     auto poll_x = [&](const uint64_t *src, unsigned tag, float &v0, float &v1) {
@@ -1078,9 +1099,9 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
         // the head's o_proj columns applied to the unnormalised output.
         u32x4 W[NI];
         uint32_t gw1 = 0;  // input-norm gains of this lane's two elements
-        // Refill for layer l at position pos: q units (k < NQ: K-step
-        // ks = (wave / QT) QK + k of the head's tile wave % QT, row
-        // 16 (wave % QT) + lane % 16, unit 4 ks + lane / 16), o_proj units
+        // Refill for layer l at position pos: q units (k < NQ: tile k / CK,
+        // row 16 (k / CK) + lane % 16 of the head, K-step ks = CK wave +
+        // k % CK of the wave's input chunk, unit 4 ks + lane / 16), o_proj units
         // (k = NQ + m OK + j: tile wave + 8 m of the H rows, row 16 t +
         // lane % 16, K-step j of the head's columns, elements
         // h HD + 32 j + 8 (lane / 16) ...), the input-norm gains and the
@@ -1096,7 +1117,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
             for (int k = 0; k < NI; ++k) {
                 uint32_t off = kNoRead;
                 if (k < NQ) {
-                    const int ks = (wave / QT) * QK + k, unit = 4 * ks + g4, row = h * HD + (wave % QT) * 16 + i16;
+                    const int ks = CK * wave + k % CK, unit = 4 * ks + g4, row = h * HD + (k / CK) * 16 + i16;
                     if (act && ks < KS && unit < nH) off = (uint32_t)row * qs + (uint32_t)unit * 16u;
                     W[k] = ld_unit(rq, off);
                 } else {
@@ -1163,29 +1184,22 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                         x1 = i0 + 1 < H ? bf16_f32(e[i0 + 1]) : 0.f;
                     }
                     stage_gx(x0, x1, gw1);
-                    wait_vm();
-                    bar();
                     mark(s, 16 * l + 1);
                     {
-                        // The head's q rows on the matrix cores: tile
-                        // wave % QT over K-steps [(wave / QT) QK, + QK),
-                        // the K parts added in wave order through LDS.
-                        const uint16_t *xq =
-                            (const uint16_t *)(lds + A()->lds_xb) + a_offset(split_stride(KP)) + 32 * (wave / QT) * QK;
-                        // All 64 lanes: the products read every lane's operands.
-                        const float y = kdot<NQ, 0>(xq, W);
-                        if (lane_here() < 16) sm.red[wave][lane_here()] = y;
+                        // The head's q rows on the matrix cores over this
+                        // wave's chunk; the chunks' sums added in wave order.
+                        chunk_products(std::integral_constant<int, QT>{}, std::integral_constant<int, 0>{}, W);
+                        wait_vm();
                         bar();
                         // Thread j < HD / 2 finishes rotation pair j (rows
                         // 2 j and 2 j + 1: norm scale, bias, RoPE).
                         const int tid = tid_here();
                         if (tid < HD / 2) {
-                            const int d0 = 2 * tid, t = d0 / 16, c0 = d0 % 16;
-                            float v0 = sm.red[t][c0], v1 = sm.red[t][c0 + 1];
-#pragma unroll
-                            for (int kp = 1; kp < QWP; ++kp) {
-                                v0 += sm.red[t + QT * kp][c0];
-                                v1 += sm.red[t + QT * kp][c0 + 1];
+                            const int d0 = 2 * tid, nch = n_chunks();
+                            float v0 = sm.red[0][d0], v1 = sm.red[0][d0 + 1];
+                            for (int w = 1; w < nch; ++w) {
+                                v0 += sm.red[w][d0];
+                                v1 += sm.red[w][d0 + 1];
                             }
                             const float inv = norm_scale();
                             v0 = inv * v0;
@@ -1369,9 +1383,10 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
         // add the residual.
         u32x4 W[NF];
         uint32_t gw2 = 0;  // FFN-norm gains of this lane's two elements
-        // Refill for layer l: gate/up units (k < NG: tile T = wave % GT2,
-        // gate tiles first, then up; K-step ks = (wave / GT2) GK + k; row
-        // f rb + 16 (T % GT) + lane % 16, unit 4 ks + lane / 16), down units
+        // Refill for layer l: gate/up units (k < NG: tile T = k / CK, gate
+        // tiles first, then up; K-step ks = CK wave + k % CK of the wave's
+        // input chunk; row f rb + 16 (T % GT) + lane % 16, unit 4 ks +
+        // lane / 16), down units
         // (k = NG + m: tile wave + 8 m of the H rows, row 16 t + lane % 16
         // of the block's down_cols, unit lane / 16) and the gains of the FFN
         // norm.
@@ -1381,13 +1396,13 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
             const int rb = A()->rb, rp = A()->rp, f = fIdx(), I = A()->I;
             const Rsrc rg = rsrc(LY(l)->gate, (size_t)I * gs), ru = rsrc(LY(l)->up, (size_t)I * gs);
             const Rsrc rd = rsrc(LY(l)->down_cols, (size_t)A()->nf * H * rp * 2);
-            const int T = wave % GT2, jj = (T % GT) * 16 + i16, row = f * rb + jj;
             gw2 = load_gains(LY(l)->ln2, act);
 #pragma unroll
             for (int k = 0; k < NF; ++k) {
                 uint32_t off = kNoRead;
                 if (k < NG) {
-                    const int ks = (wave / GT2) * GK + k, unit = 4 * ks + g4;
+                    const int T = k / CK, jj = (T % GT) * 16 + i16, row = f * rb + jj;
+                    const int ks = CK * wave + k % CK, unit = 4 * ks + g4;
                     if (act && jj < rb && row < I && ks < KS && unit < nH) off = (uint32_t)row * gs + (uint32_t)unit * 16u;
                     W[k] = ld_unit(T < GT ? rg : ru, off);
                 } else {
@@ -1430,32 +1445,51 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                     mark(s, 16 * l + 8);
                     float contrib = 0.f;
                     const int ln = lane_here();
-                    if (ln < Q) {
-                        // Every split's max, sum and partial of this row
-                        // (splits past S weigh nothing), then the fold in
-                        // split order.
+                    {
+                        // Lane (k, h) = (ln / HP, ln % HP), HP the q heads
+                        // rounded up to 16, 32 or 64, takes head h's runs
+                        // k, k + 64 / HP, ...: their maxima, sums and this
+                        // row's partials (16-byte reads of the max and sum
+                        // pairs); the lanes of one head then agree on its max
+                        // M_h, weigh their runs by exp(m_s - M_h) and add up
+                        // across lanes (xor shuffles), and lanes k = 0 hold
+                        // the head's output A_h / L_h.
+                        const int HP = Q <= 16 ? 16 : (Q <= 32 ? 32 : 64), SP = 64 / HP;
+                        const int h = ln & (HP - 1), k = ln / HP;
                         const uint64_t *ml = tb + round_up(na, kChunk);
-                        float ms[kMaxSplits], ls[kMaxSplits], ps[kMaxSplits];
+                        float mv[kMaxSplits], lv[kMaxSplits], pv[kMaxSplits], mloc = -INFINITY;
 #pragma unroll
-                        for (int sp = 0; sp < kMaxSplits; ++sp) {
-                            const int it = min(sp, S - 1) * Q + ln;
-                            ms[sp] = sp < S ? val_of(ml[2 * it]) : -INFINITY;
-                            ls[sp] = val_of(ml[2 * it + 1]);
-                            ps[sp] = val_of(tb[it * kOwn + wave]);
-                        }
-                        float mx = -INFINITY;
-#pragma unroll
-                        for (int sp = 0; sp < kMaxSplits; ++sp) mx = fmaxf(mx, ms[sp]);
-                        float Ls = 0.f, acc = 0.f;
-#pragma unroll
-                        for (int sp = 0; sp < kMaxSplits; ++sp) {
-                            if (sp < S) {
-                                const float w = expf(ms[sp] - mx);
-                                Ls = fmaf(w, ls[sp], Ls);
-                                acc = fmaf(w, ps[sp], acc);
+                        for (int c = 0; c < kMaxSplits; ++c) {
+                            mv[c] = -INFINITY;
+                            lv[c] = pv[c] = 0.f;
+                            if (c * SP < S) {
+                                const int sp = c * SP + k;
+                                const int it = min(sp, S - 1) * Q + min(h, Q - 1);
+                                const u32x4 pair = *(const u32x4 *)(ml + 2 * it);
+                                const float pp = val_of(tb[it * kOwn + wave]);
+                                if (h < Q && sp < S) {
+                                    mv[c] = __uint_as_float(pair[0]);
+                                    lv[c] = __uint_as_float(pair[2]);
+                                    pv[c] = pp;
+                                }
+                                mloc = fmaxf(mloc, mv[c]);
                             }
                         }
-                        contrib = acc * (1.0f / Ls);
+                        for (int off = HP; off < 64; off <<= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, off, 64));
+                        float A = 0.f, Lh = 0.f;
+#pragma unroll
+                        for (int c = 0; c < kMaxSplits; ++c) {
+                            if (c * SP < S) {
+                                const float f = mv[c] == -INFINITY ? 0.f : expf(mv[c] - mloc);
+                                A = fmaf(f, pv[c], A);
+                                Lh = fmaf(f, lv[c], Lh);
+                            }
+                        }
+                        for (int off = HP; off < 64; off <<= 1) {
+                            A += __shfl_xor(A, off, 64);
+                            Lh += __shfl_xor(Lh, off, 64);
+                        }
+                        if (k == 0 && h < Q) contrib = A * (1.0f / Lh);
                     }
                     const float o = wave_sum(contrib);
                     if (r < H) {
@@ -1480,18 +1514,13 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                     float x0, x1;
                     poll_x(A()->hid0, tC, x0, x1);
                     stage_gx(x0, x1, gw2);
-                    wait_vm();
-                    bar();
                     mark(s, 16 * l + 10);
                     const int rb = A()->rb, f = fIdx(), I = A()->I;
                     {
-                        // Gate and up rows on the matrix cores: tile
-                        // wave % GT2 over K-steps [(wave / GT2) GK, + GK),
-                        // the K parts added in wave order through LDS.
-                        const uint16_t *xg =
-                            (const uint16_t *)(lds + A()->lds_xb) + a_offset(split_stride(KP)) + 32 * (wave / GT2) * GK;
-                        const float y = kdot<NG, 0>(xg, W);  // all 64 lanes
-                        if (lane_here() < 16) sm.red[wave][lane_here()] = y;
+                        // Gate and up rows on the matrix cores over this
+                        // wave's chunk; the chunks' sums added in wave order.
+                        chunk_products(std::integral_constant<int, GT2>{}, std::integral_constant<int, 0>{}, W);
+                        wait_vm();
                         bar();
                         // Thread j < 32: SwiGLU of the block's row j (zero
                         // past its rows), split for the down product.
@@ -1499,12 +1528,11 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                         if (tid < 32) {
                             float v = 0.f;
                             if (tid < rb && f * rb + tid < I) {
-                                const int t = tid / 16, c = tid % 16;
-                                float gv = sm.red[t][c], uv = sm.red[GT + t][c];
-#pragma unroll
-                                for (int kp = 1; kp < GWP; ++kp) {
-                                    gv += sm.red[t + GT2 * kp][c];
-                                    uv += sm.red[GT + t + GT2 * kp][c];
+                                const int nch = n_chunks();
+                                float gv = sm.red[0][tid], uv = sm.red[0][16 * GT + tid];
+                                for (int w = 1; w < nch; ++w) {
+                                    gv += sm.red[w][tid];
+                                    uv += sm.red[w][16 * GT + tid];
                                 }
                                 const float inv = norm_scale();
                                 gv = inv * gv;
