@@ -78,10 +78,11 @@ constexpr int kKvLdsMax = 64 * 1024;   // LDS for one item's K and V rows, at mo
 constexpr int kChunk = 128;            // tagged words per wave-wide 16-byte-per-lane load
 constexpr int kXcds = 8;               // the dispatcher places block b on XCD b % 8 (each XCD has its own L2)
 
-// Blocks per attention split: q heads rounded up to the XCD count, so that
-// item (split s, head h) at block s * heads_padded + h runs on XCD h % 8
-// for every s: the splits of one head, which read the same q rows and
-// o_proj columns, share one L2.
+// Blocks per attention split: q heads rounded up to the XCD count. Item
+// (split s, head h) sits at block s * heads_padded + slot(h), on XCD
+// slot(h) % 8 for every s: the splits of one head, which read the same q
+// rows and o_proj columns, share one L2, and (fused_item_slots) the heads of
+// one KV group, which read the same K/V rows, share a set of XCDs.
 __host__ __device__ constexpr int heads_padded(int q_heads) { return (q_heads + kXcds - 1) / kXcds * kXcds; }
 constexpr long kSpinLimit = 1L << 20;
 constexpr uint32_t kNoRead = 0x80000000u;  // buffer offset past every range
@@ -203,6 +204,22 @@ __device__ __forceinline__ void dma16(const void *g, const void *lds) {
         "s_mov_b32 m0, %2\n\t"
         "s_nop 0\n\t"
         "global_load_lds_dwordx4 %1, off sc1\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(g), "s"(l)
+        : "memory");
+}
+// dma16 without the coherence bit, for data no block writes while it is
+// read (embedding and gain rows; K/V rows of positions already written,
+// which no later write touches): L2 hits across the blocks of one XCD.
+__device__ __forceinline__ void dma16_nc(const void *g, const void *lds) {
+    const uint32_t l = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, off\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
         : "v"(g), "s"(l)
@@ -695,8 +712,8 @@ __device__ __forceinline__ void load_kv_lds(CArgs *a, uint8_t *k_lds, uint8_t *v
         for (int c = wave * 1024; c < bytes; c += kWaves * 1024) {
             const int byte = c + lane * 16;
             if (byte < bytes) {
-                dma16(ks + byte, kd + c);
-                dma16(vs + byte, vd + c);
+                dma16_nc(ks + byte, kd + c);
+                dma16_nc(vs + byte, vd + c);
             }
         }
     }
@@ -914,23 +931,21 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
     const int b = blockIdx.x;
     uint64_t *tb = (uint64_t *)lds;
 
-    // Roles: items (split s, head h) at block s * heads_padded + h for
-    // s < splits (item index s * q_heads + h), KV blocks
+    // Roles: items (split s, head h) at block s * heads_padded + slot(h)
+    // for s < splits (item index s * q_heads + h), KV blocks
     // [kv0, kv0 + nkv) (wave w of KV block k: rotation pair 8 k + w of the
     // K/V rows), FFN blocks [f0, f0 + nf): block f owns gate/up rows
     // [f rb, f rb + rb) (wave w rows w, w + 8, ...) and, for f < no, the
     // residual rows 8 f + w. Blocks in none of these only join the LM head.
-    auto isItem = [&]() {
-        const int qp = heads_padded(A()->q_heads);
-        return b < A()->splits * qp && b % qp < A()->q_heads;
-    };
+    auto slotHead = [&]() { return (int)A()->slot_head[b % heads_padded(A()->q_heads)]; };
+    auto isItem = [&]() { return b < A()->splits * heads_padded(A()->q_heads) && slotHead() >= 0; };
     auto isKV = [&]() { return b >= A()->kv0 && b < A()->kv0 + A()->nkv; };
     auto fIdx = [&]() { return b - A()->f0; };
     auto isFFN = [&]() { return b >= A()->f0; };
     auto isOwner = [&]() { return isFFN() && fIdx() < A()->no; };
     auto hasRows = [&]() { return isFFN() && fIdx() < A()->nbd; };
     auto hasHead = [&]() { return b * kWaves < A()->V; };
-    auto itHead = [&]() { return b % heads_padded(A()->q_heads); };
+    auto itHead = [&]() { return slotHead(); };
     auto itSplit = [&]() { return b / heads_padded(A()->q_heads); };
     auto itIdx = [&]() { return itSplit() * A()->q_heads + itHead(); };
     auto kvPair = [&]() { return (b - A()->kv0) * kWaves + wave; };
@@ -1608,9 +1623,35 @@ constexpr Variant kVariants[] = {
 
 int units_per_lane(int cols, int elems_per_unit) { return (cols / elems_per_unit + 63) / 64; }
 
+// The block slot of each q head within a run (FusedArgs::slot_head): the
+// heads of one KV group on their own XCDs (group g on XCDs g * 8 / kv_heads
+// onward, head i of the group on XCD i % (8 / kv_heads) of those, in slot
+// layer i / (8 / kv_heads)) where the group count divides the XCD count and
+// the slots allow; else head h in slot h.
+void item_slots(int q_heads, int kv_heads, int32_t (&slot_head)[64]) {
+    for (int32_t &v : slot_head) v = -1;
+    const int qp = heads_padded(q_heads), layers = qp / kXcds;
+    const int G = kv_heads > 0 ? q_heads / kv_heads : 0;
+    const int xpg = kv_heads > 0 && kv_heads <= kXcds && kXcds % kv_heads == 0 ? kXcds / kv_heads : 0;
+    if (qp <= 64 && xpg > 0 && G * kv_heads == q_heads && (G + xpg - 1) / xpg <= layers) {
+        // Head i of group g: XCD g xpg + i % xpg, slot layer i / xpg.
+        for (int h = 0; h < q_heads; ++h) {
+            const int g = h / G, i = h % G;
+            slot_head[(i / xpg) * kXcds + g * xpg + i % xpg] = h;
+        }
+        return;
+    }
+    for (int h = 0; h < q_heads && h < 64; ++h) slot_head[h] = h;
+}
+
 FusedGeom geometry(int H, int q_heads, int kv_heads, int hd, int I, bool kv_f32, int blocks) {
     FusedGeom g{};
     g.nf = blocks * 5 / 8;
+    // FFN blocks of exactly 32 gate/up rows where that many still fit and
+    // cover the owners: the down columns then fill one matrix-core K-step
+    // with no zero padding (Qwen2-0.5B: 152 blocks instead of 160 x 31 rows).
+    const int n32 = (I + 31) / 32;
+    if (n32 <= g.nf && n32 >= H / kOwn) g.nf = n32;
     g.f0 = blocks - g.nf;
     g.nkv = (kv_heads * hd + kWaves - 1) / kWaves;  // one rotation pair of K/V rows per wave
     g.kv0 = g.f0 - g.nkv;
@@ -1671,6 +1712,7 @@ int launch_one(FusedArgs a, int nb, hipStream_t s) {
     a.rb = geo.rb;
     a.rp = geo.rp;
     a.head_blocks = std::min(nb, (a.V + kWaves - 1) / kWaves);
+    item_slots(a.q_heads, a.kv_heads, a.slot_head);
     const LdsLayout lay = lds_layout(a.H, HD, (int)sizeof(KT), ip, a.ni, a.nbd, nb);
     a.lds_xs = lay.xs;
     a.lds_xb = lay.xb;

@@ -21,8 +21,9 @@ struct FusedLayer {
 
 // How the grid divides into roles for one model shape (fused_geometry).
 //   items:  one q head over one run of `ip` positions each: item (split s,
-//           head h) at block s * qp + h, qp = q_heads rounded up to 8 (the
-//           XCD count), item index s * q_heads + h
+//           head h) at block s * qp + slot(h), qp = q_heads rounded up to 8
+//           (the XCD count), slot(h) from fused_item_slots, item index
+//           s * q_heads + h
 //   KV:     blocks [kv0, kv0 + nkv): the new position's K/V rows, one
 //           rotation pair per wave
 //   FFN:    blocks [f0, f0 + nf): gate/up rows, SwiGLU, down columns; the
@@ -71,6 +72,9 @@ struct FusedArgs {
     // offsets).
     int ni, ip, splits;         // items (q_heads * splits), positions per item
     int kv0, nkv, f0, nf, no, nbd, rb, rp, head_blocks;
+    // Item placement: the q head of each of the heads_padded block slots of
+    // a run (slot j on XCD j % 8), or -1 for a slot without an item.
+    int32_t slot_head[64];  // 32-bit: read by scalar loads (a byte would take a vector load)
     int lds_xs, lds_xb, lds_q, lds_kv, lds_emb, lds_g1, lds_g2, lds_total;
 };
 

@@ -34,6 +34,19 @@ IP_MAX = 256
 MAX_SPLITS = 16
 
 
+def item_slots(q_heads: int, kv_heads: int) -> list:
+    """The block slot (within a run's heads_padded blocks, slot j on XCD
+    j % 8) of each q head, as decode_fused.hip's item_slots places them: the
+    heads of one KV group on their own XCDs where the group count divides 8
+    and the slots allow, else head h in slot h."""
+    qp = (q_heads + 7) // 8 * 8
+    G = q_heads // kv_heads if kv_heads else 0
+    xpg = 8 // kv_heads if kv_heads and kv_heads <= 8 and 8 % kv_heads == 0 else 0
+    if qp <= 64 and xpg and G * kv_heads == q_heads and (G + xpg - 1) // xpg <= qp // 8:
+        return [(h % G // xpg) * 8 + (h // G) * xpg + h % G % xpg for h in range(q_heads)]
+    return list(range(q_heads))
+
+
 def block_roles(shape, blocks: int, context: int, ctx_end: int = 0, kv_bf16: bool = True):
     """Block index sets per role at a step of context `context` in a launch
     whose last step reaches `ctx_end`, as the launcher assigns them
@@ -42,10 +55,13 @@ def block_roles(shape, blocks: int, context: int, ctx_end: int = 0, kv_bf16: boo
     qh, kvh = shape.q_heads, shape.kv_heads
     ctx_end = ctx_end or context
     nf = blocks * 5 // 8
+    n32 = (I + 31) // 32  # FFN blocks of exactly 32 rows where they fit and cover the owners
+    if H // 8 <= n32 <= nf:
+        nf = n32
     f0 = blocks - nf
     nkv = (kvh * hd + KWAVES - 1) // KWAVES
     kv0 = f0 - nkv
-    qp = (qh + 7) // 8 * 8  # item (split s, head h) at block s * qp + h
+    qp = (qh + 7) // 8 * 8  # item (split s, head h) at block s * qp + slot(h)
     s_cap = min(MAX_SPLITS, kv0 // qp)
     row = hd * (2 if kv_bf16 else 4)
     ip_max, ip = 0, 64
@@ -58,7 +74,8 @@ def block_roles(shape, blocks: int, context: int, ctx_end: int = 0, kv_bf16: boo
     rb = (I + nf - 1) // nf
     nbd = (I + rb - 1) // rb
     no = H // 8
-    items = [sp * qp + h for sp in range(S) for h in range(qh)]
+    slot = item_slots(qh, kvh)
+    items = [sp * qp + slot[h] for sp in range(S) for h in range(qh)]
     return {
         "items": items,
         "last": [b for b in items if b // qp == S - 1],

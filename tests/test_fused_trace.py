@@ -8,22 +8,28 @@ from cheetah_amd import configs, fused_trace
 
 def test_block_roles_partition_the_grid():
     roles = fused_trace.block_roles(configs.QWEN2_0_5B, 256, 544, 640)
-    # 160 FFN blocks (5/8 of the grid): 31 gate/up rows each, 157 with rows,
-    # 112 owners of 8 residual rows; 128 K/V rotation pairs over 16 KV
-    # blocks; the items below them: 14 q heads x 5 runs of 128 positions
-    # (640 positions fit 5 runs of 128 in the 80 item blocks), run s of head
-    # h at block 16 s + h, so that every run of a head is on XCD h % 8.
+    # 152 FFN blocks of exactly 32 gate/up rows (4864 = 152 x 32; at most
+    # 5/8 of the grid), 112 of them owners of 8 residual rows; 128 K/V
+    # rotation pairs over 16 KV blocks; the items below them: 14 q heads x 5
+    # runs of 128 positions
+    # (640 positions fit 5 runs of 128 in the 80 item blocks). Run s of head
+    # h sits at block 16 s + slot(h): every run of a head on one XCD, and
+    # the 7 heads of each KV group on their own 4 XCDs (2 heads per XCD).
     assert roles["ip"] == 128
-    assert roles["items"] == [16 * s + h for s in range(5) for h in range(14)]
-    assert all(b % 8 == (b % 16) % 8 for b in roles["items"])
-    assert roles["last"] == list(range(64, 78))
-    assert roles["kv"] == list(range(80, 96))
-    assert roles["owners"] == list(range(96, 208))
-    assert roles["ffn"] == list(range(96, 253))
+    slot = fused_trace.item_slots(14, 2)
+    assert sorted(slot) == sorted(set(slot)) and all(0 <= j < 16 for j in slot)
+    assert [{slot[h] % 8 for h in range(g * 7, g * 7 + 7)} for g in range(2)] == [{0, 1, 2, 3}, {4, 5, 6, 7}]
+    assert roles["items"] == [16 * s + slot[h] for s in range(5) for h in range(14)]
+    assert roles["last"] == [64 + slot[h] for h in range(14)]
+    assert roles["kv"] == list(range(88, 104))
+    assert roles["owners"] == list(range(104, 216))
+    assert roles["ffn"] == list(range(104, 256))
     # Shorter launches take shorter runs: 320 positions in 5 runs of 64
     # (the 80 item blocks hold 5 runs of each of the 14 q heads).
     short = fused_trace.block_roles(configs.QWEN2_0_5B, 256, 200, 320)
-    assert short["ip"] == 64 and short["items"] == [16 * s + h for s in range(4) for h in range(14)]
+    assert short["ip"] == 64 and short["items"] == [16 * s + slot[h] for s in range(4) for h in range(14)]
+    # Without a fitting KV-group split, head h keeps slot h.
+    assert fused_trace.item_slots(12, 3) == list(range(12))
 
 
 def test_report_recovers_known_segments():
