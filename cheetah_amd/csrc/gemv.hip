@@ -211,22 +211,6 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(Args a) {
 }
 
 // ---------------------------------------------------------------------------
-// Q4 codes as BF16 pairs: nibble n of a dword (code c, n = c mod 16) gives
-// the BF16 0x4300 | (n ^ 8) = 128 + (c + 8) = 136 + c (exact), i.e.
-// (n & 0xF) ^ 0x4308: one shift and one AND-XOR (a single three-input
-// bit operation on gfx950) per pair; pair j holds nibbles j and j + 4.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ u32x4 q4_pairs(uint32_t w) {
-    u32x4 p;
-    p[0] = (w & 0x000F000Fu) ^ 0x43084308u;
-    p[1] = ((w >> 4) & 0x000F000Fu) ^ 0x43084308u;
-    p[2] = ((w >> 8) & 0x000F000Fu) ^ 0x43084308u;
-    p[3] = ((w >> 12) & 0x000F000Fu) ^ 0x43084308u;
-    return p;
-}
-
-
-// ---------------------------------------------------------------------------
 // Aligned-unit GEMV: every row is streamed as 16-byte units from its
 // 16-byte-aligned-down start, even when the reference layout only aligns rows
 // to 4 bytes (Q4 rows of 2052 / 7172 bytes, Q8 rows of K rounded up to 4).

@@ -280,9 +280,9 @@ def test_qwen2_0_5b_greedy_bf16_kv(hip):
 @pytest.mark.parametrize("kv", ["bf16", "f32"])
 @pytest.mark.parametrize("shape", TINY + [configs.QWEN2_0_5B], ids=lambda s: s.name)
 def test_persistent_decode_matches_graph_decode(hip, shape, kv, monkeypatch):
-    """The persistent decode kernel (one launch for many steps, device-wide
-    barriers) and the per-step graph path compute the same math: same greedy
-    tokens over 40 steps and logits within 1e-4 relative."""
+    """The persistent decode kernel (one launch for many steps, no
+    device-wide barrier) and the per-step graph path compute the same math:
+    same greedy tokens over 40 steps and logits within 1e-4 relative."""
     w = weights(shape)
     prompt = synth.make_tokens(shape.vocab_size, 100, seed=11)
     runs = {}
@@ -292,6 +292,28 @@ def test_persistent_decode_matches_graph_decode(hip, shape, kv, monkeypatch):
         first = g.forward_greedy(prompt, 0, chunk_rows=64)
         toks = g.decode_greedy(first, 100, 40)
         logits = g.forward(toks[-1:], 140)
+        runs[mode] = ([first] + toks.tolist(), logits)
+        g.close()
+    assert runs["1"][0] == runs["0"][0]
+    assert rel_err(runs["1"][1], runs["0"][1]) < 1e-4
+
+
+def test_persistent_decode_long_runs_match_graph_decode(hip, monkeypatch):
+    """Near the persistent kernel's longest context (Qwen2-0.5B, BF16 K/V: 5
+    runs of 256 positions, 1,280), a 900-token prompt and 40 steps take
+    256-position attention runs: each wave of an item scores up to 32 cached
+    positions in four passes of 8, a run's last wave a partial pass. Same
+    greedy tokens as the graph path and logits within 1e-4."""
+    shape = configs.QWEN2_0_5B
+    w = weights(shape)
+    prompt = synth.make_tokens(shape.vocab_size, 900, seed=17)
+    runs = {}
+    for mode in ("1", "0"):
+        monkeypatch.setenv("CHEETAH_HIP_FUSED", mode)
+        g = hip.HipForward(shape, w, kv_capacity=1024, max_chunk_rows=128, kv="bf16")
+        first = g.forward_greedy(prompt, 0, chunk_rows=128)
+        toks = g.decode_greedy(first, 900, 40)
+        logits = g.forward(toks[-1:], 940)
         runs[mode] = ([first] + toks.tolist(), logits)
         g.close()
     assert runs["1"][0] == runs["0"][0]
