@@ -253,34 +253,52 @@ inline size_t aligned_lds_max(int K, bool norm) { return aligned_lds(K, norm, 5)
 // gfx9-family chips, and the non-temporal cache policy bit of a buffer load.
 constexpr int kBufferDword3 = 0x00020000;
 constexpr int kBufferNT = 2;
-constexpr int kAThreads = 512;  // 8 waves share one x staging
+// 16 bytes per lane from global memory into LDS at lds + 16 * lane (lds the
+// same in every lane). The copy takes its LDS base from m0, which the
+// compiler reserves, so the old value is saved and restored around it; the
+// compiler does not see the copy (the caller waits for it with
+// wait_vm_but), so its later LDS reads do not wait for the weight loads in
+// flight, as they would after the compiler's own global_load_lds builtin.
+__device__ __forceinline__ void lds_dma16(const void *g, const void *lds) {
+    const uint32_t l = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(g), "s"(l)
+        : "memory");
+}
+// Waits until at most N of this wave's vector memory operations are in
+// flight (they complete in issue order).
+template <int N>
+__device__ __forceinline__ void wait_vm_but() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+constexpr int kAThreads = 512;  // at most 8 waves share one x staging
 constexpr int kAWaves = kAThreads / 64;
 
+// One aligned GEMV (see the file head) as the work of one block: `bid` of
+// `nblk` blocks of kAThreads threads.
 template <int FMT, int R, int KS, bool NORM, bool DUAL, int UNROLL>
-__global__ __launch_bounds__(kAThreads) void gemv_aligned_kernel(Args a, int P) {
+struct AlignedGemv {
     using U = Unit<FMT, 16>;
-    constexpr int E = U::E;
-    constexpr int D = 4;
-    constexpr int GPB = kAWaves / KS;
-    constexpr int STEP = 64 * KS * UNROLL;
-    constexpr int NM = DUAL ? 2 : 1;
-    extern __shared__ float4 xs_v4[];  // 16-byte aligned
-    float *xs_all = (float *)xs_v4;
-    float *xs = xs_all + kPad;
-    __shared__ float red[kAWaves];
-    __shared__ float kred[kAWaves][NM * R];
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    // Wave-uniform, so the row pointers below live in scalar registers and
-    // make buffer descriptors without a per-lane loop.
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int sub = wave % KS, gib = wave / KS;
-    const int klane = sub * 64 + lane;
-    const int K = a.K;
-    const int row_bytes = FMT == FMT_Q4 ? (K + 1) / 2 : (FMT == FMT_Q8 ? K : 2 * K);
-    const int blocks_of_rows = (a.rows + R * P - 1) / (R * P);
-    const int groups = blocks_of_rows * P;
+    static constexpr int E = U::E;
+    static constexpr int D = 4;
+    static constexpr int STEP = 64 * KS * UNROLL;
+    static constexpr int NM = DUAL ? 2 : 1;
+    static constexpr int XL = x_shift_log2(FMT, R, DUAL);
+    static constexpr int NLOADS = UNROLL * NM * R;  // vector loads of one batch
+    typedef uint32_t Batch[UNROLL][NM][R][D];
 
+    const Args &a;
+    const int P;
+    int tid, lane, wave, sub, klane, K, row_bytes, groups, g, gstride, iters;
     const uint8_t *ap[NM][R];  // aligned-down row starts
     // One buffer descriptor per row over its nfull whole units: a load past
     // them returns zeros and moves no memory, so every batch load is issued
@@ -288,12 +306,36 @@ __global__ __launch_bounds__(kAThreads) void gemv_aligned_kernel(Args a, int P) 
     __amdgpu_buffer_rsrc_t rs[NM][R];
     int row_of[R];
     int shift = 0, nfull = 0;
-    bool gvalid = false;
-    auto set_group = [&](int g) {
-        const int blk = g / P, ph = g % P;
+    bool gvalid = false, first_issued = false;
+    Batch A, B;
+
+    __device__ __forceinline__ AlignedGemv(const Args &args, int phases, int bid, int nblk) : a(args), P(phases) {
+        tid = threadIdx.x;
+        lane = tid & 63;
+        // Wave-uniform, so the row pointers below live in scalar registers
+        // and make buffer descriptors without a per-lane loop.
+        wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        constexpr int gpb = kAWaves / KS;  // row groups per block
+        sub = wave % KS;
+        klane = sub * 64 + lane;
+        K = a.K;
+        row_bytes = FMT == FMT_Q4 ? (K + 1) / 2 : (FMT == FMT_Q8 ? K : 2 * K);
+        groups = (a.rows + R * P - 1) / (R * P) * P;
+        // The block's waves take consecutive row groups (neighbouring rows:
+        // measured faster than spreading them over the blocks, Q4 gate/up
+        // of a Llama-3-8B layer 18.8 vs 19.3 us).
+        g = bid * gpb + wave / KS;
+        gstride = nblk * gpb;
+        // Every wave of the block runs the same number of iterations (the
+        // cross-wave K reduction synchronizes the block).
+        iters = (groups - bid * gpb + gstride - 1) / gstride;
+    }
+
+    __device__ __forceinline__ void set_group(int gg) {
+        const int blk = gg / P, ph = gg % P;
         const int row0 = blk * R * P + ph;
-        // The last block of rows can leave phases without a first row: such a
-        // group loads nothing and stores nothing.
+        // The last block of rows can leave phases without a first row: such
+        // a group loads nothing and stores nothing.
         gvalid = row0 < a.rows;
         if (!gvalid) {
             nfull = 0;
@@ -318,16 +360,15 @@ __global__ __launch_bounds__(kAThreads) void gemv_aligned_kernel(Args a, int P) 
             ap[0][r] = a.w + (size_t)rr * a.stride - delta;
             if constexpr (DUAL) ap[1][r] = a.w2 + (size_t)rr * a.stride - delta;
         }
-    };
-    auto set_rsrc = [&]() {
+    }
+    __device__ __forceinline__ void set_rsrc() {
 #pragma unroll
         for (int m = 0; m < NM; ++m)
 #pragma unroll
             for (int r = 0; r < R; ++r)
                 rs[m][r] = __builtin_amdgcn_make_buffer_rsrc((void *)ap[m][r], (short)0, nfull * 16, kBufferDword3);
-    };
-    typedef uint32_t Batch[UNROLL][NM][R][D];
-    auto load_batch = [&](Batch &buf, int u0) {
+    }
+    __device__ __forceinline__ void load_batch(Batch &buf, int u0) {
 #pragma unroll
         for (int i = 0; i < UNROLL; ++i) {
             const int u = u0 + 64 * KS * i;
@@ -343,69 +384,65 @@ __global__ __launch_bounds__(kAThreads) void gemv_aligned_kernel(Args a, int P) 
                     buf[i][m][r][3] = v[3];
                 }
         }
-    };
+    }
+    // The first row group's first batch (issued at most once).
+    __device__ __forceinline__ void start() {
+        if (first_issued) return;
+        first_issued = true;
+        if (g < groups) {
+            set_group(g);
+            set_rsrc();
+            load_batch(A, klane);
+        }
+    }
+    // Waits until this wave's operations issued before start() are done,
+    // leaving the first batch in flight.
+    __device__ __forceinline__ void wait_before_first() {
+        if (g < groups) wait_vm_but<NLOADS>();
+        else wait_vm_but<0>();
+    }
 
-    int g = blockIdx.x * GPB + gib;
-    const int gstride = gridDim.x * GPB;
-    // The first row group's first batch is in flight while x is staged.
-    Batch A, B;
-    if (g < groups) {
-        set_group(g);
-        set_rsrc();
-        load_batch(A, klane);
-    }
-    constexpr int XL = x_shift_log2(FMT, R, DUAL);
-    for (int i = tid; i < kPad; i += kAThreads) {
-        xs_all[i] = 0.f;
-        xs[x_addr(K + i, XL)] = 0.f;
-    }
-    // x (and the norm gain) come in as direct global->LDS copies (padded x as
-    // 16-byte loads written to their places), all issued before one wait, so
-    // staging costs one memory round trip.
-    float *gs = xs + x_span(K, XL);  // gain as floats-of-bf16-pairs (NORM only)
-    const bool dma_x = ((uintptr_t)a.x % 16) == 0 && (K % 4) == 0;
-    const bool dma_g = NORM && ((uintptr_t)a.gain % 16) == 0 && (K % 8) == 0;
-    if (dma_x) {
-        if constexpr (XL != 0) {
-            for (int f = tid * 4; f < K; f += kAThreads * 4)
-                *(float4 *)(xs + x_addr(f, XL)) = *(const float4 *)(a.x + f);
-        } else {
-            for (int c = wave; c * 256 < K; c += kAWaves) {
-                const int f = c * 256 + lane * 4;
-                if (f < K)
-                    __builtin_amdgcn_global_load_lds(a.x + f, (__attribute__((address_space(3))) void *)(xs + c * 256),
-                                                     16, 0, 0);
+    // Zero padding, then x (and the norm gain) as direct global->LDS copies.
+    // Padded x: lanes in groups of nine, eight 16-byte pieces of one
+    // 32-element block and one that fills the 16-byte gap after it (never
+    // read), 7 blocks per instruction. Returns whether the gain went to LDS.
+    __device__ __forceinline__ bool stage_x(float *xs_all) {
+        float *xs = xs_all + kPad;
+        for (int i = tid; i < kPad; i += kAThreads) {
+            xs_all[i] = 0.f;
+            xs[x_addr(K + i, XL)] = 0.f;
+        }
+        float *gs = xs + x_span(K, XL);  // gain as floats-of-bf16-pairs (NORM only)
+        const bool dma_x = ((uintptr_t)a.x % 16) == 0 && (K % 4) == 0;
+        const bool dma_g = NORM && ((uintptr_t)a.gain % 16) == 0 && (K % 8) == 0;
+        if (dma_x) {
+            if constexpr (XL != 0) {
+                static_assert(XL == 5, "padded x in 32-element blocks");
+                const int j = lane / 9, q = lane % 9;
+                for (int c = wave; c * 224 < K; c += kAWaves) {
+                    const int blk = c * 224 + 32 * j, f = blk + 4 * (q < 8 ? q : 0);
+                    if (lane < 63 && blk < K && f + 4 <= K) lds_dma16(a.x + f, xs + x_addr(c * 224, XL));
+                }
+            } else {
+                for (int c = wave; c * 256 < K; c += kAWaves) {
+                    const int f = c * 256 + lane * 4;
+                    if (f < K) lds_dma16(a.x + f, xs + c * 256);
+                }
             }
         }
-    }
-    if (dma_g) {
-        for (int c = wave; c * 512 < K; c += kAWaves) {
-            const int f = c * 512 + lane * 8;
-            if (f < K) __builtin_amdgcn_global_load_lds(a.gain + f, (__attribute__((address_space(3))) void *)(gs + c * 256), 16, 0, 0);
+        if (dma_g) {
+            for (int c = wave; c * 512 < K; c += kAWaves) {
+                const int f = c * 512 + lane * 8;
+                if (f < K) lds_dma16(a.gain + f, gs + c * 256);
+            }
         }
+        if (!dma_x)
+            for (int i = tid; i < K; i += kAThreads) xs[x_addr(i, XL)] = a.x[i];
+        return dma_g;
     }
-    if (!dma_x)
-        for (int i = tid; i < K; i += kAThreads) xs[x_addr(i, XL)] = a.x[i];
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if constexpr (NORM) {
-        // RMSNorm (ops.rs:646-652): x * (inv * gain), inv = 1/sqrt(mean(x^2)+eps).
-        float ss = 0.f;
-        for (int i = tid; i < K; i += kAThreads) ss = fmaf(xs[x_addr(i, XL)], xs[x_addr(i, XL)], ss);
-        ss = wave_sum(ss);
-        if (lane == 0) red[wave] = ss;
-        __syncthreads();
-        float total = 0.f;
-#pragma unroll
-        for (int w = 0; w < kAWaves; ++w) total += red[w];
-        const float inv = 1.0f / sqrtf(total / (float)K + a.eps);
-        const uint16_t *gl = (const uint16_t *)gs;
-        for (int i = tid; i < K; i += kAThreads)
-            xs[x_addr(i, XL)] = xs[x_addr(i, XL)] * (inv * bf16_f32(dma_g ? gl[i] : a.gain[i]));
-        __syncthreads();
-    }
+
     // acc += the batch's weights (units u0 + 64 KS i) times x.
-    auto mac_batch = [&](const Batch &cur, int u0, float (&acc)[NM][R]) {
+    __device__ __forceinline__ void mac_batch(const Batch &cur, int u0, float (&acc)[NM][R], const float *xs) {
 #pragma unroll
         for (int i = 0; i < UNROLL; ++i) {
             const int u = u0 + 64 * KS * i;
@@ -468,113 +505,151 @@ __global__ __launch_bounds__(kAThreads) void gemv_aligned_kernel(Args a, int P) 
                     }
             }
         }
-    };
+    }
 
-    // Every wave of the block runs the same number of iterations (the
-    // cross-wave K reduction below synchronizes the block).
-    const int iters = (groups - (int)blockIdx.x * GPB + gstride - 1) / gstride;
-    for (int it = 0; it < iters; ++it, g += gstride) {
-        const bool valid = g < groups && gvalid;
-        float acc[NM][R];
-#pragma unroll
-        for (int m = 0; m < NM; ++m)
-#pragma unroll
-            for (int r = 0; r < R; ++r) acc[m][r] = 0.f;
-        if (valid) {
-            // Batches alternate between A and B, so no register copy (which
-            // would wait for the prefetch) separates a load from its use:
-            // batch j+1 streams in while batch j is multiplied. The batch
-            // count is wave-uniform; lanes past the row load zeros.
-            const int nb = (nfull - sub * 64 + STEP - 1) / STEP;
-            int j = 0;
-            // (The scheduling barriers keep the compiler from sinking a
-            // prefetch below the multiply-adds to save registers.)
-            for (; j + 2 <= nb; j += 2) {
-                load_batch(B, klane + (j + 1) * STEP);
-                __builtin_amdgcn_sched_barrier(0);
-                mac_batch(A, klane + j * STEP, acc);
-                load_batch(A, klane + (j + 2) * STEP);
-                __builtin_amdgcn_sched_barrier(0);
-                mac_batch(B, klane + (j + 1) * STEP, acc);
-            }
-            if (j < nb) mac_batch(A, klane + j * STEP, acc);
-            if constexpr (FMT == FMT_Q4) {
-#pragma unroll
-                for (int m = 0; m < NM; ++m)
-#pragma unroll
-                    for (int r = 0; r < R; ++r) acc[m][r] *= 0.0625f;
-            }
-            // Elements past the last whole unit (fewer than 16 bytes' worth).
-            for (int e = max(nfull * E - shift, 0) + klane; e < K; e += 64 * KS) {
-                const float xv = xs[x_addr(e, XL)];
-#pragma unroll
-                for (int m = 0; m < NM; ++m)
-#pragma unroll
-                    for (int r = 0; r < R; ++r)
-                        acc[m][r] = fmaf(U::element(ap[m][r] + (shift * 16 / E), e), xv, acc[m][r]);
-            }
-        }
-#pragma unroll
-        for (int m = 0; m < NM; ++m)
-#pragma unroll
-            for (int r = 0; r < R; ++r) acc[m][r] = wave_sum(acc[m][r]);
-        int orow[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) orow[r] = row_of[r];
-        // Prefetch the next group's first batch before the epilogue.
-        if (g + gstride < groups) {
-            set_group(g + gstride);
-            set_rsrc();
-            load_batch(A, klane);
-        }
-        if constexpr (KS > 1) {
-            if (lane == 0) {
-#pragma unroll
-                for (int m = 0; m < NM; ++m)
-#pragma unroll
-                    for (int r = 0; r < R; ++r) kred[wave][m * R + r] = acc[m][r];
-            }
+    // After x has landed (the caller waited and passed a block barrier): the
+    // fused RMSNorm, the products of every row group of this block, and the
+    // epilogue. red: kAWaves floats; kred: kAWaves x NM R floats (LDS).
+    __device__ __forceinline__ void finish(float *xs_all, bool dma_g, float *red, float *kred) {
+        float *xs = xs_all + kPad;
+        if constexpr (NORM) {
+            // RMSNorm (ops.rs:646-652): x * (inv * gain), inv = 1/sqrt(mean(x^2)+eps).
+            const float *gs = xs + x_span(K, XL);
+            float ss = 0.f;
+            for (int i = tid; i < K; i += kAThreads) ss = fmaf(xs[x_addr(i, XL)], xs[x_addr(i, XL)], ss);
+            ss = wave_sum(ss);
+            if (lane == 0) red[wave] = ss;
             __syncthreads();
-            if (sub == 0) {
+            float total = 0.f;
 #pragma unroll
-                for (int m = 0; m < NM; ++m)
-#pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        float s = kred[wave][m * R + r];
-#pragma unroll
-                        for (int k = 1; k < KS; ++k) s += kred[wave + k][m * R + r];
-                        acc[m][r] = s;
-                    }
-            }
+            for (int w = 0; w < kAWaves; ++w) total += red[w];
+            const float inv = 1.0f / sqrtf(total / (float)K + a.eps);
+            const uint16_t *gl = (const uint16_t *)gs;
+            for (int i = tid; i < K; i += kAThreads)
+                xs[x_addr(i, XL)] = xs[x_addr(i, XL)] * (inv * bf16_f32(dma_g ? gl[i] : a.gain[i]));
             __syncthreads();
         }
-        if (sub == 0 && valid) {
+        for (int it = 0; it < iters; ++it, g += gstride) {
+            const bool valid = g < groups && gvalid;
+            float acc[NM][R];
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const int row = orow[r];
-                if (lane == r && row < a.rows) {
-                    float v = acc[0][r];
-                    if (a.sc) v = v * a.sc[row];
-                    if constexpr (DUAL) {
-                        float u = acc[1][r];
-                        if (a.sc2) u = u * a.sc2[row];
-                        // silu_multiply, ops.rs:743-747: g * (u / (1 + exp(-g))).
-                        a.y[row] = v * (u / (1.0f + expf(-v)));
-                    } else {
-                        if (a.bias) v = v + a.bias[row];
-                        if (a.epi == EPI_RESIDUAL) a.residual[row] = a.residual[row] + v;
-                        else a.y[row] = v;
+            for (int m = 0; m < NM; ++m)
+#pragma unroll
+                for (int r = 0; r < R; ++r) acc[m][r] = 0.f;
+            if (valid) {
+                // Batches alternate between A and B, so no register copy
+                // (which would wait for the prefetch) separates a load from
+                // its use: batch j+1 streams in while batch j is multiplied.
+                // The batch count is wave-uniform; lanes past the row load
+                // zeros.
+                const int nb = (nfull - sub * 64 + STEP - 1) / STEP;
+                int j = 0;
+                // (The scheduling barriers keep the compiler from sinking a
+                // prefetch below the multiply-adds to save registers.)
+                for (; j + 2 <= nb; j += 2) {
+                    load_batch(B, klane + (j + 1) * STEP);
+                    __builtin_amdgcn_sched_barrier(0);
+                    mac_batch(A, klane + j * STEP, acc, xs);
+                    load_batch(A, klane + (j + 2) * STEP);
+                    __builtin_amdgcn_sched_barrier(0);
+                    mac_batch(B, klane + (j + 1) * STEP, acc, xs);
+                }
+                if (j < nb) mac_batch(A, klane + j * STEP, acc, xs);
+                if constexpr (FMT == FMT_Q4) {
+#pragma unroll
+                    for (int m = 0; m < NM; ++m)
+#pragma unroll
+                        for (int r = 0; r < R; ++r) acc[m][r] *= 0.0625f;
+                }
+                // Elements past the last whole unit (fewer than 16 bytes' worth).
+                for (int e = max(nfull * E - shift, 0) + klane; e < K; e += 64 * KS) {
+                    const float xv = xs[x_addr(e, XL)];
+#pragma unroll
+                    for (int m = 0; m < NM; ++m)
+#pragma unroll
+                        for (int r = 0; r < R; ++r)
+                            acc[m][r] = fmaf(U::element(ap[m][r] + (shift * 16 / E), e), xv, acc[m][r]);
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < NM; ++m)
+#pragma unroll
+                for (int r = 0; r < R; ++r) acc[m][r] = wave_sum(acc[m][r]);
+            int orow[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) orow[r] = row_of[r];
+            // Prefetch the next group's first batch before the epilogue.
+            if (g + gstride < groups) {
+                set_group(g + gstride);
+                set_rsrc();
+                load_batch(A, klane);
+            }
+            if constexpr (KS > 1) {
+                if (lane == 0) {
+#pragma unroll
+                    for (int m = 0; m < NM; ++m)
+#pragma unroll
+                        for (int r = 0; r < R; ++r) kred[wave * NM * R + m * R + r] = acc[m][r];
+                }
+                __syncthreads();
+                if (sub == 0) {
+#pragma unroll
+                    for (int m = 0; m < NM; ++m)
+#pragma unroll
+                        for (int r = 0; r < R; ++r) {
+                            float sacc = kred[wave * NM * R + m * R + r];
+#pragma unroll
+                            for (int k = 1; k < KS; ++k) sacc += kred[(wave + k) * NM * R + m * R + r];
+                            acc[m][r] = sacc;
+                        }
+                }
+                __syncthreads();
+            }
+            if (sub == 0 && valid) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const int row = orow[r];
+                    if (lane == r && row < a.rows) {
+                        float v = acc[0][r];
+                        if (a.sc) v = v * a.sc[row];
+                        if constexpr (DUAL) {
+                            float u = acc[1][r];
+                            if (a.sc2) u = u * a.sc2[row];
+                            // silu_multiply, ops.rs:743-747: g * (u / (1 + exp(-g))).
+                            a.y[row] = v * (u / (1.0f + expf(-v)));
+                        } else {
+                            if (a.bias) v = v + a.bias[row];
+                            if (a.epi == EPI_RESIDUAL) a.residual[row] = a.residual[row] + v;
+                            else a.y[row] = v;
+                        }
                     }
                 }
             }
         }
     }
+};
+
+template <int FMT, int R, int KS, bool NORM, bool DUAL, int UNROLL>
+__global__ __launch_bounds__(kAThreads) void gemv_aligned_kernel(Args a, int P) {
+    using G = AlignedGemv<FMT, R, KS, NORM, DUAL, UNROLL>;
+    extern __shared__ float4 xs_v4[];  // 16-byte aligned
+    __shared__ float red[kAWaves];
+    __shared__ float kred[kAWaves * G::NM * R];
+    float *xs_all = (float *)xs_v4;
+    G gm(a, P, (int)blockIdx.x, (int)gridDim.x);
+    // x goes first: a wave's loads complete in order, so the wait ends when
+    // x has landed while the first weight batch stays in flight.
+    const bool dma_g = gm.stage_x(xs_all);
+    gm.start();
+    gm.wait_before_first();
+    __syncthreads();
+    gm.finish(xs_all, dma_g, red, kred);
 }
 
-// Blocks of the aligned kernel one CU holds: waves per SIMD from the kernel's
-// VGPR count (512 per lane, granule 8), LDS from the device's per-CU size.
+// Waves per SIMD the aligned kernel's VGPR count allows (512 per lane,
+// granule 8, at most 8).
 template <class Kern>
-int aligned_blocks_per_cu(Kern kern, size_t lds) {
+int aligned_waves_per_simd(Kern kern) {
     static std::mutex mu;
     static std::vector<std::pair<const void *, int>> vgprs;
     int regs = 0;
@@ -589,20 +664,23 @@ int aligned_blocks_per_cu(Kern kern, size_t lds) {
             vgprs.push_back({(const void *)kern, regs});
         }
     }
-    const int waves_per_simd = std::min(8, 512 / ((regs + 7) / 8 * 8));
-    const int by_waves = waves_per_simd * 4 / kAWaves;
-    const int by_lds = (int)(device_lds_per_cu() / (lds + 1024));
-    return std::max(1, std::min(by_waves, by_lds));
+    return std::min(8, 512 / ((regs + 7) / 8 * 8));
 }
 
 template <int FMT, int R, int KS, bool NORM, bool DUAL, int UNROLL>
 int launch_aligned(const Args &a, int P, hipStream_t s) {
-    constexpr int GPB = kAWaves / KS;
     const int groups = (a.rows + R * P - 1) / (R * P) * P;
     const size_t lds = aligned_lds(a.K, NORM, x_shift_log2(FMT, R, DUAL));
     auto kern = gemv_aligned_kernel<FMT, R, KS, NORM, DUAL, UNROLL>;
-    const int cap = device_cus() * aligned_blocks_per_cu(kern, lds);
-    const int blocks = std::max(1, std::min((groups + GPB - 1) / GPB, cap));
+    // Blocks of 8 waves, as many per CU as the VGPRs and the LDS allow.
+    // (Blocks of 7 waves, which fill the 28 slots of a 7-wave-per-SIMD kernel
+    // where 8-wave blocks leave 4 idle, measured slower: the Q4 gate/up of
+    // a Llama-3-8B layer 20.4 vs 19.0 us.)
+    const int per_cu = std::max(1, std::min(4 * aligned_waves_per_simd(kern) / kAWaves,
+                                            (int)(device_lds_per_cu() / (lds + 1024))));
+    const int gpb = kAWaves / KS;
+    const int cap = device_cus() * per_cu;
+    const int blocks = std::max(1, std::min((groups + gpb - 1) / gpb, cap));
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(kAThreads), lds, s, a, P);
     CHIP_CHECK(hipGetLastError());
     return 0;
@@ -638,25 +716,34 @@ int pick_ks(const Args &a, int P, int ks, int n_units, hipStream_t s) {
 // 22.0 us). K is split when
 // the row groups are too few for the wave slots (Q4: below a quarter of
 // them, since its rows share x reads), keeping >= 2 units per lane.
-template <int FMT, bool NORM, bool DUAL>
-int pick_aligned(const Args &a, int P, hipStream_t s) {
+struct AlignedShape {
+    int R, ks, unroll;
+};
+template <int FMT>
+AlignedShape aligned_shape(const Args &a) {
     constexpr int E = Unit<FMT, 16>::E;
     const int n_units = (a.K + E - 1) / E;
     const long slots = (long)device_cus() * 16;
     int R = 1;
     // (Four Q4 rows per wave for 6144-row matrices left the grid under one
     // block per CU: 2,474 vs 2,488 tok/s on a 4-layer Llama-3-8B Q4 decode.)
-    if constexpr (FMT == FMT_Q4) {
-        if (a.rows >= slots / 2) R = 2;
-    }
+    if (FMT == FMT_Q4 && a.rows >= slots / 2) R = 2;
     const long groups = (a.rows + R - 1) / R;
     const long busy = FMT == FMT_Q4 ? slots / 4 : slots;
     int ks = 1;
     while (ks < 8 && groups * ks < busy && n_units >= 64 * 2 * ks * 2) ks *= 2;
+    return AlignedShape{R, ks, n_units / ks <= 1024 ? 1 : 2};
+}
+
+template <int FMT, bool NORM, bool DUAL>
+int pick_aligned(const Args &a, int P, hipStream_t s) {
+    constexpr int E = Unit<FMT, 16>::E;
+    const int n_units = (a.K + E - 1) / E;
+    const AlignedShape sh = aligned_shape<FMT>(a);
     if constexpr (FMT == FMT_Q4) {
-        if (R == 2) return pick_ks<FMT, 2, NORM, DUAL>(a, P, ks, n_units, s);
+        if (sh.R == 2) return pick_ks<FMT, 2, NORM, DUAL>(a, P, sh.ks, n_units, s);
     }
-    return pick_ks<FMT, 1, NORM, DUAL>(a, P, ks, n_units, s);
+    return pick_ks<FMT, 1, NORM, DUAL>(a, P, sh.ks, n_units, s);
 }
 
 template <int FMT>
@@ -698,9 +785,14 @@ int pick_mode(const Args &a, bool norm, bool dual, hipStream_t s) {
     return dual ? pick_shape<FMT, false, true>(a, s) : pick_shape<FMT, false, false>(a, s);
 }
 
-}  // namespace
-
-int launch_gemv(const GemvJob &job, hipStream_t s) {
+// A job's kernel arguments, and whether (with which row phase count P) the
+// aligned kernel takes it.
+struct Prepared {
+    Args a;
+    bool norm, dual, aligned;
+    int P;
+};
+int prepare(const GemvJob &job, Prepared &out) {
     const WMat &w = job.w;
     if (!w.base || !job.x || w.rows == 0 || w.cols == 0) return fail("HIP backend: gemv needs a weight and an input.");
     if (w.rows > (size_t)INT32_MAX || w.cols > (size_t)INT32_MAX) return fail("HIP backend: gemv shape too large.");
@@ -735,19 +827,29 @@ int launch_gemv(const GemvJob &job, hipStream_t s) {
     const bool aligned_ok = a.stride % bpe_mod == 0 && b0 % bpe_mod == 0 && (uintptr_t)w.base % 16 == 0 &&
                             (!dual || ((uintptr_t)job.w2.base % 16 == 0 && ((uintptr_t)a.w2 - b0) % 16 == 0)) &&
                             aligned_lds_max(a.K, norm) + 256 <= device_max_lds();
-    if (aligned_ok) {
-        const int sm = (int)(a.stride % 16);
-        const int P = sm == 0 ? 1 : 16 / std::gcd(sm, 16);
-        switch (w.fmt) {
-            case FMT_BF16: return pick_aligned_mode<FMT_BF16>(a, P, norm, dual, s);
-            case FMT_Q8: return pick_aligned_mode<FMT_Q8>(a, P, norm, dual, s);
-            case FMT_Q4: return pick_aligned_mode<FMT_Q4>(a, P, norm, dual, s);
+    if (w.fmt != FMT_BF16 && w.fmt != FMT_Q8 && w.fmt != FMT_Q4) return fail("HIP backend: unknown weight format.");
+    const int sm = (int)(a.stride % 16);
+    out = Prepared{a, norm, dual, aligned_ok, sm == 0 ? 1 : 16 / std::gcd(sm, 16)};
+    return 0;
+}
+
+}  // namespace
+
+int launch_gemv(const GemvJob &job, hipStream_t s) {
+    Prepared p;
+    CHIP_TRY(prepare(job, p));
+    const Args &a = p.a;
+    if (p.aligned) {
+        switch (job.w.fmt) {
+            case FMT_BF16: return pick_aligned_mode<FMT_BF16>(a, p.P, p.norm, p.dual, s);
+            case FMT_Q8: return pick_aligned_mode<FMT_Q8>(a, p.P, p.norm, p.dual, s);
+            case FMT_Q4: return pick_aligned_mode<FMT_Q4>(a, p.P, p.norm, p.dual, s);
         }
     }
-    switch (w.fmt) {
-        case FMT_BF16: return pick_mode<FMT_BF16>(a, norm, dual, s);
-        case FMT_Q8: return pick_mode<FMT_Q8>(a, norm, dual, s);
-        case FMT_Q4: return pick_mode<FMT_Q4>(a, norm, dual, s);
+    switch (job.w.fmt) {
+        case FMT_BF16: return pick_mode<FMT_BF16>(a, p.norm, p.dual, s);
+        case FMT_Q8: return pick_mode<FMT_Q8>(a, p.norm, p.dual, s);
+        case FMT_Q4: return pick_mode<FMT_Q4>(a, p.norm, p.dual, s);
     }
     return fail("HIP backend: unknown weight format.");
 }
