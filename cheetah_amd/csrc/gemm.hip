@@ -9,9 +9,10 @@
 // so two v_mfma_f32_32x32x16_bf16 per k-step carry x to ~2^-17 relative
 // error (f32 accumulation), instead of bf16's 2^-9.
 //
-// Tiling: a 256-thread block computes 64 or 128 tokens x 128 weight rows as
-// 2 x 2 waves (each 32 or 64 tokens x 64 rows); K advances 32 per LDS stage,
-// double-buffered, the next stage's global loads in flight during the MFMAs.
+// Tiling: a block of 4 or 8 waves (2 x 2 or 4 x 2) computes 64 or 128
+// tokens x 128 weight rows, each wave 32 tokens x 64 rows (the register-
+// staged fallback also 64 x 64 per wave); K advances 32 per LDS stage, the
+// next stages' copies in flight during the MFMAs.
 //
 // Accumulation order: K is cut into chunks of a depth fixed by K alone; each
 // chunk is accumulated from zero and the chunk sums are folded left to right
@@ -452,7 +453,8 @@ constexpr int vm_wait_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 <<
 // ring holds NS = 4 stages (6 measured no faster); stage s + NS - 2 is issued
 // while stage s computes.
 // Q8/Q4 codes of stage s + 1 are converted to BF16 (exactly) once per block,
-// 16 per thread, into one of three converted tiles after stage s's MFMAs;
+// 16 (4 waves) or 8 (8 waves) per thread, into one of three converted tiles
+// after stage s's MFMAs;
 // BF16 weights are read straight from the ring. One barrier per stage. The
 // MFMA sequence per output and the chunk folds are those of gemm_kernel, so
 // the results are the same bits.
@@ -460,11 +462,21 @@ constexpr int vm_wait_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 <<
 template <int FMT>
 constexpr int ring_w_row_bytes() { return FMT == FMT_BF16 ? 64 : FMT == FMT_Q8 ? 32 : 16; }
 
-template <int FMT, bool DUAL, int MT, int NS>
+// Tokens per block: WV waves as WV / 2 x 2, each 32 MT tokens x 64 rows.
+template <int MT, int WV>
+constexpr int ring_bm() { return 32 * MT * (WV / 2); }
+
+template <int FMT, bool DUAL, int MT, int NS, int WV>
 constexpr size_t ring_lds_bytes() {
-    constexpr size_t slot = 2 * (64 * MT) * 64 + (DUAL ? 2 : 1) * BN * ring_w_row_bytes<FMT>();
+    constexpr size_t slot = 2 * ring_bm<MT, WV>() * 64 + (DUAL ? 2 : 1) * BN * ring_w_row_bytes<FMT>();
     return NS * slot + (FMT == FMT_BF16 ? 0 : 3 * (DUAL ? 2 : 1) * BN * 64);
 }
+
+// Weight copy granule (bytes per lane) of the ring: Q4 rows are only 4-byte
+// aligned; Q8 stages are copied 4 bytes a lane where 16 would leave some of
+// 8 waves without a copy (every wave must issue the same count).
+template <int FMT, int WV>
+constexpr int ring_w_granule() { return FMT == FMT_Q4 ? 4 : (FMT == FMT_Q8 && WV == 8) ? 4 : 16; }
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -476,9 +488,10 @@ __device__ __forceinline__ void buf_to_lds(__amdgpu_buffer_rsrc_t r, void *lds, 
     else __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds, 4, voffset, soffset, 0, 0);
 }
 
-template <int FMT, bool DUAL, int MT, int NS>
-__global__ __launch_bounds__(kThreads) void gemm_ring_kernel(GArgs a, int split) {
-    constexpr int BM = 64 * MT;
+template <int FMT, bool DUAL, int MT, int NS, int WV>
+__global__ __launch_bounds__(64 * WV) void gemm_ring_kernel(GArgs a, int split) {
+    constexpr int NT = 64 * WV;                      // threads
+    constexpr int BM = ring_bm<MT, WV>();
     constexpr int XB = BM * 64;                      // bytes of one x half tile (BM rows x 32 BF16)
     constexpr int WRB = ring_w_row_bytes<FMT>();     // raw weight bytes per row and stage
     constexpr int WB = BN * WRB;                     // raw weight bytes per matrix and stage
@@ -486,11 +499,13 @@ __global__ __launch_bounds__(kThreads) void gemm_ring_kernel(GArgs a, int split)
     constexpr int SLOT = 2 * XB + NWM * WB;
     constexpr bool CONV = FMT != FMT_BF16;
     constexpr int WCB = BN * 64;                     // one converted BF16 weight tile
-    constexpr int GW = FMT == FMT_Q4 ? 4 : 16;       // weight copy granule (Q4 rows are 4-byte aligned)
+    constexpr int GW = ring_w_granule<FMT, WV>();    // weight copy granule
     constexpr int NIX = XB / 1024;                   // 1 KB copies per x half
     constexpr int NIW = WB / (64 * GW);              // copies per weight matrix
-    constexpr int D = 2 * NIX / 4 + NWM * NIW / 4;   // copies per wave and stage
-    static_assert(NIX % 4 == 0 && NIW % 4 == 0, "copies must split evenly over the waves");
+    constexpr int D = 2 * NIX / WV + NWM * NIW / WV; // copies per wave and stage
+    constexpr int CPT = BN * 32 / NT;                // codes each thread converts per matrix and stage
+    static_assert(NIX % WV == 0 && NIW % WV == 0, "copies must split evenly over the waves");
+    static_assert(CPT == 8 || CPT == 16, "8 or 16 codes per converting thread");
     static_assert(NS >= 4, "the converted weights trail the ring by one stage");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     uint8_t *ring = smem;
@@ -515,19 +530,20 @@ __global__ __launch_bounds__(kThreads) void gemm_ring_kernel(GArgs a, int split)
     // Per-lane source offsets of this wave's copies (fixed for the launch):
     // x copy q covers rows 16q..16q+15, lane -> row 16q + lane/4 and 16-byte
     // chunk swz(row, lane % 4) of the stage's 32 columns.
-    int xoff[NIX / 4], woff[NIW / 4];
+    int xoff[NIX / WV], woff[NIW / WV];
 #pragma unroll
-    for (int i = 0; i < NIX / 4; ++i) {
-        const int q = wave + 4 * i, r = 16 * q + (lane >> 2);
+    for (int i = 0; i < NIX / WV; ++i) {
+        const int q = wave + WV * i, r = 16 * q + (lane >> 2);
         const int m = min(m0 + r, a.M - 1);  // rows past M feed only unstored outputs
         xoff[i] = (m * a.K + 8 * swz(r, lane & 3)) * 2;
     }
 #pragma unroll
-    for (int i = 0; i < NIW / 4; ++i) {
-        const int q = wave + 4 * i;
+    for (int i = 0; i < NIW / WV; ++i) {
+        const int q = wave + WV * i;
         int r, byte;
         if constexpr (FMT == FMT_BF16) { r = 16 * q + (lane >> 2); byte = 16 * swz(r, lane & 3); }
-        else if constexpr (FMT == FMT_Q8) { r = 32 * q + (lane >> 1); byte = 16 * (lane & 1); }
+        else if constexpr (FMT == FMT_Q8 && GW == 16) { r = 32 * q + (lane >> 1); byte = 16 * (lane & 1); }
+        else if constexpr (FMT == FMT_Q8) { r = 8 * q + (lane >> 3); byte = 4 * (lane & 7); }
         else { r = 16 * q + (lane >> 2); byte = 4 * (lane & 3); }
         const int n = min(n0 + r, a.N - 1);
         woff[i] = n * (int)a.stride + byte;
@@ -540,55 +556,62 @@ __global__ __launch_bounds__(kThreads) void gemm_ring_kernel(GArgs a, int split)
         const int kx = k0 * 2;
         const int kw = FMT == FMT_BF16 ? k0 * 2 : FMT == FMT_Q8 ? k0 : k0 / 2;
 #pragma unroll
-        for (int i = 0; i < NIX / 4; ++i) {
-            const int q = wave + 4 * i;
+        for (int i = 0; i < NIX / WV; ++i) {
+            const int q = wave + WV * i;
             buf_to_lds<16>(rxh, slot + 1024 * q, xoff[i], kx);
             buf_to_lds<16>(rxl, slot + XB + 1024 * q, xoff[i], kx);
         }
 #pragma unroll
-        for (int i = 0; i < NIW / 4; ++i) {
-            const int q = wave + 4 * i;
+        for (int i = 0; i < NIW / WV; ++i) {
+            const int q = wave + WV * i;
             buf_to_lds<GW>(rw, slot + 2 * XB + 64 * GW * q, woff[i], kw);
             if constexpr (DUAL)
                 buf_to_lds<GW>(rw2, slot + 2 * XB + WB + 64 * GW * q, woff[i], kw);
         }
     };
-    // Q8/Q4: stage st's codes -> BF16 tile(s) wcv[st % 3], thread t: row t/2,
-    // codes 16 (t % 2) .. + 15, written in the swizzled layout the MFMA reads.
+    // Q8/Q4: stage st's codes -> BF16 tile(s) wcv[st % 3], thread t: row
+    // t / (32 / CPT), codes CPT (t % (32 / CPT)) .. + CPT - 1, written in the
+    // swizzled layout the MFMA reads.
     // The raw codes are read by inline assembly: the compiler, which cannot
     // tell these reads from the ring's in-flight copies, would otherwise wait
     // for every copy (all NS stages) before them. The copies they need were
     // awaited explicitly.
     auto convert = [&](int st) {
+        constexpr int TPR = 32 / CPT;  // threads per row
+        constexpr int RB = FMT == FMT_Q8 ? CPT : CPT / 2;  // raw bytes per thread
         const uint8_t *slot = ring + (st % NS) * SLOT + 2 * XB;
-        const int row = threadIdx.x >> 1, h = threadIdx.x & 1;
+        const int row = threadIdx.x / TPR, h = threadIdx.x % TPR;
         // (Each read waits for its data inside its own asm statement, so no
         // use of the result can be scheduled ahead of the wait.)
         u32x4 rv[NWM];
 #pragma unroll
         for (int mi = 0; mi < NWM; ++mi) {
-            const uint32_t addr = (uint32_t)(uintptr_t)(slot + mi * WB + row * WRB + (FMT == FMT_Q8 ? 16 : 8) * h);
-            if constexpr (FMT == FMT_Q8) {
+            const uint32_t addr = (uint32_t)(uintptr_t)(slot + mi * WB + row * WRB + RB * h);
+            if constexpr (RB == 16) {
                 asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(rv[mi]) : "v"(addr) : "memory");
-            } else {
+            } else if constexpr (RB == 8) {
                 uint2 t;
                 asm volatile("ds_read_b64 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(t) : "v"(addr) : "memory");
                 rv[mi] = u32x4{t.x, t.y, 0u, 0u};
+            } else {
+                uint32_t t;
+                asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(t) : "v"(addr) : "memory");
+                rv[mi] = u32x4{t, 0u, 0u, 0u};
             }
         }
 #pragma unroll
         for (int mi = 0; mi < NWM; ++mi) {
-            float f[16];
+            float f[CPT];
             if constexpr (FMT == FMT_Q8) {
                 const u32x4 v = rv[mi];
 #pragma unroll
-                for (int q = 0; q < 16; ++q) f[q] = (float)(int)(int8_t)(v[q >> 2] >> (8 * (q & 3)));
+                for (int q = 0; q < CPT; ++q) f[q] = (float)(int)(int8_t)(v[q >> 2] >> (8 * (q & 3)));
             } else {
                 // 16 x code: each nibble moved to the top of a byte, read as
                 // int8 in one instruction (exact in BF16; the chunk sums are
                 // scaled back by 1/16, exactly).
 #pragma unroll
-                for (int h2 = 0; h2 < 2; ++h2) {
+                for (int h2 = 0; h2 < CPT / 8; ++h2) {
                     const uint32_t wd = rv[mi][h2];
                     const uint32_t ev = (wd << 4) & 0xF0F0F0F0u, od = wd & 0xF0F0F0F0u;
                     f[8 * h2 + 0] = sbyte_f32<0>(ev);
@@ -603,11 +626,11 @@ __global__ __launch_bounds__(kThreads) void gemm_ring_kernel(GArgs a, int split)
             }
             uint8_t *dst = wcv + ((st % 3) * NWM + mi) * WCB + row * 64;
 #pragma unroll
-            for (int c = 0; c < 2; ++c) {
+            for (int c = 0; c < CPT / 8; ++c) {
                 bf16x8 b;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) b[e] = (__bf16)f[8 * c + e];
-                *(bf16x8 *)(dst + 16 * swz(row, 2 * h + c)) = b;
+                *(bf16x8 *)(dst + 16 * swz(row, (CPT / 8) * h + c)) = b;
             }
         }
     };
@@ -723,18 +746,18 @@ __global__ __launch_bounds__(kThreads) void gemm_ring_kernel(GArgs a, int split)
     }
 }
 
-template <int FMT, bool DUAL, int MT>
+template <int FMT, bool DUAL, int MT, int WV = 4>
 int launch_ring(const GArgs &a, bool split, hipStream_t s) {
-    constexpr int NS = 4, BM = 64 * MT;
-    constexpr size_t lds = ring_lds_bytes<FMT, DUAL, MT, NS>();
+    constexpr int NS = 4, BM = ring_bm<MT, WV>();
+    constexpr size_t lds = ring_lds_bytes<FMT, DUAL, MT, NS, WV>();
     static bool attr_set = false;
     if (!attr_set) {
-        CHIP_CHECK(hipFuncSetAttribute((const void *)gemm_ring_kernel<FMT, DUAL, MT, NS>,
+        CHIP_CHECK(hipFuncSetAttribute((const void *)gemm_ring_kernel<FMT, DUAL, MT, NS, WV>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         attr_set = true;
     }
     const dim3 grid((a.N + BN - 1) / BN * ((a.M + BM - 1) / BM), 1, split ? a.nchunks : 1);
-    hipLaunchKernelGGL((gemm_ring_kernel<FMT, DUAL, MT, NS>), grid, dim3(kThreads), lds, s, a, split ? 1 : 0);
+    hipLaunchKernelGGL((gemm_ring_kernel<FMT, DUAL, MT, NS, WV>), grid, dim3(64 * WV), lds, s, a, split ? 1 : 0);
     CHIP_CHECK(hipGetLastError());
     if (split && !a.defer) {
         const size_t MN = (size_t)a.M * a.N;
@@ -793,9 +816,8 @@ int launch_fmt(const GArgs &a, bool dual, size_t ws_floats, hipStream_t s, bool 
     const long n_tiles = (a.N + BN - 1) / BN;
     const long tiles128 = n_tiles * ((a.M + 127) / 128), tiles64 = n_tiles * ((a.M + 63) / 64);
     const long cus = device_cus();
-    // Many tiles: fold in registers (128-token tiles when they still fill
-    // the chip, dual always 64). Few tiles: split-K over the chunks when the
-    // workspace holds them.
+    // Many tiles: fold in registers. Few tiles: split-K over the chunks when
+    // the workspace holds them.
     const bool split = a.nchunks > 1 && tiles64 < cus && a.ws &&
                        ws_floats >= gemm_workspace_floats(a.N, a.K, a.M, dual);
     split_out = split;
@@ -805,13 +827,18 @@ int launch_fmt(const GArgs &a, bool dual, size_t ws_floats, hipStream_t s, bool 
     const bool ring = a.xh && a.K % BK == 0 && a.stride % galign == 0 &&
                       ((uintptr_t)a.w % galign) == 0 && (!dual || ((uintptr_t)a.w2 % galign) == 0) &&
                       (size_t)a.M * a.K * 2 < (1ull << 31) && (size_t)a.N * a.stride < (1ull << 31);
-    // The dual gate/up GEMM takes 128-token tiles when they still give every
-    // CU a tile (each weight tile then serves twice the tokens per copy into
-    // LDS: Qwen2-7B 1024-row and Llama-3-8B Q4 512-row prefill chunks 12-14 %
-    // faster, same bits). The single-matrix GEMMs keep 64-token tiles (two
-    // blocks per CU where the grid has them: measured 3-8 % faster than
-    // 128-token tiles on the large shapes).
-    if (ring && dual && !split && tiles128 >= cus) return launch_ring<FMT, true, 2>(a, split, s);
+    // 8-wave blocks of 128 tokens x 128 rows where those tiles cover at
+    // least 7/8 of the CUs: each converted weight tile and each x tile in
+    // LDS then serves twice the MFMAs of a 4-wave 64-token block, with the
+    // same waves per CU (one 8-wave block against two 4-wave ones). Measured
+    // at 1,024 tokens: BF16 4096x4096 358 -> 418, 4096x14336 310 -> 402,
+    // 3584x18944 298 -> 370 TFLOP/s; Llama-3-8B Q4 512-row prefill 17.2K ->
+    // 18.6K tok/s (mostly the dual gate/up, which before took 128-token tiles
+    // on 4 waves), Qwen2-7B 1,024-row 18.2K -> 19.2K; the same bits. Where
+    // the 128-token tiles cover only half the CUs (4096 rows at 512 tokens:
+    // 128 tiles), 4-wave 64-token blocks are faster (307 vs 242 TFLOP/s).
+    if (ring && !split && tiles128 * 8 >= cus * 7)
+        return dual ? launch_ring<FMT, true, 1, 8>(a, split, s) : launch_ring<FMT, false, 1, 8>(a, split, s);
     if (ring) return dual ? launch_ring<FMT, true, 1>(a, split, s) : launch_ring<FMT, false, 1>(a, split, s);
     // Otherwise (K not a multiple of the stage, x not pre-split, or operands
     // beyond the buffer loads' 32-bit offsets): the register-staged kernel.
