@@ -15,12 +15,16 @@
 // next stages' copies in flight during the MFMAs.
 //
 // Accumulation order: K is cut into chunks of a depth fixed by K alone; each
-// chunk is accumulated from zero and the chunk sums are folded left to right
-// (t = 0; t += c0; t += c1; ...). With many tiles a block folds its chunks in
-// registers; with few tiles every chunk is its own block (split-K) and a
-// reduce kernel folds the stored chunk sums in the same order. Both give the
-// same bits, so a token's outputs never depend on how many tokens share the
-// call (chunked prefill stays bit-exact however the prompt is cut).
+// chunk is accumulated from zero. A single matrix's n chunk sums are folded
+// as two halves, t = (c0 + ... + c(h-1)) + (ch + ... + c(n-1)) with
+// h = ceil(n / 2), each half left to right (for n <= 3 this is the plain left
+// fold); the dual gate/up GEMM folds its chunks left to right. With many tiles
+// a block folds its chunks in registers; with fewer tiles the chunks go to
+// split-K blocks (every chunk its own block, or a single matrix's two halves
+// one block each) and the stored sums are folded by a reduce kernel or by the
+// kernel that reads the output, in the same association. Every path gives
+// the same bits, so a token's outputs never depend on how many tokens share
+// the call (chunked prefill stays bit-exact however the prompt is cut).
 #include <algorithm>
 #include <cstdlib>
 
@@ -49,7 +53,8 @@ struct GArgs {
     int defer;          // split-K: leave the chunk sums for the caller
     int epi;
     int chunk, nchunks;  // accumulation chunk depth (multiple of BK) and count
-    float *ws;           // split-K: [nchunks][M][N] chunk sums (a second set for the dual matrix)
+    int nstored;         // split-K: sums stored per output (nchunks, or 2 halves of a single matrix)
+    float *ws;           // split-K: [nstored][M][N] sums (a second set for the dual matrix)
     int vec_x, vec_w;    // 16-byte global loads allowed
 };
 
@@ -329,8 +334,11 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GArgs a, int split) {
     const int wm = (wave >> 1) * 32 * MT, wn = (wave & 1) * 64;
     const int kbeg = split ? blockIdx.z * a.chunk : 0;
     const int kend = split ? min(a.K, kbeg + a.chunk) : a.K;
+    // Single matrix, folding in registers: the first half's total moves to
+    // th when the second half begins (two-half association).
+    const int khalf = (a.nchunks + 1) / 2 * a.chunk;
 
-    f32x16 acc[MT][2], acc2[DUAL ? MT : 1][2], tot[MT][2], tot2[DUAL ? MT : 1][2];
+    f32x16 acc[MT][2], acc2[DUAL ? MT : 1][2], tot[MT][2], tot2[DUAL ? MT : 1][2], th[DUAL ? 1 : MT][2];
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
@@ -340,6 +348,8 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GArgs a, int split) {
             if constexpr (DUAL) {
                 acc2[i][j] = f32x16{};
                 tot2[i][j] = f32x16{};
+            } else {
+                th[i][j] = f32x16{};
             }
         }
 
@@ -388,8 +398,10 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GArgs a, int split) {
                     }
                 }
         }
-        // Chunk end: fold the chunk sum into the running total (t += c).
+        // Chunk end: fold the chunk sum into the running total (t += c); a
+        // single matrix's first half ends here: th = t, t = 0.
         if (k0 + BK >= kend || ((k0 + BK) % a.chunk) == 0) {
+            const bool half_end = !DUAL && !split && k0 + BK == khalf && khalf < kend;
 #pragma unroll
             for (int i = 0; i < MT; ++i)
 #pragma unroll
@@ -399,6 +411,9 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GArgs a, int split) {
                     if constexpr (DUAL) {
                         tot2[i][j] += acc2[i][j];
                         acc2[i][j] = f32x16{};
+                    } else if (half_end) {
+                        th[i][j] = tot[i][j];
+                        tot[i][j] = f32x16{};
                     }
                 }
         }
@@ -413,6 +428,14 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GArgs a, int split) {
     }
     // D layout of the 32x32 MFMA: column = lane % 32, row = 8*(r/4) + 4*(lane/32) + r%4.
     if (!split) {
+        if constexpr (!DUAL) {
+            if (khalf < kend) {
+#pragma unroll
+                for (int i = 0; i < MT; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) tot[i][j] = th[i][j] + tot[i][j];
+            }
+        }
         epilogue_tile<DUAL, MT>(a, tot, tot2, m0 + wm, n0 + wn, lane);
         return;
     }
@@ -428,7 +451,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GArgs a, int split) {
                 if (m >= a.M) continue;
                 const size_t o = ((size_t)blockIdx.z * a.M + m) * a.N + n;
                 a.ws[o] = tot[i][j][q];
-                if constexpr (DUAL) a.ws[(size_t)a.nchunks * a.M * a.N + o] = tot2[i][j][q];
+                if constexpr (DUAL) a.ws[(size_t)a.nstored * a.M * a.N + o] = tot2[i][j][q];
             }
     }
 }
@@ -516,8 +539,11 @@ __global__ __launch_bounds__(64 * WV) void gemm_ring_kernel(GArgs a, int split) 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int wm = (wave >> 1) * 32 * MT, wn = (wave & 1) * 64;
-    const int kbeg = split ? blockIdx.z * a.chunk : 0;
-    const int kend = split ? min(a.K, kbeg + a.chunk) : a.K;
+    // split 0: all of K; 1: chunk blockIdx.z; 2: half blockIdx.z of a single
+    // matrix's chunks (the first hc chunks, then the rest).
+    const int hc = (a.nchunks + 1) / 2;
+    const int kbeg = split == 1 ? blockIdx.z * a.chunk : split == 2 && blockIdx.z ? hc * a.chunk : 0;
+    const int kend = split == 1 ? min(a.K, kbeg + a.chunk) : split == 2 && !blockIdx.z ? min(a.K, hc * a.chunk) : a.K;
     const int nst = (kend - kbeg) / BK;
 
     const __amdgpu_buffer_rsrc_t rxh = __builtin_amdgcn_make_buffer_rsrc((void *)a.xh, (short)0, a.M * a.K * 2, 0x00020000);
@@ -635,13 +661,16 @@ __global__ __launch_bounds__(64 * WV) void gemm_ring_kernel(GArgs a, int split) 
         }
     };
 
-    f32x16 acc[MT][2], acc2[DUAL ? MT : 1][2], tot[MT][2], tot2[DUAL ? MT : 1][2];
+    // th: a single matrix's first-half total while the second half runs
+    // (folding in registers over all of K).
+    f32x16 acc[MT][2], acc2[DUAL ? MT : 1][2], tot[MT][2], tot2[DUAL ? MT : 1][2], th[DUAL ? 1 : MT][2];
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             tot[i][j] = f32x16{};
             if constexpr (DUAL) tot2[i][j] = f32x16{};
+            else th[i][j] = f32x16{};
         }
 
 #pragma unroll
@@ -652,14 +681,22 @@ __global__ __launch_bounds__(64 * WV) void gemm_ring_kernel(GArgs a, int split) 
         convert(0);
     }
     const int cs = a.chunk / BK;  // stages per accumulation chunk
+    const bool halves = !DUAL && !split && hc < a.nchunks;
     for (int c0 = 0; c0 < nst; c0 += cs) {
         const int c1 = min(c0 + cs, nst);
+        // The second half begins: th = t, t = 0.
+        const bool half_start = halves && c0 == hc * cs;
 #pragma unroll
         for (int i = 0; i < MT; ++i)
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 acc[i][j] = f32x16{};
-                if constexpr (DUAL) acc2[i][j] = f32x16{};
+                if constexpr (DUAL) {
+                    acc2[i][j] = f32x16{};
+                } else if (half_start) {
+                    th[i][j] = tot[i][j];
+                    tot[i][j] = f32x16{};
+                }
             }
         for (int st = c0; st < c1; ++st) {
             issue(st + NS - 2);
@@ -726,6 +763,14 @@ __global__ __launch_bounds__(64 * WV) void gemm_ring_kernel(GArgs a, int split) 
     // Drain the copies of stages past the range before the block exits.
     __builtin_amdgcn_s_waitcnt(vm_wait_imm(0));
     if (!split) {
+        if constexpr (!DUAL) {
+            if (halves) {
+#pragma unroll
+                for (int i = 0; i < MT; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) tot[i][j] = th[i][j] + tot[i][j];
+            }
+        }
         epilogue_tile<DUAL, MT>(a, tot, tot2, m0 + wm, n0 + wn, lane);
         return;
     }
@@ -741,13 +786,13 @@ __global__ __launch_bounds__(64 * WV) void gemm_ring_kernel(GArgs a, int split) 
                 if (m >= a.M) continue;
                 const size_t o = ((size_t)blockIdx.z * a.M + m) * a.N + n;
                 a.ws[o] = tot[i][j][q];
-                if constexpr (DUAL) a.ws[(size_t)a.nchunks * a.M * a.N + o] = tot2[i][j][q];
+                if constexpr (DUAL) a.ws[(size_t)a.nstored * a.M * a.N + o] = tot2[i][j][q];
             }
     }
 }
 
 template <int FMT, bool DUAL, int MT, int WV = 4>
-int launch_ring(const GArgs &a, bool split, hipStream_t s) {
+int launch_ring(const GArgs &a, int split, hipStream_t s) {
     constexpr int NS = 4, BM = ring_bm<MT, WV>();
     constexpr size_t lds = ring_lds_bytes<FMT, DUAL, MT, NS, WV>();
     static bool attr_set = false;
@@ -756,8 +801,8 @@ int launch_ring(const GArgs &a, bool split, hipStream_t s) {
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         attr_set = true;
     }
-    const dim3 grid((a.N + BN - 1) / BN * ((a.M + BM - 1) / BM), 1, split ? a.nchunks : 1);
-    hipLaunchKernelGGL((gemm_ring_kernel<FMT, DUAL, MT, NS, WV>), grid, dim3(64 * WV), lds, s, a, split ? 1 : 0);
+    const dim3 grid((a.N + BN - 1) / BN * ((a.M + BM - 1) / BM), 1, split ? a.nstored : 1);
+    hipLaunchKernelGGL((gemm_ring_kernel<FMT, DUAL, MT, NS, WV>), grid, dim3(64 * WV), lds, s, a, split);
     CHIP_CHECK(hipGetLastError());
     if (split && !a.defer) {
         const size_t MN = (size_t)a.M * a.N;
@@ -768,30 +813,36 @@ int launch_ring(const GArgs &a, bool split, hipStream_t s) {
     return 0;
 }
 
-// Folds the stored chunk sums in chunk order (t = 0; t += c_z) and applies
-// the epilogue: the same bits as the in-register fold.
+// Folds the stored sums (a.nstored per output: every chunk's, or a single
+// matrix's two halves) in the GEMM's association and applies the epilogue:
+// the same bits as the in-register fold. Dual: left to right (t = 0;
+// t += c_z); single matrix: the first ceil(n / 2) left to right, the rest
+// left to right, then the two added.
 template <bool DUAL>
 __global__ __launch_bounds__(kThreads) void gemm_reduce_kernel(GArgs a) {
     const size_t MN = (size_t)a.M * a.N;
     const size_t e = (size_t)blockIdx.x * kThreads + threadIdx.x;
     if (e >= MN) return;
-    // Eight chunk sums (of each matrix) loaded at a time, folded in order.
-    float v = 0.f, u = 0.f;
-    for (int z0 = 0; z0 < a.nchunks; z0 += 8) {
+    const int n = a.nstored, hs = DUAL ? n : (n + 1) / 2;
+    // Eight stored sums (of each matrix) loaded at a time, folded in order.
+    float v = 0.f, v2 = 0.f, u = 0.f;
+    for (int z0 = 0; z0 < n; z0 += 8) {
         float t[8], t2[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const bool in = z0 + j < a.nchunks;
+            const bool in = z0 + j < n;
             t[j] = in ? a.ws[(size_t)(z0 + j) * MN + e] : 0.f;
-            if constexpr (DUAL) t2[j] = in ? a.ws[((size_t)a.nchunks + z0 + j) * MN + e] : 0.f;
+            if constexpr (DUAL) t2[j] = in ? a.ws[((size_t)n + z0 + j) * MN + e] : 0.f;
         }
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-            if (z0 + j < a.nchunks) {
-                v += t[j];
-                if constexpr (DUAL) u += t2[j];
-            }
+        for (int j = 0; j < 8; ++j) {
+            if (z0 + j < hs) v += t[j];
+            else if (z0 + j < n) v2 += t[j];
+            if constexpr (DUAL)
+                if (z0 + j < n) u += t2[j];
+        }
     }
+    if (!DUAL && hs < n) v = v + v2;
     epilogue<DUAL>(a, (int)(e / a.N), (int)(e % a.N), v, u);
 }
 
@@ -811,8 +862,28 @@ int launch_mt(const GArgs &a, bool split, hipStream_t s) {
     return 0;
 }
 
+// Whether `blocks` blocks of one per CU keep at least 3/4 of the CU slots of
+// their rounds busy (288 blocks on 256 CUs: a second round of 32 does not).
+bool fills_rounds(long blocks, long cus) {
+    const long rounds = (blocks + cus - 1) / cus;
+    return blocks >= 1 && 4 * blocks >= 3 * rounds * cus;
+}
+// 8-wave blocks of 128 tokens x 128 rows: their tiles cover at least 7/8 of
+// the CUs and fill their rounds.
+bool gemm_w8(int N, int M) {
+    const long tiles128 = (long)((N + BN - 1) / BN) * ((M + 127) / 128), cus = device_cus();
+    return tiles128 * 8 >= cus * 7 && fills_rounds(tiles128, cus);
+}
+// Whether a single matrix's GEMM runs as two chunk halves on 8-wave blocks:
+// two blocks per 128-token tile fill 95-100 % of the CUs in one round, and
+// it has more than one chunk.
+bool gemm_halves_split(int N, int M, int nchunks) {
+    const long tiles128 = (long)((N + BN - 1) / BN) * ((M + 127) / 128), cus = device_cus();
+    return nchunks > 1 && 2 * tiles128 * 20 >= cus * 19 && 2 * tiles128 <= cus;
+}
+
 template <int FMT>
-int launch_fmt(const GArgs &a, bool dual, size_t ws_floats, hipStream_t s, bool &split_out) {
+int launch_fmt(GArgs a, bool dual, size_t ws_floats, hipStream_t s, bool &split_out, int &stored_out) {
     const long n_tiles = (a.N + BN - 1) / BN;
     const long tiles128 = n_tiles * ((a.M + 127) / 128), tiles64 = n_tiles * ((a.M + 63) / 64);
     const long cus = device_cus();
@@ -821,6 +892,8 @@ int launch_fmt(const GArgs &a, bool dual, size_t ws_floats, hipStream_t s, bool 
     const bool split = a.nchunks > 1 && tiles64 < cus && a.ws &&
                        ws_floats >= gemm_workspace_floats(a.N, a.K, a.M, dual);
     split_out = split;
+    a.nstored = a.nchunks;
+    stored_out = a.nstored;
     // Pre-split x with K a multiple of the stage and 32-bit buffer offsets:
     // the ring kernel (weights copied 16 bytes at a time, Q4 4 at a time).
     const int galign = FMT == FMT_Q4 ? 4 : 16;
@@ -837,9 +910,19 @@ int launch_fmt(const GArgs &a, bool dual, size_t ws_floats, hipStream_t s, bool 
     // on 4 waves), Qwen2-7B 1,024-row 18.2K -> 19.2K; the same bits. Where
     // the 128-token tiles cover only half the CUs (4096 rows at 512 tokens:
     // 128 tiles), 4-wave 64-token blocks are faster (307 vs 242 TFLOP/s).
-    if (ring && !split && tiles128 * 8 >= cus * 7)
-        return dual ? launch_ring<FMT, true, 1, 8>(a, split, s) : launch_ring<FMT, false, 1, 8>(a, split, s);
-    if (ring) return dual ? launch_ring<FMT, true, 1>(a, split, s) : launch_ring<FMT, false, 1>(a, split, s);
+    if (ring && !split && gemm_w8(a.N, a.M))
+        return dual ? launch_ring<FMT, true, 1, 8>(a, 0, s) : launch_ring<FMT, false, 1, 8>(a, 0, s);
+    // A single matrix whose 128-token tiles cover half the CUs (4,096 rows
+    // at 512 tokens: 128 tiles): its two chunk halves on separate 8-wave
+    // blocks, the half sums folded by the reader.
+    if (ring && !split && !dual && gemm_halves_split(a.N, a.M, a.nchunks) && a.ws &&
+        ws_floats >= 2 * (size_t)a.M * a.N) {
+        split_out = true;
+        a.nstored = stored_out = 2;
+        return launch_ring<FMT, false, 1, 8>(a, 2, s);
+    }
+    const int sp = split ? 1 : 0;
+    if (ring) return dual ? launch_ring<FMT, true, 1>(a, sp, s) : launch_ring<FMT, false, 1>(a, sp, s);
     // Otherwise (K not a multiple of the stage, x not pre-split, or operands
     // beyond the buffer loads' 32-bit offsets): the register-staged kernel.
     if (dual) return launch_mt<FMT, true, 1>(a, split, s);
@@ -903,10 +986,16 @@ size_t gemm_workspace_floats(size_t N, size_t K, size_t M, bool dual) {
 }
 
 size_t gemm_split_workspace_floats(size_t N, size_t K, size_t m_max, bool dual) {
-    // The split path runs only while 64-token tiles leave CUs idle.
-    const size_t n_tiles = (N + BN - 1) / BN;
-    const size_t m_split = 64 * (((size_t)device_cus() + n_tiles - 1) / n_tiles);
-    return gemm_workspace_floats(N, K, std::min(m_max, m_split), dual);
+    // The per-chunk split runs only while 64-token tiles leave CUs idle; the
+    // two-half split (single matrices) while two blocks per 128-token tile
+    // fit the CUs once.
+    const size_t n_tiles = (N + BN - 1) / BN, cus = (size_t)device_cus();
+    const size_t m_split = 64 * ((cus + n_tiles - 1) / n_tiles);
+    size_t need = gemm_workspace_floats(N, K, std::min(m_max, m_split), dual);
+    const int chunk = gemm_chunk_depth((int)K);
+    if (!dual && (K + chunk - 1) / chunk > 1)
+        need = std::max(need, 2 * std::min(m_max, 128 * (cus / (2 * n_tiles))) * N);
+    return need;
 }
 
 int launch_gemm(const GemmJob &job, hipStream_t s) {
@@ -953,14 +1042,14 @@ int launch_gemm(const GemmJob &job, hipStream_t s) {
     if (w.fmt == FMT_Q4 && (a.stride % 4 != 0 || p1 % 4 != 0 || p2 % 4 != 0))
         return fail("HIP backend: Q4 rows must be 4-byte aligned.");
     bool split = false;
-    int rc = -1;
+    int stored = 0, rc = -1;
     switch (w.fmt) {
-        case FMT_BF16: rc = launch_fmt<FMT_BF16>(a, dual, job.ws_floats, s, split); break;
-        case FMT_Q8: rc = launch_fmt<FMT_Q8>(a, dual, job.ws_floats, s, split); break;
-        case FMT_Q4: rc = launch_fmt<FMT_Q4>(a, dual, job.ws_floats, s, split); break;
+        case FMT_BF16: rc = launch_fmt<FMT_BF16>(a, dual, job.ws_floats, s, split, stored); break;
+        case FMT_Q8: rc = launch_fmt<FMT_Q8>(a, dual, job.ws_floats, s, split, stored); break;
+        case FMT_Q4: rc = launch_fmt<FMT_Q4>(a, dual, job.ws_floats, s, split, stored); break;
         default: return fail("HIP backend: unknown weight format.");
     }
-    if (rc == 0 && a.defer && split) *job.deferred = a.nchunks;
+    if (rc == 0 && a.defer && split) *job.deferred = stored;
     return rc;
 }
 

@@ -64,9 +64,10 @@ struct GemmJob {
     // each, the bits launch_split_bf16 would give), for the next GEMM.
     uint16_t *yh = nullptr, *yl = nullptr;
     // EPI_RESIDUAL / EPI_STORE, optional: when the GEMM splits K, leave the
-    // chunk sums in ws ([*deferred][n][rows]) for the caller's reduction
-    // (launch_residual_rmsnorm_rows, launch_rope_append) and set *deferred to
-    // the chunk count; 0 when the GEMM applied its epilogue itself.
+    // stored sums in ws ([*deferred][n][rows]: every chunk's, or the two
+    // halves') for the caller's reduction (launch_residual_rmsnorm_rows,
+    // launch_rope_append) and set *deferred to their count; 0 when the GEMM
+    // applied its epilogue itself.
     int *deferred = nullptr;
 };
 int launch_gemm(const GemmJob &job, hipStream_t stream);
@@ -94,7 +95,9 @@ int launch_embed(const uint16_t *table, size_t hidden, const uint32_t *tokens, s
 int launch_rmsnorm_rows(const float *x, const uint16_t *gain, float eps, size_t rows, size_t n, float *out,
                         hipStream_t s, uint16_t *xh = nullptr, uint16_t *xl = nullptr);
 // A deferred residual GEMM's reduction fused with the next RMSNorm: per row
-// m and column i, v = sum over chunks z (in order) of ws[z][m][i], times
+// m and column i, v = the nchunks stored sums ws[z][m][i] folded as the
+// GEMM folds them (the first ceil(n / 2) in order, the rest in order, the
+// two added), times
 // sc[i], plus bias[i] (each optional), hidden[m][i] += v; then, with a gain,
 // the row RMSNorm of hidden into out (and BF16 halves when xh / xl are set).
 // The same operations as the GEMM's split-K reduction then
@@ -129,8 +132,9 @@ int qkv_perm_row(int stored_row, int q_heads, int kv_heads, int head_dim, int ro
 // qrot[rows][q_dim] in reference order, K and V rows are appended to the
 // paged cache. Positions are pos0 + i, where pos0 is read from *pos_dev when
 // pos_dev is set (decode graph) and is `offset` otherwise.
-// With nchunks > 0 the qkv values are a deferred split-K GEMM's: the chunk
-// sums ws[nchunks][rows][q_dim + 2*kv_dim] folded in order, times sc (if
+// With nchunks > 0 the qkv values are a deferred split-K GEMM's: the stored
+// sums ws[nchunks][rows][q_dim + 2*kv_dim] folded as the GEMM folds them (the
+// first ceil(n / 2) in order, the rest in order, the two added), times sc (if
 // set), plus bias (if set) - the GEMM epilogue's arithmetic; qkv is unused.
 int launch_rope_append(const float *qkv, float *qrot, size_t rows, int q_heads, const KvGeom &g, const KvLayer &kv,
                        const float *rope_cos, const float *rope_sin, int rotary_dim, size_t offset,

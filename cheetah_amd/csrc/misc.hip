@@ -63,11 +63,13 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_rows_kernel(const float *x, 
     }
 }
 
-// A residual GEMM's split-K reduction (chunk sums folded in order, then the
-// epilogue of gemm_reduce_kernel: row scale, bias, residual add) fused with
-// the row RMSNorm that follows it; the norm's sum of squares runs over the
-// same per-thread order as rmsnorm_rows_kernel, so every output has the bits
-// of the two separate kernels.
+// A residual GEMM's split-K reduction (its nchunks stored sums folded in a
+// single matrix's association: the first ceil(n / 2) left to right, the
+// rest left to right, then the two added; then the epilogue of
+// gemm_reduce_kernel: row scale, bias, residual add) fused with the row
+// RMSNorm that follows it; the norm's sum of squares runs over the same
+// per-thread order as rmsnorm_rows_kernel, so every output has the bits of
+// the two separate kernels.
 __global__ __launch_bounds__(kThreads) void residual_rmsnorm_rows_kernel(const float *ws, int nchunks, const float *sc,
                                                                          const float *bias, float *hidden, int rows,
                                                                          int n, const uint16_t *gain, float eps,
@@ -79,15 +81,17 @@ __global__ __launch_bounds__(kThreads) void residual_rmsnorm_rows_kernel(const f
     // A thread's elements i = tid + kThreads k, EPT of them per pass: their
     // residuals and eight chunk sums each are loaded together (one memory
     // round trip per eight chunks, not per element), then each element folds
-    // its chunks in chunk order and the squares are summed in element order.
+    // its chunks (two halves, each in chunk order) and the squares are summed
+    // in element order.
     constexpr int EPT = 4, ZB = 8;
+    const int hs = (nchunks + 1) / 2;  // sums in the first half
     float ss = 0.f;
     for (int base = 0; base < n; base += EPT * kThreads) {
-        float v[EPT], hv[EPT];
+        float v[EPT], v2[EPT], hv[EPT];
 #pragma unroll
         for (int k = 0; k < EPT; ++k) {
             const int i = base + (int)threadIdx.x + kThreads * k;
-            v[k] = 0.f;
+            v[k] = v2[k] = 0.f;
             hv[k] = i < n ? h[i] : 0.f;
         }
         for (int z0 = 0; z0 < nchunks; z0 += ZB) {
@@ -102,14 +106,16 @@ __global__ __launch_bounds__(kThreads) void residual_rmsnorm_rows_kernel(const f
 #pragma unroll
             for (int j = 0; j < ZB; ++j)
 #pragma unroll
-                for (int k = 0; k < EPT; ++k)
-                    if (z0 + j < nchunks) v[k] += t[j][k];
+                for (int k = 0; k < EPT; ++k) {
+                    if (z0 + j < hs) v[k] += t[j][k];
+                    else if (z0 + j < nchunks) v2[k] += t[j][k];
+                }
         }
 #pragma unroll
         for (int k = 0; k < EPT; ++k) {
             const int i = base + (int)threadIdx.x + kThreads * k;
             if (i < n) {
-                float x = v[k];
+                float x = hs < nchunks ? v[k] + v2[k] : v[k];
                 if (sc) x = x * sc[i];
                 if (bias) x = x + bias[i];
                 const float r = hv[k] + x;
@@ -166,12 +172,17 @@ __global__ __launch_bounds__(kThreads) void rope_append_kernel(const float *__re
     if (t >= q_dim + kv_dim) return;
     const long pos = (pos_dev ? (long)*pos_dev : offset) + row;
     const float *q = qkv + (size_t)row * width;
-    // Element col of this row: stored, or (SUM) the deferred GEMM's chunk
-    // sums folded in order, then scale and bias (its epilogue, same bits).
+    // Element col of this row: stored, or (SUM) the deferred GEMM's stored
+    // sums folded in its association (the first ceil(n / 2) left to right,
+    // the rest left to right, the two added), then scale and bias (its
+    // epilogue, same bits).
     auto val = [&](int col) -> float {
         if constexpr (SUM) {
-            float v = 0.f;
-            for (int z = 0; z < nchunks; ++z) v += ws[((size_t)z * rows + row) * width + col];
+            const int hs = (nchunks + 1) / 2;
+            float v = 0.f, v2 = 0.f;
+            for (int z = 0; z < hs; ++z) v += ws[((size_t)z * rows + row) * width + col];
+            for (int z = hs; z < nchunks; ++z) v2 += ws[((size_t)z * rows + row) * width + col];
+            if (hs < nchunks) v = v + v2;
             if (sc) v = v * sc[col];
             if (bias) v = v + bias[col];
             return v;

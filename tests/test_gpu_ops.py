@@ -132,6 +132,33 @@ def test_config3_gemm_prefill_chunk(hip, oracle, fmt):
     assert rel_err(got, ref) < 1e-4
 
 
+@pytest.mark.parametrize("fmt", ["bf16", "q8", "q4"])
+def test_gemm_bits_independent_of_token_count(hip, fmt):
+    """4096 x 4096 weights (16 accumulation chunks of 256) on 256 CUs: 1,024
+    tokens fold K in registers on 8-wave blocks, 512 tokens run the two chunk
+    halves as separate 8-wave blocks (half sums folded by the reduce), 128
+    tokens one block per chunk (all 16 sums folded by the reduce). Each path
+    folds the chunks as two halves, so a token's outputs are the same bits in
+    all three (a prompt's results do not depend on how it is chunked)."""
+    rng = np.random.default_rng(5)
+    rows = cols = 4096
+    x = rng.standard_normal((1024, cols)).astype(np.float32)
+    if fmt == "bf16":
+        wd = hip.DeviceBuffer.from_array(synth.f32_to_bf16(rng.standard_normal((rows, cols)).astype(np.float32)))
+    else:
+        wd = hip.DeviceBuffer.from_array(random_quant(rng, fmt, rows, cols))
+
+    def bits(a):
+        return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+    y1024 = hip.gemm(wd, fmt, rows, cols, x)
+    y512 = hip.gemm(wd, fmt, rows, cols, x[:512])
+    y128 = hip.gemm(wd, fmt, rows, cols, x[:128])
+    assert np.array_equal(bits(y1024[:512]), bits(y512))
+    assert np.array_equal(bits(y512[:128]), bits(y128))
+    assert np.isfinite(y1024).all() and np.abs(y1024).max() > 0
+
+
 def _attn_case(rng, q_heads, kv_heads, hd, ctx, rows):
     k = synth.f32_to_bf16(rng.standard_normal((ctx, kv_heads, hd)).astype(np.float32))
     v = synth.f32_to_bf16(rng.standard_normal((ctx, kv_heads, hd)).astype(np.float32))
