@@ -1157,6 +1157,12 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
             }
         };
         long pos = pos0;
+        // Layer 0's rows of a step after the first are loaded at the end of
+        // the step before (after its last layer's partials, while the block
+        // waits for the LM head's input), so that the token's poll at the
+        // step's start has no refill in front of it (a wave's loads complete
+        // in order).
+        bool primed = false;
         for (int s = 0;; ++s) {
             const bool run = s < A()->steps;
             const int L = A()->L, ip = A()->ip;
@@ -1170,7 +1176,7 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
             const int nc = active ? (int)(min(kv_end, pos) - kv_start) : 0;
             const bool has_new = active && kv_end == ctx;
             const unsigned tb0 = tag_base(s);
-            refill(0, active, pos);
+            if (!primed) refill(0, active, pos);
             if (s > 0) token = reduce_token(s - 1, pos - 1, token);
             if (!run) break;
             if (wave == kDmaWave) dma_bytes(lds + A()->lds_emb, A()->embed + (size_t)token * A()->H, A()->H * 2);
@@ -1284,8 +1290,16 @@ __global__ __launch_bounds__(kThreads) void decode_flow_kernel(FusedArgs) {
                     bar();
                     mark(s, 16 * l + 6);
                 }
-                if (l + 1 < L) refill(l + 1, active, pos);
+                if (l + 1 < L) {
+                    refill(l + 1, active, pos);
+                } else if (s + 1 < A()->steps) {
+                    // The next step's layer 0 at position pos + 1 (context
+                    // pos + 2): its cached rows, up to position pos, are
+                    // all written by now.
+                    refill(0, itSplit() < (int)((pos + 1 + ip) / ip), pos + 1);
+                }
             }
+            primed = s + 1 < A()->steps;
             lm_head(s);
             ++pos;
         }
