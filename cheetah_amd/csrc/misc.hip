@@ -143,6 +143,78 @@ __global__ __launch_bounds__(kThreads) void residual_rmsnorm_rows_kernel(const f
     }
 }
 
+// residual_rmsnorm_rows_kernel for a row that fits the block's registers
+// (n <= EPT * kThreads) with at most ZM stored sums: every residual, stored
+// sum, scale, bias and gain of the thread's elements is loaded in one round
+// trip, and the row stays in registers for the norm instead of being read
+// back. The arithmetic and its order are residual_rmsnorm_rows_kernel's
+// (the same bits).
+template <int EPT, int ZM>
+__global__ __launch_bounds__(kThreads) void residual_rmsnorm_rows_reg_kernel(const float *ws, int nchunks,
+                                                                             const float *sc, const float *bias,
+                                                                             float *hidden, int rows, int n,
+                                                                             const uint16_t *gain, float eps,
+                                                                             float *out, uint16_t *xh, uint16_t *xl) {
+    __shared__ float red[kThreads / 64];
+    const int m = blockIdx.x;
+    const size_t MN = (size_t)rows * n;
+    float *h = hidden + (size_t)m * n;
+    const int hs = (nchunks + 1) / 2;  // sums in the first half
+    float hv[EPT], scv[EPT], bv[EPT], gv[EPT], t[ZM][EPT];
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {
+        const int i = (int)threadIdx.x + kThreads * k;
+        const bool in = i < n;
+        hv[k] = in ? h[i] : 0.f;
+        scv[k] = sc && in ? sc[i] : 0.f;
+        bv[k] = bias && in ? bias[i] : 0.f;
+        gv[k] = gain && in ? bf16_f32(gain[i]) : 0.f;
+#pragma unroll
+        for (int j = 0; j < ZM; ++j) t[j][k] = j < nchunks && in ? ws[(size_t)j * MN + (size_t)m * n + i] : 0.f;
+    }
+    float r[EPT], ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {
+        const int i = (int)threadIdx.x + kThreads * k;
+        r[k] = 0.f;
+        if (i < n) {
+            float v = 0.f, v2 = 0.f;
+#pragma unroll
+            for (int j = 0; j < ZM; ++j) {
+                if (j < hs) v += t[j][k];
+                else if (j < nchunks) v2 += t[j][k];
+            }
+            float x = hs < nchunks ? v + v2 : v;
+            if (sc) x = x * scv[k];
+            if (bias) x = x + bv[k];
+            r[k] = hv[k] + x;
+            h[i] = r[k];
+            ss = fmaf(r[k], r[k], ss);
+        }
+    }
+    if (!gain) return;
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float total = red[0] + red[1] + red[2] + red[3];
+    const float inv = 1.0f / sqrtf(total / (float)n + eps);
+    float *dst = out + (size_t)m * n;
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {
+        const int i = (int)threadIdx.x + kThreads * k;
+        if (i < n) {
+            const float v = r[k] * (inv * gv[k]);
+            dst[i] = v;
+            if (xh) {
+                const size_t o = (size_t)m * n + i;
+                const __bf16 hb = (__bf16)v;
+                xh[o] = __builtin_bit_cast(uint16_t, hb);
+                xl[o] = __builtin_bit_cast(uint16_t, (__bf16)(v - (float)hb));
+            }
+        }
+    }
+}
+
 // rope_heads (ops.rs:693-740) with the angle's cos/sin read from a table the
 // host filled with the same libm powf/sinf/cosf the reference calls, so q and
 // k come out bit-identical to the CPU path for identical inputs; then
@@ -316,8 +388,16 @@ int launch_residual_rmsnorm_rows(const float *ws, int nchunks, const float *sc, 
     if (!ws || nchunks <= 0 || !hidden || (gain && !out)) return fail("HIP backend: residual norm is missing a buffer.");
     if (!xh != !xl) return fail("HIP backend: rmsnorm needs both BF16 halves or neither.");
     if (rows > (size_t)INT32_MAX || n > (size_t)INT32_MAX) return fail("HIP backend: residual norm shape too large.");
-    hipLaunchKernelGGL(residual_rmsnorm_rows_kernel, dim3((unsigned)rows), dim3(kThreads), 0, s, ws, nchunks, sc, bias,
-                       hidden, (int)rows, (int)n, gain, eps, out, xh, xl);
+    // A row of 1,025 to 4,096 with at most four stored sums (a GEMM's two halves) in registers: one load round
+    // trip instead of one per 1,024 elements, and no read-back for the norm. Measured: Llama-3-8B Q4 512-row
+    // chunks 26 -> 18 us per call, prefill 20.4K -> 20.7K tok/s; the same form for Qwen2-0.5B's 896-wide rows
+    // (one pass either way) was slower (prefill 63.2K -> 60.1K).
+    if (n > 4 * kThreads && n <= 16 * kThreads && nchunks <= 4)
+        hipLaunchKernelGGL((residual_rmsnorm_rows_reg_kernel<16, 4>), dim3((unsigned)rows), dim3(kThreads), 0, s, ws,
+                           nchunks, sc, bias, hidden, (int)rows, (int)n, gain, eps, out, xh, xl);
+    else
+        hipLaunchKernelGGL(residual_rmsnorm_rows_kernel, dim3((unsigned)rows), dim3(kThreads), 0, s, ws, nchunks, sc,
+                           bias, hidden, (int)rows, (int)n, gain, eps, out, xh, xl);
     CHIP_CHECK(hipGetLastError());
     return 0;
 }
