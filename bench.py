@@ -72,8 +72,7 @@ def cpu_baseline(shape, weights, prompt, decode_steps: int):
     """The CPU oracle on a bounded sample of the same workload: the full
     512-token prefill (128-row chunks) and `decode_steps` greedy decodes, on
     a pool of one thread per physical core this process may use."""
-    import numpy as np
-
+    from cheetah_amd import workloads
     from oracle import oracle
 
     cpus = host_cpus()
@@ -84,7 +83,7 @@ def cpu_baseline(shape, weights, prompt, decode_steps: int):
     logits = m.forward(prompt, 0, chunk_rows=CHUNK)
     t1 = time.perf_counter()
     for step in range(decode_steps):
-        tok = int(len(logits) - 1 - np.argmax(logits[::-1]))
+        tok = workloads.greedy_token(logits)
         logits = m.forward([tok], PROMPT + step)
     t2 = time.perf_counter()
     return {
@@ -266,7 +265,7 @@ def main() -> int:
 
     import numpy as np
 
-    from cheetah_amd import configs, hip, synth
+    from cheetah_amd import configs, hip, synth, workloads
 
     shape = configs.QWEN2_0_5B
     hip.init(0)
@@ -348,7 +347,7 @@ def main() -> int:
         out = []
         t0 = time.perf_counter()
         for step in range(DECODE):
-            tok = int(len(logits) - 1 - np.argmax(logits[::-1]))
+            tok = workloads.greedy_token(logits)
             out.append(tok)
             logits = g.forward(np.array([tok], np.uint32), PROMPT + step)
         return time.perf_counter() - t0, out

@@ -17,7 +17,23 @@ from __future__ import annotations
 
 import time
 
+import numpy as np
+
 from . import configs, hip, synth
+
+
+def greedy_token(logits) -> int:
+    """Greedy sampling as the reference engine does it on the host: the
+    index of the largest logit, the last one on ties (engine.rs:2247-2253).
+    One forward argmax; the reversed search (a strided pass, about three
+    times slower over a 152K vocabulary) runs only when a later logit ties
+    the first maximum or the maximum is NaN."""
+    logits = np.asarray(logits)
+    i = int(np.argmax(logits))
+    m = logits[i]
+    if np.isnan(m) or (i + 1 < logits.size and logits[i + 1:].max() == m):
+        return int(logits.size - 1 - np.argmax(logits[::-1]))
+    return i
 
 
 def _timed(fn, *args, **kw):
