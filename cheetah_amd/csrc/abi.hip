@@ -300,7 +300,7 @@ static AttnJob attention_job(const float *q, const cheetah_hip_kv_view *kv, uint
     j.prefill = rows > 1;
     size_t need = attention_part_floats(rows, (int)q_heads, (int)splits, (int)kv->head_dim);
     if (j.prefill && attention_prefill_on_mfma(j.g, (int)q_heads))
-        need = std::max(need, attention_part_floats(rows, (int)q_heads, attention_prefill_splits(offset + rows),
+        need = std::max(need, attention_part_floats(rows, (int)q_heads, attention_prefill_splits(offset + rows, j.span),
                                                     (int)kv->head_dim));
     *need_floats = need;
     return j;

@@ -149,6 +149,10 @@ int launch_gather_rows(const uint8_t *src, uint8_t *dst, const int32_t *map, siz
 // [0, pos0 + i]. q row stride q_stride floats. The split count (at most
 // attention_max_splits()) is the caller's: decode graphs need a fixed grid.
 // Partial buffers hold rows * q_heads * splits * (head_dim + 2) floats.
+// Keys per split of the matrix-core chunked prefill when the caller names
+// no span (attention_prefill_span gives a model's).
+constexpr int kDefaultPrefillSpan = 1024;
+
 struct AttnJob {
     const float *q = nullptr;
     size_t q_stride = 0;
@@ -166,6 +170,9 @@ struct AttnJob {
     // ignores `splits`; part must then hold part_floats >= the partials.
     bool prefill = false;
     size_t part_floats = 0;
+    // Keys per prefill split (absolute position ranges [s span, (s+1) span)):
+    // a row's bits depend on it, so a model keeps one span for its lifetime.
+    int span = kDefaultPrefillSpan;
     // Decode (one row) from the raw QKV row [q | k | v] of launch_rope_append
     // instead of q: the kernel rotates q itself and rotates and appends the
     // position's K/V row (what launch_rope_append would write; q unused).
@@ -188,7 +195,10 @@ size_t attention_part_floats(size_t rows, int q_heads, int splits, int head_dim)
 // split per 64-position tile.
 int attention_decode_splits(size_t ctx, int kv_heads, size_t rows, bool kv_f32);
 int attention_max_splits();
-int attention_prefill_splits(size_t ctx);
+int attention_prefill_splits(size_t ctx, int span = kDefaultPrefillSpan);
+// A model's prefill span from its KV capacity: the largest power of two at
+// most capacity / 8, and at least kDefaultPrefillSpan.
+int attention_prefill_span(size_t kv_capacity);
 bool attention_prefill_on_mfma(const KvGeom &g, int q_heads);
 
 // Greedy argmax (ties -> last index, total order) of logits[n]; writes the

@@ -673,7 +673,8 @@ int init_instance(cheetah_hip_model *m) {
     // Prefill partials: the fixed VALU split count, or the matrix-core
     // kernel's span splits at full capacity; decode: attention_max_splits.
     const size_t prefill_splits =
-        std::max((size_t)kPrefillSplits, (size_t)attention_prefill_splits(sh.kv_capacity));
+        std::max((size_t)kPrefillSplits,
+                 (size_t)attention_prefill_splits(sh.kv_capacity, attention_prefill_span(sh.kv_capacity)));
     const size_t part_rows = std::max(R * prefill_splits, (size_t)attention_max_splits());
     m->part_floats = part_rows * c.q_heads * (c.head_dim + 2);
     CHIP_TRY(m->mem.alloc(&m->part, m->part_floats));
@@ -1042,6 +1043,7 @@ int enqueue_chunk(cheetah_hip_model *m, const uint32_t *tokens_dev, size_t rows,
         aj.part = m->part;
         aj.part_floats = m->part_floats;
         aj.prefill = true;
+        aj.span = attention_prefill_span(m->sh->kv_capacity);
         // The matrix-core prefill writes the o_proj input halves itself.
         const bool halves = attention_prefill_on_mfma(aj.g, aj.q_heads);
         if (halves) {
