@@ -75,7 +75,7 @@ def test_llama3_8b_q4_8k_f32_kv_matches_reference(hip):
         _check_logits(info["prefill_logits"], gold["prefill_logits_head"], gold.get("prefill_vocab_sample"))
         tokens, dec = _decode(g, info["tokens"][0], 8192)
         assert tokens[:32] == gold["tokens"][:32]
-        golden_checks.check_decode_samples(dec, tokens, gold, required=False)
+        golden_checks.check_decode_samples(dec, tokens, gold, required=True)
     finally:
         g.close()
 
@@ -102,7 +102,7 @@ def test_llama3_8b_q4_8k_bf16_kv_32_greedy_steps(hip):
         _check_logits(info["prefill_logits"], gold["prefill_logits_head"], gold.get("prefill_vocab_sample"))
         tokens, dec = _decode(g, info["tokens"][0], 8192)
         assert tokens[:32] == gold["tokens"][:32]
-        golden_checks.check_decode_samples(dec, tokens, gold, required=False)
+        golden_checks.check_decode_samples(dec, tokens, gold, required=True)
         head = ref["prefill_logits_head"]
         vs_ref = golden_checks.rel(info["prefill_logits"][: len(head)], head)
         print(f"[large] bf16-KV prefill logits vs the reference: {vs_ref:.4f} relative", flush=True)
