@@ -123,9 +123,9 @@ def _qwen2_7b(hip, kv, gold):
         _check_logits(info["turn2_logits"], gold["turn2_logits_head"], gold.get("turn2_vocab_sample"))
         tokens, dec = _decode(g, info["tokens"][0], 32768)
         assert tokens[:32] == gold["tokens"][:32]
-        # The BF16-KV golden holds whole-vocabulary samples of decode steps
-        # 1, 16 and 32 (tests/golden/make_golden.py).
-        golden_checks.check_decode_samples(dec, tokens, gold, required=kv == "bf16")
+        # Both goldens hold whole-vocabulary samples of decode steps 1, 16
+        # and 32 (tests/golden/make_golden.py).
+        golden_checks.check_decode_samples(dec, tokens, gold, required=True)
     finally:
         g.close()
     return tokens
